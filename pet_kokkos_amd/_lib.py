@@ -1,0 +1,85 @@
+"""ctypes binding of libpet_attn.so, the C ABI of include/pet_attn.h.
+
+Loading fails loudly when the library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpet_attn.so")
+
+EXPORTS = (
+    "pet_attn_scale",
+    "pet_attn_strerror",
+    "pet_attn_fwd",
+    "pet_attn_bwd",
+    "pet_attention",
+    "pet_attention_bwd_workspace",
+    "pet_attention_bwd",
+)
+
+OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX = range(9)
+MAX_SLOTS = 256
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [
+        ("n_atoms", ctypes.c_int),
+        ("n_rows", ctypes.c_int),
+        ("slots", ctypes.c_int),
+        ("heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("dead", ctypes.c_int),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class PetAttnError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        self.code = code
+        super().__init__(f"{what}: {strerror(code)} (code {code})")
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with `python -m pet_kokkos_amd.build` "
+                          "(the attention has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.pet_attn_scale.restype = ctypes.c_float
+    lib.pet_attn_scale.argtypes = [ctypes.c_int, ctypes.c_double]
+    lib.pet_attn_strerror.restype = ctypes.c_char_p
+    lib.pet_attn_strerror.argtypes = [ctypes.c_int]
+    sp = ctypes.POINTER(Shape)
+    lib.pet_attn_fwd.restype = ctypes.c_int
+    lib.pet_attn_fwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
+    lib.pet_attn_bwd.restype = ctypes.c_int
+    lib.pet_attn_bwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P]
+    lib.pet_attention.restype = ctypes.c_int
+    lib.pet_attention.argtypes = [sp, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P]
+    lib.pet_attention_bwd_workspace.restype = ctypes.c_size_t
+    lib.pet_attention_bwd_workspace.argtypes = [sp]
+    lib.pet_attention_bwd.restype = ctypes.c_int
+    lib.pet_attention_bwd.argtypes = [sp, _P, _I64, ctypes.c_int, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P,
+                                      _P, _P, _P, ctypes.c_float, _P, ctypes.c_size_t, _P]
+    _lib = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    return load().pet_attn_strerror(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    if code != OK:
+        raise PetAttnError(code, what)

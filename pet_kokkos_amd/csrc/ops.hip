@@ -1,0 +1,127 @@
+// The op level of PET's attention: attention() and attention_bwd() as the
+// reference's pet::attention / pet::attention_bwd run them
+// (peterspackman/pet-kokkos src/attention.cpp:1520-1558, :1814-1907): the core
+// kernels of attention.hip plus the output and input linears, whose GEMMs go to
+// rocBLAS (fp32, atomics off so each product has one fixed summation order).
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <cstdint>
+#include <mutex>
+
+#include "../../include/pet_attn.h"
+
+namespace pet_attn {
+
+// One rocBLAS handle per device, made on first use and kept for the process.
+rocblas_handle blas_handle() {
+  static std::mutex mu;
+  static rocblas_handle handles[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!handles[dev]) {
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+    rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);
+    handles[dev] = h;
+  }
+  return handles[dev];
+}
+
+// out[M, Nout] (ld ldo, row-major) = in[M, K] W[Nout, K]^T + beta out.
+int gemm_nt(float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int Nout, int K, float beta,
+            hipStream_t st) {
+  rocblas_handle h = blas_handle();
+  if (!h) return PET_ATTN_EBLAS;
+  if (rocblas_set_stream(h, st) != rocblas_status_success) return PET_ATTN_EBLAS;
+  const float one = 1.0f;
+  // Column-major view: out^T [Nout, M] = W [Nout, K] (stored as W^T, lda K) . in^T [K, M].
+  const rocblas_status s = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, Nout, M, K, &one, W,
+                                         K, in, rocblas_int(ldi), &beta, out, rocblas_int(ldo));
+  return s == rocblas_status_success ? PET_ATTN_OK : PET_ATTN_EBLAS;
+}
+// in_adj[M, K] = out_adj[M, Nout] W[Nout, K] + beta in_adj.
+int gemm_nn(float* in_adj, int64_t ldi, const float* out_adj, int64_t ldo, const float* W, int M, int Nout, int K,
+            float beta, hipStream_t st) {
+  rocblas_handle h = blas_handle();
+  if (!h) return PET_ATTN_EBLAS;
+  if (rocblas_set_stream(h, st) != rocblas_status_success) return PET_ATTN_EBLAS;
+  const float one = 1.0f;
+  // Column-major view: in_adj^T [K, M] = W^T [K, Nout] (W stored row-major, lda K) . out_adj^T [Nout, M].
+  const rocblas_status s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, K, M, Nout, &one, W, K,
+                                         out_adj, rocblas_int(ldo), &beta, in_adj, rocblas_int(ldi));
+  return s == rocblas_status_success ? PET_ATTN_OK : PET_ATTN_EBLAS;
+}
+
+// out[r][j] = b[j] (or 0 without a bias): the bias the GEMM then accumulates onto.
+__global__ void fill_bias_kernel(float* __restrict__ out, int64_t ldo, const float* __restrict__ b, int M, int Nc) {
+  const int64_t total = int64_t(M) * Nc;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = i / Nc;
+    const int j = int(i - r * Nc);
+    out[r * ldo + j] = b ? b[j] : 0.0f;
+  }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace pet_attn
+
+using namespace pet_attn;
+
+extern "C" {
+
+int pet_attention(const pet_attn_shape* sh, float* out, int64_t ldo, const float* qkv, int64_t ldq,
+                  const float* cf_seq, int64_t ldc, const float* w_out, const float* b_out, const int* off,
+                  float* merged, float* ml, void* stream) {
+  if (!sh || !out || !w_out || !merged) return PET_ATTN_EINVAL;
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  if (ldo < D) return PET_ATTN_EINVAL;
+  if (int e = pet_attn_fwd(sh, qkv, ldq, off, cf_seq, ldc, merged, D, ml, stream)) return e;
+  if (T == 0) return PET_ATTN_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float beta = 0.0f;
+  if (b_out) {
+    const int64_t total = int64_t(T) * D;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(fill_bias_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, out, ldo,
+                       b_out, T, D);
+    if (hipGetLastError() != hipSuccess) return PET_ATTN_ELAUNCH;
+    beta = 1.0f;
+  }
+  return gemm_nt(out, ldo, merged, D, w_out, T, D, D, beta, st);
+}
+
+size_t pet_attention_bwd_workspace(const pet_attn_shape* sh) {
+  if (!sh) return 0;
+  const size_t D = size_t(sh->heads) * sh->head_dim, T = size_t(sh->n_rows);
+  return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) +
+         align256(sizeof(float) * size_t(sh->n_atoms) * sh->slots * sh->heads);
+}
+
+int pet_attention_bwd(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int d_in, float* cf_seq_adj,
+                      int64_t ldca, const float* out_adj, int64_t ldo, const float* qkv, int64_t ldq,
+                      const float* cf_seq, int64_t ldc, const float* w_in, const float* w_out, const int* off,
+                      const float* merged, const float* ml, float beta, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  if (!sh || !in_adj || !out_adj || !w_in || !w_out || d_in < 1 || ldi < d_in) return PET_ATTN_EINVAL;
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  if (ldo < D) return PET_ATTN_EINVAL;
+  if (!workspace || workspace_bytes < pet_attention_bwd_workspace(sh)) return PET_ATTN_EWORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
+  if (T == 0) return PET_ATTN_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  float* dmerged = reinterpret_cast<float*>(ws);
+  float* qkv_adj = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
+  float* cfh = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D) +
+                                        align256(sizeof(float) * size_t(T) * 3 * D));
+  if (int e = gemm_nn(dmerged, D, out_adj, ldo, w_out, T, D, D, 0.0f, st)) return e;
+  if (int e = pet_attn_bwd(sh, qkv, ldq, off, dmerged, D, merged, D, ml, cf_seq, ldc, qkv_adj, 3 * D, cfh,
+                           cf_seq_adj, ldca, stream))
+    return e;
+  return gemm_nn(in_adj, ldi, qkv_adj, 3 * D, w_in, T, 3 * D, d_in, beta, st);
+}
+
+}  // extern "C"

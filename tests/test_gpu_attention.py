@@ -1,0 +1,236 @@
+"""Parity of the HIP attention (through the C ABI) with the CPU oracle and the
+golden vectors, on an MI355X.
+
+Tolerance: every attention output and gradient within
+1e-5 relative of the oracle's fp32 result, measured as
+max|gpu - ref| / max|ref| per tensor (RTOL below); the saved statistics and
+the cf adjoint likewise. Run to run the kernels are bit-identical.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from pet_kokkos_amd import attention as A
+from pet_kokkos_amd import systems
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "attn_*.npz")))
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    den = max(np.abs(b).max(), 1e-30) if b.size else 1.0
+    return np.abs(a - b).max() / den if a.size else 0.0
+
+
+def dev(x, device, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device=device, dtype=dtype)
+
+
+def gpu_fwd_bwd(device, off, cf_seq, qkv, dm, H, hd, temperature=1.0, dead=False, cf_adj0=None):
+    N = len(off) - 1
+    q, g, cf = dev(qkv, device), dev(dm, device), dev(cf_seq, device)
+    o = dev(off, device, torch.int32)
+    merged, ml = A.attn_fwd(q, o, cf, H, hd, temperature, dead=dead)
+    start = None if cf_adj0 is None else dev(cf_adj0, device)
+    qa, ca, cfh = A.attn_bwd(q, o, g, merged, ml, cf, H, hd, temperature, cf_seq_adj=start, dead=dead)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in (merged, ml, qa, ca, cfh)]
+
+
+def check_against_oracle(device, name, off, cf_seq, qkv, dm, H, hd, temperature=1.0, dead=False, T=None):
+    say(f"[gpu] {name}: N={len(off) - 1} T={qkv.shape[0]} S={cf_seq.shape[1]} H={H} hd={hd}")
+    m, ml, qa, ca, cfh = gpu_fwd_bwd(device, off, cf_seq, qkv, dm, H, hd, temperature, dead)
+    rm, rml = oracle.attn_fwd(qkv, off, cf_seq, H, hd, temperature, dead=dead)
+    rqa, rca, rcfh = oracle.attn_bwd(qkv, off, dm, rm, rml, cf_seq, H, hd, temperature, dead=dead)
+    errs = dict(merged=rel(m, rm), qkv_adj=rel(qa, rqa), cf_seq_adj=rel(ca, rca), cfh=rel(cfh, rcfh))
+    live = rml[:, 1] > 0
+    assert np.array_equal(ml[:, 1] > 0, live), "live queries differ"
+    assert np.all(ml[~live, 0] == np.float32(-1e30)) and np.all(ml[~live, 1] == 0)
+    errs["ml.max"] = rel(ml[live, 0], rml[live, 0])
+    errs["ml.invl"] = rel(ml[live, 1], rml[live, 1])
+    say("    ", {k: f"{v:.2e}" for k, v in errs.items()})
+    for k, v in errs.items():
+        assert v <= RTOL, f"{name}: {k} off by {v:.3e} relative"
+    return m, ml, qa, ca, cfh
+
+
+def random_case(counts, H, hd, seed=0, cf_kind="random", extra=0):
+    base = systems.tokens_from_counts(counts, seed=seed, cf_kind=cf_kind)
+    tk = systems.tokens_from_counts(counts, seed=seed, cf_kind=cf_kind, slots=base.slots + extra)
+    rng = np.random.default_rng(seed + 7)
+    D = H * hd
+    qkv = rng.standard_normal((tk.n_rows, 3 * D)).astype(np.float32)
+    dm = rng.standard_normal((tk.n_rows, D)).astype(np.float32)
+    return tk, qkv, dm
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p) for p in GOLDEN])
+def test_golden_vectors(device, path):
+    g = np.load(path)
+    H, hd, temp = int(g["heads"]), int(g["head_dim"]), float(g["temperature"])
+    say(f"[gpu] golden {os.path.basename(path)}")
+    m, ml, qa, ca, cfh = gpu_fwd_bwd(device, g["off"], g["cf_seq"], g["qkv"], g["dmerged"], H, hd, temp)
+    assert rel(m, g["merged"]) <= RTOL
+    assert rel(qa, g["qkv_adj"]) <= RTOL
+    assert rel(cfh, g["cfh"]) <= 10 * RTOL
+    assert rel(ca, g["cf_seq_adj"]) <= 10 * RTOL
+    live = g["ml"][:, 1] > 0
+    assert np.array_equal(ml[:, 1] > 0, live)
+    assert rel(ml[live, 1], g["ml"][live, 1]) <= RTOL
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c4", "c3"])
+def test_configs(device, cfg):
+    conf, tk = systems.config_tokens(cfg)
+    inp = systems.attention_inputs(tk, conf.d_model, conf.heads, seed=1)
+    rng = np.random.default_rng(3)
+    dm = rng.standard_normal((tk.n_rows, conf.d_model)).astype(np.float32)
+    check_against_oracle(device, f"config {cfg} ({conf.name})", tk.off, tk.cf_seq, inp["qkv"], dm, conf.heads,
+                         conf.head_dim)
+
+
+@pytest.mark.parametrize("hd", [16, 32, 48, 64, 80, 96, 112, 128])
+def test_head_dims(device, hd):
+    counts = [0, 15, 16, 31, 47, 5, 60, 33]
+    tk, qkv, dm = random_case(counts, 2, hd, seed=hd, cf_kind="zeros", extra=2)
+    check_against_oracle(device, f"head_dim {hd}", tk.off, tk.cf_seq, qkv, dm, 2, hd, temperature=0.8)
+
+
+@pytest.mark.parametrize("hd,top", [(16, 255), (32, 200), (64, 140)])
+def test_many_slots(device, hd, top):
+    # more than 8 query blocks: the 1024-thread kernels
+    counts = [top, 3, top // 2, 130]
+    tk, qkv, dm = random_case(counts, 2, hd, seed=top, cf_kind="random")
+    check_against_oracle(device, f"many slots hd {hd} S {tk.slots}", tk.off, tk.cf_seq, qkv, dm, 2, hd)
+
+
+def test_too_many_slots_for_lds(device):
+    tk, qkv, dm = random_case([250, 3], 1, 128, seed=0)
+    with pytest.raises(RuntimeError):
+        gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 1, 128)
+
+
+def test_edge_cases(device):
+    # isolated atoms, block boundaries, cf = 0 keys and queries, padding slots
+    counts = [0, 0, 1, 14, 15, 16, 17, 31, 32, 33, 63, 0]
+    tk, qkv, dm = random_case(counts, 4, 32, seed=5, cf_kind="zeros", extra=5)
+    check_against_oracle(device, "edge cases", tk.off, tk.cf_seq, qkv, dm, 4, 32)
+
+
+def test_dead_rows(device):
+    tk, qkv, dm = random_case([10, 22, 5], 2, 32, seed=8)
+    T = tk.n_rows + 9
+    rng = np.random.default_rng(1)
+    qkv = np.concatenate([qkv, rng.standard_normal((9, qkv.shape[1])).astype(np.float32)])
+    dm = np.concatenate([dm, rng.standard_normal((9, dm.shape[1])).astype(np.float32)])
+    m, _, qa, _, _ = check_against_oracle(device, "dead rows", tk.off, tk.cf_seq, qkv, dm, 2, 32, dead=True)
+    assert np.all(m[tk.n_rows:] == 0) and np.all(qa[tk.n_rows:] == 0)
+    assert T == m.shape[0]
+
+
+def test_bit_identical_repeats(device):
+    conf, tk = systems.config_tokens("c1")
+    inp = systems.attention_inputs(tk, conf.d_model, conf.heads, seed=2)
+    dm = np.random.default_rng(4).standard_normal((tk.n_rows, conf.d_model)).astype(np.float32)
+    say("[gpu] bitwise repeats c1")
+    first = gpu_fwd_bwd(device, tk.off, tk.cf_seq, inp["qkv"], dm, conf.heads, conf.head_dim)
+    for _ in range(3):
+        again = gpu_fwd_bwd(device, tk.off, tk.cf_seq, inp["qkv"], dm, conf.heads, conf.head_dim)
+        for a, b in zip(first, again):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_cf_adjoint_accumulates(device):
+    tk, qkv, dm = random_case([12, 40, 7], 2, 32, seed=6)
+    start = np.random.default_rng(0).standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
+    say("[gpu] cf adjoint accumulates")
+    _, _, _, ca0, _ = gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 2, 32)
+    _, _, _, ca1, _ = gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 2, 32, cf_adj0=start)
+    assert np.array_equal(ca1, (start + ca0).astype(np.float32))
+
+
+def test_strided_views_and_stream(device):
+    # leading dimensions above the widths (views into wider buffers), on a side stream
+    tk, qkv, dm = random_case([20, 9, 33], 2, 32, seed=12)
+    D = 64
+    T = tk.n_rows
+    say("[gpu] strided views")
+    big = torch.zeros((T, 3 * D + 8), device=device)
+    big[:, :3 * D] = dev(qkv, device)
+    q = big[:, :3 * D]
+    gbig = torch.zeros((T, D + 4), device=device)
+    gbig[:, :D] = dev(dm, device)
+    g = gbig[:, :D]
+    cfbig = torch.zeros((tk.n_atoms, tk.slots + 4), device=device)
+    cfbig[:, :tk.slots] = dev(tk.cf_seq, device)
+    cf = cfbig[:, :tk.slots]
+    mbig = torch.full((T, D + 12), 7.0, device=device)
+    m = mbig[:, :D]
+    qabig = torch.full((T, 3 * D + 4), 7.0, device=device)
+    o = dev(tk.off, device, torch.int32)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _, ml = A.attn_fwd(q, o, cf, 2, 32, merged=m)
+        qa, ca, _ = A.attn_bwd(q, o, g, m, ml, cf, 2, 32, qkv_adj=qabig[:, :3 * D])
+    torch.cuda.synchronize()
+    rm, rml = oracle.attn_fwd(qkv, tk.off, tk.cf_seq, 2, 32)
+    rqa, rca, _ = oracle.attn_bwd(qkv, tk.off, dm, rm, rml, tk.cf_seq, 2, 32)
+    assert rel(m.cpu().numpy(), rm) <= RTOL
+    assert rel(qa.cpu().numpy(), rqa) <= RTOL
+    assert rel(ca.cpu().numpy(), rca) <= RTOL
+    assert torch.all(mbig[:, D:] == 7.0) and torch.all(qabig[:, 3 * D:] == 7.0)
+
+
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_op_level_attention(device, beta):
+    # attention()/attention_bwd() with the output and input linears, as the
+    # reference's feedforward (beta 0) and residual (beta 1) featurizers call them.
+    conf, tk = systems.config_tokens("c1")
+    H, hd, D = conf.heads, conf.head_dim, conf.d_model
+    inp = systems.attention_inputs(tk, D, H, seed=5)
+    rng = np.random.default_rng(9)
+    in_adj0 = rng.standard_normal((tk.n_rows, D)).astype(np.float32)
+    cf_adj0 = rng.standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
+    temp = 1.3
+    say(f"[gpu] op level beta={beta}")
+    ws = A.Workspace(device)
+    t = A.Tokens(dev(tk.off, device, torch.int32), tk.n_atoms)
+    out = torch.empty((tk.n_rows, D), device=device)
+    qkv, cf = dev(inp["qkv"], device), dev(tk.cf_seq, device)
+    w_in, w_out, b_out = dev(inp["w_in"], device), dev(inp["w_out"], device), dev(inp["b_out"], device)
+    A.attention(ws, "L0.a0", out, qkv, cf, w_out, b_out, t, tk.slots, H, hd, temp, True)
+    in_adj = dev(in_adj0, device)
+    cf_adj = dev(cf_adj0, device)
+    A.attention_bwd(ws, "L0.a0", in_adj, cf_adj, dev(inp["out_adj"], device), qkv, cf, w_in, w_out, t, tk.slots, H,
+                    hd, temp, beta)
+    torch.cuda.synchronize()
+    rout, rm, rml = oracle.attention(inp["qkv"], tk.off, tk.cf_seq, inp["w_out"], inp["b_out"], H, hd, temp)
+    rin, rca = oracle.attention_bwd(inp["out_adj"], inp["qkv"], tk.off, tk.cf_seq, inp["w_in"], inp["w_out"], rm, rml,
+                                    H, hd, temp, cf_seq_adj=cf_adj0, in_adj=in_adj0, beta=beta)
+    e = dict(out=rel(out.cpu().numpy(), rout), in_adj=rel(in_adj.cpu().numpy(), rin),
+             cf_seq_adj=rel(cf_adj.cpu().numpy(), rca))
+    say("    ", {k: f"{v:.2e}" for k, v in e.items()})
+    for k, v in e.items():
+        assert v <= RTOL, k
+
+
+def test_backward_before_forward_raises(device):
+    ws = A.Workspace(device)
+    with pytest.raises(RuntimeError):
+        ws.peek2("nothing:merged")
