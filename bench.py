@@ -90,7 +90,7 @@ def main():
     merged = torch.empty((T, D), device=device)
     ml = torch.empty((N * H * S, 2), device=device)
     qkv_adj = torch.empty((T, 3 * D), device=device)
-    cfh = torch.empty((N * S, H), device=device)
+    cfh = torch.empty((N, H, S), device=device)
     cf_adj = torch.zeros((N, S), device=device)
 
     def step(ev=None):

@@ -46,7 +46,7 @@ enum {
   PET_ATTN_OK = 0,
   PET_ATTN_EINVAL = 1,      /* a null pointer, negative size or leading dimension too small */
   PET_ATTN_EHEADDIM = 2,    /* head_dim not one the kernels hold (a multiple of 16, <= 128) */
-  PET_ATTN_ESLOTS = 3,      /* slots (S) above PET_ATTN_MAX_SLOTS */
+  PET_ATTN_ESLOTS = 3,      /* slots (S) above pet_attn_max_slots(head_dim) */
   PET_ATTN_EALIGN = 4,      /* a pointer or leading dimension not a multiple of 4 floats */
   PET_ATTN_ELAUNCH = 5,     /* a HIP launch or runtime call failed */
   PET_ATTN_EBLAS = 6,       /* the BLAS call of a linear failed */
@@ -73,6 +73,13 @@ PET_ATTN_API float pet_attn_scale(int head_dim, double temperature);
 
 PET_ATTN_API const char* pet_attn_strerror(int code);
 
+/* The most slots (S) both kernels hold for this head_dim on the current
+ * device, their staged rows bounded by its LDS (at most PET_ATTN_MAX_SLOTS);
+ * 0 for a head_dim they do not hold. Calls with a larger S return
+ * PET_ATTN_ESLOTS. No counterpart in the reference, whose kernels stream
+ * 16-token blocks through registers. */
+PET_ATTN_API int pet_attn_max_slots(int head_dim);
+
 /* ---- the core kernels -------------------------------------------------- */
 
 /* Forward: merged[T, D] (ld ldm) = per-head attention of qkv[T, 3D] (ld ldq);
@@ -87,9 +94,10 @@ PET_ATTN_API int pet_attn_fwd(const pet_attn_shape* shape, const float* qkv, int
 
 /* Backward of the core: from dmerged [T, D] (ld ldg, the adjoint of merged),
  * the forward's merged (ld ldm) and ml, writes qkv_adj [T, 3D] (ld lda; dQ |
- * dK | dV, dead rows zeroed), cfh [N*S, H] (scratch: per key slot and head,
- * the sum over queries of dS) and adds sum_h cfh / cf onto cf_seq_adj [N, S]
- * (ld ldca) where cf > 0.
+ * dK | dV, dead rows zeroed), cfh [N, H, S] (scratch: per atom, head and key
+ * slot, the sum over queries of dS; the reference's cfh [N*S, H] transposed so
+ * that one (atom, head) writes one contiguous row) and adds sum_h cfh / cf onto
+ * cf_seq_adj [N, S] (ld ldca) where cf > 0.
  * Replaces the kernel half of attention_bwd_impl<HD> (reference
  * src/attention.cpp:1814-1907: Queries, Keys, mfma::backward, attn_bwd_cf,
  * zero_dead). */
@@ -112,7 +120,7 @@ PET_ATTN_API int pet_attention(const pet_attn_shape* shape, float* out, int64_t 
                   const int* off, float* merged, float* ml, void* stream);
 
 /* Bytes of device workspace pet_attention_bwd needs: dmerged [T, D],
- * qkv_adj [T, 3D] and cfh [N*S, H], each 256-byte aligned. */
+ * qkv_adj [T, 3D] and cfh [N, H, S], each 256-byte aligned. */
 PET_ATTN_API size_t pet_attention_bwd_workspace(const pet_attn_shape* shape);
 
 /* attention_bwd(): dmerged = out_adj . w_out; the core backward; then

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "libpet_attn.so")
 EXPORTS = (
     "pet_attn_scale",
     "pet_attn_strerror",
+    "pet_attn_max_slots",
     "pet_attn_fwd",
     "pet_attn_bwd",
     "pet_attention",
@@ -60,6 +61,8 @@ def load() -> ctypes.CDLL:
     lib.pet_attn_scale.argtypes = [ctypes.c_int, ctypes.c_double]
     lib.pet_attn_strerror.restype = ctypes.c_char_p
     lib.pet_attn_strerror.argtypes = [ctypes.c_int]
+    lib.pet_attn_max_slots.restype = ctypes.c_int
+    lib.pet_attn_max_slots.argtypes = [ctypes.c_int]
     sp = ctypes.POINTER(Shape)
     lib.pet_attn_fwd.restype = ctypes.c_int
     lib.pet_attn_fwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]

@@ -119,7 +119,7 @@ def attn_bwd(qkv: torch.Tensor, off: torch.Tensor, dmerged: torch.Tensor, merged
              cf_seq_adj: torch.Tensor | None = None, N: int | None = None, dead: bool = False,
              qkv_adj: torch.Tensor | None = None, cfh: torch.Tensor | None = None):
     """The core backward: (qkv_adj [T, 3D], cf_seq_adj [N, S] accumulated onto,
-    cfh [N*S, H])."""
+    cfh [N, H, S], each key slot's sum over queries of dS per head)."""
     lib = _lib.load()
     D = heads * head_dim
     T = qkv.shape[0]
@@ -128,7 +128,7 @@ def attn_bwd(qkv: torch.Tensor, off: torch.Tensor, dmerged: torch.Tensor, merged
     if qkv_adj is None:
         qkv_adj = torch.empty((T, 3 * D), dtype=torch.float32, device=qkv.device)
     if cfh is None:
-        cfh = torch.empty((N * S, heads), dtype=torch.float32, device=qkv.device)
+        cfh = torch.empty((N, heads, S), dtype=torch.float32, device=qkv.device)
     if cf_seq_adj is None:
         cf_seq_adj = torch.zeros((N, S), dtype=torch.float32, device=qkv.device)
     sh = shape(N, T, S, heads, head_dim, temperature, dead)

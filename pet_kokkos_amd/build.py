@@ -39,6 +39,23 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP library cannot be built")
 
 
+CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "attention_api_test.cpp")
+CPP_TEST = os.path.join(ROOT, "tests", "cpp", "attention_api_test")
+
+
+def build_cpp_test(verbose: bool = False) -> str:
+    """The C++ caller of include/pet/attention.hpp that tests/test_gpu_cpp_api.py runs."""
+    cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+           "-o", CPP_TEST, CPP_TEST_SRC, "-L", HERE, "-lpet_attn", "-Wl,-rpath,$ORIGIN/../../pet_kokkos_amd"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed ({res.returncode}) building {CPP_TEST}")
+    return CPP_TEST
+
+
 def build(verbose: bool = False) -> str:
     """Compile every HIP source into LIB (always recompiles) and return its path."""
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
@@ -52,6 +69,7 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed ({res.returncode}) building {LIB}")
     os.replace(tmp, LIB)
+    build_cpp_test(verbose)
     return LIB
 
 

@@ -1,0 +1,61 @@
+"""A fixed workload for rocprofv3: K core attention fwd+bwd steps on one of
+the benchmark configurations, preceded by a plain device copy of known size
+(the calibration kernel that HBM byte counters are scaled by).
+
+    python -m pet_kokkos_amd.profiling --config c3 --steps 20 --copy-mib 1024
+
+Under ``rocprofv3 --kernel-trace --stats`` it gives each kernel's average
+duration; under ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``) each
+kernel's HBM kilobytes per dispatch, with the copy's own reading of a known
+``--copy-mib`` MiB read and write as the scale.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import torch
+
+from . import attention as A
+from . import systems
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", default="c3", choices=sorted(systems.CONFIGS))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--copy-mib", type=int, default=1024)
+    args = ap.parse_args(argv)
+    device = torch.device("cuda", 0)
+    conf, tk = systems.config_tokens(args.config, seed=0)
+    H, hd, D = conf.heads, conf.head_dim, conf.d_model
+    N, S, T = tk.n_atoms, tk.slots, tk.n_rows
+    g = torch.Generator(device=device)
+    g.manual_seed(7)
+    qkv = torch.randn((T, 3 * D), device=device, generator=g)
+    dm = torch.randn((T, D), device=device, generator=g)
+    off = torch.from_numpy(tk.off).to(device)
+    cf = torch.from_numpy(tk.cf_seq).to(device)
+    merged = torch.empty((T, D), device=device)
+    ml = torch.empty((N * H * S, 2), device=device)
+    qkv_adj = torch.empty((T, 3 * D), device=device)
+    cfh = torch.empty((N, H, S), device=device)
+    cf_adj = torch.zeros((N, S), device=device)
+    n = args.copy_mib * (1 << 20) // 4
+    src = torch.randn(n, device=device, generator=g)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)  # calibration: reads and writes copy_mib MiB
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        A.attn_fwd(qkv, off, cf, H, hd, merged=merged, ml=ml)
+        A.attn_bwd(qkv, off, dm, merged, ml, cf, H, hd, cf_seq_adj=cf_adj, qkv_adj=qkv_adj, cfh=cfh)
+    torch.cuda.synchronize()
+    print(json.dumps({"config": args.config, "steps": args.steps, "copy_mib": args.copy_mib, "N": N, "T": T, "S": S,
+                      "D": D, "H": H}), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -49,6 +49,8 @@ def gpu_fwd_bwd(device, off, cf_seq, qkv, dm, H, hd, temperature=1.0, dead=False
     start = None if cf_adj0 is None else dev(cf_adj0, device)
     qa, ca, cfh = A.attn_bwd(q, o, g, merged, ml, cf, H, hd, temperature, cf_seq_adj=start, dead=dead)
     torch.cuda.synchronize()
+    # cfh [N, H, S] -> the oracle's (the reference's) [N*S, H]
+    cfh = cfh.permute(0, 2, 1).reshape(N * cf_seq.shape[1], H)
     return [t.cpu().numpy() for t in (merged, ml, qa, ca, cfh)]
 
 
@@ -111,16 +113,24 @@ def test_head_dims(device, hd):
     check_against_oracle(device, f"head_dim {hd}", tk.off, tk.cf_seq, qkv, dm, 2, hd, temperature=0.8)
 
 
-@pytest.mark.parametrize("hd,top", [(16, 255), (32, 200), (64, 140)])
+@pytest.mark.parametrize("hd,top", [(16, 255), (32, 200), (64, 140), (80, 120), (128, 70)])
 def test_many_slots(device, hd, top):
-    # more than 8 query blocks: the 1024-thread kernels
-    counts = [top, 3, top // 2, 130]
+    # many query blocks (past 8: the 1024-thread kernels; the lean LDS layouts)
+    lib = A._lib.load()
+    counts = [top, 3, top // 2, min(top, 130)]
     tk, qkv, dm = random_case(counts, 2, hd, seed=top, cf_kind="random")
+    assert tk.slots <= lib.pet_attn_max_slots(hd)
     check_against_oracle(device, f"many slots hd {hd} S {tk.slots}", tk.off, tk.cf_seq, qkv, dm, 2, hd)
 
 
-def test_too_many_slots_for_lds(device):
-    tk, qkv, dm = random_case([250, 3], 1, 128, seed=0)
+def test_slots_past_capacity_raise(device):
+    lib = A._lib.load()
+    cap = lib.pet_attn_max_slots(128)
+    say(f"[gpu] max slots by head_dim: " + ", ".join(f"{h}:{lib.pet_attn_max_slots(h)}" for h in
+                                                    (16, 32, 48, 64, 80, 96, 112, 128)))
+    assert lib.pet_attn_max_slots(24) == 0
+    assert 64 <= cap < 256
+    tk, qkv, dm = random_case([cap + 5, 3], 1, 128, seed=0)
     with pytest.raises(RuntimeError):
         gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 1, 128)
 
