@@ -72,6 +72,15 @@ __device__ __forceinline__ float sum_g(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// A workgroup barrier that orders LDS traffic only. __syncthreads() also
+// fences global memory, which on gfx9 means waiting for every outstanding
+// vector-memory load -- the prefetches a barrier is meant to overlap.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // n floats from LDS (p aligned to n floats when n is 2 or 4).
 template <int n>
 __device__ __forceinline__ void lds_get(const float* p, float* out) {
@@ -190,12 +199,17 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
   f4 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int J = 0; J < at.nb; ++J) {
+  // S^T of key block J: s[r] = query i against key 16J + 4g + r.
+  auto scores = [&](int J) {
     float k[W];
     lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
     f4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < W; ++t) s = mfma(k[t], q[t], s);  // s[r]: query i, key 16J + 4g + r
+    for (int t = 0; t < W; ++t) s = mfma(k[t], q[t], s);
+    return s;
+  };
+  // Online softmax and PV of key block J from its scores s.
+  auto block = [&](int J, const f4& s) {
     float lc[4];
     lds_get<4>(lcf + 16 * J + 4 * g, lc);
     float x[4], bm = kOff;
@@ -220,7 +234,16 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
 #pragma unroll
       for (int t = 0; t < DT; ++t) acc[t] = mfma(v[t], p[r], acc[t]);  // O^T: dim (4g + r') DT + t, query i
     }
+  };
+  // The next block's scores go out before this block's softmax and PV, in
+  // one basic block the scheduler interleaves; the last block is peeled.
+  f4 s = scores(0);
+  for (int J = 0; J + 1 < at.nb; ++J) {
+    const f4 sn = scores(J + 1);
+    block(J, s);
+    s = sn;
   }
+  block(at.nb - 1, s);
   const float tot = sum_g(sum);
   // else a query on an edge at its cutoff: zeros
   out.live = i < at.cnt && (i == 0 || !is_off(lcf[i]));
@@ -291,7 +314,7 @@ __device__ __forceinline__ void attn_fwd_kernel_body(const float* __restrict__ q
     for (int t = 0; t < W; ++t) q[t] = pq[t];
     if (pending) fwd_store<HD>(done, out, S, H, merged, ldm, ml);
     const Atom cur = at;
-    __syncthreads();
+    lds_barrier();
     const int next = item + gridDim.x;
     if (next < items) {
       at = Atom(off, next, H, N, S);
@@ -301,7 +324,7 @@ __device__ __forceinline__ void attn_fwd_kernel_body(const float* __restrict__ q
     done = cur;
     pending = true;
     if (next >= items) break;
-    __syncthreads();
+    lds_barrier();
     item = next;
   }
   fwd_store<HD>(done, out, S, H, merged, ldm, ml);
@@ -346,7 +369,7 @@ __global__ void __launch_bounds__(MAXT) attn_fwd1_kernel(const float* __restrict
     pv.template store<P>(Vs);
     if (int(threadIdx.x) < R) lcf[threadIdx.x] = pcf > 0.f ? __logf(pcf) : kOff;
   }
-  __syncthreads();
+  lds_barrier();
   FwdOut<HD> out;
   fwd_item<HD>(at, Ks, Vs, lcf, q, sc, out);
   fwd_store<HD>(at, out, S, H, merged, ldm, ml);
@@ -620,7 +643,7 @@ __global__ void __launch_bounds__(MAXT) attn_fwd4_kernel(const float* __restrict
   bool pending = false;
   for (;;) {
     wait_vm_all();
-    __syncthreads();
+    lds_barrier();
     float q[W];
 #pragma unroll
     for (int t = 0; t < W; ++t) q[t] = pq[t];
@@ -676,63 +699,83 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
   for (int t = 0; t < DT; ++t) dq[t] = dk[t] = dv[t] = f4{0.f, 0.f, 0.f, 0.f};
   float cfa = 0.f;
   const int nb = at.nb;
-  for (int s = 0; s < nb; ++s) {
+  // Phase 1 of step s: tile (query block w, key block J = (w + s) mod nb):
+  // S^T and dP^T, then A and dS, the dQ share, and A, dS left in LDS.
+  auto phase1 = [&](int s, bool v_staged) {
     float* tb = Tb + (nbuf == 2 ? (s & 1) : 0) * (NW * 2 * TILE);
-    if (active) {
-      // Tile (query block w, key block J): S^T and dP^T, then A and dS.
-      int J = w + s;
-      if (J >= nb) J -= nb;
-      f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-      {
-        float k[W], v[W];
-        lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
-        if (vlds)
-          lds_get<W>(Vs + (16 * J + c) * P + g * W, v);
-        else if (16 * J + c < at.cnt)
-          gmem_get<W>(qkv + at.row(16 * J + c) * ldq + 2 * D + at.h * HD + g * W, v);
-        else
+    int J = w + s;
+    if (J >= nb) J -= nb;
+    f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+    {
+      float k[W], v[W];
+      lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
+      if (v_staged)
+        lds_get<W>(Vs + (16 * J + c) * P + g * W, v);
+      else if (16 * J + c < at.cnt)
+        gmem_get<W>(qkv + at.row(16 * J + c) * ldq + 2 * D + at.h * HD + g * W, v);
+      else
 #pragma unroll
-          for (int t = 0; t < W; ++t) v[t] = 0.f;
+        for (int t = 0; t < W; ++t) v[t] = 0.f;
 #pragma unroll
-        for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st), dp = mfma(v[t], go[t], dp);
-      }
-      float lc[4], a[4], ds[4];
-      lds_get<4>(lcf + 16 * J + 4 * g, lc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {  // query i, key 16J + 4g + r
-        a[r] = li > 0.f && !is_off(lc[r]) ? __expf(st[r] * sc + lc[r] - mi) * li : 0.f;
-        ds[r] = a[r] * (dp[r] - dqi);
-      }
-      // dQ^T += K^T dS^T over the tile's keys.
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float kk[DT];
-        lds_get<DT>(Ks + (16 * J + 4 * g + r) * P + c * DT, kk);
-#pragma unroll
-        for (int t = 0; t < DT; ++t) dq[t] = mfma(kk[t], ds[r], dq[t]);
-      }
-      float* ta = tb + (2 * w) * TILE;
-      *reinterpret_cast<float4*>(ta + c * TP + 4 * g) = make_float4(a[0], a[1], a[2], a[3]);
-      *reinterpret_cast<float4*>(ta + TILE + c * TP + 4 * g) = make_float4(ds[0], ds[1], ds[2], ds[3]);
+      for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st), dp = mfma(v[t], go[t], dp);
     }
-    __syncthreads();
-    if (active) {
-      // Key block w's tile from query block Ip: dK^T += Q^T dS, dV^T += dO^T A.
-      int Ip = w - s;
-      if (Ip < 0) Ip += nb;
-      const float* ta = tb + (2 * Ip) * TILE;
+    float lc[4], a[4], ds[4];
+    lds_get<4>(lcf + 16 * J + 4 * g, lc);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float av = ta[(4 * g + r) * TP + c], dsv = ta[TILE + (4 * g + r) * TP + c];
-        cfa += dsv;
-        float qq[DT], gg[DT];
-        lds_get<DT>(Qs + (16 * Ip + 4 * g + r) * P + c * DT, qq);
-        lds_get<DT>(Gs + (16 * Ip + 4 * g + r) * P + c * DT, gg);
-#pragma unroll
-        for (int t = 0; t < DT; ++t) dk[t] = mfma(qq[t], dsv, dk[t]), dv[t] = mfma(gg[t], av, dv[t]);
-      }
+    for (int r = 0; r < 4; ++r) {  // query i, key 16J + 4g + r
+      a[r] = li > 0.f && !is_off(lc[r]) ? __expf(st[r] * sc + lc[r] - mi) * li : 0.f;
+      ds[r] = a[r] * (dp[r] - dqi);
     }
-    if (nbuf == 1) __syncthreads();  // the owners are done with the only buffer
+    // dQ^T += K^T dS^T over the tile's keys.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float kk[DT];
+      lds_get<DT>(Ks + (16 * J + 4 * g + r) * P + c * DT, kk);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) dq[t] = mfma(kk[t], ds[r], dq[t]);
+    }
+    float* ta = tb + (2 * w) * TILE;
+    *reinterpret_cast<float4*>(ta + c * TP + 4 * g) = make_float4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<float4*>(ta + TILE + c * TP + 4 * g) = make_float4(ds[0], ds[1], ds[2], ds[3]);
+  };
+  // Phase 2 of step s: key block w's tile from query block Ip = (w - s) mod nb:
+  // dK^T += Q^T dS, dV^T += dO^T A, and the key's dS summed.
+  auto phase2 = [&](int s) {
+    const float* tb = Tb + (nbuf == 2 ? (s & 1) : 0) * (NW * 2 * TILE);
+    int Ip = w - s;
+    if (Ip < 0) Ip += nb;
+    const float* ta = tb + (2 * Ip) * TILE;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float av = ta[(4 * g + r) * TP + c], dsv = ta[TILE + (4 * g + r) * TP + c];
+      cfa += dsv;
+      float qq[DT], gg[DT];
+      lds_get<DT>(Qs + (16 * Ip + 4 * g + r) * P + c * DT, qq);
+      lds_get<DT>(Gs + (16 * Ip + 4 * g + r) * P + c * DT, gg);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) dk[t] = mfma(qq[t], dsv, dk[t]), dv[t] = mfma(gg[t], av, dv[t]);
+    }
+  };
+  if (nbuf == 2 && vlds) {
+    // Software-pipelined: between two barriers a wave has phase 2 of the last
+    // step and phase 1 of this one, independent work the scheduler interleaves.
+    if (active) phase1(0, true);
+    lds_barrier();
+    for (int s = 1; s < nb; ++s) {
+      if (active) {
+        phase2(s - 1);
+        phase1(s, true);
+      }
+      lds_barrier();
+    }
+    if (active) phase2(nb - 1);
+  } else {
+    for (int s = 0; s < nb; ++s) {
+      if (active) phase1(s, vlds != 0);
+      lds_barrier();
+      if (active) phase2(s);
+      if (nbuf == 1) lds_barrier();  // the owners are done with the only buffer
+    }
   }
   out.cft = sum_g(cfa);
 #pragma unroll
@@ -814,7 +857,7 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
     const float mi = pm, li = pl;
     if (pending) bwd_store<HD>(done, out, S, H, sc, qkv_adj, lda, cfh);
     const Atom cur = at;
-    __syncthreads();
+    lds_barrier();
     const int next = item + gridDim.x;
     if (next < items) {
       at = Atom(off, next, H, N, S);
@@ -824,7 +867,7 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
     done = cur;
     pending = true;
     if (next >= items) break;
-    __syncthreads();
+    lds_barrier();
     item = next;
   }
   bwd_store<HD>(done, out, S, H, sc, qkv_adj, lda, cfh);
@@ -874,9 +917,226 @@ __global__ void __launch_bounds__(MAXT) attn_bwd1_kernel(const float* __restrict
     if (vlds) pv.template store<P>(Vs);
     if (int(threadIdx.x) < R) lcf[threadIdx.x] = pcf > 0.f ? __logf(pcf) : kOff;
   }
-  __syncthreads();
+  lds_barrier();
   BwdOut<HD> out;
   bwd_item<HD>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, H, sc, out);
+  bwd_store<HD>(at, out, S, H, sc, qkv_adj, lda, cfh);
+}
+
+// ---- backward v2: 3 workgroups a CU ---------------------------------------------
+// Q, K and dO staged at pitch hd (no padding): float4 q of row r sits at
+// q ^ key(r), key(r) = r & 7 when a row covers the 32 banks (hd a multiple of
+// 32), (r >> 1) & 3 at hd 16 (two rows per 32 banks). Eight consecutive rows
+// read at one float4 column (the MFMA row operands) and one row read across
+// its columns (the transposed operands) then touch distinct banks.
+template <int HD>
+struct SwSlice {
+  static constexpr int C4 = HD / 4;
+  __device__ static __forceinline__ int key(int r) { return HD == 16 ? (r >> 1) & 3 : r & 7; }
+  __device__ static __forceinline__ int f4(int r, int q) { return r * C4 + (q ^ key(r)); }
+  __device__ static __forceinline__ int fl(int r, int x) { return 4 * f4(r, x >> 2) + (x & 3); }
+};
+// A 16 x 16 tile at pitch 16: row r stored as row r ^ ((r >> 2) & 1), its
+// float4 q at q ^ ((stored row >> 1) & 3). The producer's 128-bit row writes
+// (eight rows a pass) and the consumer's 32-bit column reads (rows 4g + r of
+// two g a pass) are then both free of bank conflicts.
+struct SwTile {
+  __device__ static __forceinline__ int prow(int r) { return r ^ ((r >> 2) & 1); }
+  __device__ static __forceinline__ int f4(int r, int q) {
+    const int p = prow(r);
+    return 4 * p + (q ^ ((p >> 1) & 3));
+  }
+  __device__ static __forceinline__ int fl(int r, int x) { return 4 * f4(r, x >> 2) + (x & 3); }
+};
+
+// DT consecutive floats x0 .. x0 + DT - 1 (x0 a multiple of DT) of row r.
+template <int HD, int DT>
+__device__ __forceinline__ void sw_get(const float* base, int r, int x0, float* out) {
+  if constexpr (DT % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < DT; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(base + 4 * SwSlice<HD>::f4(r, (x0 + j) >> 2));
+      out[j] = v.x, out[j + 1] = v.y, out[j + 2] = v.z, out[j + 3] = v.w;
+    }
+  } else if constexpr (DT % 2 == 0) {
+#pragma unroll
+    for (int j = 0; j < DT; j += 2) {
+      const float2 v = *reinterpret_cast<const float2*>(base + SwSlice<HD>::fl(r, x0 + j));
+      out[j] = v.x, out[j + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < DT; ++j) out[j] = base[SwSlice<HD>::fl(r, x0 + j)];
+  }
+}
+
+template <int HD>
+struct LdsV2 {
+  // Q, K, dO at pitch hd, log cf, two buffers of [NW producers][A, dS] tiles.
+  static size_t floats(int NW) { return size_t(3) * NW * 16 * HD + NW * 16 + size_t(2) * NW * 2 * 256; }
+};
+
+template <int HD, int MAXT>
+__global__ void __launch_bounds__(MAXT) attn_bwd2_kernel(const float* __restrict__ qkv, int64_t ldq,
+                                                         const int* __restrict__ off, int N, int S, int H, float sc,
+                                                         const float* __restrict__ dmerged, int64_t ldg,
+                                                         const float* __restrict__ merged, int64_t ldm,
+                                                         const float* __restrict__ ml,
+                                                         const float* __restrict__ cf_seq, int64_t ldc,
+                                                         float* __restrict__ qkv_adj, int64_t lda,
+                                                         float* __restrict__ cfh) {
+  constexpr int W = HD / 4, DT = HD / 16, C4 = HD / 4;
+  extern __shared__ float lds[];
+  const int NW = blockDim.x >> 6, R = NW * 16, D = H * HD;
+  float* Qs = lds;
+  float* Ks = Qs + R * HD;
+  float* Gs = Ks + R * HD;
+  float* lcf = Gs + R * HD;
+  float* Tb = lcf + R;  // [2][NW][A, dS][256]
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int i = 16 * w + c;
+  const Atom at(off, blockIdx.x, H, N, S);
+  const int nb = at.nb;
+  const bool active = w < nb;
+  const float* Vg = qkv + 2 * D + at.h * HD;
+  // V row 16J + c, this lane's slice. A row past the count loads the atom's
+  // own row instead: finite values for a key whose weight is zero, and no
+  // select on the loaded registers, which would wait for the load.
+  auto load_v = [&](int J, float* v) {
+    const int r = 16 * J + c;
+    gmem_get<W>(Vg + at.row(r < at.cnt ? r : 0) * ldq + g * W, v);
+  };
+  float oo[W], vcur[W], mi = kOff, li = 0.f;
+  {
+    SliceRegs<HD> pq, pk, pg;
+    pq.load(qkv, ldq, at.h * HD, at);
+    pk.load(qkv, ldq, D + at.h * HD, at);
+    pg.load(dmerged, ldg, at.h * HD, at);
+    const float pcf = int(threadIdx.x) < at.cnt ? cf_seq[size_t(at.n) * ldc + threadIdx.x] : 0.f;
+    if (i < at.cnt) {
+      gmem_get<W>(merged + at.row(i) * ldm + at.h * HD + g * W, oo);
+      const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
+      mi = m2[0], li = m2[1];
+    } else {
+#pragma unroll
+      for (int t = 0; t < W; ++t) oo[t] = 0.f;
+    }
+    if (active) load_v(w, vcur);  // step 0's key block is w
+#pragma unroll
+    for (int k = 0; k < SliceRegs<HD>::PER; ++k) {
+      const int idx = threadIdx.x + k * blockDim.x, r = idx / C4, q = idx - r * C4;
+      const int o = 4 * SwSlice<HD>::f4(r, q);
+      *reinterpret_cast<float4*>(Qs + o) = pq.v[k];
+      *reinterpret_cast<float4*>(Ks + o) = pk.v[k];
+      *reinterpret_cast<float4*>(Gs + o) = pg.v[k];
+    }
+    if (int(threadIdx.x) < R) lcf[threadIdx.x] = pcf > 0.f ? __logf(pcf) : kOff;
+  }
+  lds_barrier();
+
+  float q[W], go[W], dqi = 0.f;
+  if (active) {
+#pragma unroll
+    for (int u = 0; u < W / 4; ++u) {
+      const float4 a = *reinterpret_cast<const float4*>(Qs + 4 * SwSlice<HD>::f4(i, g * (W / 4) + u));
+      const float4 b = *reinterpret_cast<const float4*>(Gs + 4 * SwSlice<HD>::f4(i, g * (W / 4) + u));
+      q[4 * u] = a.x, q[4 * u + 1] = a.y, q[4 * u + 2] = a.z, q[4 * u + 3] = a.w;
+      go[4 * u] = b.x, go[4 * u + 1] = b.y, go[4 * u + 2] = b.z, go[4 * u + 3] = b.w;
+    }
+    float d = 0.f;
+#pragma unroll
+    for (int t = 0; t < W; ++t) d += go[t] * oo[t];
+    dqi = sum_g(d);  // Dq = dO . O of query i
+  }
+  f4 dq[DT], dk[DT], dv[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) dq[t] = dk[t] = dv[t] = f4{0.f, 0.f, 0.f, 0.f};
+  float cfa = 0.f;
+  auto phase1 = [&](int s, const float* v) {
+    float* ta = Tb + ((s & 1) * NW + w) * 512;
+    int J = w + s;
+    if (J >= nb) J -= nb;
+    f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+    {
+      const int rk = 16 * J + c;
+      float k[W];
+#pragma unroll
+      for (int u = 0; u < W / 4; ++u) {
+        const float4 a = *reinterpret_cast<const float4*>(Ks + 4 * SwSlice<HD>::f4(rk, g * (W / 4) + u));
+        k[4 * u] = a.x, k[4 * u + 1] = a.y, k[4 * u + 2] = a.z, k[4 * u + 3] = a.w;
+      }
+#pragma unroll
+      for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st), dp = mfma(v[t], go[t], dp);
+    }
+    float lc[4], a[4], ds[4];
+    lds_get<4>(lcf + 16 * J + 4 * g, lc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      a[r] = li > 0.f && !is_off(lc[r]) ? __expf(st[r] * sc + lc[r] - mi) * li : 0.f;
+      ds[r] = a[r] * (dp[r] - dqi);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float kk[DT];
+      sw_get<HD, DT>(Ks, 16 * J + 4 * g + r, c * DT, kk);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) dq[t] = mfma(kk[t], ds[r], dq[t]);
+    }
+    *reinterpret_cast<float4*>(ta + 4 * SwTile::f4(c, g)) = make_float4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<float4*>(ta + 256 + 4 * SwTile::f4(c, g)) = make_float4(ds[0], ds[1], ds[2], ds[3]);
+  };
+  auto phase2 = [&](int s) {
+    int Ip = w - s;
+    if (Ip < 0) Ip += nb;
+    const float* ta = Tb + ((s & 1) * NW + Ip) * 512;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = SwTile::fl(4 * g + r, c);
+      const float av = ta[o], dsv = ta[256 + o];
+      cfa += dsv;
+      float qq[DT], gg[DT];
+      sw_get<HD, DT>(Qs, 16 * Ip + 4 * g + r, c * DT, qq);
+      sw_get<HD, DT>(Gs, 16 * Ip + 4 * g + r, c * DT, gg);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) dk[t] = mfma(qq[t], dsv, dk[t]), dv[t] = mfma(gg[t], av, dv[t]);
+    }
+  };
+  // Pipelined steps: between two barriers a wave has phase 2 of the last step,
+  // phase 1 of this one and the V rows of the next in flight. The V rows
+  // alternate between two register sets (steps taken two at a time), so a
+  // load is first used a whole step after it is issued.
+  float valt[W];
+  auto key_block = [&](int s) {
+    int J = w + s;
+    while (J >= nb) J -= nb;
+    return J;
+  };
+  if (active) {
+    load_v(key_block(1), valt);
+    phase1(0, vcur);
+  }
+  lds_barrier();
+  for (int s = 1; s < nb; s += 2) {
+    if (active) {
+      load_v(key_block(s + 1), vcur);  // step s + 1's rows, into the set step s - 1 used
+      phase2(s - 1);
+      phase1(s, valt);
+    }
+    lds_barrier();
+    if (s + 1 < nb) {
+      if (active) {
+        load_v(key_block(s + 2), valt);
+        phase2(s);
+        phase1(s + 1, vcur);
+      }
+      lds_barrier();
+    }
+  }
+  if (active) phase2(nb - 1);
+  BwdOut<HD> out;
+  out.cft = sum_g(cfa);
+#pragma unroll
+  for (int t = 0; t < DT; ++t) out.dq[t] = dq[t], out.dk[t] = dk[t], out.dv[t] = dv[t];
   bwd_store<HD>(at, out, S, H, sc, qkv_adj, lda, cfh);
 }
 
@@ -1040,7 +1300,18 @@ int launch_bwd(const pet_attn_shape& sh, const float* qkv, int64_t ldq, const in
   const int64_t items = int64_t(sh.n_atoms) * sh.heads;
   const int block = 64 * NW;
   static const int variant = env_int("PET_ATTN_BWD_VARIANT");
-  if (variant != 9) {  // one item per workgroup (the default)
+  constexpr bool v2_layout = HD == 16 || HD % 32 == 0;
+  const size_t b2 = sizeof(float) * LdsV2<HD>::floats(NW);
+  if constexpr (v2_layout) {
+    if (variant == 2 && b2 <= cap) {
+      auto k2 = NW <= 8 ? attn_bwd2_kernel<HD, 512> : attn_bwd2_kernel<HD, 1024>;
+      allow_lds(k2, b2);
+      hipLaunchKernelGGL(k2, dim3(unsigned(items)), dim3(block), b2, st, qkv, ldq, off, sh.n_atoms, sh.slots,
+                         sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh);
+      return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+    }
+  }
+  if (variant != 9) {  // one item per workgroup, padded layout
     auto k1 = NW <= 8 ? attn_bwd1_kernel<HD, 512> : attn_bwd1_kernel<HD, 1024>;
     allow_lds(k1, bytes);
     hipLaunchKernelGGL(k1, dim3(unsigned(items)), dim3(block), bytes, st, qkv, ldq, off, sh.n_atoms, sh.slots,
