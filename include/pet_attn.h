@@ -106,6 +106,41 @@ PET_ATTN_API int pet_attn_bwd(const pet_attn_shape* shape, const float* qkv, int
                  const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh,
                  float* cf_seq_adj, int64_t ldca, void* stream);
 
+/* ---- runs of atoms: the kernels of attention_chunked / _bwd_chunked ------ */
+
+/* The forward of atoms [n0, n1) only, whose token rows come as a chunk qkv
+ * [Tc, 3D]: the run's own rows first (atom n at row n - n0), then its edges'
+ * (edge k at row (n1 - n0) + k - e0), e0 = off[n0], Tc = (n1 - n0) +
+ * off[n1] - e0 -- the chunk of the reference's attention_chunked (run_qkv,
+ * src/attention.cpp:2055-2081). merged and ml are written at the whole's rows
+ * (merged [T, D]) and slots; no dead rows are touched.
+ * Replaces the per-run launch of mfma::forward in attention_chunked
+ * (src/attention.cpp:2096-2117). */
+PET_ATTN_API int pet_attn_fwd_run(const pet_attn_shape* shape, int n0, int n1, int e0, const float* qkv_chunk,
+                                  int64_t ldq, const int* off, const float* cf_seq, int64_t ldc, float* merged,
+                                  int64_t ldm, float* ml, void* stream);
+
+/* The backward of atoms [n0, n1): qkv_chunk, dmerged_chunk [Tc, D] and
+ * qkv_adj_chunk [Tc, 3D] in the run's chunk rows, merged (whole rows), ml and
+ * cfh [N, H, S] at the whole's slots. No cf adjoint, no dead rows (see
+ * pet_attn_cf_adjoint, pet_attn_zero_dead).
+ * Replaces the per-run launch of mfma::backward in attention_bwd_chunked
+ * (src/attention.cpp:2131-2171). */
+PET_ATTN_API int pet_attn_bwd_run(const pet_attn_shape* shape, int n0, int n1, int e0, const float* qkv_chunk,
+                                  int64_t ldq, const int* off, const float* dmerged_chunk, int64_t ldg,
+                                  const float* merged, int64_t ldm, const float* ml, const float* cf_seq, int64_t ldc,
+                                  float* qkv_adj_chunk, int64_t lda, float* cfh, void* stream);
+
+/* cf_seq_adj[n][k] += (sum over heads h in order of cfh[n][h][k]) / cf_seq[n][k]
+ * where cf_seq[n][k] > 0 -- the reference's attn_bwd_cf (src/attention.cpp:1829-1838). */
+PET_ATTN_API int pet_attn_cf_adjoint(const pet_attn_shape* shape, const float* cfh, const float* cf_seq,
+                                     int64_t ldc, float* cf_seq_adj, int64_t ldca, void* stream);
+
+/* Rows N + off[N] .. T-1 of x [T, width] set to zero when shape->dead -- the
+ * reference's zero_dead (src/attention.cpp:1510-1518). */
+PET_ATTN_API int pet_attn_zero_dead(const pet_attn_shape* shape, float* x, int64_t ld, int width, const int* off,
+                                    void* stream);
+
 /* ---- the op level: attention() / attention_bwd() ----------------------- */
 
 /* attention(): pet_attn_fwd into merged (ld D), then out[T, D] (ld ldo) =
@@ -134,6 +169,41 @@ PET_ATTN_API int pet_attention_bwd(const pet_attn_shape* shape, float* in_adj, i
                       const float* cf_seq, int64_t ldc, const float* w_in, const float* w_out,
                       const int* off, const float* merged, const float* ml, float beta, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* ---- the op level over runs of atoms: attention_chunked() ---------------- */
+
+/* Writes the qkv rows of tokens [r0, r1) of the whole token matrix into
+ * qkv_rows (row 0 = token r0, leading dimension ld), enqueued on stream: the
+ * reference's QkvRows (src/ops.hpp:136-139). */
+typedef void (*pet_attn_make_qkv)(void* ctx, float* qkv_rows, int64_t ld, int r0, int r1, void* stream);
+
+/* Bytes of device workspace attention_chunked and attention_bwd_chunked need
+ * for runs of at most `chunk` tokens (atom_runs over off_host, the host copy of
+ * off, N+1 entries): the run's qkv, dmerged and qkv_adj and cfh [N, H, S],
+ * each 256-byte aligned. */
+PET_ATTN_API size_t pet_attention_chunked_workspace(const pet_attn_shape* shape, const int* off_host, int chunk);
+
+/* attention() over runs of consecutive atoms of about `chunk` tokens each
+ * (at least one atom a run, the reference's atom_runs, src/attention.cpp:2060-2070),
+ * so that qkv is only ever a run's rows, made by make_qkv: the same results
+ * as pet_attention with the whole qkv. merged and ml are the saves.
+ * Replaces pet::attention_chunked (src/ops.hpp:140-143, src/attention.cpp:2084-2129). */
+PET_ATTN_API int pet_attention_chunked(const pet_attn_shape* shape, float* out, int64_t ldo, pet_attn_make_qkv make_qkv,
+                                       void* ctx, const float* cf_seq, int64_t ldc, const float* w_out,
+                                       const float* b_out, const int* off, const int* off_host, float* merged,
+                                       float* ml, int chunk, void* workspace, size_t workspace_bytes, void* stream);
+
+/* attention_bwd() over the same runs: per run dmerged = out_adj . w_out on its
+ * rows, the core backward, in_adj rows = qkv_adj . w_in + beta * in_adj; then
+ * the cf adjoint, and dead rows of in_adj scaled by beta (set to 0 when beta
+ * is 0), as the whole's zeroed qkv adjoint gives them.
+ * Replaces pet::attention_bwd_chunked (src/ops.hpp:144-146, src/attention.cpp:2131-2187). */
+PET_ATTN_API int pet_attention_bwd_chunked(const pet_attn_shape* shape, float* in_adj, int64_t ldi, int d_in,
+                                           float* cf_seq_adj, int64_t ldca, const float* out_adj, int64_t ldo,
+                                           pet_attn_make_qkv make_qkv, void* ctx, const float* cf_seq, int64_t ldc,
+                                           const float* w_in, const float* w_out, const int* off,
+                                           const int* off_host, const float* merged, const float* ml, float beta,
+                                           int chunk, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

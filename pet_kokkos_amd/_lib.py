@@ -14,11 +14,18 @@ EXPORTS = (
     "pet_attn_scale",
     "pet_attn_strerror",
     "pet_attn_max_slots",
+    "pet_attn_fwd_run",
+    "pet_attn_bwd_run",
+    "pet_attn_cf_adjoint",
+    "pet_attn_zero_dead",
     "pet_attn_fwd",
     "pet_attn_bwd",
     "pet_attention",
     "pet_attention_bwd_workspace",
     "pet_attention_bwd",
+    "pet_attention_chunked_workspace",
+    "pet_attention_chunked",
+    "pet_attention_bwd_chunked",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX = range(9)
@@ -46,6 +53,9 @@ class PetAttnError(RuntimeError):
 _lib = None
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
+_I = ctypes.c_int
+# void make_qkv(void* ctx, float* qkv_rows, int64_t ld, int r0, int r1, void* stream)
+MAKE_QKV = ctypes.CFUNCTYPE(None, _P, _P, _I64, _I, _I, _P)
 
 
 def load() -> ctypes.CDLL:
@@ -68,6 +78,23 @@ def load() -> ctypes.CDLL:
     lib.pet_attn_fwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
     lib.pet_attn_bwd.restype = ctypes.c_int
     lib.pet_attn_bwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P]
+    lib.pet_attn_fwd_run.restype = ctypes.c_int
+    lib.pet_attn_fwd_run.argtypes = [sp, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
+    lib.pet_attn_bwd_run.restype = ctypes.c_int
+    lib.pet_attn_bwd_run.argtypes = [sp, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P,
+                                     _P]
+    lib.pet_attn_cf_adjoint.restype = ctypes.c_int
+    lib.pet_attn_cf_adjoint.argtypes = [sp, _P, _P, _I64, _P, _I64, _P]
+    lib.pet_attn_zero_dead.restype = ctypes.c_int
+    lib.pet_attn_zero_dead.argtypes = [sp, _P, _I64, _I, _P, _P]
+    lib.pet_attention_chunked_workspace.restype = ctypes.c_size_t
+    lib.pet_attention_chunked_workspace.argtypes = [sp, _P, _I]
+    lib.pet_attention_chunked.restype = ctypes.c_int
+    lib.pet_attention_chunked.argtypes = [sp, _P, _I64, MAKE_QKV, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I, _P,
+                                          ctypes.c_size_t, _P]
+    lib.pet_attention_bwd_chunked.restype = ctypes.c_int
+    lib.pet_attention_bwd_chunked.argtypes = [sp, _P, _I64, _I, _P, _I64, _P, _I64, MAKE_QKV, _P, _P, _I64, _P, _P,
+                                              _P, _P, _P, _P, ctypes.c_float, _I, _P, ctypes.c_size_t, _P]
     lib.pet_attention.restype = ctypes.c_int
     lib.pet_attention.argtypes = [sp, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P]
     lib.pet_attention_bwd_workspace.restype = ctypes.c_size_t

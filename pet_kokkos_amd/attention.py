@@ -8,7 +8,12 @@ dimension, ``out`` overwritten, ``in_adj`` computed onto ``beta * in_adj``,
 ``key + ":merged"`` and ``key + ":ml"`` for the backward to find. Errors raise
 (PetAttnError, a RuntimeError, as the reference's std::runtime_error).
 
-``attn_fwd`` / ``attn_bwd`` expose the core kernels alone (no linears). All
+``attention_chunked`` / ``attention_bwd_chunked`` mirror the reference's
+chunked forms (src/ops.hpp:133-146): runs of atoms of about ``chunk`` tokens,
+qkv made per run by a ``make_qkv(qkv_rows, r0, r1)`` callable.
+
+``attn_fwd`` / ``attn_bwd`` expose the core kernels alone (no linears),
+``attn_fwd_run`` / ``attn_bwd_run`` their per-run forms. All
 work runs in libpet_attn.so on the current torch stream; torch only provides
 device memory and the stream.
 """
@@ -181,3 +186,128 @@ def attention_bwd(ws: Workspace, key: str, in_adj: torch.Tensor, cf_seq_adj: tor
                                      _weight(w_out, "w_out"), tk.off.data_ptr(), merged.data_ptr(),
                                      ml.data_ptr(), float(beta), scratch.data_ptr(), scratch.numel(), _stream()),
                "pet_attention_bwd")
+
+
+def attn_fwd_run(n0: int, n1: int, e0: int, qkv_chunk: torch.Tensor, off: torch.Tensor, cf_seq: torch.Tensor,
+                 merged: torch.Tensor, ml: torch.Tensor | None, heads: int, head_dim: int, T: int,
+                 temperature: float = 1.0) -> None:
+    """The core forward of atoms [n0, n1) from their chunk of qkv rows (own
+    rows, then edges' rows from edge e0); merged [T, D] and ml at the whole's
+    rows and slots."""
+    lib = _lib.load()
+    D = heads * head_dim
+    N = off.shape[0] - 1
+    sh = shape(N, T, cf_seq.shape[1], heads, head_dim, temperature)
+    _lib.check(lib.pet_attn_fwd_run(sh, n0, n1, e0, qkv_chunk.data_ptr(), _mat(qkv_chunk, "qkv_chunk", 3 * D),
+                                    off.data_ptr(), cf_seq.data_ptr(), _mat(cf_seq, "cf_seq"), merged.data_ptr(),
+                                    _mat(merged, "merged", D), _ptr(ml), _stream()), "pet_attn_fwd_run")
+
+
+def attn_bwd_run(n0: int, n1: int, e0: int, qkv_chunk: torch.Tensor, off: torch.Tensor, dmerged_chunk: torch.Tensor,
+                 merged: torch.Tensor, ml: torch.Tensor, cf_seq: torch.Tensor, qkv_adj_chunk: torch.Tensor,
+                 cfh: torch.Tensor, heads: int, head_dim: int, T: int, temperature: float = 1.0) -> None:
+    """The core backward of atoms [n0, n1) in their chunk rows; cfh [N, H, S]
+    at the whole's slots (no cf adjoint, no dead rows)."""
+    lib = _lib.load()
+    D = heads * head_dim
+    N = off.shape[0] - 1
+    sh = shape(N, T, cf_seq.shape[1], heads, head_dim, temperature)
+    _lib.check(lib.pet_attn_bwd_run(sh, n0, n1, e0, qkv_chunk.data_ptr(), _mat(qkv_chunk, "qkv_chunk", 3 * D),
+                                    off.data_ptr(), dmerged_chunk.data_ptr(),
+                                    _mat(dmerged_chunk, "dmerged_chunk", D), merged.data_ptr(),
+                                    _mat(merged, "merged", D), ml.data_ptr(), cf_seq.data_ptr(),
+                                    _mat(cf_seq, "cf_seq"), qkv_adj_chunk.data_ptr(),
+                                    _mat(qkv_adj_chunk, "qkv_adj_chunk", 3 * D), cfh.data_ptr(), _stream()),
+               "pet_attn_bwd_run")
+
+
+def atom_runs(off_host, chunk: int):
+    """Runs [n0, n1) of consecutive atoms of at most about ``chunk`` tokens (at
+    least one atom), with their first and end edges: the reference's atom_runs
+    (src/attention.cpp:2060-2070)."""
+    N = len(off_host) - 1
+    runs, n0 = [], 0
+    while n0 < N:
+        n1 = n0 + 1
+        while n1 < N and (n1 + 1 - n0) + (int(off_host[n1 + 1]) - int(off_host[n0])) <= chunk:
+            n1 += 1
+        runs.append((n0, n1, int(off_host[n0]), int(off_host[n1])))
+        n0 = n1
+    return runs
+
+
+class _RunRows:
+    """The make_qkv callback the library calls: the pointer it passes is inside
+    the workspace tensor, so the Python callable gets a torch view of it."""
+
+    def __init__(self, make_qkv, ws: torch.Tensor, width: int):
+        self.make_qkv = make_qkv
+        self.ws = ws.view(torch.float32) if ws.dtype == torch.uint8 else ws
+        self.base = ws.data_ptr()
+        self.width = width
+        self.error = None
+        self.cfunc = _lib.MAKE_QKV(self)
+
+    def __call__(self, ctx, ptr, ld, r0, r1, stream):
+        try:
+            start = (ptr - self.base) // 4
+            rows = self.ws[start:start + (r1 - r0) * ld].view(r1 - r0, ld)[:, :self.width]
+            self.make_qkv(rows, r0, r1)
+        except BaseException as e:  # an exception cannot cross the C frame
+            self.error = e
+
+
+def _chunk_workspace(ws: Workspace, tk: Tokens, off_host, sh, chunk: int):
+    lib = _lib.load()
+    import numpy as np
+    oh = np.ascontiguousarray(off_host, dtype=np.int32)
+    nbytes = lib.pet_attention_chunked_workspace(sh, oh.ctypes.data, chunk)
+    return oh, ws.bytes("attention_chunked:scratch", nbytes), nbytes
+
+
+def attention_chunked(ws: Workspace, key: str, out: torch.Tensor, make_qkv, cf_seq: torch.Tensor, w_out: torch.Tensor,
+                      b_out: torch.Tensor | None, tk: Tokens, off_host, S: int, heads: int, head_dim: int,
+                      temperature: float, save: bool, chunk: int) -> None:
+    """pet::attention_chunked: attention() over runs of atoms of about
+    ``chunk`` tokens; ``make_qkv(qkv_rows, r0, r1)`` writes the qkv rows of
+    tokens [r0, r1) into ``qkv_rows``. ``off_host`` is off on the host."""
+    lib = _lib.load()
+    D = heads * head_dim
+    T = out.shape[0]
+    merged = ws.n2(key + ":merged", T, D) if save else torch.empty((T, D), dtype=torch.float32, device=out.device)
+    ml = ws.n2(key + ":ml", tk.N * heads * S, 2) if save else None
+    sh = shape(tk.N, T, S, heads, head_dim, temperature, tk.dead)
+    oh, scratch, nbytes = _chunk_workspace(ws, tk, off_host, sh, chunk)
+    cb = _RunRows(make_qkv, scratch, 3 * D)
+    code = lib.pet_attention_chunked(sh, out.data_ptr(), _mat(out, "out", D), cb.cfunc, None, cf_seq.data_ptr(),
+                                     _mat(cf_seq, "cf_seq"), _weight(w_out, "w_out"),
+                                     None if b_out is None else _weight(b_out, "b_out"), tk.off.data_ptr(),
+                                     oh.ctypes.data, merged.data_ptr(), _ptr(ml), chunk, scratch.data_ptr(), nbytes,
+                                     _stream())
+    if cb.error is not None:
+        raise cb.error
+    _lib.check(code, "pet_attention_chunked")
+
+
+def attention_bwd_chunked(ws: Workspace, key: str, in_adj: torch.Tensor, cf_seq_adj: torch.Tensor,
+                          out_adj: torch.Tensor, make_qkv, cf_seq: torch.Tensor, w_in: torch.Tensor,
+                          w_out: torch.Tensor, tk: Tokens, off_host, S: int, heads: int, head_dim: int,
+                          temperature: float, beta: float, chunk: int) -> None:
+    """pet::attention_bwd_chunked over the same runs."""
+    lib = _lib.load()
+    D = heads * head_dim
+    T = in_adj.shape[0]
+    merged, ml = ws.peek2(key + ":merged"), ws.peek2(key + ":ml")
+    sh = shape(tk.N, T, S, heads, head_dim, temperature, tk.dead)
+    oh, scratch, nbytes = _chunk_workspace(ws, tk, off_host, sh, chunk)
+    cb = _RunRows(make_qkv, scratch, 3 * D)
+    d_in = w_in.shape[1]
+    code = lib.pet_attention_bwd_chunked(sh, in_adj.data_ptr(), _mat(in_adj, "in_adj", d_in), d_in,
+                                         cf_seq_adj.data_ptr(), _mat(cf_seq_adj, "cf_seq_adj"), out_adj.data_ptr(),
+                                         _mat(out_adj, "out_adj", D), cb.cfunc, None, cf_seq.data_ptr(),
+                                         _mat(cf_seq, "cf_seq"), _weight(w_in, "w_in"), _weight(w_out, "w_out"),
+                                         tk.off.data_ptr(), oh.ctypes.data, merged.data_ptr(), ml.data_ptr(),
+                                         float(beta), chunk, scratch.data_ptr(), nbytes, _stream())
+    if cb.error is not None:
+        raise cb.error
+    _lib.check(code, "pet_attention_bwd_chunked")

@@ -6,8 +6,10 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <vector>
 
 #include "../../include/pet_attn.h"
 
@@ -66,6 +68,56 @@ __global__ void fill_bias_kernel(float* __restrict__ out, int64_t ldo, const flo
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Rows N + off[N] .. T-1 of x [T, width]: 0 when beta is 0, else beta times
+// themselves (what in_adj's dead rows get from a zeroed qkv adjoint).
+__global__ void scale_dead_kernel(float* __restrict__ x, int64_t ld, int width, int N, int T,
+                                  const int* __restrict__ off, float beta) {
+  const int64_t first = int64_t(N) + off[N];
+  const int64_t total = (int64_t(T) - N) * width;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = N + i / width;
+    if (r >= first) {
+      float* p = x + r * ld + (i % width);
+      *p = beta == 0.0f ? 0.0f : beta * *p;
+    }
+  }
+}
+
+// Runs of consecutive atoms, each of at most about `chunk` tokens (at least
+// one atom), with their first edges: the reference's atom_runs
+// (src/attention.cpp:2060-2070).
+struct Run {
+  int n0, n1, e0, e1;
+};
+std::vector<Run> atom_runs(const int* off, int N, int chunk) {
+  std::vector<Run> runs;
+  for (int n0 = 0; n0 < N;) {
+    int n1 = n0 + 1;
+    while (n1 < N && (n1 + 1 - n0) + (off[n1 + 1] - off[n0]) <= chunk) ++n1;
+    runs.push_back({n0, n1, off[n0], off[n1]});
+    n0 = n1;
+  }
+  return runs;
+}
+int64_t max_run_rows(const std::vector<Run>& runs) {
+  int64_t m = 0;
+  for (const Run& r : runs) m = std::max<int64_t>(m, int64_t(r.n1 - r.n0) + (r.e1 - r.e0));
+  return m;
+}
+struct ChunkWs {
+  float *qkv, *dm, *qa, *cfh;
+  size_t bytes;
+};
+ChunkWs chunk_ws(const pet_attn_shape& sh, int64_t rows, void* base) {
+  const size_t D = size_t(sh.heads) * sh.head_dim, Tc = size_t(rows);
+  const size_t a = align256(sizeof(float) * Tc * 3 * D), b = align256(sizeof(float) * Tc * D),
+               c = align256(sizeof(float) * Tc * 3 * D),
+               d = align256(sizeof(float) * size_t(sh.n_atoms) * sh.heads * sh.slots);
+  char* p = static_cast<char*>(base);
+  return {reinterpret_cast<float*>(p), reinterpret_cast<float*>(p + a), reinterpret_cast<float*>(p + a + b),
+          reinterpret_cast<float*>(p + a + b + c), a + b + c + d};
+}
+
 }  // namespace pet_attn
 
 using namespace pet_attn;
@@ -122,6 +174,87 @@ int pet_attention_bwd(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int 
                            cf_seq_adj, ldca, stream))
     return e;
   return gemm_nn(in_adj, ldi, qkv_adj, 3 * D, w_in, T, 3 * D, d_in, beta, st);
+}
+
+size_t pet_attention_chunked_workspace(const pet_attn_shape* sh, const int* off_host, int chunk) {
+  if (!sh || !off_host || sh->n_atoms < 0) return 0;
+  return chunk_ws(*sh, max_run_rows(atom_runs(off_host, sh->n_atoms, chunk)), nullptr).bytes;
+}
+
+int pet_attention_chunked(const pet_attn_shape* sh, float* out, int64_t ldo, pet_attn_make_qkv make_qkv, void* ctx,
+                          const float* cf_seq, int64_t ldc, const float* w_out, const float* b_out, const int* off,
+                          const int* off_host, float* merged, float* ml, int chunk, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (!sh || !out || !make_qkv || !w_out || !merged || !off_host) return PET_ATTN_EINVAL;
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows, N = sh->n_atoms;
+  if (ldo < D) return PET_ATTN_EINVAL;
+  const std::vector<Run> runs = atom_runs(off_host, N, chunk);
+  const ChunkWs ws = chunk_ws(*sh, max_run_rows(runs), workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return PET_ATTN_EWORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  for (const Run& r : runs) {
+    const int Nc = r.n1 - r.n0;
+    make_qkv(ctx, ws.qkv, 3 * D, r.n0, r.n1, stream);
+    if (r.e1 > r.e0) make_qkv(ctx, ws.qkv + int64_t(Nc) * 3 * D, 3 * D, N + r.e0, N + r.e1, stream);
+    if (int e = pet_attn_fwd_run(sh, r.n0, r.n1, r.e0, ws.qkv, 3 * D, off, cf_seq, ldc, merged, D, ml, stream))
+      return e;
+  }
+  if (int e = pet_attn_zero_dead(sh, merged, D, D, off, stream)) return e;
+  if (T == 0) return PET_ATTN_OK;
+  float beta = 0.0f;
+  if (b_out) {
+    const int64_t total = int64_t(T) * D;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(fill_bias_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, out, ldo,
+                       b_out, T, D);
+    if (hipGetLastError() != hipSuccess) return PET_ATTN_ELAUNCH;
+    beta = 1.0f;
+  }
+  return gemm_nt(out, ldo, merged, D, w_out, T, D, D, beta, st);
+}
+
+int pet_attention_bwd_chunked(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int d_in, float* cf_seq_adj,
+                              int64_t ldca, const float* out_adj, int64_t ldo, pet_attn_make_qkv make_qkv, void* ctx,
+                              const float* cf_seq, int64_t ldc, const float* w_in, const float* w_out, const int* off,
+                              const int* off_host, const float* merged, const float* ml, float beta, int chunk,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (!sh || !in_adj || !out_adj || !make_qkv || !w_in || !w_out || !off_host || d_in < 1 || ldi < d_in)
+    return PET_ATTN_EINVAL;
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows, N = sh->n_atoms;
+  if (ldo < D) return PET_ATTN_EINVAL;
+  const std::vector<Run> runs = atom_runs(off_host, N, chunk);
+  const ChunkWs ws = chunk_ws(*sh, max_run_rows(runs), workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return PET_ATTN_EWORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  for (const Run& r : runs) {
+    const int Nc = r.n1 - r.n0, Ec = r.e1 - r.e0;
+    make_qkv(ctx, ws.qkv, 3 * D, r.n0, r.n1, stream);
+    if (Ec > 0) make_qkv(ctx, ws.qkv + int64_t(Nc) * 3 * D, 3 * D, N + r.e0, N + r.e1, stream);
+    if (int e = gemm_nn(ws.dm, D, out_adj + int64_t(r.n0) * ldo, ldo, w_out, Nc, D, D, 0.0f, st)) return e;
+    if (Ec > 0)
+      if (int e = gemm_nn(ws.dm + int64_t(Nc) * D, D, out_adj + (int64_t(N) + r.e0) * ldo, ldo, w_out, Ec, D, D, 0.0f,
+                          st))
+        return e;
+    if (int e = pet_attn_bwd_run(sh, r.n0, r.n1, r.e0, ws.qkv, 3 * D, off, ws.dm, D, merged, D, ml, cf_seq, ldc,
+                                 ws.qa, 3 * D, ws.cfh, stream))
+      return e;
+    if (int e = gemm_nn(in_adj + int64_t(r.n0) * ldi, ldi, ws.qa, 3 * D, w_in, Nc, 3 * D, d_in, beta, st)) return e;
+    if (Ec > 0)
+      if (int e = gemm_nn(in_adj + (int64_t(N) + r.e0) * ldi, ldi, ws.qa + int64_t(Nc) * 3 * D, 3 * D, w_in, Ec,
+                          3 * D, d_in, beta, st))
+        return e;
+  }
+  if (int e = pet_attn_cf_adjoint(sh, ws.cfh, cf_seq, ldc, cf_seq_adj, ldca, stream)) return e;
+  if (sh->dead && T > N) {
+    const int64_t total = (int64_t(T) - N) * d_in;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(scale_dead_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, in_adj,
+                       ldi, d_in, N, T, off, beta);
+    if (hipGetLastError() != hipSuccess) return PET_ATTN_ELAUNCH;
+  }
+  return PET_ATTN_OK;
 }
 
 }  // extern "C"
