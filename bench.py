@@ -51,6 +51,74 @@ def algorithmic(tk, D, H):
     )
 
 
+def _timed(fn, reps):
+    """Average microseconds of fn() over reps calls, HIP events on the current stream."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device):
+    """The path's other rows on the same workload: the token norm (HBM-bound:
+    bytes / time against 8 TB/s), the layer-level attention (norm, QKV linear,
+    attention, output linear and their backward), and the forces' edge term and
+    fold on the workload's own edge list."""
+    import numpy as np
+    import torch
+
+    from pet_kokkos_amd import attention as A
+    from pet_kokkos_amd import forces as F
+    from pet_kokkos_amd import layer as L
+    from pet_kokkos_amd import systems
+
+    H, hd, D = conf.heads, conf.head_dim, conf.d_model
+    N, S, T = tk.n_atoms, tk.slots, tk.n_rows
+    reps = max(10, args.steps // 2)
+    out = {}
+    nw = torch.ones(D, device=device)
+    nb = torch.zeros(D, device=device)
+    y = torch.empty_like(x)
+    g = torch.empty_like(x)
+    for name, bias in (("rmsnorm", None), ("layernorm", nb)):
+        us_f = _timed(lambda: L.norm_rows(y, x, nw, bias), reps)
+        us_b = _timed(lambda: L.norm_rows_bwd(g, dm, x, nw, bias is not None), reps)
+        fb, bb = 2 * 4.0 * T * D, 3 * 4.0 * T * D
+        out[name] = dict(fwd_us=us_f, bwd_us=us_b, fwd_gbps=fb / us_f / 1e3, bwd_gbps=bb / us_b / 1e3,
+                         fwd_frac_hbm=fb / us_f / 1e3 / (PEAK_HBM / 1e9), bwd_frac_hbm=bb / us_b / 1e3 / (PEAK_HBM / 1e9))
+    ws = A.Workspace(device)
+    tkd = A.Tokens(off, N)
+    o = torch.empty((T, D), device=device)
+    tadj = torch.empty((T, D), device=device)
+    ca = torch.zeros((N, S), device=device)
+    out["layer_fwd_bwd_us"] = _timed(lambda: (
+        L.attention_layer(ws, "b", o, x, nw, None, w_in, b_in, cf, w_out, b_out, tkd, S, H, hd, 1.0),
+        L.attention_layer_bwd(ws, "b", tadj, ca, dm, x, nw, None, w_in, b_in, cf, w_out, tkd, S, H, hd, 1.0)), reps)
+    out["layer_note"] = ("attention block of a PET layer: RMSNorm, QKV linear, attention, output linear, and the "
+                         "backward (rebuilt norm and QKV, attention_bwd, norm backward into the token adjoint)")
+    cfgs = systems.CONFIGS[args.config]
+    s = systems.build_structure(cfgs.structure, 0)
+    pk = systems.packed_edges(len(s.positions), systems.neighbor_list(s, cfgs.cutoff), cfgs.cutoff, cfgs.width)
+    E = len(pk.center)
+    dpk = F.PackedEdges.from_host(pk, device)
+    x4 = torch.randn((E, 4), device=device)
+    csa = torch.randn((N, int(np.diff(pk.off).max()) + 1), device=device)
+    grad = torch.empty((E, 3), dtype=torch.float64, device=device)
+    us_e = _timed(lambda: F.edge_grad(dpk, x4, None, csa, cfgs.width, "cosine", grad), reps)
+    us_f = _timed(lambda: F.fold_edge_gradients(dpk, N, grad, -1.0), reps)
+    eb = E * (16 + 4 + 4 + 24 + 8 + 8 + 4 + 24)
+    out["edge_grad"] = dict(us=us_e, edges=E, gbps=eb / us_e / 1e3)
+    out["fold"] = dict(us=us_f, atoms=len(s.positions))
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -59,6 +127,8 @@ def main():
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-op-level", action="store_true", help="skip the op-level (with linears) timing")
+    ap.add_argument("--no-rows", action="store_true",
+                    help="skip the timing of the path's other rows (token norm, layer level, forces' edge term)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -128,7 +198,7 @@ def main():
     bwd_mfma_bound = alg["bwd_flops"] / PEAK_FP32_MFMA >= alg["bwd_bytes"] / PEAK_HBM
     if bwd_mfma_bound:
         achieved = alg["bwd_flops"] / (bwd_avg * 1e-6) / 1e12
-        roof = dict(kernel="attn_bwd_kernel<32> (+ attn_cf_adjoint_kernel)", bound="mfma", achieved=achieved,
+        roof = dict(kernel=f"attn_bwd_kernel<{hd}, 512> (+ attn_cf_adjoint_kernel)", bound="mfma", achieved=achieved,
                     peak=PEAK_FP32_MFMA / 1e12, unit="TFLOP/s", frac=achieved / (PEAK_FP32_MFMA / 1e12))
     else:
         achieved = alg["bwd_bytes"] / (bwd_avg * 1e-6) / 1e9
@@ -176,6 +246,9 @@ def main():
         torch.cuda.synchronize()
         extra["op_level_us"] = s0.elapsed_time(s1) * 1e3 / reps
         extra["op_level_note"] = "attention()+attention_bwd(): core + W_out fwd, W_out^T and W_in^T GEMMs (rocBLAS)"
+
+    if not args.no_rows:
+        extra["rows"] = time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device)
 
     cpu = None
     if not args.no_cpu:

@@ -205,6 +205,97 @@ PET_ATTN_API int pet_attention_bwd_chunked(const pet_attn_shape* shape, float* i
                                            const int* off_host, const float* merged, const float* ml, float beta,
                                            int chunk, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- the attention's input: cf_seq, the token norm and its callers -------- */
+
+/* cf_seq[n][0] = 1, cf_seq[n][1 + m] = cut[off[n] + m] for m < off[n+1] - off[n],
+ * 0 for the slots past the atom's count: the attention bias source, from each
+ * kept edge's smooth cutoff factor in packed (CSR) order.
+ * Replaces the device pet_cfseq pass (reference src/device_neighbors.cpp:318-323)
+ * and its host twin (src/model.cpp:375-377). */
+PET_ATTN_API int pet_attn_cf_seq(const pet_attn_shape* shape, const int* off, const float* cut, float* cf_seq,
+                                 int64_t ldc, void* stream);
+
+/* out[rows, width] = norm(in) row by row: RMSNorm, (x) / sqrt(mean(x^2) + eps)
+ * * weight with eps = 2^-23, or LayerNorm when bias is not NULL, (x - mean) /
+ * sqrt(var + 1e-5) * weight + bias; in fp32, the row's sums in a fixed order.
+ * out may be in. Replaces norm_rows (reference src/ops.hpp:376-407). */
+PET_ATTN_API int pet_norm_rows(int rows, int width, float* out, int64_t ldo, const float* in, int64_t ldi,
+                               const float* weight, const float* bias, void* stream);
+
+/* in_adj = beta * in_adj + the adjoint of norm(in) for out_adj, row by row:
+ * inv (g w - [mean(g w), LayerNorm] - xhat mean(g w xhat)), xhat = (x - mu) inv.
+ * beta 0 overwrites (in_adj is not read). ln nonzero: LayerNorm.
+ * Replaces norm_rows_bwd (reference src/ops.hpp:409-436). */
+PET_ATTN_API int pet_norm_rows_bwd(int rows, int width, float* in_adj, int64_t lda, float beta,
+                                   const float* out_adj, int64_t ldg, const float* in, int64_t ldi,
+                                   const float* weight, int ln, void* stream);
+
+/* Bytes of device workspace pet_attention_layer / _layer_bwd need: the
+ * normed tokens [T, D] and qkv [T, 3D], with pet_attention_bwd_workspace's,
+ * each 256-byte aligned. */
+PET_ATTN_API size_t pet_attention_layer_workspace(const pet_attn_shape* shape);
+
+/* The attention of one PET layer from its tokens [T, D] (ld ldt): normed =
+ * norm(tokens) (norm_w, norm_b: RMSNorm, or LayerNorm when norm_b is not NULL),
+ * qkv = normed . w_in^T + b_in (w_in [3D, D]), then pet_attention into out
+ * with the saves merged and ml.
+ * Replaces the attention block of PetModel::ff_layer (reference
+ * src/feedforward.cpp:96-123: norm_rows "norm_tok", linear, attention). */
+PET_ATTN_API int pet_attention_layer(const pet_attn_shape* shape, float* out, int64_t ldo, const float* tokens,
+                                     int64_t ldt, const float* norm_w, const float* norm_b, const float* w_in,
+                                     const float* b_in, const float* cf_seq, int64_t ldc, const float* w_out,
+                                     const float* b_out, const int* off, float* merged, float* ml,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Its backward: normed and qkv rebuilt from tokens (as the reference's
+ * rebuild()), pet_attention_bwd into the normed tokens' adjoint, then the
+ * norm's backward into tokens_adj [T, D] (ld lda): rows < N set (beta 0) and
+ * live edge rows N .. N + off[N] - 1 accumulated, as the reference's sink
+ * (input_node_adj = g, edge_adj += g); dead rows untouched. cf_seq_adj
+ * accumulates.
+ * Replaces the attention block of PetModel::ff_layer_bwd (reference
+ * src/feedforward.cpp:292-329: attention_bwd, norm_rows_bwd "norm_tok_bwd"). */
+PET_ATTN_API int pet_attention_layer_bwd(const pet_attn_shape* shape, float* tokens_adj, int64_t lda,
+                                         float* cf_seq_adj, int64_t ldca, const float* out_adj, int64_t ldo,
+                                         const float* tokens, int64_t ldt, const float* norm_w, const float* norm_b,
+                                         const float* w_in, const float* b_in, const float* cf_seq, int64_t ldc,
+                                         const float* w_out, const int* off, const float* merged, const float* ml,
+                                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- the consumer of cf_seq_adj: the forces' edge term --------------------- */
+
+/* Per packed edge k < off[n_centres] (of atom n = center[k], its m-th, m =
+ * k - off[n]), in fp64:
+ *   cutoff_total = cutoff_adj[k] + cf_seq_adj[n][1 + m],
+ *   dist_adj     = x4_adj[k][3] + cutoff_total * dcf/dd(dist[k]; pcut[k], width),
+ *   grad[k][c]   = x4_adj[k][c] + dist_adj * vec[k][c] / dist[k]   (0 at dist 0),
+ * and grad = 0 for the dead rows k >= off[n_centres] up to n_edges. The
+ * cutoff's derivative is in fp32 arithmetic as the reference evaluates it
+ * (kind 0 bump, 1 cosine, 2 smooth). x4_adj [E, 4] (ld ldx) and cf_seq_adj
+ * (ld ldca) are fp32; cutoff_adj [E] fp32 or NULL (zeros); vec [E, 3], dist,
+ * pcut [E] and grad [E, 3] fp64.
+ * Replaces the edge_grad pass of forces_and_virial (reference
+ * src/forces.cpp:364-378, cutoff_ddist :21-42). */
+PET_ATTN_API int pet_edge_grad(int n_centres, int n_edges, const int* off, const int* center, const float* x4_adj,
+                               int64_t ldx, const float* cutoff_adj, const float* cf_seq_adj, int64_t ldca,
+                               const double* vec, const double* dist, const double* pcut, double width, int kind,
+                               double* grad, void* stream);
+
+/* forces[i] = scale * sum over atom i's edges k (in order) of
+ * (grad[k] - grad[reverse[k]]) (the reverse term where reverse[k] >= 0), and
+ * virial_atom[i][3a + b] = scale * sum_k vec[k][a] grad[k][b], for atoms
+ * i < n_atoms (those >= n_centres own no edges). fp64.
+ * Replaces fold_edge_gradients' per-atom pass (reference src/forces.cpp:50-68). */
+PET_ATTN_API int pet_fold_edge_gradients(int n_atoms, int n_centres, const int* off, const int* reverse,
+                                         const double* vec, const double* grad, double scale, double* forces,
+                                         double* virial_atom, void* stream);
+
+/* out[b][t] (= or +=, accumulate nonzero) sum over atoms soff[b] .. soff[b+1]-1
+ * of x[a][t], for n_struct structures and width columns, fp64, in a fixed order.
+ * Replaces sum_by_structure (reference src/forces.cpp:287-302). */
+PET_ATTN_API int pet_sum_by_structure(int n_struct, int width, const int* soff, const double* x, double* out,
+                                      int accumulate, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

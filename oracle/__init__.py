@@ -1,5 +1,6 @@
 """TEST INFRASTRUCTURE ONLY: numpy bindings of the CPU oracle
-(attention_oracle.cpp, a restatement of the reference's host attention path).
+(attention_oracle.cpp, a restatement of the reference's host attention path;
+rows_forces_oracle.cpp, of its token norm, cf_seq and the forces' edge term).
 
 Imported by tests/, by __graft_entry__.smoke() as the checker, and by bench.py's
 cpu_baseline leg -- never by the product package.
@@ -141,3 +142,95 @@ def attention_bwd(out_adj, qkv, off, cf_seq, w_in, w_out, merged, ml, heads, hea
     qkv_adj, cf_seq_adj, _ = attn_bwd(qkv, off, dmerged, merged, ml, cf_seq, heads, head_dim, temperature,
                                       cf_seq_adj, N, dead)
     return linear_bwd(qkv_adj, w_in, beta, in_adj), cf_seq_adj
+
+
+# ---- the attention's input side and the consumer of its cf adjoint ---------
+
+def cf_seq(off, cut, S):
+    """cf_seq [N, S]: 1, then the atom's edges' cutoff factors, then 0
+    (src/device_neighbors.cpp:318-323)."""
+    lib = load()
+    off = _c(off, np.int32)
+    cut = _c(cut, np.float32)
+    N = len(off) - 1
+    out = np.zeros((N, S), dtype=np.float32)
+    lib.oracle_cf_seq(N, S, _p(off), _p(cut), _p(out), ctypes.c_int64(S))
+    return out
+
+
+def norm_rows(x, w, b=None, dtype=np.float32):
+    """RMSNorm (b None) or LayerNorm of each row (src/ops.hpp:376-407)."""
+    lib = load()
+    x, w = _c(x, dtype), _c(w, dtype)
+    b = None if b is None else _c(b, dtype)
+    rows, D = x.shape
+    out = np.zeros_like(x)
+    fn = lib.oracle_norm_rows_f32 if dtype == np.float32 else lib.oracle_norm_rows_f64
+    fn(rows, D, _p(out), ctypes.c_int64(D), _p(x), ctypes.c_int64(D), _p(w), _p(b))
+    return out
+
+
+def norm_rows_bwd(g, x, w, ln, beta=0.0, in_adj=None, dtype=np.float32):
+    """beta in_adj + the norm's input adjoint for output adjoint g (src/ops.hpp:409-436)."""
+    lib = load()
+    g, x, w = _c(g, dtype), _c(x, dtype), _c(w, dtype)
+    rows, D = x.shape
+    out = np.zeros_like(x) if in_adj is None else _c(in_adj, dtype).copy()
+    if dtype == np.float32:
+        lib.oracle_norm_rows_bwd_f32(rows, D, _p(out), ctypes.c_int64(D), ctypes.c_float(beta), _p(g),
+                                     ctypes.c_int64(D), _p(x), ctypes.c_int64(D), _p(w), int(ln))
+    else:
+        lib.oracle_norm_rows_bwd_f64(rows, D, _p(out), ctypes.c_int64(D), ctypes.c_double(beta), _p(g),
+                                     ctypes.c_int64(D), _p(x), ctypes.c_int64(D), _p(w), int(ln))
+    return out
+
+
+def cutoff(d, rc, width, kind, f64=False):
+    """(value, d value / d dist) of the smooth cutoff `kind` (0 bump, 1 cosine,
+    2 smooth), transcendentals in float as the reference's CutT unless f64
+    (include/pet/cutoff.hpp:17-35, src/forces.cpp:21-42)."""
+    lib = load()
+    d = _c(np.atleast_1d(d), np.float64)
+    rc = _c(np.broadcast_to(rc, d.shape), np.float64)
+    v, dd = np.zeros_like(d), np.zeros_like(d)
+    lib.oracle_cutoff(len(d), _p(d), _p(rc), ctypes.c_double(width), int(kind), int(f64), _p(v), _p(dd))
+    return v, dd
+
+
+def edge_grad(off, center, x4_adj, cutoff_adj, cf_seq_adj, vec, dist, pcut, width, kind, n_edges=None):
+    """grad [E, 3] fp64 of forces_and_virial's edge pass (src/forces.cpp:364-378)."""
+    lib = load()
+    off, center = _c(off, np.int32), _c(center, np.int32)
+    x4_adj = _c(x4_adj, np.float32)
+    cutoff_adj = None if cutoff_adj is None else _c(cutoff_adj, np.float32)
+    cf_seq_adj = _c(cf_seq_adj, np.float32)
+    vec, dist, pcut = _c(vec, np.float64), _c(dist, np.float64), _c(pcut, np.float64)
+    E = len(center) if n_edges is None else n_edges
+    grad = np.zeros((E, 3), dtype=np.float64)
+    lib.oracle_edge_grad(len(off) - 1, E, _p(off), _p(center), _p(x4_adj), ctypes.c_int64(4), _p(cutoff_adj),
+                         _p(cf_seq_adj), ctypes.c_int64(cf_seq_adj.shape[1]), _p(vec), _p(dist), _p(pcut),
+                         ctypes.c_double(width), int(kind), _p(grad))
+    return grad
+
+
+def fold(N, off, rev, vec, grad, scale=1.0):
+    """(forces [N, 3], per-atom virial [N, 9]) of fold_edge_gradients (src/forces.cpp:50-68)."""
+    lib = load()
+    off, rev = _c(off, np.int32), _c(rev, np.int32)
+    vec, grad = _c(vec, np.float64), _c(grad, np.float64)
+    forces = np.zeros((N, 3), dtype=np.float64)
+    vir = np.zeros((N, 9), dtype=np.float64)
+    lib.oracle_fold(N, len(off) - 1, _p(off), _p(rev), _p(vec), _p(grad), ctypes.c_double(scale), _p(forces),
+                    _p(vir))
+    return forces, vir
+
+
+def struct_sum(soff, x, out=None, acc=False):
+    """Per-structure sums of x's rows (src/forces.cpp:287-302)."""
+    lib = load()
+    soff = _c(soff, np.int32)
+    x = _c(x, np.float64)
+    NS, W = len(soff) - 1, x.shape[1]
+    out = np.zeros((NS, W), dtype=np.float64) if out is None else _c(out, np.float64).copy()
+    lib.oracle_struct_sum(NS, W, _p(soff), _p(x), _p(out), int(acc))
+    return out

@@ -26,6 +26,15 @@ EXPORTS = (
     "pet_attention_chunked_workspace",
     "pet_attention_chunked",
     "pet_attention_bwd_chunked",
+    "pet_attn_cf_seq",
+    "pet_norm_rows",
+    "pet_norm_rows_bwd",
+    "pet_attention_layer_workspace",
+    "pet_attention_layer",
+    "pet_attention_layer_bwd",
+    "pet_edge_grad",
+    "pet_fold_edge_gradients",
+    "pet_sum_by_structure",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX = range(9)
@@ -102,6 +111,28 @@ def load() -> ctypes.CDLL:
     lib.pet_attention_bwd.restype = ctypes.c_int
     lib.pet_attention_bwd.argtypes = [sp, _P, _I64, ctypes.c_int, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P,
                                       _P, _P, _P, ctypes.c_float, _P, ctypes.c_size_t, _P]
+    _F = ctypes.c_float
+    _D = ctypes.c_double
+    lib.pet_attn_cf_seq.restype = ctypes.c_int
+    lib.pet_attn_cf_seq.argtypes = [sp, _P, _P, _P, _I64, _P]
+    lib.pet_norm_rows.restype = ctypes.c_int
+    lib.pet_norm_rows.argtypes = [_I, _I, _P, _I64, _P, _I64, _P, _P, _P]
+    lib.pet_norm_rows_bwd.restype = ctypes.c_int
+    lib.pet_norm_rows_bwd.argtypes = [_I, _I, _P, _I64, _F, _P, _I64, _P, _I64, _P, _I, _P]
+    lib.pet_attention_layer_workspace.restype = ctypes.c_size_t
+    lib.pet_attention_layer_workspace.argtypes = [sp]
+    lib.pet_attention_layer.restype = ctypes.c_int
+    lib.pet_attention_layer.argtypes = [sp, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
+                                        ctypes.c_size_t, _P]
+    lib.pet_attention_layer_bwd.restype = ctypes.c_int
+    lib.pet_attention_layer_bwd.argtypes = [sp, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _P,
+                                            _P, _P, _P, _P, ctypes.c_size_t, _P]
+    lib.pet_edge_grad.restype = ctypes.c_int
+    lib.pet_edge_grad.argtypes = [_I, _I, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _D, _I, _P, _P]
+    lib.pet_fold_edge_gradients.restype = ctypes.c_int
+    lib.pet_fold_edge_gradients.argtypes = [_I, _I, _P, _P, _P, _P, _D, _P, _P, _P]
+    lib.pet_sum_by_structure.restype = ctypes.c_int
+    lib.pet_sum_by_structure.argtypes = [_I, _I, _P, _P, _P, _I, _P]
     _lib = lib
     return lib
 

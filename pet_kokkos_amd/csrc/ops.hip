@@ -122,6 +122,32 @@ ChunkWs chunk_ws(const pet_attn_shape& sh, int64_t rows, void* base) {
 
 using namespace pet_attn;
 
+// rows.hip: the norm's backward with the reference's sink
+int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, const float* out_adj, int64_t ldg,
+                           const float* in, int64_t ldi, const float* weight, int ln, int n_node, float beta_node,
+                           float beta_edge, const int* live_off, hipStream_t st);
+
+namespace {
+
+// qkv [T, 3D] = norm(tokens) . w_in^T + b_in, the normed tokens left in normed.
+int layer_input(const pet_attn_shape* sh, float* normed, float* qkv, const float* tokens, int64_t ldt,
+                const float* norm_w, const float* norm_b, const float* w_in, const float* b_in, hipStream_t st) {
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  if (int e = pet_norm_rows(T, D, normed, D, tokens, ldt, norm_w, norm_b, st)) return e;
+  float beta = 0.0f;
+  if (b_in) {
+    const int64_t total = int64_t(T) * 3 * D;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(fill_bias_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, qkv,
+                       int64_t(3) * D, b_in, T, 3 * D);
+    if (hipGetLastError() != hipSuccess) return PET_ATTN_ELAUNCH;
+    beta = 1.0f;
+  }
+  return gemm_nt(qkv, 3 * D, normed, D, w_in, T, 3 * D, D, beta, st);
+}
+
+}  // namespace
+
 extern "C" {
 
 int pet_attention(const pet_attn_shape* sh, float* out, int64_t ldo, const float* qkv, int64_t ldq,
@@ -255,6 +281,55 @@ int pet_attention_bwd_chunked(const pet_attn_shape* sh, float* in_adj, int64_t l
     if (hipGetLastError() != hipSuccess) return PET_ATTN_ELAUNCH;
   }
   return PET_ATTN_OK;
+}
+
+size_t pet_attention_layer_workspace(const pet_attn_shape* sh) {
+  if (!sh) return 0;
+  const size_t D = size_t(sh->heads) * sh->head_dim, T = size_t(sh->n_rows);
+  return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) + pet_attention_bwd_workspace(sh);
+}
+
+int pet_attention_layer(const pet_attn_shape* sh, float* out, int64_t ldo, const float* tokens, int64_t ldt,
+                        const float* norm_w, const float* norm_b, const float* w_in, const float* b_in,
+                        const float* cf_seq, int64_t ldc, const float* w_out, const float* b_out, const int* off,
+                        float* merged, float* ml, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!sh || !tokens || !norm_w || !w_in) return PET_ATTN_EINVAL;
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  if (ldt < D) return PET_ATTN_EINVAL;
+  if (!workspace || workspace_bytes < pet_attention_layer_workspace(sh)) return PET_ATTN_EWORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
+  if (T == 0) return PET_ATTN_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  float* normed = reinterpret_cast<float*>(ws);
+  float* qkv = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
+  if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) return e;
+  return pet_attention(sh, out, ldo, qkv, 3 * D, cf_seq, ldc, w_out, b_out, off, merged, ml, stream);
+}
+
+int pet_attention_layer_bwd(const pet_attn_shape* sh, float* tokens_adj, int64_t lda, float* cf_seq_adj, int64_t ldca,
+                            const float* out_adj, int64_t ldo, const float* tokens, int64_t ldt, const float* norm_w,
+                            const float* norm_b, const float* w_in, const float* b_in, const float* cf_seq,
+                            int64_t ldc, const float* w_out, const int* off, const float* merged, const float* ml,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (!sh || !tokens_adj || !tokens || !norm_w || !w_in || !off) return PET_ATTN_EINVAL;
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  if (ldt < D || lda < D) return PET_ATTN_EINVAL;
+  if (!workspace || workspace_bytes < pet_attention_layer_workspace(sh)) return PET_ATTN_EWORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
+  if (T == 0) return PET_ATTN_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t a0 = align256(sizeof(float) * size_t(T) * D), a1 = align256(sizeof(float) * size_t(T) * 3 * D);
+  float* normed = reinterpret_cast<float*>(ws);
+  float* qkv = reinterpret_cast<float*>(ws + a0);
+  if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) return e;
+  // the normed tokens' adjoint overwrites them: the backward reads only qkv
+  if (int e = pet_attention_bwd(sh, normed, D, D, cf_seq_adj, ldca, out_adj, ldo, qkv, 3 * D, cf_seq, ldc, w_in,
+                                w_out, off, merged, ml, 0.0f, ws + a0 + a1, workspace_bytes - a0 - a1, stream))
+    return e;
+  return pet_rows_norm_bwd_sink(T, D, tokens_adj, lda, normed, D, tokens, ldt, norm_w, norm_b != nullptr,
+                                sh->n_atoms, 0.0f, 1.0f, off, st);
 }
 
 }  // extern "C"

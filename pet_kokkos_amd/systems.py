@@ -100,6 +100,7 @@ class Edges:
     neigh: np.ndarray  # [E] int32
     vec: np.ndarray  # [E, 3] float64, r_j + shift - r_i
     dist: np.ndarray  # [E] float64
+    shift: np.ndarray | None = None  # [E, 3] int, the image of r_j in cell units
 
 
 def neighbor_list(s: Structure, cutoff: float) -> Edges:
@@ -112,10 +113,11 @@ def neighbor_list(s: Structure, cutoff: float) -> Edges:
     x = s.positions
     N = len(x)
     c2 = cutoff * cutoff
-    cen, nei, vecs, dists = [], [], [], []
+    cen, nei, vecs, dists, shs = [], [], [], [], []
     # images of every atom: [N, I, 3], flattened j-major then image, the reference's loop order
     img = (x[:, None, :] + svec[None, :, :]).reshape(-1, 3)
     jj = np.repeat(np.arange(N, dtype=np.int32), len(svec))
+    ss = np.tile(shifts.astype(np.int64), (N, 1))
     for i in range(N):
         v = img - x[i]
         d2 = np.einsum("ij,ij->i", v, v)
@@ -125,12 +127,45 @@ def neighbor_list(s: Structure, cutoff: float) -> Edges:
         nei.append(jj[idx])
         vecs.append(v[idx])
         dists.append(np.sqrt(d2[idx]))
-    return Edges(np.concatenate(cen), np.concatenate(nei), np.concatenate(vecs), np.concatenate(dists))
+        shs.append(ss[idx])
+    return Edges(np.concatenate(cen), np.concatenate(nei), np.concatenate(vecs), np.concatenate(dists),
+                 np.concatenate(shs))
 
 
 def cosine_cutoff(d: np.ndarray, rc: float, width: float) -> np.ndarray:
     x = np.clip((d - (rc - width)) / width, 0.0, 1.0)
     return 0.5 * (1.0 + np.cos(np.pi * x))
+
+
+@dataclasses.dataclass
+class PackedEdges:
+    """An atom's kept edges contiguous (CSR ``off``), as the reference's
+    PackedEdges (include/pet/model.hpp:153-168): each edge's centre, its
+    reverse (j, i, -shift) edge or -1, vector, length, pair cutoff and smooth
+    cutoff factor."""
+    off: np.ndarray  # [N+1] int32
+    center: np.ndarray  # [E] int32
+    neigh: np.ndarray  # [E] int32
+    reverse: np.ndarray  # [E] int32
+    vec: np.ndarray  # [E, 3] float64
+    dist: np.ndarray  # [E] float64
+    pcut: np.ndarray  # [E] float64
+    cut: np.ndarray  # [E] float32
+
+
+def packed_edges(n_atoms: int, e: Edges, cutoff: float, width: float = 0.5) -> PackedEdges:
+    """The full directed edge list in the raw order (already grouped by centre),
+    with reverse indices from the image shifts and cosine cutoff factors."""
+    E = len(e.centre)
+    counts = np.bincount(e.centre, minlength=n_atoms)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    assert np.all(np.diff(e.centre) >= 0), "edges must be grouped by centre"
+    index = {(int(i), int(j), *map(int, sh)): k for k, (i, j, sh) in enumerate(zip(e.centre, e.neigh, e.shift))}
+    rev = np.array([index.get((int(j), int(i), *map(int, -sh)), -1) for i, j, sh in zip(e.centre, e.neigh, e.shift)],
+                   dtype=np.int32) if E else np.zeros(0, dtype=np.int32)
+    cut = cosine_cutoff(e.dist, cutoff, width).astype(np.float32)
+    return PackedEdges(off, e.centre.astype(np.int32), e.neigh.astype(np.int32), rev, e.vec.astype(np.float64),
+                       e.dist.astype(np.float64), np.full(E, cutoff, dtype=np.float64), cut)
 
 
 @dataclasses.dataclass

@@ -1,0 +1,253 @@
+"""GPU parity of the attention's input side (cf_seq, the token norm, the
+layer-level attention) and of the consumer of its cf adjoint (edge gradient,
+fold, structure sums), against the oracle, on an MI355X, through the C ABI.
+
+Tolerances: fp32 outputs within 1e-5 relative (max-abs error over max-abs
+reference, per tensor); the fp64 edge term within 1e-5 relative as well, since
+its cutoff derivative is evaluated in fp32 (the device's and the host's sinf /
+tanhf differ by ulps); fold and structure sums, which only add fp64 products,
+within 1e-12. Every result is also checked bitwise repeatable.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from pet_kokkos_amd import attention as A
+from pet_kokkos_amd import forces as F
+from pet_kokkos_amd import layer as L
+from pet_kokkos_amd import systems
+
+pytestmark = pytest.mark.gpu
+RTOL = 1e-5
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-300))
+
+
+def dev(a, device, dt=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return (t if dt is None else t.to(dt)).to(device)
+
+
+@pytest.mark.parametrize("D", [64, 96, 128, 200, 256, 512, 2048])
+@pytest.mark.parametrize("ln", [False, True])
+def test_norm_rows(device, D, ln):
+    print(f"[gpu] norm_rows D {D} ln {ln}", flush=True)
+    rng = np.random.default_rng(D * 2 + ln)
+    rows = 1031
+    x = (rng.standard_normal((rows, D)) * 2 + 0.3).astype(np.float32)
+    w = rng.standard_normal(D).astype(np.float32)
+    b = rng.standard_normal(D).astype(np.float32) if ln else None
+    g = rng.standard_normal((rows, D)).astype(np.float32)
+    xt, wt, gt = dev(x, device), dev(w, device), dev(g, device)
+    bt = dev(b, device) if ln else None
+    out = torch.empty_like(xt)
+    L.norm_rows(out, xt, wt, bt)
+    adj = torch.empty_like(xt)
+    L.norm_rows_bwd(adj, gt, xt, wt, ln)
+    prev = rng.standard_normal((rows, D)).astype(np.float32)
+    acc = dev(prev, device)
+    L.norm_rows_bwd(acc, gt, xt, wt, ln, beta=1.0)
+    out2 = torch.empty_like(xt)
+    L.norm_rows(out2, xt, wt, bt)
+    torch.cuda.synchronize()
+    assert rel(out.cpu().numpy(), oracle.norm_rows(x, w, b)) <= RTOL
+    ref_adj = oracle.norm_rows_bwd(g, x, w, ln)
+    assert rel(adj.cpu().numpy(), ref_adj) <= RTOL
+    assert rel(acc.cpu().numpy(), prev + ref_adj) <= RTOL
+    assert torch.equal(out, out2)
+
+
+def test_norm_rows_strided_and_in_place(device):
+    print("[gpu] norm_rows strided / in place", flush=True)
+    rng = np.random.default_rng(1)
+    D = 256
+    big = rng.standard_normal((300, 3 * D)).astype(np.float32)
+    w = rng.standard_normal(D).astype(np.float32)
+    bt = dev(big, device)
+    view = bt[:, D:2 * D]  # leading dimension 3D
+    ref = oracle.norm_rows(big[:, D:2 * D], w, None)
+    L.norm_rows(view, view, dev(w, device), None)  # in place
+    torch.cuda.synchronize()
+    assert rel(bt[:, D:2 * D].cpu().numpy(), ref) <= RTOL
+    assert np.array_equal(bt[:, :D].cpu().numpy(), big[:, :D])  # neighbours untouched
+
+
+def test_cf_seq(device):
+    print("[gpu] cf_seq", flush=True)
+    conf, tk = systems.config_tokens("c4")
+    rng = np.random.default_rng(0)
+    cut = rng.random(tk.n_edges).astype(np.float32)
+    got = L.cf_seq(dev(tk.off, device), dev(cut, device), tk.n_atoms, tk.slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.cf_seq(tk.off, cut, tk.slots))
+
+
+def _edges(config="c1", seed=0):
+    cfg = systems.CONFIGS[config]
+    s = systems.build_structure(cfg.structure, seed)
+    e = systems.neighbor_list(s, cfg.cutoff)
+    pk = systems.packed_edges(len(s.positions), e, cfg.cutoff, cfg.width)
+    return cfg, s, pk
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("config", ["c1", "c3"])
+def test_edge_grad_and_fold(device, kind, config):
+    print(f"[gpu] edge_grad + fold {config} kind {kind}", flush=True)
+    cfg, s, pk = _edges(config)
+    N, E = len(s.positions), len(pk.center)
+    S = int(np.diff(pk.off).max()) + 1
+    rng = np.random.default_rng(kind)
+    x4 = rng.standard_normal((E, 4)).astype(np.float32)
+    cadj = rng.standard_normal(E).astype(np.float32)
+    csa = rng.standard_normal((N, S)).astype(np.float32)
+    width = 0.5
+    dpk = F.PackedEdges.from_host(pk, device)
+    grad = F.edge_grad(dpk, dev(x4, device), dev(cadj, device), dev(csa, device), width, kind)
+    forces, vir = F.fold_edge_gradients(dpk, N, grad, scale=-1.0)
+    grad2 = F.edge_grad(dpk, dev(x4, device), dev(cadj, device), dev(csa, device), width, kind)
+    torch.cuda.synchronize()
+    ref = oracle.edge_grad(pk.off, pk.center, x4, cadj, csa, pk.vec, pk.dist, pk.pcut, width, kind)
+    assert rel(grad.cpu().numpy(), ref) <= RTOL
+    assert torch.equal(grad, grad2)
+    g = grad.cpu().numpy()
+    rf, rv = oracle.fold(N, pk.off, pk.reverse, pk.vec, g, scale=-1.0)
+    assert rel(forces.cpu().numpy(), rf) <= 1e-12
+    assert rel(vir.cpu().numpy(), rv) <= 1e-12
+
+
+def test_edge_grad_dead_rows_and_neighbour_only_atoms(device):
+    print("[gpu] edge_grad dead rows", flush=True)
+    cfg, s, pk = _edges("c1")
+    N, E = len(s.positions), len(pk.center)
+    S = int(np.diff(pk.off).max()) + 1
+    rng = np.random.default_rng(7)
+    x4 = rng.standard_normal((E + 9, 4)).astype(np.float32)
+    csa = rng.standard_normal((N, S)).astype(np.float32)
+    pad = lambda a, v: np.concatenate([a, np.full((9,) + a.shape[1:], v, dtype=a.dtype)])
+    host = systems.PackedEdges(pk.off, pad(pk.center, 0), pad(pk.neigh, 0), pad(pk.reverse, -1), pad(pk.vec, 1.0),
+                               pad(pk.dist, 1.0), pad(pk.pcut, cfg.cutoff), pad(pk.cut, 0.0))
+    dpk = F.PackedEdges.from_host(host, device)
+    grad = F.edge_grad(dpk, dev(x4, device), None, dev(csa, device), 0.5, "cosine")
+    # two more atoms that only neighbour (n_atoms > n_centres)
+    forces, vir = F.fold_edge_gradients(dpk, N + 2, grad)
+    torch.cuda.synchronize()
+    g = grad.cpu().numpy()
+    assert np.all(g[E:] == 0.0)
+    ref = oracle.edge_grad(host.off, host.center, x4, None, csa, host.vec, host.dist, host.pcut, 0.5, 1)
+    assert rel(g, ref) <= RTOL
+    assert np.all(forces.cpu().numpy()[N:] == 0.0) and np.all(vir.cpu().numpy()[N:] == 0.0)
+
+
+def test_sum_by_structure(device):
+    print("[gpu] sum_by_structure", flush=True)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((11392, 9))
+    sizes = [64, 648] * 16
+    soff = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    out = F.sum_by_structure(dev(soff, device), dev(x, device))
+    acc = F.sum_by_structure(dev(soff, device), dev(x, device), out.clone(), accumulate=True)
+    torch.cuda.synchronize()
+    ref = oracle.struct_sum(soff, x)
+    assert rel(out.cpu().numpy(), ref) <= 1e-12
+    assert rel(acc.cpu().numpy(), 2 * ref) <= 1e-12
+
+
+@pytest.mark.parametrize("ln", [False, True])
+@pytest.mark.parametrize("dead", [False, True])
+def test_attention_layer_fwd_bwd(device, ln, dead):
+    """tokens -> norm -> qkv -> attention -> out, and back to the tokens'
+    adjoint (atom rows set, live edge rows accumulated, dead rows untouched),
+    against the oracle's chain of the same steps."""
+    print(f"[gpu] attention_layer ln {ln} dead {dead}", flush=True)
+    conf, tk = systems.config_tokens("c1")
+    H, hd, D = conf.heads, conf.head_dim, conf.d_model
+    inp = systems.attention_inputs(tk, D, H, seed=9)
+    rng = np.random.default_rng(11)
+    T = tk.n_rows + (7 if dead else 0)
+    tokens = rng.standard_normal((T, D)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    nb = (0.1 * rng.standard_normal(D)).astype(np.float32) if ln else None
+    out_adj = rng.standard_normal((T, D)).astype(np.float32)
+    tok_adj0 = rng.standard_normal((T, D)).astype(np.float32)
+    csa0 = rng.standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
+    temp = 1.1
+    t = A.Tokens(dev(tk.off, device), tk.n_atoms, dead)
+    ws = A.Workspace(device)
+    w_in, b_in, w_out, b_out = (dev(inp[k], device) for k in ("w_in", "b_in", "w_out", "b_out"))
+    tok, cf = dev(tokens, device), dev(tk.cf_seq, device)
+    nwt, nbt = dev(nw, device), dev(nb, device) if ln else None
+    out = torch.empty((T, D), device=device)
+    L.attention_layer(ws, "l", out, tok, nwt, nbt, w_in, b_in, cf, w_out, b_out, t, tk.slots, H, hd, temp)
+    tadj, csa = dev(tok_adj0, device), dev(csa0, device)
+    L.attention_layer_bwd(ws, "l", tadj, csa, dev(out_adj, device), tok, nwt, nbt, w_in, b_in, cf, w_out, t,
+                          tk.slots, H, hd, temp)
+    torch.cuda.synchronize()
+    # the oracle's chain
+    normed = oracle.norm_rows(tokens, nw, nb)
+    qkv = oracle.linear(normed, inp["w_in"], inp["b_in"])
+    rout, merged, ml = oracle.attention(qkv, tk.off, tk.cf_seq, inp["w_out"], inp["b_out"], H, hd, temp,
+                                        N=tk.n_atoms, dead=dead)
+    assert rel(out.cpu().numpy(), rout) <= RTOL
+    n_adj, rcsa = oracle.attention_bwd(out_adj, qkv, tk.off, tk.cf_seq, inp["w_in"], inp["w_out"], merged, ml, H,
+                                       hd, temp, cf_seq_adj=csa0, N=tk.n_atoms, dead=dead)
+    g = oracle.norm_rows_bwd(n_adj, tokens, nw, ln)
+    live = tk.n_rows
+    ref = tok_adj0.copy()
+    ref[:tk.n_atoms] = g[:tk.n_atoms]
+    ref[tk.n_atoms:live] += g[tk.n_atoms:live]
+    got = tadj.cpu().numpy()
+    assert rel(got, ref) <= RTOL
+    assert np.array_equal(got[live:], tok_adj0[live:])  # dead rows untouched
+    assert rel(csa.cpu().numpy(), rcsa) <= RTOL
+
+
+def test_layer_to_forces_chain(device):
+    """The path end to end on C1: the layer's backward accumulates cf_seq_adj,
+    which the edge term turns into per-edge gradients and the fold into forces,
+    all on the device, against the oracle's same chain."""
+    print("[gpu] layer -> cf_seq_adj -> forces (c1)", flush=True)
+    cfg, s, pk = _edges("c1")
+    N, E = len(s.positions), len(pk.center)
+    tk = systems.tokens_from_edges(N, systems.neighbor_list(s, cfg.cutoff), cfg.cutoff, cfg.width)
+    assert np.array_equal(tk.off, pk.off) and tk.n_edges == E
+    H, hd, D = cfg.heads, cfg.head_dim, cfg.d_model
+    inp = systems.attention_inputs(tk, D, H, seed=4)
+    rng = np.random.default_rng(5)
+    tokens = rng.standard_normal((tk.n_rows, D)).astype(np.float32)
+    nw = np.ones(D, np.float32)
+    out_adj = rng.standard_normal((tk.n_rows, D)).astype(np.float32)
+    x4 = rng.standard_normal((E, 4)).astype(np.float32)
+    t = A.Tokens(dev(tk.off, device), N, False)
+    ws = A.Workspace(device)
+    w_in, b_in, w_out, b_out = (dev(inp[k], device) for k in ("w_in", "b_in", "w_out", "b_out"))
+    cf = L.cf_seq(t.off, dev(pk.cut, device), N, tk.slots)
+    tok = dev(tokens, device)
+    out = torch.empty((tk.n_rows, D), device=device)
+    L.attention_layer(ws, "a", out, tok, dev(nw, device), None, w_in, b_in, cf, w_out, b_out, t, tk.slots, H, hd, 1.0)
+    tadj = torch.zeros((tk.n_rows, D), device=device)
+    csa = torch.zeros((N, tk.slots), device=device)
+    L.attention_layer_bwd(ws, "a", tadj, csa, dev(out_adj, device), tok, dev(nw, device), None, w_in, b_in, cf,
+                          w_out, t, tk.slots, H, hd, 1.0)
+    dpk = F.PackedEdges.from_host(pk, device)
+    soff = dev(np.array([0, N], np.int32), device)
+    forces, vir9, grad = F.forces_and_virial(dpk, N, soff, dev(x4, device), None, csa, cfg.width, "cosine",
+                                             scale=-1.0)
+    torch.cuda.synchronize()
+    rcf = oracle.cf_seq(pk.off, pk.cut, tk.slots)
+    assert np.array_equal(cf.cpu().numpy(), rcf)
+    qkv = oracle.linear(oracle.norm_rows(tokens, nw, None), inp["w_in"], inp["b_in"])
+    _, merged, ml = oracle.attention(qkv, pk.off, rcf, inp["w_out"], inp["b_out"], H, hd, 1.0)
+    _, rcsa = oracle.attention_bwd(out_adj, qkv, pk.off, rcf, inp["w_in"], inp["w_out"], merged, ml, H, hd, 1.0)
+    assert rel(csa.cpu().numpy(), rcsa) <= RTOL
+    rg = oracle.edge_grad(pk.off, pk.center, x4, None, rcsa, pk.vec, pk.dist, pk.pcut, cfg.width, 1)
+    assert rel(grad.cpu().numpy(), rg) <= RTOL
+    rf, rv = oracle.fold(N, pk.off, pk.reverse, pk.vec, rg, scale=-1.0)
+    assert rel(forces.cpu().numpy(), rf) <= RTOL
+    assert rel(vir9.cpu().numpy()[0], rv.sum(axis=0)) <= RTOL
