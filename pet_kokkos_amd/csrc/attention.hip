@@ -34,6 +34,7 @@
 // order, and nothing is atomic: the result is bit-identical run to run.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -202,7 +203,10 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
   constexpr int W = HD / 4, DT = HD / 16, P = Lds<HD>::P;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const int i = 16 * w + c;  // this lane's query slot
-  if (w >= at.nb) return;    // slots past the atom's tokens
+  if (w >= at.nb) {  // slots past the atom's tokens: only the workgroup barrier
+    lds_barrier();
+    return;
+  }
   float mx = kOff, sum = 0.f;
   f4 acc[DT];
 #pragma unroll
@@ -243,15 +247,24 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
       for (int t = 0; t < DT; ++t) acc[t] = mfma(v[t], p[r], acc[t]);  // O^T: dim (4g + r') DT + t, query i
     }
   };
-  // The next block's scores go out before this block's softmax and PV, in
-  // one basic block the scheduler interleaves; the last block is peeled.
-  f4 s = scores(0);
-  for (int J = 0; J + 1 < at.nb; ++J) {
-    const f4 sn = scores(J + 1);
+  // The wave's own key block first: it is all the wave itself staged, so it
+  // runs before the workgroup barrier, under the other waves' loads. Then the
+  // others in the order w + 1, w + 2, ... (mod nb), the next block's scores
+  // issued before this block's softmax and PV, the last block peeled.
+  block(w, scores(w));
+  lds_barrier();
+  if (at.nb > 1) {
+    int J = w + 1 < at.nb ? w + 1 : 0;
+    f4 s = scores(J);
+    for (int t = 2; t < at.nb; ++t) {
+      const int Jn = J + 1 < at.nb ? J + 1 : 0;
+      const f4 sn = scores(Jn);
+      block(J, s);
+      s = sn;
+      J = Jn;
+    }
     block(J, s);
-    s = sn;
   }
-  block(at.nb - 1, s);
   const float tot = sum_g(sum);
   // else a query on an edge at its cutoff: zeros
   out.live = i < at.cnt && (i == 0 || !is_off(lcf[i]));
@@ -291,24 +304,33 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
   float* Ks = lds;
   float* Vs = Ks + R * P;
   float* lcf = Vs + R * P;
-  const int l = threadIdx.x & 63, g = l >> 4, i = 16 * (threadIdx.x >> 6) + (l & 15);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, i = 16 * w + (l & 15);
   const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  // Each wave stages its own block -- rows 16w .. 16w+15 of K and V, lane
+  // (c, g) the slice of row 16w + c it also loads q from -- and its keys' cf;
+  // the workgroup barrier is inside fwd_item, after the wave's own block.
   float q[W];
-  {
-    SliceRegs<HD> pk, pv;
-    pk.load(qkv, ldq, D + at.h * HD, at);
-    pv.load(qkv, ldq, 2 * D + at.h * HD, at);
-    const float pcf = int(threadIdx.x) < at.cnt ? cf_seq[size_t(at.n) * ldc + threadIdx.x] : 0.f;
-    if (i < at.cnt)
-      gmem_get<W>(qkv + at.row(i) * ldq + at.h * HD + g * W, q);
-    else
+  if (w < at.nb) {
+    float k[W], v[W];
+    const bool real = i < at.cnt;
+    if (real) {
+      const size_t r = at.row(i);
+      gmem_get<W>(qkv + r * ldq + at.h * HD + g * W, q);
+      gmem_get<W>(qkv + r * ldq + D + at.h * HD + g * W, k);
+      gmem_get<W>(qkv + r * ldq + 2 * D + at.h * HD + g * W, v);
+    } else {
 #pragma unroll
-      for (int t = 0; t < W; ++t) q[t] = 0.f;
-    pk.template store<P>(Ks);
-    pv.template store<P>(Vs);
-    if (int(threadIdx.x) < R) lcf[threadIdx.x] = pcf > 0.f ? __logf(pcf) : kOff;
+      for (int t = 0; t < W; ++t) q[t] = k[t] = v[t] = 0.f;
+    }
+    const float pcf = real && g == 0 ? cf_seq[size_t(at.n) * ldc + i] : 0.f;
+    float* o = Ks + i * P + g * W;
+#pragma unroll
+    for (int t = 0; t < W; t += 4) {
+      *reinterpret_cast<float4*>(o + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
+      *reinterpret_cast<float4*>(o + (Vs - Ks) + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+    }
+    if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
   }
-  lds_barrier();
   FwdOut<HD> out;
   fwd_item<HD>(at, Ks, Vs, lcf, q, sc, out);
   fwd_store<HD>(at, out, S, H, merged, ldm, ml);
@@ -469,31 +491,41 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
   float* Vs = Gs + R * P;  // when vlds
   float* lcf = Vs + (vlds ? R * P : 0);
   float* Tb = lcf + R;
-  const int l = threadIdx.x & 63, g = l >> 4, i = 16 * (threadIdx.x >> 6) + (l & 15);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, i = 16 * w + (l & 15);
   const Atom at(off, blockIdx.x, H, N, S, n0, eb);
   float oo[W], mi = kOff, li = 0.f;
-  {
-    SliceRegs<HD> pq, pk, pg, pv;
-    pq.load(qkv, ldq, at.h * HD, at);
-    pk.load(qkv, ldq, D + at.h * HD, at);
-    pg.load(dmerged, ldg, at.h * HD, at);
-    if (vlds) pv.load(qkv, ldq, 2 * D + at.h * HD, at);
-    const float pcf = int(threadIdx.x) < at.cnt ? cf_seq[size_t(at.n) * ldc + threadIdx.x] : 0.f;
-    if (i < at.cnt) {
+  // Each wave stages its own block -- rows 16w .. 16w+15 of Q, K, dO (and V),
+  // lane (c, g) the slice of row 16w + c that is its MFMA operand -- and the
+  // cf of its own keys. Step 0 of the tile schedule (tile (w, w)) reads only
+  // that block, so a wave starts computing as soon as its own loads are in,
+  // and the first workgroup barrier comes after step 0, not before it.
+  if (w < at.nb) {
+    float q[W], k[W], go[W], v[W];
+    const bool real = i < at.cnt;
+    if (real) {
+      const size_t r = at.row(i);
+      gmem_get<W>(qkv + r * ldq + at.h * HD + g * W, q);
+      gmem_get<W>(qkv + r * ldq + D + at.h * HD + g * W, k);
+      gmem_get<W>(dmerged + r * ldg + at.h * HD + g * W, go);
+      if (vlds) gmem_get<W>(qkv + r * ldq + 2 * D + at.h * HD + g * W, v);
       gmem_get<W>(merged + at.grow(i) * ldm + at.h * HD + g * W, oo);  // the whole's rows
       const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
       mi = m2[0], li = m2[1];
     } else {
 #pragma unroll
-      for (int t = 0; t < W; ++t) oo[t] = 0.f;
+      for (int t = 0; t < W; ++t) q[t] = k[t] = go[t] = v[t] = oo[t] = 0.f;
     }
-    pq.template store<P>(Qs);
-    pk.template store<P>(Ks);
-    pg.template store<P>(Gs);
-    if (vlds) pv.template store<P>(Vs);
-    if (int(threadIdx.x) < R) lcf[threadIdx.x] = pcf > 0.f ? __logf(pcf) : kOff;
+    const float pcf = real && g == 0 ? cf_seq[size_t(at.n) * ldc + i] : 0.f;
+    float* o = Qs + i * P + g * W;
+#pragma unroll
+    for (int t = 0; t < W; t += 4) {
+      *reinterpret_cast<float4*>(o + t) = make_float4(q[t], q[t + 1], q[t + 2], q[t + 3]);
+      *reinterpret_cast<float4*>(o + (Ks - Qs) + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
+      *reinterpret_cast<float4*>(o + (Gs - Qs) + t) = make_float4(go[t], go[t + 1], go[t + 2], go[t + 3]);
+      if (vlds) *reinterpret_cast<float4*>(o + (Vs - Qs) + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+    }
+    if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
   }
-  lds_barrier();
   BwdOut<HD> out;
   bwd_item<HD>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, H, sc, out);
   bwd_store<HD>(at, out, S, H, sc, qkv_adj, lda, cfh);
@@ -574,6 +606,29 @@ void allow_lds(K k, size_t bytes) {
 }
 
 // The forward over atoms [n0, n1), qkv a chunk whose edge 0 is row eb.
+// Workgroups of kernel k (NW waves, lds bytes) resident on all CUs at once,
+// by the rules measured on gfx950 with spin kernels: a SIMD holds
+// min(8, 512 / vgprs) waves (vgprs rounded up to 8); workgroups of a wave
+// count not a multiple of 4 lose one slot a SIMD in the packing, floor((4c -
+// 4) / NW) of them a CU (c waves a SIMD), else floor(4c / NW); LDS goes in
+// 2 KB granules of 160 KB. The runtime's occupancy query counts more than fit
+// for 5-wave workgroups, and a persistent grid past residency leaves its last
+// workgroups to start only when others have finished all their items.
+template <class K>
+int64_t resident_grid(K k, int NW, size_t lds) {
+  int dev = 0, cus = 1;
+  (void)hipGetDevice(&dev);
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  hipFuncAttributes fa{};
+  if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(k)) != hipSuccess) return int64_t(cus);
+  const int vg = std::max(8, (fa.numRegs + 7) / 8 * 8);
+  const int c = std::min(8, 512 / vg);
+  const int by_vgpr = NW % 4 ? (4 * c - 4) / NW : 4 * c / NW;
+  const size_t gran = (lds + 2047) / 2048 * 2048;
+  const int by_lds = gran ? int(163840 / gran) : 8;
+  return int64_t(cus) * std::max(1, std::min(by_vgpr, by_lds));
+}
+
 template <int HD>
 int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
                const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, hipStream_t st) {
