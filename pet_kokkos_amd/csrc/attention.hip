@@ -134,31 +134,6 @@ struct Atom {
   __device__ size_t grow(int s) const { return s == 0 ? size_t(n) : size_t(N) + size_t(o0) + size_t(s - 1); }
 };
 
-// A thread's share of one head slice of an item's rows [0, 16 NW) (chunk
-// rows), loaded into registers and then stored to LDS: blockDim = 64 NW
-// threads, hd/16 float4 each.
-template <int HD>
-struct SliceRegs {
-  static constexpr int C4 = HD / 4, PER = HD / 16;
-  float4 v[PER];
-  __device__ __forceinline__ void load(const float* src, int64_t ld, int col, const Atom& at) {
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int idx = threadIdx.x + k * blockDim.x, r = idx / C4, c4 = idx - r * C4;
-      v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (r < at.cnt) v[k] = *reinterpret_cast<const float4*>(src + at.row(r) * ld + col + 4 * c4);
-    }
-  }
-  template <int P>
-  __device__ __forceinline__ void store(float* dst) const {
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int idx = threadIdx.x + k * blockDim.x, r = idx / C4, c4 = idx - r * C4;
-      *reinterpret_cast<float4*>(dst + r * P + 4 * c4) = v[k];
-    }
-  }
-};
-
 // Element e of a lane's hd/4 slice, from the DT result tiles: e = r * DT + t.
 template <int DT>
 __device__ __forceinline__ float tile_elem(const f4* acc, int e) {
