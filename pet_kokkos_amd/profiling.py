@@ -26,6 +26,8 @@ def main(argv=None):
     ap.add_argument("--config", default="c3", choices=sorted(systems.CONFIGS))
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--rows", action="store_true",
+                    help="also run the token norm (forward, backward) and the forces' edge term and fold each step")
     args = ap.parse_args(argv)
     device = torch.device("cuda", 0)
     conf, tk = systems.config_tokens(args.config, seed=0)
@@ -48,9 +50,30 @@ def main(argv=None):
     torch.cuda.synchronize()
     dst.copy_(src)  # calibration: reads and writes copy_mib MiB
     torch.cuda.synchronize()
+    rows = None
+    if args.rows:
+        from . import forces as F
+        from . import layer as L
+        cfgs = systems.CONFIGS[args.config]
+        s = systems.build_structure(cfgs.structure, 0)
+        pk = F.PackedEdges.from_host(systems.packed_edges(len(s.positions),
+                                                          systems.neighbor_list(s, cfgs.cutoff), cfgs.cutoff,
+                                                          cfgs.width), device)
+        x4 = torch.randn((pk.n_edges, 4), device=device, generator=g)
+        nw = torch.ones(D, device=device)
+        y, gx = torch.empty_like(dm), torch.empty_like(dm)
+        grad = torch.empty((pk.n_edges, 3), dtype=torch.float64, device=device)
+
+        def rows():
+            L.norm_rows(y, dm, nw, None)
+            L.norm_rows_bwd(gx, y, dm, nw, False)
+            F.edge_grad(pk, x4, None, cf_adj, cfgs.width, "cosine", grad)
+            F.fold_edge_gradients(pk, N, grad, -1.0)
     for _ in range(args.steps):
         A.attn_fwd(qkv, off, cf, H, hd, merged=merged, ml=ml)
         A.attn_bwd(qkv, off, dm, merged, ml, cf, H, hd, cf_seq_adj=cf_adj, qkv_adj=qkv_adj, cfh=cfh)
+        if rows:
+            rows()
     torch.cuda.synchronize()
     print(json.dumps({"config": args.config, "steps": args.steps, "copy_mib": args.copy_mib, "N": N, "T": T, "S": S,
                       "D": D, "H": H}), flush=True)
