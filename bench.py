@@ -116,7 +116,64 @@ def time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device):
     eb = E * (16 + 4 + 4 + 24 + 8 + 8 + 4 + 24)
     out["edge_grad"] = dict(us=us_e, edges=E, gbps=eb / us_e / 1e3)
     out["fold"] = dict(us=us_f, atoms=len(s.positions))
+    out["c2_attention_share_of_ef_ms"] = c2_attention_share(device, reps)
     return out
+
+
+def c2_attention_share(device, reps):
+    """The attention path's share of one energy+forces evaluation of the C2
+    model (648-atom water, d_model 128, 4 heads of 32, 2 GNN layers x 2
+    transformer layers = 4 attention blocks): per block the layer-level
+    forward and backward (norm, QKV linear, attention, output linear and back
+    to the tokens' adjoint, cf_seq_adj accumulated), then the forces' edge
+    term and fold from the accumulated cf_seq_adj. The rest of the model
+    (embeddings, MLPs, readout) is not built here, so this is not the whole
+    E+F time."""
+    import numpy as np
+    import torch
+
+    from pet_kokkos_amd import attention as A
+    from pet_kokkos_amd import forces as F
+    from pet_kokkos_amd import layer as L
+    from pet_kokkos_amd import systems
+
+    cfg = systems.CONFIGS["c2"]
+    s = systems.build_structure(cfg.structure, 0)
+    e = systems.neighbor_list(s, cfg.cutoff)
+    N = len(s.positions)
+    tk = systems.tokens_from_edges(N, e, cfg.cutoff, cfg.width)
+    pk = F.PackedEdges.from_host(systems.packed_edges(N, e, cfg.cutoff, cfg.width), device)
+    H, hd, D = cfg.heads, cfg.head_dim, cfg.d_model
+    T, S = tk.n_rows, tk.slots
+    gen = torch.Generator(device=device)
+    gen.manual_seed(5)
+    blocks = []
+    for _ in range(4):
+        blocks.append(dict(nw=torch.ones(D, device=device), w_in=torch.randn((3 * D, D), device=device, generator=gen) / D ** 0.5,
+                           b_in=torch.zeros(3 * D, device=device), w_out=torch.randn((D, D), device=device, generator=gen) / D ** 0.5,
+                           b_out=torch.zeros(D, device=device)))
+    tok = torch.randn((T, D), device=device, generator=gen)
+    out_adj = torch.randn((T, D), device=device, generator=gen)
+    off = torch.from_numpy(tk.off).to(device)
+    cf = torch.from_numpy(tk.cf_seq).to(device)
+    t = A.Tokens(off, N)
+    ws = A.Workspace(device)
+    out = torch.empty((T, D), device=device)
+    tadj = torch.empty((T, D), device=device)
+    csa = torch.zeros((N, S), device=device)
+    x4 = torch.randn((pk.n_edges, 4), device=device, generator=gen)
+    soff = torch.tensor([0, N], dtype=torch.int32, device=device)
+
+    def ef():
+        for b, p in enumerate(blocks):
+            L.attention_layer(ws, f"b{b}", out, tok, p["nw"], None, p["w_in"], p["b_in"], cf, p["w_out"], p["b_out"],
+                              t, S, H, hd, 1.0)
+        for b, p in reversed(list(enumerate(blocks))):
+            L.attention_layer_bwd(ws, f"b{b}", tadj, csa, out_adj, tok, p["nw"], None, p["w_in"], p["b_in"], cf,
+                                  p["w_out"], t, S, H, hd, 1.0)
+        F.forces_and_virial(pk, N, soff, x4, None, csa, cfg.width, "cosine", -1.0)
+
+    return _timed(ef, max(5, reps // 4)) / 1e3
 
 
 def main():

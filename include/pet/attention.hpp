@@ -1,6 +1,7 @@
 // pet/attention.hpp -- the reference's C++ attention interface over the C ABI.
 //
-// pet::attention and pet::attention_bwd with the arguments, meaning, conventions
+// pet::attention and pet::attention_bwd (and the token norm, cf_seq and the
+// layer-level attention block around them) with the arguments, meaning, conventions
 // and error behaviour of peterspackman/pet-kokkos's (src/ops.hpp:121-132,
 // src/attention.cpp:2189-2206), for a caller that holds plain device pointers
 // instead of Kokkos views:
@@ -151,6 +152,71 @@ inline void attention_bwd(Workspace& ws, const std::string& key, View2D in_adj, 
                           cf_seq.data(), cf_seq.stride(0), w_in.v.data(), w_out.v.data(), tk.off, merged.data(),
                           ml.data(), beta, scratch, need, stream),
         "attention_bwd");
+}
+
+// ---- the attention's input side ------------------------------------------
+
+// cf_seq [N, S]: 1, then the atom's kept edges' cutoff factors (cut, packed
+// order), then 0 (the reference's pet_cfseq, src/device_neighbors.cpp:318-323).
+inline void cf_seq(View2D out, const Tokens& tk, const float* cut, int S, hipStream_t stream = nullptr) {
+  pet_attn_shape sh = make_shape(tk, tk.N, S, 1, 16, 1.0);
+  sh.n_rows = tk.N + (cut ? 1 : 0);
+  check(pet_attn_cf_seq(&sh, tk.off, cut, out.data(), out.stride(0), stream), "cf_seq");
+}
+
+// out = norm(in) row by row: RMSNorm, or LayerNorm when bias has data
+// (norm_rows, src/ops.hpp:376-407, with the identity prologue).
+inline void norm_rows(View2D out, View2D in, View1D weight, View1D bias, hipStream_t stream = nullptr) {
+  check(pet_norm_rows(in.extent(0), in.extent(1), out.data(), out.stride(0), in.data(), in.stride(0), weight.data(),
+                      bias.data(), stream),
+        "norm_rows");
+}
+
+// in_adj = beta in_adj + the norm's input adjoint (norm_rows_bwd,
+// src/ops.hpp:409-436, with the sink "in_adj(r, d) = beta in_adj + g").
+inline void norm_rows_bwd(View2D in_adj, View2D out_adj, View2D in, View1D weight, bool ln, Net beta = 0,
+                          hipStream_t stream = nullptr) {
+  check(pet_norm_rows_bwd(in.extent(0), in.extent(1), in_adj.data(), in_adj.stride(0), beta, out_adj.data(),
+                          out_adj.stride(0), in.data(), in.stride(0), weight.data(), ln ? 1 : 0, stream),
+        "norm_rows_bwd");
+}
+
+// The attention block of a PET layer from its tokens (PetModel::ff_layer,
+// src/feedforward.cpp:96-123): norm, qkv = linear(normed, w_in, b_in),
+// attention; the saves under `key`.
+inline void attention_layer(Workspace& ws, const std::string& key, View2D out, View2D tokens, View1D norm_w,
+                            View1D norm_b, const WeightRef& w_in, View1D b_in, View2D cf_seq, const WeightRef& w_out,
+                            View1D b_out, const Tokens& tk, int S, int heads, int head_dim, double temperature,
+                            hipStream_t stream = nullptr) {
+  const int D = heads * head_dim, T = tokens.extent(0);
+  const pet_attn_shape sh = make_shape(tk, T, S, heads, head_dim, temperature);
+  const View2D merged = ws.n2(key + ":merged", T, D);
+  const View2D ml = ws.n2(key + ":ml", tk.N * heads * S, 2);
+  const size_t need = pet_attention_layer_workspace(&sh);
+  void* scratch = ws.bytes("attention_layer:scratch", need);
+  check(pet_attention_layer(&sh, out.data(), out.stride(0), tokens.data(), tokens.stride(0), norm_w.data(),
+                            norm_b.data(), w_in.v.data(), b_in.data(), cf_seq.data(), cf_seq.stride(0),
+                            w_out.v.data(), b_out.data(), tk.off, merged.data(), ml.data(), scratch, need, stream),
+        "attention_layer");
+}
+
+// Its backward (PetModel::ff_layer_bwd, src/feedforward.cpp:292-329): the
+// tokens' adjoint, atom rows set and live edge rows accumulated as the
+// reference's sink does; cf_seq_adj accumulates.
+inline void attention_layer_bwd(Workspace& ws, const std::string& key, View2D tokens_adj, View2D cf_seq_adj,
+                                View2D out_adj, View2D tokens, View1D norm_w, View1D norm_b, const WeightRef& w_in,
+                                View1D b_in, View2D cf_seq, const WeightRef& w_out, const Tokens& tk, int S,
+                                int heads, int head_dim, double temperature, hipStream_t stream = nullptr) {
+  const int T = tokens.extent(0);
+  const pet_attn_shape sh = make_shape(tk, T, S, heads, head_dim, temperature);
+  const View2D merged = ws.peek2(key + ":merged"), ml = ws.peek2(key + ":ml");
+  const size_t need = pet_attention_layer_workspace(&sh);
+  void* scratch = ws.bytes("attention_layer:scratch", need);
+  check(pet_attention_layer_bwd(&sh, tokens_adj.data(), tokens_adj.stride(0), cf_seq_adj.data(), cf_seq_adj.stride(0),
+                                out_adj.data(), out_adj.stride(0), tokens.data(), tokens.stride(0), norm_w.data(),
+                                norm_b.data(), w_in.v.data(), b_in.data(), cf_seq.data(), cf_seq.stride(0),
+                                w_out.v.data(), tk.off, merged.data(), ml.data(), scratch, need, stream),
+        "attention_layer_bwd");
 }
 
 }  // namespace pet

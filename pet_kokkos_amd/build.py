@@ -41,18 +41,22 @@ def hipcc() -> str:
 
 CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "attention_api_test.cpp")
 CPP_TEST = os.path.join(ROOT, "tests", "cpp", "attention_api_test")
+CPP_TEST2_SRC = os.path.join(ROOT, "tests", "cpp", "layer_forces_test.cpp")
+CPP_TEST2 = os.path.join(ROOT, "tests", "cpp", "layer_forces_test")
 
 
 def build_cpp_test(verbose: bool = False) -> str:
-    """The C++ caller of include/pet/attention.hpp that tests/test_gpu_cpp_api.py runs."""
-    cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
-           "-o", CPP_TEST, CPP_TEST_SRC, "-L", HERE, "-lpet_attn", "-Wl,-rpath,$ORIGIN/../../pet_kokkos_amd"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {CPP_TEST}")
+    """The C++ callers of include/pet/attention.hpp and include/pet/forces.hpp
+    that tests/test_gpu_cpp_api.py runs."""
+    for src, exe in ((CPP_TEST_SRC, CPP_TEST), (CPP_TEST2_SRC, CPP_TEST2)):
+        cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+               "-o", exe, src, "-L", HERE, "-lpet_attn", "-Wl,-rpath,$ORIGIN/../../pet_kokkos_amd"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"hipcc failed ({res.returncode}) building {exe}")
     return CPP_TEST
 
 

@@ -51,3 +51,50 @@ def test_cpp_attention_api(tmp_path, beta, temperature):
     assert rel(in_adj, rin) <= RTOL
     assert rel(cf_adj, rca) <= RTOL
     assert (tmp_path / "repeat.ok").exists(), "a warm workspace's second backward differed"
+
+
+def test_cpp_layer_and_forces_api(tmp_path):
+    """cf_seq, attention_layer, attention_layer_bwd and forces_and_virial
+    (include/pet/attention.hpp, include/pet/forces.hpp) from a compiled C++
+    caller on the C1 geometry, against the oracle's chain of the same steps."""
+    if not os.path.exists(B.CPP_TEST2):
+        pytest.fail(f"{B.CPP_TEST2} is not built (python -m pet_kokkos_amd.build)")
+    cfg = systems.CONFIGS["c1"]
+    s = systems.build_structure(cfg.structure, 0)
+    e = systems.neighbor_list(s, cfg.cutoff)
+    N = len(s.positions)
+    pk = systems.packed_edges(N, e, cfg.cutoff, cfg.width)
+    tk = systems.tokens_from_edges(N, e, cfg.cutoff, cfg.width)
+    H, hd, D, E, S, T = cfg.heads, cfg.head_dim, cfg.d_model, len(pk.center), tk.slots, tk.n_rows
+    inp = systems.attention_inputs(tk, D, H, seed=8)
+    rng = np.random.default_rng(9)
+    tokens = rng.standard_normal((T, D)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    x4 = rng.standard_normal((E, 4)).astype(np.float32)
+    f32 = dict(tokens=tokens, nw=nw, w_in=inp["w_in"], b_in=inp["b_in"], w_out=inp["w_out"], b_out=inp["b_out"],
+               cut=pk.cut, out_adj=inp["out_adj"], x4=x4)
+    for k, v in f32.items():
+        np.ascontiguousarray(v, dtype=np.float32).tofile(tmp_path / f"{k}.f32")
+    for k, v in dict(off=pk.off, center=pk.center, reverse=pk.reverse).items():
+        np.ascontiguousarray(v, dtype=np.int32).tofile(tmp_path / f"{k}.i32")
+    for k, v in dict(vec=pk.vec, dist=pk.dist, pcut=pk.pcut).items():
+        np.ascontiguousarray(v, dtype=np.float64).tofile(tmp_path / f"{k}.f64")
+    print("[gpu] C++ layer + forces API diamond-64", flush=True)
+    res = subprocess.run([str(a) for a in (B.CPP_TEST2, tmp_path, N, T, S, H, hd, E)], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    rd = lambda k, dt, shp: np.fromfile(tmp_path / k, dtype=dt).reshape(shp)
+    rcf = oracle.cf_seq(pk.off, pk.cut, S)
+    assert np.array_equal(rd("cf.f32", np.float32, (N, S)), rcf)
+    qkv = oracle.linear(oracle.norm_rows(tokens, nw, None), inp["w_in"], inp["b_in"])
+    rout, rm, rml = oracle.attention(qkv, pk.off, rcf, inp["w_out"], inp["b_out"], H, hd, 1.0)
+    assert rel(rd("out.f32", np.float32, (T, D)), rout) <= RTOL
+    n_adj, rcsa = oracle.attention_bwd(inp["out_adj"], qkv, pk.off, rcf, inp["w_in"], inp["w_out"], rm, rml, H, hd, 1.0)
+    rtadj = oracle.norm_rows_bwd(n_adj, tokens, nw, False)
+    assert rel(rd("tokens_adj.f32", np.float32, (T, D)), rtadj) <= RTOL
+    assert rel(rd("cf_adj.f32", np.float32, (N, S)), rcsa) <= RTOL
+    rg = oracle.edge_grad(pk.off, pk.center, x4, None, rcsa, pk.vec, pk.dist, pk.pcut, 0.5, 1)
+    assert rel(rd("grad.f64", np.float64, (E, 3)), rg) <= RTOL
+    rf, rv = oracle.fold(N, pk.off, pk.reverse, pk.vec, rg, scale=-1.0)
+    assert rel(rd("forces.f64", np.float64, (N, 3)), rf) <= RTOL
+    assert rel(rd("vir9.f64", np.float64, (9,)), rv.sum(axis=0)) <= RTOL
