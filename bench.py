@@ -117,7 +117,44 @@ def time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device):
     out["edge_grad"] = dict(us=us_e, edges=E, gbps=eb / us_e / 1e3)
     out["fold"] = dict(us=us_f, atoms=len(s.positions))
     out["c2_attention_share_of_ef_ms"] = c2_attention_share(device, reps)
+    out["other_configs"] = other_configs(device, reps)
     return out
+
+
+def other_configs(device, reps):
+    """Core fwd and bwd times of the ragged (C4) and batched (C5) workloads,
+    with their fraction of the same roofline."""
+    import torch
+
+    from pet_kokkos_amd import attention as A
+    from pet_kokkos_amd import systems
+
+    res = {}
+    for name in ("c4", "c5"):
+        conf, tk = systems.config_tokens(name, seed=0)
+        H, hd, D = conf.heads, conf.head_dim, conf.d_model
+        N, S, T = tk.n_atoms, tk.slots, tk.n_rows
+        gen = torch.Generator(device=device)
+        gen.manual_seed(3)
+        qkv = torch.randn((T, 3 * D), device=device, generator=gen)
+        dm = torch.randn((T, D), device=device, generator=gen)
+        off = torch.from_numpy(tk.off).to(device)
+        cf = torch.from_numpy(tk.cf_seq).to(device)
+        merged = torch.empty((T, D), device=device)
+        ml = torch.empty((N * H * S, 2), device=device)
+        qa = torch.empty((T, 3 * D), device=device)
+        cfh = torch.empty((N, H, S), device=device)
+        ca = torch.zeros((N, S), device=device)
+        f_us = _timed(lambda: A.attn_fwd(qkv, off, cf, H, hd, merged=merged, ml=ml), reps)
+        b_us = _timed(lambda: A.attn_bwd(qkv, off, dm, merged, ml, cf, H, hd, cf_seq_adj=ca, qkv_adj=qa, cfh=cfh), reps)
+        alg = algorithmic(tk, D, H)
+        bound = max((alg["fwd_flops"] + alg["bwd_flops"]) / PEAK_FP32_MFMA,
+                    (alg["fwd_bytes"] + alg["bwd_bytes"]) / PEAK_HBM) * 1e6
+        res[name] = dict(workload=conf.name, atoms=N, tokens=T, head_dim=hd, fwd_us=f_us, bwd_us=b_us,
+                         bound_us=bound, frac_of_roofline=bound / (f_us + b_us))
+        del qkv, dm, merged, ml, qa, cfh, ca
+        torch.cuda.empty_cache()
+    return res
 
 
 def c2_attention_share(device, reps):

@@ -254,7 +254,25 @@ CONFIGS = {
     "c4": AttnConfig("ragged-4096", "random:4096:0.1", 256, 8, 5.0),
     # configs[1] geometry at the attention shapes of its model (d 128, 4 heads)
     "c2": AttnConfig("water-648", "water:6:18.6", 128, 4, 4.5),
+    # 32 structures in one call, alternating diamond-64 and water-648
+    "c5": AttnConfig("batch-32", "batch:16", 512, 8, 4.5),
 }
+
+
+def batch_edges(n_pairs: int = 16, cutoff: float = 4.5, seed: int = 0):
+    """2 n_pairs independent structures (diamond-64 and water-648 alternating,
+    each seeded by its index) as one atom list: (atoms, edges with atom
+    indices offset per structure, per-structure atom offsets soff)."""
+    parts, soff, base = [], [0], 0
+    for k in range(2 * n_pairs):
+        st = diamond(2, jitter=0.01, seed=seed + k) if k % 2 == 0 else water_box(6, 18.6, seed=seed + k)
+        e = neighbor_list(st, cutoff)
+        parts.append(Edges(e.centre + base, e.neigh + base, e.vec, e.dist, e.shift))
+        base += len(st.positions)
+        soff.append(base)
+    cat = lambda f: np.concatenate([getattr(p, f) for p in parts])
+    return base, Edges(cat("centre").astype(np.int32), cat("neigh").astype(np.int32), cat("vec"), cat("dist"),
+                       cat("shift")), np.array(soff, dtype=np.int32)
 
 
 def build_structure(spec: str, seed: int = 0) -> Structure:
@@ -270,6 +288,9 @@ def build_structure(spec: str, seed: int = 0) -> Structure:
 
 def config_tokens(name: str, seed: int = 0) -> tuple[AttnConfig, Tokens]:
     cfg = CONFIGS[name]
+    if cfg.structure.startswith("batch:"):
+        N, e, _ = batch_edges(int(cfg.structure.split(":")[1]), cfg.cutoff, seed)
+        return cfg, tokens_from_edges(N, e, cfg.cutoff, cfg.width)
     s = build_structure(cfg.structure, seed)
     e = neighbor_list(s, cfg.cutoff)
     return cfg, tokens_from_edges(len(s.positions), e, cfg.cutoff, cfg.width)

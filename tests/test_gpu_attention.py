@@ -96,13 +96,16 @@ def test_golden_vectors(device, path):
     assert rel(ml[live, 1], g["ml"][live, 1]) <= RTOL
 
 
-@pytest.mark.parametrize("cfg", ["c1", "c2", "c4", "c3"])
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c4", "c3", "c5"])
 def test_configs(device, cfg):
     conf, tk = systems.config_tokens(cfg)
-    inp = systems.attention_inputs(tk, conf.d_model, conf.heads, seed=1)
     rng = np.random.default_rng(3)
-    dm = rng.standard_normal((tk.n_rows, conf.d_model)).astype(np.float32)
-    check_against_oracle(device, f"config {cfg} ({conf.name})", tk.off, tk.cf_seq, inp["qkv"], dm, conf.heads,
+    if cfg == "c5":  # 32 structures, 510k token rows at d 512: qkv drawn directly
+        qkv = rng.standard_normal((tk.n_rows, 3 * conf.d_model), dtype=np.float32)
+    else:
+        qkv = systems.attention_inputs(tk, conf.d_model, conf.heads, seed=1)["qkv"]
+    dm = rng.standard_normal((tk.n_rows, conf.d_model), dtype=np.float32)
+    check_against_oracle(device, f"config {cfg} ({conf.name})", tk.off, tk.cf_seq, qkv, dm, conf.heads,
                          conf.head_dim)
 
 
