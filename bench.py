@@ -210,7 +210,12 @@ def c2_attention_share(device, reps):
                                   p["w_out"], t, S, H, hd, 1.0)
         F.forces_and_virial(pk, N, soff, x4, None, csa, cfg.width, "cosine", -1.0)
 
-    return _timed(ef, max(5, reps // 4)) / 1e3
+    from pet_kokkos_amd import graph as G
+
+    eager_ms = _timed(ef, max(5, reps // 4)) / 1e3
+    cache = G.GraphCache()
+    return dict(eager_ms=eager_ms, graph_ms=_timed(lambda: cache.run("c2-ef", ef), max(5, reps // 4)) / 1e3,
+                graph_note="the same work recorded once as a HIP graph and replayed (pet_kokkos_amd.graph)")
 
 
 def main():

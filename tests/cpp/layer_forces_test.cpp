@@ -8,13 +8,19 @@
 // DIR/{off,center,reverse}.i32 and DIR/{vec,dist,pcut}.f64, then: cf_seq from
 // the edges' cutoff factors, attention_layer, attention_layer_bwd (cf_seq_adj
 // from zero) and forces_and_virial (cosine cutoff, width 0.5, scale -1); writes
-// DIR/{cf,out,tokens_adj,cf_adj}.f32 and DIR/{forces,vir9,grad}.f64.
+// DIR/{cf,out,tokens_adj,cf_adj}.f32 and DIR/{forces,vir9,grad}.f64; then runs
+// the same chain four more times through a pet::GraphCache on a stream of its
+// own (eager, captured, replayed, replayed) and writes DIR/graph.ok when every
+// run gave the first one's bits.
 #include <cstdio>
 #include <cstdlib>
 #include <string>
 #include <vector>
 
+#include <cstring>
+
 #include "pet/forces.hpp"
+#include "pet/graph.hpp"
 
 template <class T>
 static std::vector<T> read(const std::string& path, size_t n) {
@@ -45,6 +51,10 @@ static std::vector<T> host(const T* p, size_t n) {
   std::vector<T> h(n);
   if (hipMemcpy(h.data(), p, sizeof(T) * n, hipMemcpyDeviceToHost) != hipSuccess) std::exit(5);
   return h;
+}
+
+__global__ void fill0(float* p, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) p[i] = 0.0f;
 }
 
 int main(int argc, char** argv) {
@@ -116,6 +126,48 @@ int main(int argc, char** argv) {
   write(dir + "/forces.f64", host(forces.data(), size_t(N) * 3));
   write(dir + "/vir9.f64", host(vir9.data(), size_t(9)));
   write(dir + "/grad.f64", host(grad.data(), size_t(E) * 3));
+  // the chain recorded as a graph and replayed: every run's bits as the first's
+  {
+    hipStream_t st = nullptr;
+    if (hipStreamCreate(&st) != hipSuccess) return 9;
+    const auto ref_t = host(tadj, size_t(T) * D);
+    const auto ref_c = host(csa, size_t(N) * S);
+    const auto ref_f = host(forces.data(), size_t(N) * 3);
+    pet::GraphCache cache(st);
+    const pet::GraphCache::Key key{uintptr_t(tokens), uintptr_t(T), uintptr_t(D)};
+    bool same = true;
+    try {
+      for (int rep = 0; rep < 4; ++rep) {
+        cache.run(key, [&] {
+          // the accumulated outputs start from zero: a fill kernel, no memset node
+          hipLaunchKernelGGL(fill0, dim3(256), dim3(256), 0, st, tadj, size_t(T) * D);
+          hipLaunchKernelGGL(fill0, dim3(64), dim3(256), 0, st, csa, size_t(N) * S);
+          pet::attention_layer(ws, "L0.a0", pet::View2D(out, T, D), pet::View2D(tokens, T, D), pet::View1D{nw, D},
+                               pet::View1D{}, pet::WeightRef(pet::View2D(w_in, 3 * D, D)), pet::View1D{b_in, 3 * D},
+                               pet::View2D(cf, N, S), pet::WeightRef(pet::View2D(w_out, D, D)), pet::View1D{b_out, D},
+                               tk, S, H, HD, 1.0, st);
+          pet::attention_layer_bwd(ws, "L0.a0", pet::View2D(tadj, T, D), pet::View2D(csa, N, S),
+                                   pet::View2D(out_adj, T, D), pet::View2D(tokens, T, D), pet::View1D{nw, D},
+                                   pet::View1D{}, pet::WeightRef(pet::View2D(w_in, 3 * D, D)),
+                                   pet::View1D{b_in, 3 * D}, pet::View2D(cf, N, S),
+                                   pet::WeightRef(pet::View2D(w_out, D, D)), tk, S, H, HD, 1.0, st);
+          pet::forces_and_virial(ws, pk, N, soff, 1, pet::View2D(x4, E, 4), pet::View1D{}, pet::View2D(csa, N, S),
+                                 0.5, pet::CutoffFunction::Cosine, -1.0, forces, vir9, grad, st);
+        });
+        if (hipStreamSynchronize(st) != hipSuccess) return 10;
+        const auto t2 = host(tadj, size_t(T) * D), c2 = host(csa, size_t(N) * S);
+        const auto f2 = host(forces.data(), size_t(N) * 3);
+        same = same && std::memcmp(t2.data(), ref_t.data(), t2.size() * 4) == 0 &&
+               std::memcmp(c2.data(), ref_c.data(), c2.size() * 4) == 0 &&
+               std::memcmp(f2.data(), ref_f.data(), f2.size() * 8) == 0;
+      }
+    } catch (const std::exception& e) {
+      std::fprintf(stderr, "graph: %s\n", e.what());
+      return 11;
+    }
+    if (same && !cache.broken() && cache.size() == 1) write(dir + "/graph.ok", std::vector<char>{'1'});
+    (void) hipStreamDestroy(st);
+  }
   std::printf("ok\n");
   return 0;
 }
