@@ -311,6 +311,100 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
   fwd_store<HD>(at, out, S, H, merged, ldm, ml);
 }
 
+// ---- forward on the vector ALUs (for comparison) ----------------------------
+// The same forward with no matrix cores: a thread per query slot, the item's K
+// and V rows staged in LDS and read by every lane at once (broadcast), online
+// softmax over the keys four at a time. No padding to 16-token blocks, but each
+// score and each weighted V row is hd fp32 FMAs on the vector ALUs (a wave64
+// instruction every 4 cycles) instead of a quarter of a matrix-core product.
+// Selected by PET_ATTN_FWD=3 (head_dim <= 64); the matrix-core kernel is the
+// default.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_fwd_valu_kernel(const float* __restrict__ qkv, int64_t ldq,
+                                                            const int* __restrict__ off, int N, int n0, int64_t eb,
+                                                            int S, int H, float sc, const float* __restrict__ cf_seq,
+                                                            int64_t ldc, float* __restrict__ merged, int64_t ldm,
+                                                            float* __restrict__ ml) {
+  constexpr int C4 = HD / 4;
+  extern __shared__ float lds[];
+  const int D = H * HD, R = blockDim.x;
+  float* Ks = lds;
+  float* Vs = Ks + R * HD;
+  float* lcf = Vs + R * HD;
+  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  for (int f = threadIdx.x; f < at.cnt * C4; f += blockDim.x) {
+    const int r = f / C4, c4 = f - r * C4;
+    const float* src = qkv + at.row(r) * ldq + at.h * HD + 4 * c4;
+    *reinterpret_cast<float4*>(Ks + r * HD + 4 * c4) = *reinterpret_cast<const float4*>(src + D);
+    *reinterpret_cast<float4*>(Vs + r * HD + 4 * c4) = *reinterpret_cast<const float4*>(src + 2 * D);
+  }
+  const int i = threadIdx.x;
+  if (i < at.cnt) {
+    const float cv = cf_seq[size_t(at.n) * ldc + i];
+    lcf[i] = cv > 0.f ? __logf(cv) : kOff;
+  }
+  float q[HD], acc[HD];
+  if (i < at.cnt) gmem_get<HD>(qkv + at.row(i) * ldq + at.h * HD, q);
+  __syncthreads();
+  if (i >= S) return;
+  float mx = kOff, sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < HD; ++t) acc[t] = 0.f;
+  if (i < at.cnt) {
+    for (int k0 = 0; k0 < at.cnt; k0 += 4) {
+      float x[4], bm = kOff;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int k = k0 + u;
+        const float lc = k < at.cnt ? lcf[k] : kOff;
+        float d = 0.f;
+        if (!is_off(lc)) {
+#pragma unroll
+          for (int t = 0; t < HD; t += 4) {
+            const float4 kk = *reinterpret_cast<const float4*>(Ks + k * HD + t);
+            d = fmaf(q[t], kk.x, d), d = fmaf(q[t + 1], kk.y, d), d = fmaf(q[t + 2], kk.z, d), d = fmaf(q[t + 3], kk.w, d);
+          }
+        }
+        x[u] = is_off(lc) ? kOff : d * sc + lc;
+        bm = fmaxf(bm, x[u]);
+      }
+      const float nm = fmaxf(mx, bm);
+      const float alpha = __expf(mx - nm);
+      float p[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) p[u] = is_off(x[u]) ? 0.f : __expf(x[u] - nm);
+      sum = sum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+      mx = nm;
+#pragma unroll
+      for (int t = 0; t < HD; ++t) acc[t] *= alpha;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (p[u] == 0.f) continue;
+        const int k = k0 + u;
+#pragma unroll
+        for (int t = 0; t < HD; t += 4) {
+          const float4 vv = *reinterpret_cast<const float4*>(Vs + k * HD + t);
+          acc[t] = fmaf(p[u], vv.x, acc[t]), acc[t + 1] = fmaf(p[u], vv.y, acc[t + 1]);
+          acc[t + 2] = fmaf(p[u], vv.z, acc[t + 2]), acc[t + 3] = fmaf(p[u], vv.w, acc[t + 3]);
+        }
+      }
+    }
+  }
+  const bool real = i < at.cnt;
+  const bool live = real && (i == 0 || !is_off(lcf[i]));
+  const float invl = live && sum > 0.f ? 1.0f / sum : 0.f;
+  if (real) {
+    float* o = merged + at.grow(i) * ldm + at.h * HD;
+#pragma unroll
+    for (int t = 0; t < HD; t += 4)
+      *reinterpret_cast<float4*>(o + t) = make_float4(acc[t] * invl, acc[t + 1] * invl, acc[t + 2] * invl, acc[t + 3] * invl);
+  }
+  if (ml) {
+    float* mlq = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
+    mlq[0] = live ? mx : kOff, mlq[1] = invl;
+  }
+}
+
 // ---- backward --------------------------------------------------------------
 // A lane's share of one item's backward result, held until it is stored.
 template <int HD>
@@ -612,6 +706,17 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   if (bytes > size_t(max_lds_bytes())) return PET_ATTN_ESLOTS;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
+  static const int choice = env_int("PET_ATTN_FWD");  // 3: the vector-ALU kernel, for comparison
+  if constexpr (HD <= 64) {
+    const int threads = 64 * ((sh.slots + 63) / 64);
+    const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
+    if (choice == 3 && threads <= 256 && vb <= size_t(max_lds_bytes())) {
+      allow_lds(attn_fwd_valu_kernel<HD>, vb);
+      hipLaunchKernelGGL(attn_fwd_valu_kernel<HD>, dim3(unsigned(items)), dim3(threads), vb, st, qkv, ldq, off,
+                         sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml);
+      return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+    }
+  }
   auto k = NW <= 8 ? attn_fwd_kernel<HD, 512> : attn_fwd_kernel<HD, 1024>;
   allow_lds(k, bytes);
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
