@@ -675,29 +675,6 @@ void allow_lds(K k, size_t bytes) {
 }
 
 // The forward over atoms [n0, n1), qkv a chunk whose edge 0 is row eb.
-// Workgroups of kernel k (NW waves, lds bytes) resident on all CUs at once,
-// by the rules measured on gfx950 with spin kernels: a SIMD holds
-// min(8, 512 / vgprs) waves (vgprs rounded up to 8); workgroups of a wave
-// count not a multiple of 4 lose one slot a SIMD in the packing, floor((4c -
-// 4) / NW) of them a CU (c waves a SIMD), else floor(4c / NW); LDS goes in
-// 2 KB granules of 160 KB. The runtime's occupancy query counts more than fit
-// for 5-wave workgroups, and a persistent grid past residency leaves its last
-// workgroups to start only when others have finished all their items.
-template <class K>
-int64_t resident_grid(K k, int NW, size_t lds) {
-  int dev = 0, cus = 1;
-  (void)hipGetDevice(&dev);
-  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  hipFuncAttributes fa{};
-  if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(k)) != hipSuccess) return int64_t(cus);
-  const int vg = std::max(8, (fa.numRegs + 7) / 8 * 8);
-  const int c = std::min(8, 512 / vg);
-  const int by_vgpr = NW % 4 ? (4 * c - 4) / NW : 4 * c / NW;
-  const size_t gran = (lds + 2047) / 2048 * 2048;
-  const int by_lds = gran ? int(163840 / gran) : 8;
-  return int64_t(cus) * std::max(1, std::min(by_vgpr, by_lds));
-}
-
 template <int HD>
 int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
                const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, hipStream_t st) {
