@@ -424,14 +424,23 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bool active = w < at.nb;
   const int i = 16 * w + c;  // this lane's query slot, and its key slot
-  float q[W], go[W], dqi = 0.f;
+  // The wave's own q and dO rows: held in registers across the steps, or at
+  // head_dim 64 and up re-read from LDS in each step (32+ fewer registers,
+  // which is what lets two workgroups share a CU there).
+  constexpr bool QG_LDS = HD >= 64;
+  float q[QG_LDS ? 1 : W], go[QG_LDS ? 1 : W], dqi = 0.f;
   if (active) {
-    lds_get<W>(Qs + i * P + g * W, q);
-    lds_get<W>(Gs + i * P + g * W, go);
+    float qa[W], ga[W];
+    lds_get<W>(Qs + i * P + g * W, qa);
+    lds_get<W>(Gs + i * P + g * W, ga);
     float d = 0.f;
 #pragma unroll
-    for (int t = 0; t < W; ++t) d += go[t] * oo[t];
+    for (int t = 0; t < W; ++t) d += ga[t] * oo[t];
     dqi = sum_g(d);  // Dq = dO . O of query i
+    if constexpr (!QG_LDS) {
+#pragma unroll
+      for (int t = 0; t < W; ++t) q[t] = qa[t], go[t] = ga[t];
+    }
   }
   f4 dq[DT], dk[DT], dv[DT];
 #pragma unroll
@@ -455,8 +464,16 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
       else
 #pragma unroll
         for (int t = 0; t < W; ++t) v[t] = 0.f;
+      if constexpr (QG_LDS) {
+        float qa[W], ga[W];
+        lds_get<W>(Qs + i * P + g * W, qa);
+        lds_get<W>(Gs + i * P + g * W, ga);
 #pragma unroll
-      for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st), dp = mfma(v[t], go[t], dp);
+        for (int t = 0; t < W; ++t) st = mfma(k[t], qa[t], st), dp = mfma(v[t], ga[t], dp);
+      } else {
+#pragma unroll
+        for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st), dp = mfma(v[t], go[t], dp);
+      }
     }
     float lc[4], a[4], ds[4];
     lds_get<4>(lcf + 16 * J + 4 * g, lc);
@@ -701,22 +718,57 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
+// Workgroups of kernel k (NW waves, lds bytes of LDS) one CU holds at once,
+// by the rules measured on gfx950 with spin kernels: a SIMD holds
+// min(8, 512 / vgprs) waves (vgprs rounded up to 8); workgroups whose wave
+// count is not a multiple of 4 lose a wave slot a SIMD in the packing,
+// floor((4c - 4) / NW) of them a CU (c waves a SIMD), else floor(4c / NW);
+// LDS goes in 2 KB granules of 160 KB. (The runtime's occupancy query counts
+// more than fit for 5-wave workgroups.)
+int resident_wgs(const void* k, int NW, size_t lds) {
+  hipFuncAttributes fa{};
+  if (hipFuncGetAttributes(&fa, k) != hipSuccess) return 1;
+  const int vg = std::max(8, (fa.numRegs + 7) / 8 * 8);
+  const int c = std::min(8, 512 / vg);
+  const int by_vgpr = NW % 4 ? (4 * c - 4) / NW : 4 * c / NW;
+  const size_t gran = (lds + 2047) / 2048 * 2048;
+  const int by_lds = gran ? int(163840 / gran) : 8;
+  return std::max(1, std::min(by_vgpr, by_lds));
+}
+
 // The backward over atoms [n0, n1); qkv, dmerged and qkv_adj are the chunk's.
 template <int HD>
 int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
                const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
                const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, hipStream_t st) {
   const int NW = waves_for(sh.slots);
-  // The fullest layout that fits: V staged and two tile buffers, else V from
-  // global memory, else also one tile buffer. PET_ATTN_BWD_VLDS (1 staged,
-  // 2 not) and PET_ATTN_BWD_NBUF (1, 2) force one where it fits.
+  auto k = NW <= 8 ? attn_bwd_kernel<HD, 512> : attn_bwd_kernel<HD, 1024>;
+  // The fullest layout that fits (V staged and two tile buffers, else V from
+  // global memory, else also one tile buffer) -- unless it leaves one
+  // workgroup a CU and a leaner one fits more: then the leaner. Measured on
+  // MI355X: at head_dim 32 the fullest is fastest though the leanest would fit
+  // a third workgroup (C3 backward 429 us against 466-493 us); at head_dim 64
+  // the fullest holds one workgroup a CU and V-from-global with one buffer two
+  // (C5 backward 3853 -> 3244 us). PET_ATTN_BWD_VLDS (1 staged, 2 not) and
+  // PET_ATTN_BWD_NBUF (1, 2) force a layout where it fits.
   static const int force_v = env_int("PET_ATTN_BWD_VLDS"), force_b = env_int("PET_ATTN_BWD_NBUF");
   const size_t cap = size_t(max_lds_bytes());
-  int nbuf = 2, vlds = 1;
+  const int layouts[3][2] = {{1, 2}, {0, 2}, {0, 1}};  // (vlds, nbuf), fullest first
+  int best = -1, best_res = 0;
+  for (int j = 0; j < 3; ++j) {
+    const size_t b = sizeof(float) * Lds<HD>::bwd_floats(NW, layouts[j][1], layouts[j][0]);
+    if (b > cap) continue;
+    const int res = resident_wgs(reinterpret_cast<const void*>(k), NW, b);
+    if (best < 0) {
+      best = j, best_res = res;
+      if (res > 1) break;  // the fullest that fits holds more than one: keep it
+    } else if (res > best_res) {
+      best = j, best_res = res;
+    }
+  }
+  if (best < 0) return PET_ATTN_ESLOTS;
+  int vlds = layouts[best][0], nbuf = layouts[best][1];
   size_t bytes = sizeof(float) * Lds<HD>::bwd_floats(NW, nbuf, vlds);
-  if (bytes > cap) vlds = 0, bytes = sizeof(float) * Lds<HD>::bwd_floats(NW, nbuf, vlds);
-  if (bytes > cap) nbuf = 1, bytes = sizeof(float) * Lds<HD>::bwd_floats(NW, nbuf, vlds);
-  if (bytes > cap) return PET_ATTN_ESLOTS;
   if (force_v || force_b) {
     const int v = force_v ? (force_v == 1) : vlds, b = force_b ? force_b : nbuf;
     const size_t fb = sizeof(float) * Lds<HD>::bwd_floats(NW, b, v);
@@ -724,7 +776,6 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   }
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
-  auto k = NW <= 8 ? attn_bwd_kernel<HD, 512> : attn_bwd_kernel<HD, 1024>;
   allow_lds(k, bytes);
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
                      sh.slots, sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh,
