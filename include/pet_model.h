@@ -1,0 +1,105 @@
+/* pet_model.h -- the whole PET energy / forces evaluation on gfx950 over a C ABI.
+ *
+ * The caller of the attention path: peterspackman/pet-kokkos's PetModel with
+ * the feedforward featurizer (PreLN, RMSNorm, SwiGLU, d_node != d_pet), its
+ * forward pass ff_pass / ff_layer and analytic backward ff_layer_bwd
+ * (src/feedforward.cpp:34-411), the readout and energy assembly
+ * (src/model.cpp:656-780, src/ops.cpp:406-425) and forces_and_virial
+ * (src/forces.cpp:345-386) for a fixed cutoff. Every kernel is this library's
+ * (the attention, norms, activations, gathers, folds); the dense layers go to
+ * rocBLAS fp32 with atomics off, so results repeat bit for bit.
+ *
+ * Weights come as the checkpoint stores them (include/pet/checkpoint.hpp,
+ * src/model.cpp:180-289: torch Linear layout, a SwiGLU w_in as [value | gate]
+ * rows, compress.0 unfolded); pet_model_create folds and interleaves them on
+ * the host in double, as the reference's load_all does. All device buffers
+ * of an evaluation come from a workspace the model owns and keeps between
+ * calls (the reference's Workspace, include/pet/kokkos.hpp:65-84): after the
+ * first call at a size, an evaluation allocates nothing.
+ *
+ * Return codes are pet_attn.h's PET_ATTN_* plus those below; pet_attn_strerror
+ * names them all. One model serves one stream at a time.
+ */
+#ifndef PET_MODEL_H
+#define PET_MODEL_H
+
+#include <stdint.h>
+
+#include "pet_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  PET_MODEL_EMISSING = 20, /* a tensor the architecture needs is not among those given */
+  PET_MODEL_ESHAPE = 21,   /* a tensor's shape disagrees with the hyperparameters */
+  PET_MODEL_EMEMORY = 22   /* a device allocation failed */
+};
+
+/* The hyperparameters evaluation needs (include/pet/config.hpp:30-70). */
+typedef struct pet_model_hypers {
+  int d_pet, d_node, d_head;
+  int num_heads;             /* head_dim = d_pet / num_heads */
+  int num_gnn_layers, num_attention_layers;
+  int n_species;             /* rows of the embedding tables */
+  int cutoff_function;       /* 0 bump, 1 cosine, 2 smooth (pet::CutoffFunction) */
+  double cutoff_width;       /* the smooth cutoff's width */
+  double attention_temperature;
+  double energy_scale;       /* per-atom energy = energy_scale * net + composition[species] */
+} pet_model_hypers;
+
+/* One checkpoint tensor, row-major float64 on the host: cols = 0 for a vector. */
+typedef struct pet_model_tensor {
+  const char* name;
+  int rows, cols;
+  const double* data;
+} pet_model_tensor;
+
+typedef struct pet_model pet_model;
+
+/* Replaces PetModel::PetModel / load_all (src/model.cpp:61-112, :180-344):
+ * uploads, folds compress.0 into its geometry matrix, bias, species table and
+ * input_edge block, and interleaves each SwiGLU w_in to (v_j, g_j) rows.
+ * composition [n_species] (may be null: zeros). Uses the current device. */
+PET_ATTN_API int pet_model_create(const pet_model_hypers* hypers, const pet_model_tensor* tensors, int n_tensors,
+                                  const double* composition, pet_model** out);
+PET_ATTN_API void pet_model_destroy(pet_model* model);
+
+/* A batch of structures with its kept edges, packed (the reference's
+ * PackedEdges, include/pet/model.hpp:153-168, and DeviceEdgeData's species,
+ * struct_id and max_neighbors, :60-112). All device pointers. */
+typedef struct pet_model_edges {
+  int n_atoms;         /* N; every atom is a centre */
+  int n_edges;         /* E = off[N] */
+  int max_neighbors;   /* M >= every atom's edge count; attention slots S = M + 1 */
+  int n_struct;        /* B */
+  const int* struct_off; /* [B + 1] atom offsets of the structures (contiguous atoms) */
+  const int* species;    /* [N] species index */
+  const int* off;        /* [N + 1] atom n's edges are off[n] .. off[n+1]-1 */
+  const int* center;     /* [E] */
+  const int* neigh_species; /* [E] the neighbour's species index */
+  const int* reverse;    /* [E] the (j, i, -shift) edge, -1 if none */
+  const double* vec;     /* [E, 3] r_j + shift - r_i */
+  const double* dist;    /* [E] |vec| */
+  const double* pcut;    /* [E] the pair cutoff (the cutoff factor's rc) */
+  const float* cut;      /* [E] the smooth cutoff factor of dist */
+} pet_model_edges;
+
+/* One evaluation (PetModel::compute / energy_forces_batch, src/model.cpp:782-811,
+ * :927-1010, with ff_pass src/feedforward.cpp:338-411). Outputs are device fp64:
+ * energy [B], per_atom [N] (either may be null); with forces nonzero also
+ * forces [N, 3], virial [B, 9] (row-major 3x3, W = sum v (x) dE/dv) and, unless
+ * null, edge_grad [E, 3] (dE/dv per edge, scaled). */
+PET_ATTN_API int pet_model_compute(pet_model* model, const pet_model_edges* edges, int forces, double* energy,
+                                   double* per_atom, double* forces_out, double* virial, double* edge_grad,
+                                   void* stream);
+
+/* Bytes of device workspace the model holds now (its high-water mark). */
+PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PET_MODEL_H */

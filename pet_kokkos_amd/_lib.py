@@ -35,6 +35,10 @@ EXPORTS = (
     "pet_edge_grad",
     "pet_fold_edge_gradients",
     "pet_sum_by_structure",
+    "pet_model_create",
+    "pet_model_destroy",
+    "pet_model_compute",
+    "pet_model_workspace_bytes",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX = range(9)
@@ -51,6 +55,24 @@ class Shape(ctypes.Structure):
         ("dead", ctypes.c_int),
         ("scale", ctypes.c_float),
     ]
+
+
+class ModelHypers(ctypes.Structure):
+    """pet_model_hypers (include/pet_model.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("d_pet", "d_node", "d_head", "num_heads", "num_gnn_layers",
+                                             "num_attention_layers", "n_species", "cutoff_function")] + \
+               [(n, ctypes.c_double) for n in ("cutoff_width", "attention_temperature", "energy_scale")]
+
+
+class ModelTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("rows", ctypes.c_int), ("cols", ctypes.c_int), ("data", ctypes.c_void_p)]
+
+
+class ModelEdges(ctypes.Structure):
+    """pet_model_edges (include/pet_model.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("n_atoms", "n_edges", "max_neighbors", "n_struct")] + \
+               [(n, ctypes.c_void_p) for n in ("struct_off", "species", "off", "center", "neigh_species", "reverse",
+                                               "vec", "dist", "pcut", "cut")]
 
 
 class PetAttnError(RuntimeError):
@@ -133,6 +155,15 @@ def load() -> ctypes.CDLL:
     lib.pet_fold_edge_gradients.argtypes = [_I, _I, _P, _P, _P, _P, _D, _P, _P, _P]
     lib.pet_sum_by_structure.restype = ctypes.c_int
     lib.pet_sum_by_structure.argtypes = [_I, _I, _P, _P, _P, _I, _P]
+    lib.pet_model_create.restype = ctypes.c_int
+    lib.pet_model_create.argtypes = [ctypes.POINTER(ModelHypers), ctypes.POINTER(ModelTensor), _I, _P,
+                                     ctypes.POINTER(_P)]
+    lib.pet_model_destroy.restype = None
+    lib.pet_model_destroy.argtypes = [_P]
+    lib.pet_model_compute.restype = ctypes.c_int
+    lib.pet_model_compute.argtypes = [_P, ctypes.POINTER(ModelEdges), _I, _P, _P, _P, _P, _P, _P]
+    lib.pet_model_workspace_bytes.restype = ctypes.c_size_t
+    lib.pet_model_workspace_bytes.argtypes = [_P]
     _lib = lib
     return lib
 

@@ -837,6 +837,9 @@ const char* pet_attn_strerror(int code) {
     case PET_ATTN_EBLAS: return "the BLAS call of a linear failed";
     case PET_ATTN_EWORKSPACE: return "workspace smaller than the matching *_workspace() size";
     case PET_ATTN_EINDEX: return "an index does not fit 2^31";
+    case 20: return "a tensor the model's architecture needs is missing";
+    case 21: return "a tensor's shape disagrees with the model's hyperparameters";
+    case 22: return "a device allocation failed";
     default: return "unknown pet_attn error";
   }
 }

@@ -1,0 +1,846 @@
+// The whole PET energy / forces evaluation on gfx950: the feedforward
+// featurizer's forward and analytic backward around this library's attention
+// (peterspackman/pet-kokkos src/feedforward.cpp:34-411), the readout and energy
+// (src/model.cpp:656-780, src/ops.cpp:406-425) and forces_and_virial
+// (src/forces.cpp:345-386) for a fixed cutoff.
+//
+// Every step outside the GEMMs is a kernel of this library: the attention
+// (attention.hip), the norms (rows.hip), the edge term and folds (forces.hip)
+// and, here, the gathers, compress.0's folded form, SiLU / SwiGLU and their
+// backwards, the residual sums, the combination's concat and the readout. The
+// dense layers go to rocBLAS fp32 (ops.hip's gemm_nt / gemm_nn, atomics off).
+// The elementwise passes are HBM-bound: grid-stride loops over contiguous
+// row-major buffers, one read and one write per value, residual sums fused
+// into the pass that produces their operands.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/pet_model.h"
+
+namespace pet_attn {
+int gemm_nt(float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int Nout, int K, float beta,
+            hipStream_t st);
+int gemm_nn(float* in_adj, int64_t ldi, const float* out_adj, int64_t ldo, const float* W, int M, int Nout, int K,
+            float beta, hipStream_t st);
+}  // namespace pet_attn
+int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, const float* out_adj, int64_t ldg,
+                           const float* in, int64_t ldi, const float* weight, int ln, int n_node, float beta_node,
+                           float beta_edge, const int* live_off, hipStream_t st);
+
+namespace pet_model_impl {
+
+using pet_attn::gemm_nn;
+using pet_attn::gemm_nt;
+
+// ---- activations ---------------------------------------------------------------
+//
+// The SiLU / SwiGLU sigmoid of the dense layers is the hardware exp and
+// reciprocal (the reference's fast_sigmoid on an AMD GPU in fp32,
+// include/pet/kokkos.hpp:246-259); compress.0's SiLU takes the accurate one
+// (src/ops.cpp:360 calls silu(), include/pet/kokkos.hpp:238-244).
+__device__ __forceinline__ float sig_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float sig_exact(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+#define GRID_LOOP(i, n) \
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < (n); i += int64_t(gridDim.x) * blockDim.x)
+
+// out[r, :] = table[idx[r], :]
+__global__ void gather_rows_kernel(float* __restrict__ out, const float* __restrict__ table,
+                                   const int* __restrict__ idx, int64_t R, int W) {
+  GRID_LOOP(i, R * W) {
+    const int64_t r = i / W;
+    const int d = int(i - r * W);
+    out[i] = table[int64_t(idx[r]) * W + d];
+  }
+}
+
+// out[r, :] = b (or 0), the bias a GEMM then accumulates onto
+__global__ void fill_rows_kernel(float* __restrict__ out, const float* __restrict__ b, int64_t R, int W) {
+  GRID_LOOP(i, R * W) out[i] = b ? b[i % W] : 0.0f;
+}
+
+__global__ void fill0_kernel(float* __restrict__ x, int64_t n) {
+  GRID_LOOP(i, n) x[i] = 0.0f;
+}
+
+// s = a + c (saved when s is non-null), then out = s + b: a residual sum and
+// the bias of the GEMM that accumulates onto it.
+__global__ void residual_kernel(float* __restrict__ s, float* __restrict__ out, const float* __restrict__ a,
+                                const float* __restrict__ c, const float* __restrict__ b, int64_t R, int W) {
+  GRID_LOOP(i, R * W) {
+    const float v = a[i] + c[i];
+    if (s) s[i] = v;
+    out[i] = v + b[i % W];
+  }
+}
+
+// x += b per row
+__global__ void add_bias_kernel(float* __restrict__ x, const float* __restrict__ b, int64_t R, int W) {
+  GRID_LOOP(i, R * W) x[i] += b[i % W];
+}
+
+// out = silu(z), fast sigmoid (linear_silu, src/ops.cpp:54-76)
+__global__ void silu_kernel(float* __restrict__ out, const float* __restrict__ z, int64_t n) {
+  GRID_LOOP(i, n) {
+    const float v = z[i];
+    out[i] = v * sig_fast(v);
+  }
+}
+
+// g *= silu'(pre) (silu_bwd, src/ops.cpp:78-101)
+__global__ void silu_bwd_kernel(float* __restrict__ g, const float* __restrict__ pre, int64_t n) {
+  GRID_LOOP(i, n) {
+    const float x = pre[i], sg = sig_fast(x);
+    g[i] *= sg * (1.0f + x * (1.0f - sg));
+  }
+}
+
+// h[r, c] = pre[r, 2c] * sigmoid(pre[r, 2c+1]): pre's rows interleaved (v_j, g_j)
+// (swiglu_in, src/ops.cpp:248-271)
+__global__ void swiglu_kernel(float* __restrict__ h, const float2* __restrict__ pre, int64_t n) {
+  GRID_LOOP(i, n) {
+    const float2 p = pre[i];
+    h[i] = p.x * sig_fast(p.y);
+  }
+}
+
+// pre_adj from h_adj (swiglu_bwd, src/ops.cpp:281-324)
+__global__ void swiglu_bwd_kernel(float2* __restrict__ pre_adj, const float* __restrict__ h_adj,
+                                  const float2* __restrict__ pre, int64_t n) {
+  GRID_LOOP(i, n) {
+    const float2 p = pre[i];
+    const float sg = sig_fast(p.y), g = h_adj[i];
+    pre_adj[i] = make_float2(g * sg, g * p.x * sg * (1.0f - sg));
+  }
+}
+
+// compress.0 through its fold (compress_fwd, src/ops.cpp:326-371):
+// z = [gemm] + b + tab[nsp] + wx (v, |v|); sav = z, out = silu(z), accurate sigmoid.
+__global__ void compress_kernel(float* __restrict__ sav, float* __restrict__ out, int gemm,
+                                const float* __restrict__ b, const float* __restrict__ tab,
+                                const int* __restrict__ nsp, const float* __restrict__ wx,
+                                const double* __restrict__ vec, const double* __restrict__ dist, int64_t E, int D) {
+  GRID_LOOP(i, E * D) {
+    const int64_t k = i / D;
+    const int d = int(i - k * D);
+    const float e0 = float(vec[3 * k]), e1 = float(vec[3 * k + 1]), e2 = float(vec[3 * k + 2]), e3 = float(dist[k]);
+    const float* w = wx + 4 * d;
+    const float z = (gemm ? out[i] : 0.0f) + b[d] + tab[int64_t(nsp[k]) * D + d] + w[0] * e0 + w[1] * e1 +
+                    w[2] * e2 + w[3] * e3;
+    sav[i] = z;
+    out[i] = z * sig_exact(z);
+  }
+}
+
+// compress_bwd's pass (src/ops.cpp:373-404): a wavefront a row, g *= silu'(pre)
+// in place, and x4_adj[r] += the four sums g . wx[:, c] (a fixed butterfly).
+__global__ void __launch_bounds__(256) compress_bwd_kernel(float* __restrict__ g, const float* __restrict__ pre,
+                                                           const float* __restrict__ wx, float* __restrict__ x4_adj,
+                                                           int E, int D) {
+  const int r = blockIdx.x * 4 + int(threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (r >= E) return;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  float* gr = g + int64_t(r) * D;
+  const float* pr = pre + int64_t(r) * D;
+  for (int d = l; d < D; d += 64) {
+    const float x = pr[d], sg = sig_fast(x);
+    const float gd = gr[d] * (sg * (1.0f + x * (1.0f - sg)));
+    gr[d] = gd;
+    a0 += gd * wx[4 * d], a1 += gd * wx[4 * d + 1], a2 += gd * wx[4 * d + 2], a3 += gd * wx[4 * d + 3];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a0 += __shfl_xor(a0, o), a1 += __shfl_xor(a1, o);
+    a2 += __shfl_xor(a2, o), a3 += __shfl_xor(a3, o);
+  }
+  if (l == 0) {
+    float* x = x4_adj + 4 * int64_t(r);
+    x[0] += a0, x[1] += a1, x[2] += a2, x[3] += a3;
+  }
+}
+
+// The combination's input (src/feedforward.cpp:179-192): concat[k] = [oe(k) |
+// oe(rev k) or 0], and input_edge += oe.
+__global__ void concat_kernel(float* __restrict__ concat, float* __restrict__ ie, const float* __restrict__ oe,
+                              const int* __restrict__ rev, int64_t E, int D) {
+  GRID_LOOP(i, E * D) {
+    const int64_t k = i / D;
+    const int d = int(i - k * D), r = rev[k];
+    const float v = oe[i];
+    ie[i] += v;
+    concat[k * 2 * D + d] = v;
+    concat[k * 2 * D + D + d] = r >= 0 ? oe[int64_t(r) * D + d] : 0.0f;
+  }
+}
+
+// edge_adj[k] = ie_adj[k] + ca[k, :D] + ca[rev k, D:] (bw_concat, src/feedforward.cpp:254-259)
+__global__ void concat_bwd_kernel(float* __restrict__ edge_adj, const float* __restrict__ ie_adj,
+                                  const float* __restrict__ ca, const int* __restrict__ rev, int64_t E, int D) {
+  GRID_LOOP(i, E * D) {
+    const int64_t k = i / D;
+    const int d = int(i - k * D), r = rev[k];
+    const float back = r >= 0 ? ca[int64_t(r) * 2 * D + D + d] : 0.0f;
+    edge_adj[i] = ie_adj[i] + ca[k * 2 * D + d] + back;
+  }
+}
+
+// net[n] = node_pred[n] + sum over n's edges of cut * edge_pred, in double and
+// in edge order (readout_accumulate, src/ops.cpp:406-418); then per_atom =
+// scale * net + composition[species] (assemble_energy, :420-425).
+__global__ void readout_kernel(double* __restrict__ per_atom, const float* __restrict__ node_pred,
+                               const float* __restrict__ edge_pred, const int* __restrict__ off,
+                               const float* __restrict__ cut, const int* __restrict__ species,
+                               const double* __restrict__ comp, double scale, int N) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  double s = node_pred[n];
+  for (int k = off[n]; k < off[n + 1]; ++k) s += double(cut[k]) * double(edge_pred[k]);
+  const float net = float(s);
+  per_atom[n] = scale * double(net) + comp[species[n]];
+}
+
+// The readout's adjoint seeds (readout_bwd, src/model.cpp:749-767): node_pred's
+// is 1, edge_pred's the edge's cutoff factor, and cutoff_adj = edge_pred.
+__global__ void readout_seed_kernel(float* __restrict__ npa, float* __restrict__ epa, float* __restrict__ cutoff_adj,
+                                    const float* __restrict__ cut, const float* __restrict__ epred, int N, int E) {
+  GRID_LOOP(i, int64_t(N) + E) {
+    if (i < N) {
+      npa[i] = 1.0f;
+    } else {
+      const int64_t k = i - N;
+      epa[k] = cut[k];
+      cutoff_adj[k] = epred[k];
+    }
+  }
+}
+
+inline dim3 grid_for(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return dim3(unsigned(b < 8192 ? (b > 0 ? b : 1) : 8192));
+}
+
+// ---- device memory -------------------------------------------------------------
+
+// A bump arena over device blocks, kept across calls; mark / release reuse a
+// scope's memory. After the first evaluation at a size nothing is allocated.
+class Arena {
+ public:
+  ~Arena() {
+    for (auto& b : blocks_) (void) hipFree(b.p);
+  }
+  struct Mark {
+    size_t block, off;
+  };
+  Mark mark() const { return {cur_, off_}; }
+  void release(Mark m) { cur_ = m.block, off_ = m.off; }
+  void reset() { cur_ = 0, off_ = 0; }
+  size_t bytes() const {
+    size_t s = 0;
+    for (auto& b : blocks_) s += b.size;
+    return s;
+  }
+  // nullptr when the device is out of memory
+  void* take(size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes == 0) bytes = 256;
+    while (cur_ < blocks_.size()) {
+      if (off_ + bytes <= blocks_[cur_].size) {
+        void* p = static_cast<char*>(blocks_[cur_].p) + off_;
+        off_ += bytes;
+        return p;
+      }
+      ++cur_, off_ = 0;
+    }
+    const size_t size = std::max(bytes, size_t(1) << 30);
+    void* p = nullptr;
+    if (hipMalloc(&p, size) != hipSuccess) return nullptr;
+    blocks_.push_back({p, size});
+    cur_ = blocks_.size() - 1;
+    off_ = bytes;
+    return p;
+  }
+
+ private:
+  struct Block {
+    void* p;
+    size_t size;
+  };
+  std::vector<Block> blocks_;
+  size_t cur_ = 0, off_ = 0;
+};
+
+struct Mat {
+  float* p = nullptr;
+  int rows = 0, cols = 0;
+};
+
+struct Error {
+  int code;
+};
+inline void ok(int e) {
+  if (e) throw Error{e};
+}
+inline void launched() {
+  if (hipGetLastError() != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
+}
+
+}  // namespace pet_model_impl
+
+using namespace pet_model_impl;
+
+struct pet_model {
+  pet_model_hypers h{};
+  int hd = 0, cw = 0, ew = 0;  // head_dim, center / edge MLP pre-activation widths
+  std::unordered_map<std::string, Mat> m;
+  void* weights = nullptr;
+  double* comp = nullptr;
+  Arena ws;
+
+  ~pet_model() {
+    (void) hipDeviceSynchronize();
+    if (weights) (void) hipFree(weights);
+    if (comp) (void) hipFree(comp);
+  }
+  const Mat& w(const std::string& name) const {
+    auto it = m.find(name);
+    if (it == m.end()) throw Error{PET_MODEL_EMISSING};
+    return it->second;
+  }
+  const float* p(const std::string& name) const { return w(name).p; }
+  float* f(int64_t n) {
+    void* q = ws.take(sizeof(float) * size_t(n));
+    if (!q) throw Error{PET_MODEL_EMEMORY};
+    return static_cast<float*>(q);
+  }
+};
+
+namespace {
+
+// out[M, Nout] = in W^T + b (b may be null)
+void linear(pet_model& md, float* out, const float* in, int M, int K, const std::string& key, hipStream_t st,
+            bool bias = true) {
+  const Mat& W = md.w(key + ".weight");
+  if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
+  if (M == 0) return;
+  const float* b = bias ? md.p(key + ".bias") : nullptr;
+  hipLaunchKernelGGL(fill_rows_kernel, grid_for(int64_t(M) * W.rows), dim3(256), 0, st, out, b, int64_t(M), W.rows);
+  launched();
+  ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
+}
+// out += in W^T (the caller has put residual + bias in out)
+void linear_acc(pet_model& md, float* out, const float* in, int M, int K, const std::string& key, hipStream_t st) {
+  const Mat& W = md.w(key + ".weight");
+  if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
+  if (M) ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
+}
+// in_adj[M, K] = out_adj W + beta in_adj
+void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const std::string& key, float beta,
+                hipStream_t st) {
+  const Mat& W = md.w(key + ".weight");
+  if (M) ok(gemm_nn(in_adj, W.cols, out_adj, W.rows, W.p, M, W.rows, W.cols, beta, st));
+}
+void silu(float* out, const float* z, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(silu_kernel, grid_for(n), dim3(256), 0, st, out, z, n);
+  launched();
+}
+void silu_bwd(float* g, const float* pre, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(silu_bwd_kernel, grid_for(n), dim3(256), 0, st, g, pre, n);
+  launched();
+}
+void norm(pet_model& md, float* out, const float* in, int R, int W, const std::string& key, bool ln, hipStream_t st) {
+  ok(pet_norm_rows(R, W, out, W, in, W, md.p(key + ".weight"), ln ? md.p(key + ".bias") : nullptr, st));
+}
+void fill0(float* x, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(fill0_kernel, grid_for(n), dim3(256), 0, st, x, n);
+  launched();
+}
+
+// What one GNN layer keeps for its backward (the reference's LayerSaves,
+// include/pet/model.hpp:183-198), every block's wide activations included.
+struct Block {
+  float *tok, *qkv, *merged, *ml, *eps, *node_res, *pre_c, *pre_e;
+};
+struct Layer {
+  float *cpre, *concat, *cph;
+  std::vector<Block> b;
+};
+
+struct Pass {
+  pet_model& md;
+  const pet_model_edges& e;
+  hipStream_t st;
+  int N, E, T, S, D, Dn, Dh, A, G;
+  pet_attn_shape sh{};
+  float* cf_seq = nullptr;
+
+  Pass(pet_model& m, const pet_model_edges& ed, hipStream_t s) : md(m), e(ed), st(s) {
+    N = e.n_atoms, E = e.n_edges, T = N + E, S = e.max_neighbors + 1;
+    D = md.h.d_pet, Dn = md.h.d_node, Dh = md.h.d_head, A = md.h.num_attention_layers, G = md.h.num_gnn_layers;
+    sh.n_atoms = N, sh.n_rows = T, sh.slots = S, sh.heads = md.h.num_heads, sh.head_dim = md.hd, sh.dead = 0;
+    sh.scale = pet_attn_scale(md.hd, md.h.attention_temperature);
+  }
+  std::string g(int L) const { return "gnn_layers." + std::to_string(L); }
+  std::string t(int L, int a) const { return g(L) + ".trans.layers." + std::to_string(a); }
+
+  // One GNN layer forward (ff_layer, src/feedforward.cpp:34-198, every save kept).
+  void layer_fwd(int L, float*& node, float* input_edge, Layer& sv) {
+    const std::string c0 = g(L) + ".compress.0";
+    sv.cpre = md.f(int64_t(E) * D);
+    sv.b.resize(A);
+    for (int a = 0; a < A; ++a) sv.b[a].tok = md.f(int64_t(T) * D);
+    float* out_edge = md.f(int64_t(E) * D);
+    {
+      auto scope = md.ws.mark();
+      float* cact = md.f(int64_t(E) * D);
+      if (L > 0) ok(gemm_nt(cact, D, input_edge, D, md.p(c0 + "@in"), E, D, D, 0.0f, st));
+      if (E) {
+        hipLaunchKernelGGL(compress_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, sv.cpre, cact, L > 0 ? 1 : 0,
+                           md.p(c0 + "@b"), md.p(c0 + "@tab"), e.neigh_species, md.p(c0 + "@x4"), e.vec, e.dist,
+                           int64_t(E), D);
+        launched();
+      }
+      linear(md, sv.b[0].tok + int64_t(N) * D, cact, E, D, g(L) + ".compress.2", st);
+      md.ws.release(scope);
+    }
+    float* node_cur = node;
+    const float* edge_cur = sv.b[0].tok + int64_t(N) * D;
+    for (int a = 0; a < A; ++a) {
+      const std::string tl = t(L, a);
+      Block& b = sv.b[a];
+      b.qkv = md.f(int64_t(T) * 3 * D), b.merged = md.f(int64_t(T) * D), b.ml = md.f(int64_t(N) * md.h.num_heads * S * 2);
+      b.eps = md.f(int64_t(E) * D), b.node_res = md.f(int64_t(N) * Dn);
+      b.pre_c = md.f(int64_t(N) * md.cw), b.pre_e = md.f(int64_t(E) * md.ew);
+      float* node_next = md.f(int64_t(N) * Dn);
+      float* edge_next = a + 1 < A ? sv.b[a + 1].tok + int64_t(N) * D : out_edge;
+      auto scope = md.ws.mark();
+      linear(md, b.tok, node_cur, N, Dn, tl + ".center_contraction", st);
+      float* normed = md.f(int64_t(T) * D);
+      norm(md, normed, b.tok, T, D, tl + ".norm_attention", false, st);
+      linear(md, b.qkv, normed, T, D, tl + ".attention.input_linear", st);
+      ok(pet_attn_fwd(&sh, b.qkv, 3 * D, e.off, cf_seq, S, b.merged, D, b.ml, st));
+      float* attn_out = normed;  // normed is consumed
+      linear(md, attn_out, b.merged, T, D, tl + ".attention.output_linear", st);
+      float* node_exp = md.f(int64_t(N) * Dn);
+      linear(md, node_exp, attn_out, N, D, tl + ".center_expansion", st);
+      // eps = attention's edge rows + edge_cur; edge_next = eps + mlp's output bias
+      if (E) {
+        hipLaunchKernelGGL(residual_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, b.eps, edge_next,
+                           attn_out + int64_t(N) * D, edge_cur, md.p(tl + ".mlp.w_out.bias"), int64_t(E), D);
+        launched();
+      }
+      if (N) {
+        hipLaunchKernelGGL(residual_kernel, grid_for(int64_t(N) * Dn), dim3(256), 0, st, b.node_res, node_next,
+                           node_cur, node_exp, md.p(tl + ".center_mlp.w_out.bias"), int64_t(N), Dn);
+        launched();
+      }
+      // node_next += center_mlp(norm(node_res)); edge_next += mlp(norm(eps))
+      float* nn = node_exp;  // consumed
+      norm(md, nn, b.node_res, N, Dn, tl + ".norm_center_features", false, st);
+      linear(md, b.pre_c, nn, N, Dn, tl + ".center_mlp.w_in", st);
+      float* hc = md.f(int64_t(N) * md.cw / 2);
+      if (N) {
+        hipLaunchKernelGGL(swiglu_kernel, grid_for(int64_t(N) * md.cw / 2), dim3(256), 0, st, hc,
+                           reinterpret_cast<const float2*>(b.pre_c), int64_t(N) * md.cw / 2);
+        launched();
+      }
+      linear_acc(md, node_next, hc, N, md.cw / 2, tl + ".center_mlp.w_out", st);
+      float* en = attn_out;  // consumed: its edge rows were read by the residual pass
+      norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
+      linear(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
+      float* he = md.f(int64_t(E) * md.ew / 2);
+      if (E) {
+        hipLaunchKernelGGL(swiglu_kernel, grid_for(int64_t(E) * md.ew / 2), dim3(256), 0, st, he,
+                           reinterpret_cast<const float2*>(b.pre_e), int64_t(E) * md.ew / 2);
+        launched();
+      }
+      linear_acc(md, edge_next, he, E, md.ew / 2, tl + ".mlp.w_out", st);
+      md.ws.release(scope);
+      node_cur = node_next;
+      edge_cur = edge_next;
+    }
+    node = node_cur;
+    // input_edge += out_edge + comb_mlp(layernorm([out_edge | out_edge(rev)]))
+    const std::string ls = std::to_string(L);
+    sv.concat = md.f(int64_t(E) * 2 * D), sv.cph = md.f(int64_t(E) * 2 * D);
+    auto scope = md.ws.mark();
+    if (E) {
+      hipLaunchKernelGGL(concat_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, sv.concat, input_edge, out_edge,
+                         e.reverse, int64_t(E), D);
+      launched();
+    }
+    float* cn = md.f(int64_t(E) * 2 * D);
+    norm(md, cn, sv.concat, E, 2 * D, "combination_norms." + ls, true, st);
+    linear(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
+    silu(cn, sv.cph, int64_t(E) * 2 * D, st);
+    if (E) {
+      hipLaunchKernelGGL(add_bias_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge,
+                         md.p("combination_mlps." + ls + ".2.bias"), int64_t(E), D);
+      launched();
+    }
+    linear_acc(md, input_edge, cn, E, 2 * D, "combination_mlps." + ls + ".2", st);
+    md.ws.release(scope);
+  }
+
+  // Its backward (ff_layer_bwd, src/feedforward.cpp:200-336): node_adj and
+  // ie_adj from the layer's outputs' adjoints to its inputs', in place; x4_adj
+  // and cf_seq_adj accumulate.
+  void layer_bwd(int L, const Layer& sv, float* node_adj, float* ie_adj, float* x4_adj, float* cf_seq_adj) {
+    const std::string ls = std::to_string(L);
+    auto scope = md.ws.mark();
+    float* tok_adj = md.f(int64_t(T) * D);
+    float* edge_adj = tok_adj + int64_t(N) * D;
+    {
+      auto s2 = md.ws.mark();
+      float* cph_adj = md.f(int64_t(E) * 2 * D);
+      float* cn_adj = md.f(int64_t(E) * 2 * D);
+      linear_bwd(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", 0.0f, st);
+      silu_bwd(cph_adj, sv.cph, int64_t(E) * 2 * D, st);
+      linear_bwd(md, cn_adj, cph_adj, E, "combination_mlps." + ls + ".0", 0.0f, st);
+      float* ca = cph_adj;  // consumed
+      ok(pet_norm_rows_bwd(E, 2 * D, ca, 2 * D, 0.0f, cn_adj, 2 * D, sv.concat, 2 * D,
+                           md.p("combination_norms." + ls + ".weight"), 1, st));
+      if (E) {
+        hipLaunchKernelGGL(concat_bwd_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, edge_adj, ie_adj, ca,
+                           e.reverse, int64_t(E), D);
+        launched();
+      }
+      md.ws.release(s2);
+    }
+    for (int a = A - 1; a >= 0; --a) {
+      const std::string tl = t(L, a);
+      const Block& b = sv.b[a];
+      auto s2 = md.ws.mark();
+      {  // the two MLPs: edge_adj and node_adj become eps's and node_res's
+        float* h_adj = md.f(int64_t(E) * md.ew / 2);
+        float* pre_adj = md.f(int64_t(E) * md.ew);
+        float* en_adj = md.f(int64_t(E) * D);
+        linear_bwd(md, h_adj, edge_adj, E, tl + ".mlp.w_out", 0.0f, st);
+        if (E) {
+          hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(int64_t(E) * md.ew / 2), dim3(256), 0, st,
+                             reinterpret_cast<float2*>(pre_adj), h_adj, reinterpret_cast<const float2*>(b.pre_e),
+                             int64_t(E) * md.ew / 2);
+          launched();
+        }
+        linear_bwd(md, en_adj, pre_adj, E, tl + ".mlp.w_in", 0.0f, st);
+        ok(pet_norm_rows_bwd(E, D, edge_adj, D, 1.0f, en_adj, D, b.eps, D, md.p(tl + ".norm_mlp.weight"), 0, st));
+        float* hc_adj = md.f(int64_t(N) * md.cw / 2);
+        float* prec_adj = md.f(int64_t(N) * md.cw);
+        float* cn_adj = md.f(int64_t(N) * Dn);
+        linear_bwd(md, hc_adj, node_adj, N, tl + ".center_mlp.w_out", 0.0f, st);
+        if (N) {
+          hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(int64_t(N) * md.cw / 2), dim3(256), 0, st,
+                             reinterpret_cast<float2*>(prec_adj), hc_adj, reinterpret_cast<const float2*>(b.pre_c),
+                             int64_t(N) * md.cw / 2);
+          launched();
+        }
+        linear_bwd(md, cn_adj, prec_adj, N, tl + ".center_mlp.w_in", 0.0f, st);
+        ok(pet_norm_rows_bwd(N, Dn, node_adj, Dn, 1.0f, cn_adj, Dn, b.node_res, Dn,
+                             md.p(tl + ".norm_center_features.weight"), 0, st));
+      }
+      md.ws.release(s2);
+      // The attention: its output's adjoint is the expansion's input adjoint on
+      // the atom rows and eps's (edge_adj, in place) on the edge rows.
+      linear_bwd(md, tok_adj, node_adj, N, tl + ".center_expansion", 0.0f, st);
+      float* dmerged = md.f(int64_t(T) * D);
+      float* qkv_adj = md.f(int64_t(T) * 3 * D);
+      float* cfh = md.f(int64_t(N) * md.h.num_heads * S);
+      float* in_adj = dmerged;
+      linear_bwd(md, dmerged, tok_adj, T, tl + ".attention.output_linear", 0.0f, st);
+      ok(pet_attn_bwd(&sh, b.qkv, 3 * D, e.off, dmerged, D, b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh,
+                      cf_seq_adj, S, st));
+      linear_bwd(md, in_adj, qkv_adj, T, tl + ".attention.input_linear", 0.0f, st);
+      // through the norm: atom rows set (input_node's adjoint), edge rows onto edge_adj
+      ok(pet_rows_norm_bwd_sink(T, D, tok_adj, D, in_adj, D, b.tok, D, md.p(tl + ".norm_attention.weight"), 0, N,
+                                0.0f, 1.0f, e.off, st));
+      linear_bwd(md, node_adj, tok_adj, N, tl + ".center_contraction", 1.0f, st);
+      md.ws.release(s2);
+    }
+    // edge_adj is et's: back through compress.2 and compress.0's fold
+    const std::string c0 = g(L) + ".compress.0";
+    float* ga = md.f(int64_t(E) * D);
+    linear_bwd(md, ga, edge_adj, E, g(L) + ".compress.2", 0.0f, st);
+    if (E) {
+      hipLaunchKernelGGL(compress_bwd_kernel, dim3(unsigned((E + 3) / 4)), dim3(256), 0, st, ga, sv.cpre,
+                         md.p(c0 + "@x4"), x4_adj, E, D);
+      launched();
+    }
+    if (L > 0 && E) ok(gemm_nn(ie_adj, D, ga, D, md.p(c0 + "@in"), E, D, D, 1.0f, st));
+    md.ws.release(scope);
+  }
+
+  void run(bool grad, double* energy, double* per_atom_out, double* forces, double* virial, double* edge_grad_out) {
+    md.ws.reset();
+    cf_seq = md.f(int64_t(N) * S);
+    ok(pet_attn_cf_seq(&sh, e.off, e.cut, cf_seq, S, st));
+    float* node = md.f(int64_t(N) * Dn);
+    float* input_edge = md.f(int64_t(E) * D);
+    if (N) {
+      hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(N) * Dn), dim3(256), 0, st, node,
+                         md.p("node_embedders.0.weight"), e.species, int64_t(N), Dn);
+      launched();
+    }
+    if (E) {
+      hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge,
+                         md.p("edge_embedder.weight"), e.neigh_species, int64_t(E), D);
+      launched();
+    }
+    std::vector<Layer> sv(G);
+    for (int L = 0; L < G; ++L) layer_fwd(L, node, input_edge, sv[L]);
+
+    // readout (src/model.cpp:656-691): two SiLU layers and a last linear a side
+    float *nh0 = md.f(int64_t(N) * Dh), *nh1 = md.f(int64_t(N) * Dh), *eh0 = md.f(int64_t(E) * Dh),
+          *eh1 = md.f(int64_t(E) * Dh), *npred = md.f(N), *epred = md.f(E);
+    {
+      auto scope = md.ws.mark();
+      float* x = md.f(std::max<int64_t>(int64_t(N), int64_t(E)) * Dh);
+      linear(md, nh0, node, N, Dn, "node_heads.energy.0.0", st);
+      silu(x, nh0, int64_t(N) * Dh, st);
+      linear(md, nh1, x, N, Dh, "node_heads.energy.0.2", st);
+      silu(x, nh1, int64_t(N) * Dh, st);
+      linear(md, npred, x, N, Dh, "node_last_layers.energy.0.energy___0", st);
+      linear(md, eh0, input_edge, E, D, "edge_heads.energy.0.0", st);
+      silu(x, eh0, int64_t(E) * Dh, st);
+      linear(md, eh1, x, E, Dh, "edge_heads.energy.0.2", st);
+      silu(x, eh1, int64_t(E) * Dh, st);
+      linear(md, epred, x, E, Dh, "edge_last_layers.energy.0.energy___0", st);
+      md.ws.release(scope);
+    }
+    double* per_atom = per_atom_out ? per_atom_out : reinterpret_cast<double*>(md.f(2 * int64_t(N)));
+    if (N) {
+      hipLaunchKernelGGL(readout_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st, per_atom, npred, epred,
+                         e.off, e.cut, e.species, md.comp, md.h.energy_scale, N);
+      launched();
+    }
+    if (energy) ok(pet_sum_by_structure(e.n_struct, 1, e.struct_off, per_atom, energy, 0, st));
+    if (!grad) return;
+
+    // backward (ff_pass, src/feedforward.cpp:396-410)
+    float* x4_adj = md.f(int64_t(E) * 4);
+    float* cf_seq_adj = md.f(int64_t(N) * S);
+    float* cutoff_adj = md.f(E);
+    float* node_adj = md.f(int64_t(N) * Dn);
+    float* ie_adj = md.f(int64_t(E) * D);
+    fill0(x4_adj, int64_t(E) * 4, st);
+    fill0(cf_seq_adj, int64_t(N) * S, st);
+    {
+      auto scope = md.ws.mark();
+      float *npa = md.f(N), *epa = md.f(E), *a1 = md.f(std::max<int64_t>(N, E) * Dh),
+            *a0 = md.f(std::max<int64_t>(N, E) * Dh);
+      if (N + E) {
+        hipLaunchKernelGGL(readout_seed_kernel, grid_for(int64_t(N) + E), dim3(256), 0, st, npa, epa, cutoff_adj,
+                           e.cut, epred, N, E);
+        launched();
+      }
+      linear_bwd(md, a1, npa, N, "node_last_layers.energy.0.energy___0", 0.0f, st);
+      silu_bwd(a1, nh1, int64_t(N) * Dh, st);
+      linear_bwd(md, a0, a1, N, "node_heads.energy.0.2", 0.0f, st);
+      silu_bwd(a0, nh0, int64_t(N) * Dh, st);
+      linear_bwd(md, node_adj, a0, N, "node_heads.energy.0.0", 0.0f, st);
+      linear_bwd(md, a1, epa, E, "edge_last_layers.energy.0.energy___0", 0.0f, st);
+      silu_bwd(a1, eh1, int64_t(E) * Dh, st);
+      linear_bwd(md, a0, a1, E, "edge_heads.energy.0.2", 0.0f, st);
+      silu_bwd(a0, eh0, int64_t(E) * Dh, st);
+      linear_bwd(md, ie_adj, a0, E, "edge_heads.energy.0.0", 0.0f, st);
+      md.ws.release(scope);
+    }
+    for (int L = G - 1; L >= 0; --L) layer_bwd(L, sv[L], node_adj, ie_adj, x4_adj, cf_seq_adj);
+
+    // forces_and_virial (src/forces.cpp:345-386)
+    double* grad_e = edge_grad_out ? edge_grad_out : reinterpret_cast<double*>(md.f(6 * int64_t(E)));
+    ok(pet_edge_grad(N, E, e.off, e.center, x4_adj, 4, cutoff_adj, cf_seq_adj, S, e.vec, e.dist, e.pcut,
+                     md.h.cutoff_width, md.h.cutoff_function, grad_e, st));
+    double* vir_atom = reinterpret_cast<double*>(md.f(18 * int64_t(N)));
+    ok(pet_fold_edge_gradients(N, N, e.off, e.reverse, e.vec, grad_e, md.h.energy_scale, forces, vir_atom, st));
+    if (virial) ok(pet_sum_by_structure(e.n_struct, 9, e.struct_off, vir_atom, virial, 0, st));
+  }
+};
+
+// Host-side load (src/model.cpp:180-289), in double.
+struct Loader {
+  const pet_model_hypers& h;
+  std::unordered_map<std::string, const pet_model_tensor*> in;
+  std::vector<std::pair<std::string, std::vector<float>>> out;
+  std::vector<std::pair<int, int>> shapes;
+
+  const pet_model_tensor& get(const std::string& n, int rows, int cols) const {
+    auto it = in.find(n);
+    if (it == in.end()) throw Error{PET_MODEL_EMISSING};
+    const pet_model_tensor& t = *it->second;
+    const int tc = t.cols ? t.cols : 1, want_c = cols ? cols : 1;
+    if (t.rows != rows || tc != want_c || !t.data) throw Error{PET_MODEL_ESHAPE};
+    return t;
+  }
+  void put(const std::string& n, int rows, int cols, const std::vector<double>& d) {
+    std::vector<float> f(d.size());
+    for (size_t i = 0; i < d.size(); ++i) f[i] = float(d[i]);
+    out.emplace_back(n, std::move(f));
+    shapes.emplace_back(rows, cols);
+  }
+  void copy(const std::string& n, int rows, int cols) {
+    const pet_model_tensor& t = get(n, rows, cols);
+    put(n, rows, cols ? cols : 1, std::vector<double>(t.data, t.data + size_t(rows) * (cols ? cols : 1)));
+  }
+  void linear(const std::string& p, int o, int i) { copy(p + ".weight", o, i), copy(p + ".bias", o, 0); }
+  // [v | g] rows to (v_j, g_j) pairs (src/model.cpp:211-222)
+  void swiglu_in(const std::string& p, int F2, int K) {
+    const pet_model_tensor &W = get(p + ".weight", F2, K), &b = get(p + ".bias", F2, 0);
+    const int F = F2 / 2;
+    std::vector<double> w(size_t(F2) * K), bi(F2);
+    for (int j = 0; j < F2; ++j) {
+      const int src = j % 2 ? F + j / 2 : j / 2;
+      std::memcpy(&w[size_t(j) * K], W.data + size_t(src) * K, sizeof(double) * K);
+      bi[j] = b.data[src];
+    }
+    put(p + ".weight", F2, K, w);
+    put(p + ".bias", F2, 1, bi);
+  }
+  // compress.0 folded (src/model.cpp:236-262): its input is [edge_emb(x4) |
+  // species table | input_edge], edge_emb linear in x4 = (v, |v|).
+  void fold(int L) {
+    const int D = h.d_pet, ns = h.n_species, K = (L == 0 ? 2 : 3) * D;
+    const std::string g = "gnn_layers." + std::to_string(L), c0 = g + ".compress.0";
+    const pet_model_tensor &W = get(c0 + ".weight", D, K), &b0 = get(c0 + ".bias", D, 0);
+    const pet_model_tensor &We = get(g + ".edge_embedder.weight", D, 4), &be = get(g + ".edge_embedder.bias", D, 0);
+    const pet_model_tensor& Tb = get(L == 0 ? "edge_embedder.weight" : g + ".neighbor_embedder.weight", ns, D);
+    std::vector<double> wx(size_t(D) * 4, 0.0), b(b0.data, b0.data + D), tab(size_t(ns) * D, 0.0);
+    for (int d = 0; d < D; ++d) {
+      const double* wr = W.data + size_t(d) * K;
+      for (int j = 0; j < D; ++j) {
+        for (int c = 0; c < 4; ++c) wx[size_t(d) * 4 + c] += wr[j] * We.data[size_t(j) * 4 + c];
+        b[d] += wr[j] * be.data[j];
+        for (int s = 0; s < ns; ++s) tab[size_t(s) * D + d] += Tb.data[size_t(s) * D + j] * wr[D + j];
+      }
+    }
+    put(c0 + "@x4", D, 4, wx);
+    put(c0 + "@b", D, 1, b);
+    put(c0 + "@tab", ns, D, tab);
+    if (L == 0) return;
+    std::vector<double> wi(size_t(D) * D);
+    for (int d = 0; d < D; ++d)
+      for (int j = 0; j < D; ++j) wi[size_t(d) * D + j] = W.data[size_t(d) * K + 2 * D + j];
+    put(c0 + "@in", D, D, wi);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors, int n_tensors,
+                     const double* composition, pet_model** out) {
+  if (!hy || !out || (n_tensors > 0 && !tensors) || n_tensors < 0) return PET_ATTN_EINVAL;
+  *out = nullptr;
+  const pet_model_hypers& h = *hy;
+  if (h.d_pet < 1 || h.d_node < 1 || h.d_head < 1 || h.num_heads < 1 || h.d_pet % h.num_heads ||
+      h.num_gnn_layers < 1 || h.num_attention_layers < 1 || h.n_species < 1 || h.cutoff_function < 0 ||
+      h.cutoff_function > 2 || !(h.cutoff_width > 0.0) || !(h.attention_temperature > 0.0) || h.d_node == h.d_pet)
+    return PET_ATTN_EINVAL;
+  const int hd = h.d_pet / h.num_heads;
+  if (hd % 16 || hd > 128) return PET_ATTN_EHEADDIM;
+  auto md = new pet_model();
+  md->h = h, md->hd = hd;
+  try {
+    Loader ld{h, {}, {}, {}};
+    for (int i = 0; i < n_tensors; ++i) {
+      if (!tensors[i].name) throw Error{PET_ATTN_EINVAL};
+      ld.in[tensors[i].name] = &tensors[i];
+    }
+    const int D = h.d_pet, Dn = h.d_node, Dh = h.d_head, ns = h.n_species;
+    // the MLP widths from the checkpoint (ffn_pre_width, src/model.cpp:635)
+    const std::string t0 = "gnn_layers.0.trans.layers.0";
+    auto rows_of = [&](const std::string& n) {
+      auto it = ld.in.find(n);
+      if (it == ld.in.end()) throw Error{PET_MODEL_EMISSING};
+      return it->second->rows;
+    };
+    md->ew = rows_of(t0 + ".mlp.w_in.weight"), md->cw = rows_of(t0 + ".center_mlp.w_in.weight");
+    if (md->ew % 2 || md->cw % 2) throw Error{PET_MODEL_ESHAPE};
+    for (int L = 0; L < h.num_gnn_layers; ++L) {
+      const std::string g = "gnn_layers." + std::to_string(L), ls = std::to_string(L);
+      ld.fold(L);
+      ld.linear(g + ".compress.2", D, D);
+      for (int a = 0; a < h.num_attention_layers; ++a) {
+        const std::string tl = g + ".trans.layers." + std::to_string(a);
+        ld.linear(tl + ".attention.input_linear", 3 * D, D);
+        ld.linear(tl + ".attention.output_linear", D, D);
+        ld.copy(tl + ".norm_attention.weight", D, 0);
+        ld.copy(tl + ".norm_mlp.weight", D, 0);
+        ld.swiglu_in(tl + ".mlp.w_in", md->ew, D);
+        ld.linear(tl + ".mlp.w_out", D, md->ew / 2);
+        ld.linear(tl + ".center_contraction", D, Dn);
+        ld.linear(tl + ".center_expansion", Dn, D);
+        ld.copy(tl + ".norm_center_features.weight", Dn, 0);
+        ld.swiglu_in(tl + ".center_mlp.w_in", md->cw, Dn);
+        ld.linear(tl + ".center_mlp.w_out", Dn, md->cw / 2);
+      }
+      ld.copy("combination_norms." + ls + ".weight", 2 * D, 0);
+      ld.copy("combination_norms." + ls + ".bias", 2 * D, 0);
+      ld.linear("combination_mlps." + ls + ".0", 2 * D, 2 * D);
+      ld.linear("combination_mlps." + ls + ".2", D, 2 * D);
+    }
+    ld.copy("edge_embedder.weight", ns, D);
+    ld.copy("node_embedders.0.weight", ns, Dn);
+    ld.linear("node_heads.energy.0.0", Dh, Dn);
+    ld.linear("node_heads.energy.0.2", Dh, Dh);
+    ld.linear("edge_heads.energy.0.0", Dh, D);
+    ld.linear("edge_heads.energy.0.2", Dh, Dh);
+    ld.linear("node_last_layers.energy.0.energy___0", 1, Dh);
+    ld.linear("edge_last_layers.energy.0.energy___0", 1, Dh);
+
+    size_t total = 0;
+    std::vector<size_t> at;
+    for (auto& [n, v] : ld.out) at.push_back(total), total += (sizeof(float) * v.size() + 255) & ~size_t(255);
+    if (hipMalloc(&md->weights, total) != hipSuccess) throw Error{PET_MODEL_EMEMORY};
+    std::vector<char> host(total, 0);
+    for (size_t i = 0; i < ld.out.size(); ++i) {
+      std::memcpy(host.data() + at[i], ld.out[i].second.data(), sizeof(float) * ld.out[i].second.size());
+      md->m[ld.out[i].first] = {reinterpret_cast<float*>(static_cast<char*>(md->weights) + at[i]), ld.shapes[i].first,
+                                ld.shapes[i].second};
+    }
+    if (hipMemcpy(md->weights, host.data(), total, hipMemcpyHostToDevice) != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
+    std::vector<double> comp(ns, 0.0);
+    if (composition) comp.assign(composition, composition + ns);
+    if (hipMalloc(&md->comp, sizeof(double) * ns) != hipSuccess) throw Error{PET_MODEL_EMEMORY};
+    if (hipMemcpy(md->comp, comp.data(), sizeof(double) * ns, hipMemcpyHostToDevice) != hipSuccess)
+      throw Error{PET_ATTN_ELAUNCH};
+  } catch (const Error& err) {
+    delete md;
+    return err.code;
+  }
+  *out = md;
+  return PET_ATTN_OK;
+}
+
+void pet_model_destroy(pet_model* model) { delete model; }
+
+size_t pet_model_workspace_bytes(const pet_model* model) { return model ? model->ws.bytes() : 0; }
+
+int pet_model_compute(pet_model* md, const pet_model_edges* e, int forces, double* energy, double* per_atom,
+                      double* forces_out, double* virial, double* edge_grad, void* stream) {
+  if (!md || !e || e->n_atoms < 0 || e->n_edges < 0 || e->max_neighbors < 0 || e->n_struct < 0) return PET_ATTN_EINVAL;
+  if (e->n_atoms == 0) return PET_ATTN_OK;
+  if (!e->species || !e->off || (e->n_edges > 0 && (!e->center || !e->neigh_species || !e->reverse || !e->vec ||
+                                                    !e->dist || !e->pcut || !e->cut)))
+    return PET_ATTN_EINVAL;
+  if (energy && (!e->struct_off || e->n_struct < 1)) return PET_ATTN_EINVAL;
+  if (forces && (!forces_out || (virial && (!e->struct_off || e->n_struct < 1)))) return PET_ATTN_EINVAL;
+  if (e->max_neighbors + 1 > pet_attn_max_slots(md->hd)) return PET_ATTN_ESLOTS;
+  if (edge_grad && md->h.energy_scale != 1.0) return PET_ATTN_EINVAL;
+  if (int64_t(e->n_atoms) + e->n_edges >= (int64_t(1) << 31) / std::max(3 * md->h.d_pet, md->ew))
+    return PET_ATTN_EINDEX;
+  try {
+    Pass p(*md, *e, reinterpret_cast<hipStream_t>(stream));
+    p.run(forces != 0, energy, per_atom, forces_out, virial, edge_grad);
+  } catch (const Error& err) {
+    return err.code;
+  }
+  return PET_ATTN_OK;
+}
+
+}  // extern "C"

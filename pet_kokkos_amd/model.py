@@ -1,0 +1,160 @@
+"""The whole PET evaluation over torch device memory: the Python mirror of the
+reference's PetModel / Calculator for the feedforward featurizer
+(peterspackman/pet-kokkos include/pet/model.hpp, include/pet/calculator.hpp:
+187-239, src/model.cpp:782-811, src/feedforward.cpp:338-411), every step in
+libpet_attn.so (include/pet_model.h). There is no CPU path: without the
+library, or without a GPU, construction fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+
+import numpy as np
+import torch
+
+from . import _lib
+from .attention import _stream
+from .forces import CUTOFF_KINDS
+from .systems import Edges, Structure, neighbor_list, packed_edges
+from .weights import Hypers
+
+
+@dataclasses.dataclass
+class ModelInput:
+    """A batch on the device in the layout pet_model_compute reads
+    (DeviceEdgeData + PackedEdges, include/pet/model.hpp:60-168)."""
+    n_atoms: int
+    n_edges: int
+    max_neighbors: int
+    struct_off: torch.Tensor  # int32 [B + 1]
+    species: torch.Tensor  # int32 [N]
+    off: torch.Tensor  # int32 [N + 1]
+    center: torch.Tensor  # int32 [E]
+    neigh_species: torch.Tensor  # int32 [E]
+    reverse: torch.Tensor  # int32 [E]
+    vec: torch.Tensor  # float64 [E, 3]
+    dist: torch.Tensor  # float64 [E]
+    pcut: torch.Tensor  # float64 [E]
+    cut: torch.Tensor  # float32 [E]
+    host: object = None  # the host PackedEdges, for checks
+
+    @property
+    def n_struct(self) -> int:
+        return int(self.struct_off.numel()) - 1
+
+    def c(self) -> _lib.ModelEdges:
+        p = lambda t: t.data_ptr() if t.numel() else None
+        return _lib.ModelEdges(self.n_atoms, self.n_edges, self.max_neighbors, self.n_struct, p(self.struct_off),
+                               p(self.species), p(self.off), p(self.center), p(self.neigh_species), p(self.reverse),
+                               p(self.vec), p(self.dist), p(self.pcut), p(self.cut))
+
+
+def species_index(numbers, atomic_types) -> np.ndarray:
+    lut = {int(z): i for i, z in enumerate(atomic_types)}
+    try:
+        return np.array([lut[int(z)] for z in numbers], dtype=np.int32)
+    except KeyError as e:
+        raise ValueError(f"atomic number {e.args[0]} is not among the model's types {tuple(atomic_types)}") from None
+
+
+def make_input(h: Hypers, species: np.ndarray, edges: Edges, struct_off: np.ndarray, device="cuda:0",
+               cut: np.ndarray | None = None) -> ModelInput:
+    """Pack a host neighbour list (already grouped by centre) for the device."""
+    N = len(species)
+    pk = packed_edges(N, edges, h.cutoff, h.cutoff_width)
+    if cut is not None:
+        pk.cut = np.asarray(cut, dtype=np.float32)
+    E = int(pk.off[-1])
+    counts = np.diff(pk.off)
+    t = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt).to(device)
+    return ModelInput(N, E, int(counts.max()) if N else 0, t(struct_off, torch.int32), t(species, torch.int32),
+                      t(pk.off, torch.int32), t(pk.center, torch.int32), t(species[pk.neigh], torch.int32),
+                      t(pk.reverse, torch.int32), t(pk.vec, torch.float64), t(pk.dist, torch.float64),
+                      t(pk.pcut, torch.float64), t(pk.cut, torch.float32), pk)
+
+
+def structures_input(h: Hypers, structures: list[Structure], device="cuda:0") -> ModelInput:
+    """A batch of structures: each one's neighbour list at the model's cutoff,
+    atoms concatenated (energy_forces_batch, src/model.cpp:782-793)."""
+    parts, species, soff, base = [], [], [0], 0
+    for s in structures:
+        e = neighbor_list(s, h.cutoff)
+        parts.append(Edges(e.centre + base, e.neigh + base, e.vec, e.dist, e.shift))
+        species.append(species_index(s.numbers, h.atomic_types))
+        base += len(s.positions)
+        soff.append(base)
+    cat = lambda f: np.concatenate([getattr(p, f) for p in parts])
+    edges = Edges(cat("centre").astype(np.int32), cat("neigh").astype(np.int32), cat("vec"), cat("dist"), cat("shift"))
+    return make_input(h, np.concatenate(species), edges, np.array(soff, dtype=np.int32), device)
+
+
+class PetModel:
+    """Weights on the device and energy / forces / virial from packed edges
+    (the reference's PetModel, include/pet/model.hpp)."""
+
+    def __init__(self, h: Hypers, weights: dict[str, np.ndarray], composition=None, energy_scale: float = 1.0):
+        self.h = h
+        lib = _lib.load()
+        hy = _lib.ModelHypers(h.d_pet, h.d_node, h.d_head, h.num_heads, h.num_gnn_layers, h.num_attention_layers,
+                              h.n_species, CUTOFF_KINDS[h.cutoff_function], h.cutoff_width, h.attention_temperature,
+                              energy_scale)
+        keep = [np.ascontiguousarray(v, dtype=np.float64) for v in weights.values()]
+        arr = (_lib.ModelTensor * len(keep))()
+        for i, (name, v) in enumerate(zip(weights.keys(), keep)):
+            arr[i] = _lib.ModelTensor(name.encode(), v.shape[0], v.shape[1] if v.ndim == 2 else 0, v.ctypes.data)
+        comp = None if composition is None else np.ascontiguousarray(composition, dtype=np.float64)
+        handle = ctypes.c_void_p()
+        _lib.check(lib.pet_model_create(ctypes.byref(hy), arr, len(keep), None if comp is None else comp.ctypes.data,
+                                        ctypes.byref(handle)), "pet_model_create")
+        self._handle = handle
+        self._lib = lib
+
+    def __del__(self):
+        if getattr(self, "_handle", None) and self._handle.value:
+            self._lib.pet_model_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(self._lib.pet_model_workspace_bytes(self._handle))
+
+    def compute(self, x: ModelInput, forces: bool = True, edge_grad: bool = False, out: dict | None = None) -> dict:
+        """energy [B], per_atom [N] and, with forces, forces [N, 3], virial
+        [B, 3, 3] (and edge_grad [E, 3]): fp64 device tensors. `out` reuses
+        the tensors of an earlier call of the same shapes."""
+        dev = x.species.device
+        f64 = dict(dtype=torch.float64, device=dev)
+        if out is None:
+            out = {"energy": torch.empty(x.n_struct, **f64), "per_atom": torch.empty(x.n_atoms, **f64)}
+            if forces:
+                out["forces"] = torch.empty(x.n_atoms, 3, **f64)
+                out["virial"] = torch.empty(x.n_struct, 3, 3, **f64)
+            if edge_grad:
+                out["edge_grad"] = torch.empty(x.n_edges, 3, **f64)
+        p = lambda k: out[k].data_ptr() if k in out and out[k].numel() else None
+        e = x.c()
+        _lib.check(self._lib.pet_model_compute(self._handle, ctypes.byref(e), int(forces), p("energy"), p("per_atom"),
+                                               p("forces") if forces else None, p("virial") if forces else None,
+                                               p("edge_grad") if forces else None, _stream()),
+                   "pet_model_compute")
+        return out
+
+
+class Calculator:
+    """pet::Calculator::compute's shape (include/pet/calculator.hpp:187-239):
+    a structure in, energy (eV), forces [N, 3] (eV/A) and virial [3, 3] out,
+    on the host."""
+
+    def __init__(self, model: PetModel, device="cuda:0"):
+        self.model, self.device = model, device
+
+    def compute(self, s: Structure, forces: bool = True):
+        x = structures_input(self.model.h, [s], self.device)
+        o = self.model.compute(x, forces)
+        torch.cuda.synchronize()
+        res = {"energy": float(o["energy"][0]), "per_atom": o["per_atom"].cpu().numpy()}
+        if forces:
+            res["forces"] = o["forces"].cpu().numpy()
+            res["virial"] = o["virial"][0].cpu().numpy()
+        return res
