@@ -303,7 +303,7 @@ struct pet_model {
   Arena ws;
 
   ~pet_model() {
-    (void) hipDeviceSynchronize();
+    if (weights || comp || ws.bytes()) (void) hipDeviceSynchronize();
     if (weights) (void) hipFree(weights);
     if (comp) (void) hipFree(comp);
   }

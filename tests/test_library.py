@@ -1,5 +1,5 @@
 """The C-ABI library without a GPU: it loads, exports every function
-include/pet_attn.h declares, and rejects bad arguments before touching the
+include/pet_attn.h and include/pet_model.h declare, and rejects bad arguments before touching the
 device."""
 from __future__ import annotations
 
@@ -14,11 +14,11 @@ import oracle
 from pet_kokkos_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "pet_attn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("pet_attn.h", "pet_model.h")]
 
 
 def declared():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"PET_ATTN_API\s+[\w\s\*]+?\b(pet_\w+)\s*\(", text)))
 
 
@@ -64,3 +64,37 @@ def test_error_raises():
         _lib.check(_lib.EHEADDIM, "x")
     assert issubclass(_lib.PetAttnError, RuntimeError)
     _ = np
+
+
+def _model_create(tensors, **over):
+    from pet_kokkos_amd import weights
+    h = weights.MODELS["tiny"]
+    hy = dict(d_pet=h.d_pet, d_node=h.d_node, d_head=h.d_head, num_heads=h.num_heads,
+              num_gnn_layers=h.num_gnn_layers, num_attention_layers=h.num_attention_layers, n_species=h.n_species,
+              cutoff_function=1, cutoff_width=0.5, attention_temperature=1.0, energy_scale=1.0)
+    hy.update(over)
+    keep = [np.ascontiguousarray(v, dtype=np.float64) for v in tensors.values()]
+    arr = (_lib.ModelTensor * max(1, len(keep)))()
+    for i, (name, v) in enumerate(zip(tensors.keys(), keep)):
+        arr[i] = _lib.ModelTensor(name.encode(), v.shape[0], v.shape[1] if v.ndim == 2 else 0, v.ctypes.data)
+    out = ctypes.c_void_p()
+    code = _lib.load().pet_model_create(ctypes.byref(_lib.ModelHypers(**hy)), arr, len(keep), None, ctypes.byref(out))
+    return code, out
+
+
+def test_model_create_rejects_before_the_device():
+    """Checks that fail before any device memory is touched (pet_model_create)."""
+    from pet_kokkos_amd import weights
+    w = weights.random_weights(weights.MODELS["tiny"], 0)
+    missing = dict(w)
+    del missing["gnn_layers.1.trans.layers.0.mlp.w_out.weight"]
+    assert _model_create(missing)[0] == 20  # PET_MODEL_EMISSING
+    bad = dict(w)
+    bad["gnn_layers.0.compress.2.weight"] = np.zeros((3, 3))
+    assert _model_create(bad)[0] == 21  # PET_MODEL_ESHAPE
+    assert _model_create(w, d_node=64)[0] == _lib.EINVAL  # the feedforward family needs d_node != d_pet
+    assert _model_create(w, num_heads=3)[0] == _lib.EINVAL  # d_pet not a multiple of the heads
+    assert _model_create(w, num_heads=8)[0] == _lib.EHEADDIM  # head_dim 8
+    assert "missing" in _lib.strerror(20)
+    lib = _lib.load()
+    assert lib.pet_model_compute(None, None, 1, None, None, None, None, None, None) == _lib.EINVAL
