@@ -116,7 +116,6 @@ def time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device):
     eb = E * (16 + 4 + 4 + 24 + 8 + 8 + 4 + 24)
     out["edge_grad"] = dict(us=us_e, edges=E, gbps=eb / us_e / 1e3)
     out["fold"] = dict(us=us_f, atoms=len(s.positions))
-    out["c2_attention_share_of_ef_ms"] = c2_attention_share(device, reps)
     out["other_configs"] = other_configs(device, reps)
     return out
 
@@ -157,65 +156,52 @@ def other_configs(device, reps):
     return res
 
 
-def c2_attention_share(device, reps):
-    """The attention path's share of one energy+forces evaluation of the C2
-    model (648-atom water, d_model 128, 4 heads of 32, 2 GNN layers x 2
-    transformer layers = 4 attention blocks): per block the layer-level
-    forward and backward (norm, QKV linear, attention, output linear and back
-    to the tokens' adjoint, cf_seq_adj accumulated), then the forces' edge
-    term and fold from the accumulated cf_seq_adj. The rest of the model
-    (embeddings, MLPs, readout) is not built here, so this is not the whole
-    E+F time."""
+def time_ef(device, reps, cpu: bool):
+    """Energy+forces evaluations of the whole model (pet_model_compute): C2
+    (configs[1], 648-atom water, d 128 / 4 heads / 2 x 2 layers / FFN 512)
+    and C5 (configs[4], 32 structures, d 512 / 8 heads of 64). ms per
+    evaluation with inputs resident, the contraction roofline of its FLOPs
+    (dense fp32 on the matrix cores: a lower bound that leaves out the
+    HBM-bound elementwise passes) and, for C2, the CPU oracle (float32 torch on
+    this host's cores) on the same structure."""
     import numpy as np
     import torch
 
-    from pet_kokkos_amd import attention as A
-    from pet_kokkos_amd import forces as F
-    from pet_kokkos_amd import layer as L
-    from pet_kokkos_amd import systems
+    from pet_kokkos_amd.model import PetModel, ef_flops, ef_workload, structures_input
 
-    cfg = systems.CONFIGS["c2"]
-    s = systems.build_structure(cfg.structure, 0)
-    e = systems.neighbor_list(s, cfg.cutoff)
-    N = len(s.positions)
-    tk = systems.tokens_from_edges(N, e, cfg.cutoff, cfg.width)
-    pk = F.PackedEdges.from_host(systems.packed_edges(N, e, cfg.cutoff, cfg.width), device)
-    H, hd, D = cfg.heads, cfg.head_dim, cfg.d_model
-    T, S = tk.n_rows, tk.slots
-    gen = torch.Generator(device=device)
-    gen.manual_seed(5)
-    blocks = []
-    for _ in range(4):
-        blocks.append(dict(nw=torch.ones(D, device=device), w_in=torch.randn((3 * D, D), device=device, generator=gen) / D ** 0.5,
-                           b_in=torch.zeros(3 * D, device=device), w_out=torch.randn((D, D), device=device, generator=gen) / D ** 0.5,
-                           b_out=torch.zeros(D, device=device)))
-    tok = torch.randn((T, D), device=device, generator=gen)
-    out_adj = torch.randn((T, D), device=device, generator=gen)
-    off = torch.from_numpy(tk.off).to(device)
-    cf = torch.from_numpy(tk.cf_seq).to(device)
-    t = A.Tokens(off, N)
-    ws = A.Workspace(device)
-    out = torch.empty((T, D), device=device)
-    tadj = torch.empty((T, D), device=device)
-    csa = torch.zeros((N, S), device=device)
-    x4 = torch.randn((pk.n_edges, 4), device=device, generator=gen)
-    soff = torch.tensor([0, N], dtype=torch.int32, device=device)
-
-    def ef():
-        for b, p in enumerate(blocks):
-            L.attention_layer(ws, f"b{b}", out, tok, p["nw"], None, p["w_in"], p["b_in"], cf, p["w_out"], p["b_out"],
-                              t, S, H, hd, 1.0)
-        for b, p in reversed(list(enumerate(blocks))):
-            L.attention_layer_bwd(ws, f"b{b}", tadj, csa, out_adj, tok, p["nw"], None, p["w_in"], p["b_in"], cf,
-                                  p["w_out"], t, S, H, hd, 1.0)
-        F.forces_and_virial(pk, N, soff, x4, None, csa, cfg.width, "cosine", -1.0)
-
-    from pet_kokkos_amd import graph as G
-
-    eager_ms = _timed(ef, max(5, reps // 4)) / 1e3
-    cache = G.GraphCache()
-    return dict(eager_ms=eager_ms, graph_ms=_timed(lambda: cache.run("c2-ef", ef), max(5, reps // 4)) / 1e3,
-                graph_note="the same work recorded once as a HIP graph and replayed (pet_kokkos_amd.graph)")
+    res = {}
+    for name in ("c2", "c5"):
+        h, w, comp, sts = ef_workload(name)
+        m = PetModel(h, w, comp)
+        x = structures_input(h, sts, device)
+        cnt = np.diff(x.host.off).astype(np.float64) + 1
+        fl = ef_flops(h, x.n_atoms, x.n_edges, float((cnt * cnt).sum()))
+        n = max(3, reps // (2 if name == "c2" else 20))
+        o = m.compute(x, True)
+        e_ms = _timed(lambda: m.compute(x, False, out=o), n) / 1e3
+        ef_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
+        r = dict(structures=len(sts), atoms=x.n_atoms, edges=x.n_edges, d_pet=h.d_pet, heads=h.num_heads,
+                 ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
+                 ef_bound_ms=fl["forces"] / PEAK_FP32_MFMA * 1e3, ef_frac_of_roofline=fl["forces"] / PEAK_FP32_MFMA
+                 * 1e3 / ef_ms, workspace_gb=m.workspace_bytes / 1e9)
+        if name == "c2" and cpu:
+            from oracle import pet_model as om
+            sp = x.species.cpu().numpy()
+            om.evaluate(h, w, sp, x.host, comp, dtype=torch.float32)
+            t = []
+            for _ in range(2):
+                c0 = time.perf_counter()
+                om.evaluate(h, w, sp, x.host, comp, dtype=torch.float32)
+                t.append(time.perf_counter() - c0)
+            r["cpu_ms"] = min(t) * 1e3
+            r["cpu_note"] = (f"oracle/pet_model.py in float32 torch on {torch.get_num_threads()} host threads, "
+                             "forces by autograd, best of 2 after a warmup")
+        res[name] = r
+        del m, x, o
+        torch.cuda.empty_cache()
+    res["note"] = ("random-init PET-shaped models (feedforward featurizer: RMSNorm, SwiGLU, d_node 2 d_pet, "
+                   "d_head 128); neighbour list built on the host beforehand and not timed")
+    return res
 
 
 def main():
@@ -228,6 +214,7 @@ def main():
     ap.add_argument("--no-op-level", action="store_true", help="skip the op-level (with linears) timing")
     ap.add_argument("--no-rows", action="store_true",
                     help="skip the timing of the path's other rows (token norm, layer level, forces' edge term)")
+    ap.add_argument("--no-ef", action="store_true", help="skip the whole-model energy+forces timing (C2, C5)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -348,6 +335,8 @@ def main():
 
     if not args.no_rows:
         extra["rows"] = time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device)
+    if not args.no_ef:
+        extra["ef"] = time_ef(device, max(10, args.steps // 2), not args.no_cpu)
 
     cpu = None
     if not args.no_cpu:

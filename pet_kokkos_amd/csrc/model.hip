@@ -85,38 +85,48 @@ __global__ void add_bias_kernel(float* __restrict__ x, const float* __restrict__
   GRID_LOOP(i, R * W) x[i] += b[i % W];
 }
 
-// out = silu(z), fast sigmoid (linear_silu, src/ops.cpp:54-76)
-__global__ void silu_kernel(float* __restrict__ out, const float* __restrict__ z, int64_t n) {
-  GRID_LOOP(i, n) {
-    const float v = z[i];
+// The dense layers before an activation run with beta 0 and no bias: their
+// output z is kept as is (the saved pre-activation is z + b) and the
+// activation passes, forward and backward, add the bias as they read it --
+// one write and one read of the pre-activation fewer than a bias fill the
+// GEMM accumulates onto.
+
+// out = silu(z + b), fast sigmoid (linear_silu, src/ops.cpp:54-76)
+__global__ void silu_kernel(float* __restrict__ out, const float* __restrict__ z, const float* __restrict__ b,
+                            int64_t R, int W) {
+  GRID_LOOP(i, R * W) {
+    const float v = z[i] + b[i % W];
     out[i] = v * sig_fast(v);
   }
 }
 
-// g *= silu'(pre) (silu_bwd, src/ops.cpp:78-101)
-__global__ void silu_bwd_kernel(float* __restrict__ g, const float* __restrict__ pre, int64_t n) {
-  GRID_LOOP(i, n) {
-    const float x = pre[i], sg = sig_fast(x);
+// g *= silu'(pre + b) (silu_bwd, src/ops.cpp:78-101)
+__global__ void silu_bwd_kernel(float* __restrict__ g, const float* __restrict__ pre, const float* __restrict__ b,
+                                int64_t R, int W) {
+  GRID_LOOP(i, R * W) {
+    const float x = pre[i] + b[i % W], sg = sig_fast(x);
     g[i] *= sg * (1.0f + x * (1.0f - sg));
   }
 }
 
-// h[r, c] = pre[r, 2c] * sigmoid(pre[r, 2c+1]): pre's rows interleaved (v_j, g_j)
-// (swiglu_in, src/ops.cpp:248-271)
-__global__ void swiglu_kernel(float* __restrict__ h, const float2* __restrict__ pre, int64_t n) {
-  GRID_LOOP(i, n) {
-    const float2 p = pre[i];
-    h[i] = p.x * sig_fast(p.y);
+// h[r, c] = v * sigmoid(g), (v, g) = pre[r, 2c .. 2c+1] + b[2c .. 2c+1]: pre's
+// rows interleaved (v_j, g_j) (swiglu_in, src/ops.cpp:248-271)
+__global__ void swiglu_kernel(float* __restrict__ h, const float2* __restrict__ pre, const float2* __restrict__ b,
+                              int64_t R, int F) {
+  GRID_LOOP(i, R * F) {
+    const float2 p = pre[i], bb = b[i % F];
+    const float v = p.x + bb.x, g = p.y + bb.y;
+    h[i] = v * sig_fast(g);
   }
 }
 
 // pre_adj from h_adj (swiglu_bwd, src/ops.cpp:281-324)
 __global__ void swiglu_bwd_kernel(float2* __restrict__ pre_adj, const float* __restrict__ h_adj,
-                                  const float2* __restrict__ pre, int64_t n) {
-  GRID_LOOP(i, n) {
-    const float2 p = pre[i];
-    const float sg = sig_fast(p.y), g = h_adj[i];
-    pre_adj[i] = make_float2(g * sg, g * p.x * sg * (1.0f - sg));
+                                  const float2* __restrict__ pre, const float2* __restrict__ b, int64_t R, int F) {
+  GRID_LOOP(i, R * F) {
+    const float2 p = pre[i], bb = b[i % F];
+    const float v = p.x + bb.x, sg = sig_fast(p.y + bb.y), g = h_adj[i];
+    pre_adj[i] = make_float2(g * sg, g * v * sg * (1.0f - sg));
   }
 }
 
@@ -345,12 +355,39 @@ void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const
   const Mat& W = md.w(key + ".weight");
   if (M) ok(gemm_nn(in_adj, W.cols, out_adj, W.rows, W.p, M, W.rows, W.cols, beta, st));
 }
-void silu(float* out, const float* z, int64_t n, hipStream_t st) {
-  hipLaunchKernelGGL(silu_kernel, grid_for(n), dim3(256), 0, st, out, z, n);
+// z[M, Nout] = in W^T, no bias: the pre-activation an activation pass reads with its bias
+void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const std::string& key, hipStream_t st) {
+  const Mat& W = md.w(key + ".weight");
+  if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
+  if (M) ok(gemm_nt(z, W.rows, in, K, W.p, M, W.rows, K, 0.0f, st));
+}
+// out = silu(z + b) of linear_pre's z under `key`
+void silu(pet_model& md, float* out, const float* z, int64_t R, const std::string& key, hipStream_t st) {
+  const Mat& b = md.w(key + ".bias");
+  if (R == 0) return;
+  hipLaunchKernelGGL(silu_kernel, grid_for(R * b.rows), dim3(256), 0, st, out, z, b.p, R, b.rows);
   launched();
 }
-void silu_bwd(float* g, const float* pre, int64_t n, hipStream_t st) {
-  hipLaunchKernelGGL(silu_bwd_kernel, grid_for(n), dim3(256), 0, st, g, pre, n);
+void silu_bwd(pet_model& md, float* g, const float* z, int64_t R, const std::string& key, hipStream_t st) {
+  const Mat& b = md.w(key + ".bias");
+  if (R == 0) return;
+  hipLaunchKernelGGL(silu_bwd_kernel, grid_for(R * b.rows), dim3(256), 0, st, g, z, b.p, R, b.rows);
+  launched();
+}
+// h = swiglu(z + b) of linear_pre's z under `key` (a .w_in)
+void swiglu(pet_model& md, float* h, const float* z, int64_t R, const std::string& key, hipStream_t st) {
+  const Mat& b = md.w(key + ".bias");
+  if (R == 0) return;
+  hipLaunchKernelGGL(swiglu_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st, h,
+                     reinterpret_cast<const float2*>(z), reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
+  launched();
+}
+void swiglu_bwd(pet_model& md, float* z_adj, const float* h_adj, const float* z, int64_t R, const std::string& key,
+                hipStream_t st) {
+  const Mat& b = md.w(key + ".bias");
+  if (R == 0) return;
+  hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st, reinterpret_cast<float2*>(z_adj),
+                     h_adj, reinterpret_cast<const float2*>(z), reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
   launched();
 }
 void norm(pet_model& md, float* out, const float* in, int R, int W, const std::string& key, bool ln, hipStream_t st) {
@@ -442,23 +479,15 @@ struct Pass {
       // node_next += center_mlp(norm(node_res)); edge_next += mlp(norm(eps))
       float* nn = node_exp;  // consumed
       norm(md, nn, b.node_res, N, Dn, tl + ".norm_center_features", false, st);
-      linear(md, b.pre_c, nn, N, Dn, tl + ".center_mlp.w_in", st);
+      linear_pre(md, b.pre_c, nn, N, Dn, tl + ".center_mlp.w_in", st);
       float* hc = md.f(int64_t(N) * md.cw / 2);
-      if (N) {
-        hipLaunchKernelGGL(swiglu_kernel, grid_for(int64_t(N) * md.cw / 2), dim3(256), 0, st, hc,
-                           reinterpret_cast<const float2*>(b.pre_c), int64_t(N) * md.cw / 2);
-        launched();
-      }
+      swiglu(md, hc, b.pre_c, N, tl + ".center_mlp.w_in", st);
       linear_acc(md, node_next, hc, N, md.cw / 2, tl + ".center_mlp.w_out", st);
       float* en = attn_out;  // consumed: its edge rows were read by the residual pass
       norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
-      linear(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
+      linear_pre(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
       float* he = md.f(int64_t(E) * md.ew / 2);
-      if (E) {
-        hipLaunchKernelGGL(swiglu_kernel, grid_for(int64_t(E) * md.ew / 2), dim3(256), 0, st, he,
-                           reinterpret_cast<const float2*>(b.pre_e), int64_t(E) * md.ew / 2);
-        launched();
-      }
+      swiglu(md, he, b.pre_e, E, tl + ".mlp.w_in", st);
       linear_acc(md, edge_next, he, E, md.ew / 2, tl + ".mlp.w_out", st);
       md.ws.release(scope);
       node_cur = node_next;
@@ -476,8 +505,8 @@ struct Pass {
     }
     float* cn = md.f(int64_t(E) * 2 * D);
     norm(md, cn, sv.concat, E, 2 * D, "combination_norms." + ls, true, st);
-    linear(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
-    silu(cn, sv.cph, int64_t(E) * 2 * D, st);
+    linear_pre(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
+    silu(md, cn, sv.cph, E, "combination_mlps." + ls + ".0", st);
     if (E) {
       hipLaunchKernelGGL(add_bias_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge,
                          md.p("combination_mlps." + ls + ".2.bias"), int64_t(E), D);
@@ -500,7 +529,7 @@ struct Pass {
       float* cph_adj = md.f(int64_t(E) * 2 * D);
       float* cn_adj = md.f(int64_t(E) * 2 * D);
       linear_bwd(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", 0.0f, st);
-      silu_bwd(cph_adj, sv.cph, int64_t(E) * 2 * D, st);
+      silu_bwd(md, cph_adj, sv.cph, E, "combination_mlps." + ls + ".0", st);
       linear_bwd(md, cn_adj, cph_adj, E, "combination_mlps." + ls + ".0", 0.0f, st);
       float* ca = cph_adj;  // consumed
       ok(pet_norm_rows_bwd(E, 2 * D, ca, 2 * D, 0.0f, cn_adj, 2 * D, sv.concat, 2 * D,
@@ -521,24 +550,14 @@ struct Pass {
         float* pre_adj = md.f(int64_t(E) * md.ew);
         float* en_adj = md.f(int64_t(E) * D);
         linear_bwd(md, h_adj, edge_adj, E, tl + ".mlp.w_out", 0.0f, st);
-        if (E) {
-          hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(int64_t(E) * md.ew / 2), dim3(256), 0, st,
-                             reinterpret_cast<float2*>(pre_adj), h_adj, reinterpret_cast<const float2*>(b.pre_e),
-                             int64_t(E) * md.ew / 2);
-          launched();
-        }
+        swiglu_bwd(md, pre_adj, h_adj, b.pre_e, E, tl + ".mlp.w_in", st);
         linear_bwd(md, en_adj, pre_adj, E, tl + ".mlp.w_in", 0.0f, st);
         ok(pet_norm_rows_bwd(E, D, edge_adj, D, 1.0f, en_adj, D, b.eps, D, md.p(tl + ".norm_mlp.weight"), 0, st));
         float* hc_adj = md.f(int64_t(N) * md.cw / 2);
         float* prec_adj = md.f(int64_t(N) * md.cw);
         float* cn_adj = md.f(int64_t(N) * Dn);
         linear_bwd(md, hc_adj, node_adj, N, tl + ".center_mlp.w_out", 0.0f, st);
-        if (N) {
-          hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(int64_t(N) * md.cw / 2), dim3(256), 0, st,
-                             reinterpret_cast<float2*>(prec_adj), hc_adj, reinterpret_cast<const float2*>(b.pre_c),
-                             int64_t(N) * md.cw / 2);
-          launched();
-        }
+        swiglu_bwd(md, prec_adj, hc_adj, b.pre_c, N, tl + ".center_mlp.w_in", st);
         linear_bwd(md, cn_adj, prec_adj, N, tl + ".center_mlp.w_in", 0.0f, st);
         ok(pet_norm_rows_bwd(N, Dn, node_adj, Dn, 1.0f, cn_adj, Dn, b.node_res, Dn,
                              md.p(tl + ".norm_center_features.weight"), 0, st));
@@ -599,15 +618,15 @@ struct Pass {
     {
       auto scope = md.ws.mark();
       float* x = md.f(std::max<int64_t>(int64_t(N), int64_t(E)) * Dh);
-      linear(md, nh0, node, N, Dn, "node_heads.energy.0.0", st);
-      silu(x, nh0, int64_t(N) * Dh, st);
-      linear(md, nh1, x, N, Dh, "node_heads.energy.0.2", st);
-      silu(x, nh1, int64_t(N) * Dh, st);
+      linear_pre(md, nh0, node, N, Dn, "node_heads.energy.0.0", st);
+      silu(md, x, nh0, N, "node_heads.energy.0.0", st);
+      linear_pre(md, nh1, x, N, Dh, "node_heads.energy.0.2", st);
+      silu(md, x, nh1, N, "node_heads.energy.0.2", st);
       linear(md, npred, x, N, Dh, "node_last_layers.energy.0.energy___0", st);
-      linear(md, eh0, input_edge, E, D, "edge_heads.energy.0.0", st);
-      silu(x, eh0, int64_t(E) * Dh, st);
-      linear(md, eh1, x, E, Dh, "edge_heads.energy.0.2", st);
-      silu(x, eh1, int64_t(E) * Dh, st);
+      linear_pre(md, eh0, input_edge, E, D, "edge_heads.energy.0.0", st);
+      silu(md, x, eh0, E, "edge_heads.energy.0.0", st);
+      linear_pre(md, eh1, x, E, Dh, "edge_heads.energy.0.2", st);
+      silu(md, x, eh1, E, "edge_heads.energy.0.2", st);
       linear(md, epred, x, E, Dh, "edge_last_layers.energy.0.energy___0", st);
       md.ws.release(scope);
     }
@@ -638,14 +657,14 @@ struct Pass {
         launched();
       }
       linear_bwd(md, a1, npa, N, "node_last_layers.energy.0.energy___0", 0.0f, st);
-      silu_bwd(a1, nh1, int64_t(N) * Dh, st);
+      silu_bwd(md, a1, nh1, N, "node_heads.energy.0.2", st);
       linear_bwd(md, a0, a1, N, "node_heads.energy.0.2", 0.0f, st);
-      silu_bwd(a0, nh0, int64_t(N) * Dh, st);
+      silu_bwd(md, a0, nh0, N, "node_heads.energy.0.0", st);
       linear_bwd(md, node_adj, a0, N, "node_heads.energy.0.0", 0.0f, st);
       linear_bwd(md, a1, epa, E, "edge_last_layers.energy.0.energy___0", 0.0f, st);
-      silu_bwd(a1, eh1, int64_t(E) * Dh, st);
+      silu_bwd(md, a1, eh1, E, "edge_heads.energy.0.2", st);
       linear_bwd(md, a0, a1, E, "edge_heads.energy.0.2", 0.0f, st);
-      silu_bwd(a0, eh0, int64_t(E) * Dh, st);
+      silu_bwd(md, a0, eh0, E, "edge_heads.energy.0.0", st);
       linear_bwd(md, ie_adj, a0, E, "edge_heads.energy.0.0", 0.0f, st);
       md.ws.release(scope);
     }

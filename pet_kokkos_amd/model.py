@@ -158,3 +158,39 @@ class Calculator:
             res["forces"] = o["forces"].cpu().numpy()
             res["virial"] = o["virial"][0].cpu().numpy()
         return res
+
+
+def ef_flops(h: Hypers, n_atoms: int, n_edges: int, sum_cnt2: float) -> dict:
+    """Algorithmic FLOPs of one evaluation, the reference's accounting
+    (tools/roofline.py:188-260): 2 M N K per dense layer, the attention's
+    4 (forward) and 10 (backward) sum(cnt^2) D per block; the backward's
+    GEMMs are the input adjoints only (forces need no weight gradients), one
+    per forward GEMM."""
+    N, E, T = n_atoms, n_edges, n_atoms + n_edges
+    D, Dn, Dh, cw, ew = h.d_pet, h.d_node, h.d_head, h.center_width, h.edge_width
+    g = 0.0
+    for L in range(h.num_gnn_layers):
+        g += (E * D * D if L else 0) + E * D * D  # compress.0's input_edge block, compress.2
+        g += h.num_attention_layers * (N * D * Dn + T * 3 * D * D + T * D * D + N * Dn * D + N * cw * Dn
+                                       + N * Dn * cw // 2 + E * ew * D + E * D * ew // 2)
+        g += E * 2 * D * 2 * D + E * D * 2 * D  # combination MLP
+    g += N * Dh * Dn + N * Dh * Dh + N * Dh + E * Dh * D + E * Dh * Dh + E * Dh  # readout
+    blocks = h.num_gnn_layers * h.num_attention_layers
+    return dict(energy=2.0 * g + blocks * 4.0 * sum_cnt2 * D,
+                forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D)
+
+
+def ef_workload(name: str, seed: int = 0):
+    """(hypers, weights, composition, structures) of an energy+forces workload:
+    "c2" configs[1] (648-atom water), "c5" configs[4] (32 structures,
+    diamond-64 and water-648 alternating, each seeded by its index)."""
+    from . import systems, weights
+    h = weights.MODELS[name]
+    if name == "c2":
+        sts = [systems.water_box(6, 18.6, seed=seed)]
+    elif name == "c5":
+        sts = [systems.diamond(2, jitter=0.01, seed=seed + k) if k % 2 == 0 else
+               systems.water_box(6, 18.6, seed=seed + k) for k in range(32)]
+    else:
+        raise ValueError(name)
+    return h, weights.random_weights(h, seed), weights.random_composition(h, seed), sts

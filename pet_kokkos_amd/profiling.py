@@ -3,6 +3,10 @@ the benchmark configurations, preceded by a plain device copy of known size
 (the calibration kernel that HBM byte counters are scaled by).
 
     python -m pet_kokkos_amd.profiling --config c3 --steps 20 --copy-mib 1024
+    python -m pet_kokkos_amd.profiling --model c2 --steps 10
+
+With ``--model`` the steps are whole energy+forces evaluations of the PET
+model on that workload (C2: 648-atom water; C5: 32 structures) instead.
 
 Under ``rocprofv3 --kernel-trace --stats`` it gives each kernel's average
 duration; under ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``) each
@@ -28,8 +32,11 @@ def main(argv=None):
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--rows", action="store_true",
                     help="also run the token norm (forward, backward) and the forces' edge term and fold each step")
+    ap.add_argument("--model", choices=["c2", "c5"], help="profile whole energy+forces evaluations instead")
     args = ap.parse_args(argv)
     device = torch.device("cuda", 0)
+    if args.model:
+        return profile_model(args, device)
     conf, tk = systems.config_tokens(args.config, seed=0)
     H, hd, D = conf.heads, conf.head_dim, conf.d_model
     N, S, T = tk.n_atoms, tk.slots, tk.n_rows
@@ -77,6 +84,24 @@ def main(argv=None):
     torch.cuda.synchronize()
     print(json.dumps({"config": args.config, "steps": args.steps, "copy_mib": args.copy_mib, "N": N, "T": T, "S": S,
                       "D": D, "H": H}), flush=True)
+    return 0
+
+
+def profile_model(args, device):
+    from .model import PetModel, ef_workload, structures_input
+    h, w, comp, sts = ef_workload(args.model)
+    m = PetModel(h, w, comp)
+    x = structures_input(h, sts, device)
+    src = torch.randn(args.copy_mib * (1 << 20) // 4, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    del src, dst
+    out = m.compute(x, True)
+    for _ in range(args.steps):
+        m.compute(x, True, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"model": args.model, "steps": args.steps, "atoms": x.n_atoms, "edges": x.n_edges}), flush=True)
     return 0
 
 
