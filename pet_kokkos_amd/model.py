@@ -110,6 +110,13 @@ class PetModel:
         self._handle = handle
         self._lib = lib
 
+    @classmethod
+    def from_checkpoint(cls, json_path: str, safetensors_path: str) -> "PetModel":
+        """A converted reference checkpoint (pet_kokkos_amd.checkpoint)."""
+        from . import checkpoint
+        c = checkpoint.load(json_path, safetensors_path)
+        return cls(c.hypers, c.weights, c.composition, c.energy_scale)
+
     def __del__(self):
         if getattr(self, "_handle", None) and self._handle.value:
             self._lib.pet_model_destroy(self._handle)

@@ -120,3 +120,20 @@ def test_calculator(device):
     ref = oracle_of(h, w, comp, x)
     assert abs(r["energy"] - ref["energy"][0]) <= 1e-6 * abs(ref["energy"][0])
     assert np.abs(r["forces"] - ref["forces"]).max() <= 1e-5 * np.abs(ref["forces"]).max()
+
+
+def test_from_checkpoint(device, tmp_path):
+    """A model read from the converted-checkpoint files evaluates bit for bit
+    as one built from the same (float32-rounded) weights."""
+    from pet_kokkos_amd import checkpoint
+    h = weights.MODELS["tiny"]
+    w = weights.random_weights(h, 15)
+    comp = weights.random_composition(h)
+    jp, sp = checkpoint.save(str(tmp_path / "m"), h, w, comp, energy_scale=1.25)
+    x = structures_input(h, CASES["water-24"](), device)
+    a = PetModel.from_checkpoint(jp, sp).compute(x)
+    w32 = {k: v.astype(np.float32).astype(np.float64) for k, v in w.items()}
+    b = PetModel(h, w32, comp, energy_scale=1.25).compute(x)
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
