@@ -43,12 +43,14 @@ CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "attention_api_test.cpp")
 CPP_TEST = os.path.join(ROOT, "tests", "cpp", "attention_api_test")
 CPP_TEST2_SRC = os.path.join(ROOT, "tests", "cpp", "layer_forces_test.cpp")
 CPP_TEST2 = os.path.join(ROOT, "tests", "cpp", "layer_forces_test")
+CPP_TEST3_SRC = os.path.join(ROOT, "tests", "cpp", "model_test.cpp")
+CPP_TEST3 = os.path.join(ROOT, "tests", "cpp", "model_test")
 
 
 def build_cpp_test(verbose: bool = False) -> str:
-    """The C++ callers of include/pet/attention.hpp and include/pet/forces.hpp
-    that tests/test_gpu_cpp_api.py runs."""
-    for src, exe in ((CPP_TEST_SRC, CPP_TEST), (CPP_TEST2_SRC, CPP_TEST2)):
+    """The C++ callers of include/pet/attention.hpp, include/pet/forces.hpp and
+    include/pet/model.hpp that tests/test_gpu_cpp_api.py runs."""
+    for src, exe in ((CPP_TEST_SRC, CPP_TEST), (CPP_TEST2_SRC, CPP_TEST2), (CPP_TEST3_SRC, CPP_TEST3)):
         cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
                "-o", exe, src, "-L", HERE, "-lpet_attn", "-Wl,-rpath,$ORIGIN/../../pet_kokkos_amd"]
         if verbose:

@@ -1,0 +1,99 @@
+// Drives the whole PET evaluation through the C++ interface
+// (include/pet/model.hpp: PetModel, build_edges, Calculator) as a C++ caller
+// of the reference's would, for tests/test_gpu_cpp_api.py:
+//
+//   model_test DIR
+//
+// reads DIR/hypers.txt (d_pet d_node d_head heads gnn_layers attention_layers
+// n_species cutoff_function cutoff_width temperature energy_scale cutoff),
+// DIR/manifest.txt ("name rows cols" a tensor, cols 0 for a vector) with
+// DIR/weights.f64 (the tensors back to back), DIR/composition.f64,
+// DIR/s2i.txt (species_to_index) and DIR/system.txt (N, the cell's 9 numbers,
+// then "Z x y z" an atom). Writes DIR/result.f64 = [energy, per_atom (N),
+// forces (3N), virial (9)], DIR/repeat.ok when a second evaluation gives the
+// same bits, and DIR/fd.f64 = [central difference of the energy in atom 0's x
+// (step 1e-3 A, energy-only runs), the force's x].
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <string>
+#include <vector>
+
+#include "pet/model.hpp"
+
+static void fail(const std::string& what) {
+  std::fprintf(stderr, "model_test: %s\n", what.c_str());
+  std::exit(2);
+}
+
+int main(int argc, char** argv) {
+  if (argc != 2) fail("usage: model_test DIR");
+  const std::string dir = argv[1];
+  std::ifstream hf(dir + "/hypers.txt");
+  pet_model_hypers h{};
+  double cutoff = 0;
+  if (!(hf >> h.d_pet >> h.d_node >> h.d_head >> h.num_heads >> h.num_gnn_layers >> h.num_attention_layers >>
+        h.n_species >> h.cutoff_function >> h.cutoff_width >> h.attention_temperature >> h.energy_scale >> cutoff))
+    fail("hypers.txt");
+  std::ifstream mf(dir + "/manifest.txt");
+  FILE* wf = std::fopen((dir + "/weights.f64").c_str(), "rb");
+  if (!wf) fail("weights.f64");
+  std::map<std::string, pet::Tensor> w;
+  std::string name;
+  int rows = 0, cols = 0;
+  while (mf >> name >> rows >> cols) {
+    pet::Tensor t;
+    t.shape = cols ? std::vector<int64_t>{rows, cols} : std::vector<int64_t>{rows};
+    t.data.resize(size_t(rows) * (cols ? cols : 1));
+    if (std::fread(t.data.data(), sizeof(double), t.data.size(), wf) != t.data.size()) fail("weights.f64 short");
+    w[name] = std::move(t);
+  }
+  std::fclose(wf);
+  std::vector<double> comp(h.n_species);
+  FILE* cf = std::fopen((dir + "/composition.f64").c_str(), "rb");
+  if (!cf || std::fread(comp.data(), sizeof(double), comp.size(), cf) != comp.size()) fail("composition.f64");
+  std::fclose(cf);
+  std::ifstream sf(dir + "/s2i.txt");
+  std::vector<int> s2i;
+  for (int v; sf >> v;) s2i.push_back(v);
+  std::ifstream yf(dir + "/system.txt");
+  pet::System s;
+  int N = 0;
+  yf >> N;
+  for (auto& r : s.cell)
+    for (double& c : r) yf >> c;
+  s.positions.resize(N), s.numbers.resize(N);
+  for (int n = 0; n < N; ++n) yf >> s.numbers[n] >> s.positions[n][0] >> s.positions[n][1] >> s.positions[n][2];
+  if (!yf) fail("system.txt");
+
+  try {
+    pet::PetModel model(h, w, comp);
+    pet::Calculator calc(model, cutoff, s2i);
+    const pet::EnergyResult r = calc.compute(s, true);
+    std::vector<double> out{r.total};
+    out.insert(out.end(), r.per_atom.begin(), r.per_atom.end());
+    out.insert(out.end(), r.forces.begin(), r.forces.end());
+    out.insert(out.end(), r.virial, r.virial + 9);
+    FILE* of = std::fopen((dir + "/result.f64").c_str(), "wb");
+    std::fwrite(out.data(), sizeof(double), out.size(), of);
+    std::fclose(of);
+
+    const pet::EnergyResult r2 = calc.compute(s, true);
+    if (r2.total == r.total && std::memcmp(r2.forces.data(), r.forces.data(), sizeof(double) * r.forces.size()) == 0 &&
+        std::memcmp(r2.virial, r.virial, sizeof r.virial) == 0)
+      std::fclose(std::fopen((dir + "/repeat.ok").c_str(), "wb"));
+
+    const double step = 1e-3;
+    pet::System sp = s, sm = s;
+    sp.positions[0][0] += step, sm.positions[0][0] -= step;
+    const double ep = calc.compute(sp, false).total, em = calc.compute(sm, false).total;
+    const double fd[2] = {-(ep - em) / (2 * step), r.forces[0]};
+    FILE* ff = std::fopen((dir + "/fd.f64").c_str(), "wb");
+    std::fwrite(fd, sizeof(double), 2, ff);
+    std::fclose(ff);
+  } catch (const std::exception& e) {
+    fail(e.what());
+  }
+  return 0;
+}

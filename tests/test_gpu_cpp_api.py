@@ -99,3 +99,54 @@ def test_cpp_layer_and_forces_api(tmp_path):
     assert rel(rd("forces.f64", np.float64, (N, 3)), rf) <= RTOL
     assert rel(rd("vir9.f64", np.float64, (9,)), rv.sum(axis=0)) <= RTOL
     assert (tmp_path / "graph.ok").exists(), "pet::GraphCache: a captured or replayed run differed from the eager one"
+
+
+def test_cpp_model_calculator(tmp_path):
+    """pet::PetModel + pet::Calculator (include/pet/model.hpp) from C++: the
+    C++ host neighbour list, the model's energy / forces / virial against the
+    CPU oracle, a repeat bit for bit, and forces against a central difference
+    of the energy."""
+    from oracle import pet_model as om
+    from pet_kokkos_amd import weights
+    from pet_kokkos_amd.forces import CUTOFF_KINDS
+    from pet_kokkos_amd.model import species_index
+
+    if not os.path.exists(B.CPP_TEST3):
+        pytest.fail(f"{B.CPP_TEST3} is not built (python -m pet_kokkos_amd.build)")
+    h = weights.MODELS["tiny"]
+    w = weights.random_weights(h, 21)
+    comp = weights.random_composition(h)
+    s = systems.water_box(2, 6.2, seed=8)
+    N = len(s.positions)
+    with open(tmp_path / "hypers.txt", "w") as f:
+        f.write(f"{h.d_pet} {h.d_node} {h.d_head} {h.num_heads} {h.num_gnn_layers} {h.num_attention_layers} "
+                f"{h.n_species} {CUTOFF_KINDS[h.cutoff_function]} {h.cutoff_width} {h.attention_temperature} 1.0 "
+                f"{h.cutoff}\n")
+    with open(tmp_path / "manifest.txt", "w") as f, open(tmp_path / "weights.f64", "wb") as g:
+        for k, v in w.items():
+            f.write(f"{k} {v.shape[0]} {v.shape[1] if v.ndim == 2 else 0}\n")
+            np.ascontiguousarray(v, dtype=np.float64).tofile(g)
+    np.ascontiguousarray(comp, dtype=np.float64).tofile(tmp_path / "composition.f64")
+    s2i = [-1] * (max(h.atomic_types) + 1)
+    for i, z in enumerate(h.atomic_types):
+        s2i[z] = i
+    (tmp_path / "s2i.txt").write_text(" ".join(map(str, s2i)))
+    with open(tmp_path / "system.txt", "w") as f:
+        f.write(f"{N}\n" + " ".join(f"{c:.17g}" for c in s.cell.reshape(-1)) + "\n")
+        for z, p in zip(s.numbers, s.positions):
+            f.write(f"{int(z)} {p[0]:.17g} {p[1]:.17g} {p[2]:.17g}\n")
+    print("[gpu] C++ model water-24", flush=True)
+    res = subprocess.run([B.CPP_TEST3, str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    r = np.fromfile(tmp_path / "result.f64", dtype=np.float64)
+    energy, pa, forces, vir = r[0], r[1:1 + N], r[1 + N:1 + 4 * N].reshape(N, 3), r[1 + 4 * N:].reshape(3, 3)
+    pk = systems.packed_edges(N, systems.neighbor_list(s, h.cutoff), h.cutoff, h.cutoff_width)
+    rpa, eg = om.evaluate(h, w, species_index(s.numbers, h.atomic_types), pk, comp)
+    rf, rvir = om.fold_forces(N, pk, eg)
+    assert abs(energy - rpa.sum()) <= 1e-6 * abs(rpa.sum())
+    assert np.abs(pa - rpa).max() <= 1e-5 * np.abs(rpa).max()
+    assert np.abs(forces - rf).max() <= 1e-5 * np.abs(rf).max()
+    assert np.abs(vir - rvir.sum(0).reshape(3, 3)).max() <= 1e-5 * np.abs(rvir).sum(0).max()
+    assert os.path.exists(tmp_path / "repeat.ok")
+    fd, f0 = np.fromfile(tmp_path / "fd.f64", dtype=np.float64)
+    assert abs(fd - f0) <= 1e-2 + 1e-3 * abs(f0), (fd, f0)
