@@ -9,12 +9,15 @@
 //     grouped by centre, images in increasing shift order), with each edge's
 //     reverse and its cosine or bump cutoff factor;
 //   - Calculator::compute runs both for one structure: energy, forces and
-//     virial on the host, as the reference's compute() returns them.
+//     virial on the host, as the reference's compute() returns them; its
+//     set_neighbors / compute_step / compute_edges keep an MD engine's list on
+//     the device between steps.
 // Errors throw std::runtime_error with the C ABI's message.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <array>
 #include <cmath>
 #include <cstdint>
@@ -90,7 +93,7 @@ struct System {
 
 // A host neighbour list, packed: atom n's edges off[n] .. off[n+1]-1.
 struct HostEdges {
-  std::vector<int> off, center, neigh, reverse;
+  std::vector<int> off, center, neigh, reverse, shift;  // shift [E, 3]
   std::vector<double> vec, dist, pcut;  // [E, 3], [E], [E]
   std::vector<float> cut;
   int max_neighbors = 0;
@@ -157,6 +160,7 @@ inline HostEdges build_edges(const System& s, double cutoff, double width, int k
             index[Key{i, j, x, y, z}] = int(e.center.size());
             keys.push_back(Key{i, j, x, y, z});
             e.center.push_back(i), e.neigh.push_back(j);
+            e.shift.insert(e.shift.end(), {x, y, z});
             e.vec.insert(e.vec.end(), v, v + 3);
             e.dist.push_back(d), e.pcut.push_back(cutoff);
             e.cut.push_back(float(cutoff_factor(d, cutoff, width, kind)));
@@ -179,9 +183,27 @@ struct EnergyResult {
   double virial[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};  // sum v (x) dE/dv, row-major 3x3, eV
 };
 
-// One structure in, energy / forces / virial out (pet::Calculator::compute,
-// include/pet/calculator.hpp:187-239), for a fixed-cutoff model. Device
-// buffers are kept between calls and grown when a structure needs more.
+// An MD engine's full neighbour list (the reference's EdgeListView,
+// include/pet/device_geometry.hpp:93-110): atom i's neighbours are
+// neighbors[offsets[i] .. offsets[i+1]-1], each with an optional lattice shift
+// (cell rows); every atom is a centre and owned.
+struct EdgeListView {
+  int n_atoms = 0;
+  const double* positions = nullptr;  // [n_atoms, 3] A
+  const int* atomic_numbers = nullptr;
+  const int* offsets = nullptr;       // [n_atoms + 1]
+  const int* neighbors = nullptr;     // [offsets[n_atoms]]
+  const int* shifts = nullptr;        // [offsets[n_atoms], 3], optional
+  const double* cell = nullptr;       // [9], with shifts
+};
+
+// One structure in, energy / forces / virial out (pet::Calculator,
+// include/pet/calculator.hpp:187-239), for a fixed-cutoff model. compute()
+// builds the neighbour list on the host; set_neighbors() + compute_step() keep
+// an engine's list on the device and move only positions each step (pairs that
+// drift past the cutoff weigh nothing); compute_edges() is both at once. Edge
+// geometry is always made on the device (pet_edge_geometry). Device buffers
+// are kept between calls and grown when a structure needs more.
 class Calculator {
  public:
   Calculator(PetModel& model, double cutoff, std::vector<int> species_to_index, hipStream_t stream = nullptr)
@@ -195,45 +217,112 @@ class Calculator {
   EnergyResult compute(const System& s, bool forces = true) {
     const auto& h = model_.hypers();
     const HostEdges e = build_edges(s, cutoff_, h.cutoff_width, h.cutoff_function);
-    const int N = int(s.positions.size()), E = e.off[N];
-    std::vector<int> sp(N), nsp(E), soff{0, N};
+    const int N = int(s.positions.size());
+    std::vector<int> z(s.numbers), nb(e.neigh);
+    std::vector<double> pos(3 * size_t(N)), cell(9);
+    for (int n = 0; n < N; ++n)
+      for (int c = 0; c < 3; ++c) pos[3 * size_t(n) + c] = s.positions[n][c];
+    for (int r = 0; r < 3; ++r)
+      for (int c = 0; c < 3; ++c) cell[3 * r + c] = s.cell[r][c];
+    EdgeListView v;
+    v.n_atoms = N, v.positions = pos.data(), v.atomic_numbers = z.data(), v.offsets = e.off.data();
+    v.neighbors = nb.data(), v.shifts = e.shift.data(), v.cell = cell.data();
+    return compute_edges(v, forces);
+  }
+
+  // set_neighbors then compute_step (Calculator::compute_edges, include/pet/calculator.hpp:219-227).
+  EnergyResult compute_edges(const EdgeListView& v, bool forces = true, std::vector<double>* edge_gradient = nullptr) {
+    set_neighbors(v);
+    return compute_step(v.positions, v.cell, forces, edge_gradient);
+  }
+
+  // The list's topology to the device, once per rebuild (Calculator::set_neighbors).
+  void set_neighbors(const EdgeListView& v) {
+    const int N = v.n_atoms;
+    if (N < 0 || (N > 0 && (!v.atomic_numbers || !v.offsets))) throw std::runtime_error("pet: bad neighbour list");
+    const int E = N ? v.offsets[N] : 0;
+    if (E > 0 && !v.neighbors) throw std::runtime_error("pet: bad neighbour list");
+    std::vector<int> sp(N), nsp(E), center(E), rev(E, -1);
+    int maxc = 0;
     for (int n = 0; n < N; ++n) {
-      const int z = s.numbers[n];
+      const int z = v.atomic_numbers[n];
       sp[n] = z >= 0 && z < int(s2i_.size()) ? s2i_[z] : -1;
       if (sp[n] < 0) throw std::runtime_error("pet: atomic number " + std::to_string(z) + " not in the model");
+      if (v.offsets[n + 1] < v.offsets[n]) throw std::runtime_error("pet: offsets not increasing");
+      maxc = std::max(maxc, v.offsets[n + 1] - v.offsets[n]);
+      for (int k = v.offsets[n]; k < v.offsets[n + 1]; ++k) center[k] = n;
     }
-    for (int k = 0; k < E; ++k) nsp[k] = sp[e.neigh[k]];
-    pet_model_edges d{};
-    d.n_atoms = N, d.n_edges = E, d.max_neighbors = e.max_neighbors, d.n_struct = 1;
-    d.struct_off = up("soff", soff), d.species = up("sp", sp), d.off = up("off", e.off), d.center = up("c", e.center);
-    d.neigh_species = up("nsp", nsp), d.reverse = up("rev", e.reverse), d.vec = up("vec", e.vec);
-    d.dist = up("dist", e.dist), d.pcut = up("pcut", e.pcut), d.cut = up("cut", e.cut);
+    // each edge's reverse (j, i, -shift), by a hash of (i, j, shift)
+    struct Hash {
+      size_t operator()(const std::array<int, 5>& k) const {
+        size_t x = 1469598103934665603ull;
+        for (int t : k) x = (x ^ size_t(uint32_t(t))) * 1099511628211ull;
+        return x;
+      }
+    };
+    std::unordered_map<std::array<int, 5>, int, Hash> index;
+    auto key = [&](int k, int sign) {
+      const int* sh = v.shifts ? v.shifts + 3 * size_t(k) : nullptr;
+      return sign > 0 ? std::array<int, 5>{center[k], v.neighbors[k], sh ? sh[0] : 0, sh ? sh[1] : 0, sh ? sh[2] : 0}
+                      : std::array<int, 5>{v.neighbors[k], center[k], sh ? -sh[0] : 0, sh ? -sh[1] : 0,
+                                           sh ? -sh[2] : 0};
+    };
+    for (int k = 0; k < E; ++k) {
+      if (v.neighbors[k] < 0 || v.neighbors[k] >= N) throw std::runtime_error("pet: neighbour index out of range");
+      nsp[k] = sp[v.neighbors[k]];
+      index[key(k, 1)] = k;
+    }
+    for (int k = 0; k < E; ++k) {
+      auto it = index.find(key(k, -1));
+      rev[k] = it == index.end() ? -1 : it->second;
+    }
+    std::vector<int> soff{0, N}, off(v.offsets, v.offsets + N + 1), nb(v.neighbors, v.neighbors + E);
+    std::vector<int> sh(v.shifts ? v.shifts : nullptr, v.shifts ? v.shifts + 3 * size_t(E) : nullptr);
+    d_ = pet_model_edges{};
+    d_.n_atoms = N, d_.n_edges = E, d_.max_neighbors = maxc, d_.n_struct = 1;
+    d_.struct_off = up("soff", soff), d_.species = up("sp", sp), d_.off = up("off", off), d_.center = up("c", center);
+    d_.neigh_species = up("nsp", nsp), d_.reverse = up("rev", rev);
+    neigh_ = up("nb", nb), shift_ = v.shifts ? up("sh", sh) : nullptr;
+    d_.vec = buf<double>("vec", 3 * size_t(E)), d_.dist = buf<double>("dist", E), d_.pcut = buf<double>("pcut", E);
+    d_.cut = buf<float>("cut", E);
+    model_check(hipStreamSynchronize(stream_) == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH, "synchronize");
+    have_list_ = true;
+  }
+
+  // One step on the list set_neighbors holds, with the atoms' positions in its
+  // order (Calculator::compute_step, include/pet/calculator.hpp:228-230).
+  EnergyResult compute_step(const double* positions, const double* cell = nullptr, bool forces = true,
+                            std::vector<double>* edge_gradient = nullptr) {
+    if (!have_list_) throw std::runtime_error("pet: compute_step before set_neighbors");
+    if (shift_ && !cell) throw std::runtime_error("pet: the list has shifts, so compute_step needs the cell");
+    const auto& h = model_.hypers();
+    const int N = d_.n_atoms, E = d_.n_edges;
+    double* pos = buf<double>("pos", 3 * size_t(N));
+    double* dcell = buf<double>("cell", 9);
+    copy_in(pos, positions, 3 * size_t(N));
+    if (cell) copy_in(dcell, cell, 9);
+    model_check(pet_edge_geometry(E, d_.center, neigh_, shift_, pos, shift_ ? dcell : nullptr, cutoff_,
+                                  h.cutoff_width, h.cutoff_function, const_cast<double*>(d_.vec),
+                                  const_cast<double*>(d_.dist), const_cast<double*>(d_.pcut),
+                                  const_cast<float*>(d_.cut), stream_),
+                "edge geometry");
     DeviceOut o;
     o.energy = buf<double>("energy", 1), o.per_atom = buf<double>("per_atom", N);
     if (forces) o.forces = buf<double>("forces", 3 * size_t(N)), o.virial = buf<double>("virial", 9);
-    model_.compute(d, forces, o, stream_);
+    if (forces && edge_gradient) o.edge_grad = buf<double>("edge_grad", 3 * size_t(E));
+    model_.compute(d_, forces, o, stream_);
     EnergyResult r;
     r.per_atom.resize(N);
-    model_check(hipMemcpyAsync(&r.total, o.energy, sizeof(double), hipMemcpyDeviceToHost, stream_) == hipSuccess
-                    ? PET_ATTN_OK
-                    : PET_ATTN_ELAUNCH,
-                "copy");
-    model_check(hipMemcpyAsync(r.per_atom.data(), o.per_atom, sizeof(double) * N, hipMemcpyDeviceToHost, stream_) ==
-                        hipSuccess
-                    ? PET_ATTN_OK
-                    : PET_ATTN_ELAUNCH,
-                "copy");
+    copy_out(&r.total, o.energy, 1);
+    copy_out(r.per_atom.data(), o.per_atom, N);
     if (forces) {
       r.forces.resize(3 * size_t(N));
-      model_check(hipMemcpyAsync(r.forces.data(), o.forces, sizeof(double) * 3 * N, hipMemcpyDeviceToHost, stream_) ==
-                          hipSuccess
-                      ? PET_ATTN_OK
-                      : PET_ATTN_ELAUNCH,
-                  "copy");
-      model_check(hipMemcpyAsync(r.virial, o.virial, sizeof(double) * 9, hipMemcpyDeviceToHost, stream_) == hipSuccess
-                      ? PET_ATTN_OK
-                      : PET_ATTN_ELAUNCH,
-                  "copy");
+      copy_out(r.forces.data(), o.forces, 3 * size_t(N));
+      copy_out(r.virial, o.virial, 9);
+      if (edge_gradient) {
+        edge_gradient->resize(3 * size_t(E));
+        copy_out(edge_gradient->data(), o.edge_grad, 3 * size_t(E));
+      }
     }
     model_check(hipStreamSynchronize(stream_) == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH, "synchronize");
     return r;
@@ -258,13 +347,25 @@ class Calculator {
     return static_cast<T*>(b.p);
   }
   template <class T>
-  T* up(const std::string& k, const std::vector<T>& v) {
-    T* p = buf<T>(k, v.size());
-    if (!v.empty())
-      model_check(hipMemcpyAsync(p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, stream_) == hipSuccess
+  void copy_in(T* dst, const T* src, size_t n) {
+    if (n)
+      model_check(hipMemcpyAsync(dst, src, sizeof(T) * n, hipMemcpyHostToDevice, stream_) == hipSuccess
                       ? PET_ATTN_OK
                       : PET_ATTN_ELAUNCH,
                   "upload");
+  }
+  template <class T>
+  void copy_out(T* dst, const T* src, size_t n) {
+    if (n)
+      model_check(hipMemcpyAsync(dst, src, sizeof(T) * n, hipMemcpyDeviceToHost, stream_) == hipSuccess
+                      ? PET_ATTN_OK
+                      : PET_ATTN_ELAUNCH,
+                  "download");
+  }
+  template <class T>
+  T* up(const std::string& k, const std::vector<T>& v) {
+    T* p = buf<T>(k, v.size());
+    copy_in(p, v.data(), v.size());
     return p;
   }
 
@@ -273,6 +374,10 @@ class Calculator {
   std::vector<int> s2i_;
   hipStream_t stream_;
   std::map<std::string, Buf> bufs_;
+  pet_model_edges d_{};
+  const int* neigh_ = nullptr;
+  const int* shift_ = nullptr;
+  bool have_list_ = false;
 };
 
 }  // namespace pet

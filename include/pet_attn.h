@@ -296,6 +296,20 @@ PET_ATTN_API int pet_fold_edge_gradients(int n_atoms, int n_centres, const int* 
 PET_ATTN_API int pet_sum_by_structure(int n_struct, int width, const int* soff, const double* x, double* out,
                                       int accumulate, void* stream);
 
+/* Each edge's geometry from positions, for a neighbour list kept between steps:
+ * vec[e] = pos[neigh[e]] + shift[e] . cell - pos[center[e]] (cell [9] row-major,
+ * lattice vectors as rows; shift [E, 3] ints, NULL for none), dist[e] = |vec[e]|
+ * (1e30 for a coincident pair), pcut[e] = cutoff and cut[e] the smooth cutoff
+ * factor of dist (kind 0 bump, 1 cosine, 2 smooth; transcendentals in fp32 as the
+ * reference's CutT). positions [N, 3], cell, vec, dist, pcut fp64; cut fp32.
+ * Pairs past the cutoff get factor 0 and weigh nothing in the model.
+ * Replaces the per-step "nef_vectors" pass (reference src/device_geometry.cpp:
+ * 335-345) and the cutoff factor of edge_geometry (src/device_neighbors.cpp:214-260,
+ * include/pet/cutoff.hpp:17-40). */
+PET_ATTN_API int pet_edge_geometry(int n_edges, const int* center, const int* neigh, const int* shift,
+                                   const double* positions, const double* cell, double cutoff, double width, int kind,
+                                   double* vec, double* dist, double* pcut, float* cut, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

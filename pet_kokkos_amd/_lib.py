@@ -35,6 +35,7 @@ EXPORTS = (
     "pet_edge_grad",
     "pet_fold_edge_gradients",
     "pet_sum_by_structure",
+    "pet_edge_geometry",
     "pet_model_create",
     "pet_model_destroy",
     "pet_model_compute",
@@ -155,6 +156,8 @@ def load() -> ctypes.CDLL:
     lib.pet_fold_edge_gradients.argtypes = [_I, _I, _P, _P, _P, _P, _D, _P, _P, _P]
     lib.pet_sum_by_structure.restype = ctypes.c_int
     lib.pet_sum_by_structure.argtypes = [_I, _I, _P, _P, _P, _I, _P]
+    lib.pet_edge_geometry.restype = ctypes.c_int
+    lib.pet_edge_geometry.argtypes = [_I, _P, _P, _P, _P, _P, _D, _D, _I, _P, _P, _P, _P, _P]
     lib.pet_model_create.restype = ctypes.c_int
     lib.pet_model_create.argtypes = [ctypes.POINTER(ModelHypers), ctypes.POINTER(ModelTensor), _I, _P,
                                      ctypes.POINTER(_P)]

@@ -42,6 +42,53 @@ __device__ __forceinline__ double cutoff_ddist(double d, double rc, double w, in
   return kind == 0 ? bump_ddist(d, rc, w) : kind == 1 ? cosine_ddist(d, rc, w) : smooth_ddist(d, rc, w);
 }
 
+// The smooth cutoff factor of a distance (include/pet/cutoff.hpp:17-40): the
+// transcendentals in float (the reference's CutT), the rest in double.
+__device__ __forceinline__ double cutoff_value(double d, double rc, double w, int kind) {
+  if (kind == 0) {
+    const float x = float((d - (rc - w)) / w);
+    if (x <= 0.0f) return 1.0;
+    if (x >= 1.0f) return 0.0;
+    return 0.5 * (1.0 + double(tanhf(1.0f / tanf(float(kPi) * x))));
+  }
+  if (kind == 1) {
+    const float x = fminf(fmaxf(float((d - (rc - w)) / w), 0.0f), 1.0f);
+    return 0.5 * (1.0 + double(cosf(float(kPi) * x)));
+  }
+  const double x = fmin(fmax((d - (rc - w)) / w, 0.0), 1.0);
+  const double x4 = x * x * x * x;
+  return 1.0 - x4 * (35.0 - 84.0 * x + 70.0 * x * x - 20.0 * x * x * x);
+}
+
+// An edge list's vectors, lengths and cutoff factors from positions
+// (nef_vectors, src/device_geometry.cpp:335-345, then the factor of
+// src/device_neighbors.cpp:214-260): v = r_j + shift . cell - r_i, a
+// coincident pair's length 1e30 (it weighs nothing).
+__global__ void edge_geometry_kernel(int E, const int* __restrict__ center, const int* __restrict__ neigh,
+                                     const int* __restrict__ shift, const double* __restrict__ pos,
+                                     const double* __restrict__ cell, double cutoff, double width, int kind,
+                                     double* __restrict__ vec, double* __restrict__ dist, double* __restrict__ pcut,
+                                     float* __restrict__ cut) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int i = center[e], j = neigh[e];
+  const int s0 = shift ? shift[3 * e] : 0, s1 = shift ? shift[3 * e + 1] : 0, s2 = shift ? shift[3 * e + 2] : 0;
+  double d2 = 0.0;
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    const double sh = cell ? __dadd_rn(__dadd_rn(__dmul_rn(s0, cell[d]), __dmul_rn(s1, cell[3 + d])),
+                                       __dmul_rn(s2, cell[6 + d]))
+                           : 0.0;
+    const double x = __dsub_rn(__dadd_rn(pos[3 * j + d], sh), pos[3 * i + d]);
+    vec[3 * e + d] = x;
+    d2 = __dadd_rn(d2, __dmul_rn(x, x));
+  }
+  const double r = d2 > 1e-24 ? sqrt(d2) : 1e30;
+  dist[e] = r;
+  pcut[e] = cutoff;
+  cut[e] = float(cutoff_value(r, cutoff, width, kind));
+}
+
 __global__ void edge_grad_kernel(int nc, int E, const int* __restrict__ off, const int* __restrict__ center,
                                  const float* __restrict__ x4_adj, int64_t ldx, const float* __restrict__ cutoff_adj,
                                  const float* __restrict__ cf_seq_adj, int64_t ldca, const double* __restrict__ vec,
@@ -136,6 +183,18 @@ int pet_fold_edge_gradients(int n_atoms, int n_centres, const int* off, const in
   hipLaunchKernelGGL(fold_kernel, dim3(unsigned((n_atoms + 127) / 128)), dim3(128), 0,
                      reinterpret_cast<hipStream_t>(stream), n_atoms, n_centres, off, reverse, vec, grad, scale, forces,
                      virial_atom);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+int pet_edge_geometry(int n_edges, const int* center, const int* neigh, const int* shift, const double* positions,
+                      const double* cell, double cutoff, double width, int kind, double* vec, double* dist,
+                      double* pcut, float* cut, void* stream) {
+  if (n_edges < 0 || kind < 0 || kind > 2 || !(width > 0.0) || !(cutoff > 0.0)) return PET_ATTN_EINVAL;
+  if (n_edges == 0) return PET_ATTN_OK;
+  if (!center || !neigh || !positions || !vec || !dist || !pcut || !cut || (shift && !cell)) return PET_ATTN_EINVAL;
+  hipLaunchKernelGGL(edge_geometry_kernel, dim3(unsigned((n_edges + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), n_edges, center, neigh, shift, positions, cell, cutoff,
+                     width, kind, vec, dist, pcut, cut);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 

@@ -149,22 +149,75 @@ class PetModel:
 
 
 class Calculator:
-    """pet::Calculator::compute's shape (include/pet/calculator.hpp:187-239):
-    a structure in, energy (eV), forces [N, 3] (eV/A) and virial [3, 3] out,
-    on the host."""
+    """pet::Calculator's evaluation calls (include/pet/calculator.hpp:187-239):
+    compute() for a structure (host neighbour list), and for an MD engine that
+    keeps its own list, set_neighbors() once per rebuild then compute_step()
+    every step with new positions -- the list stays on the device and only
+    positions move; pairs that drift past the cutoff weigh nothing --, or
+    compute_edges() for both at once. Results on the host."""
 
     def __init__(self, model: PetModel, device="cuda:0"):
         self.model, self.device = model, device
+        self._x = None
 
     def compute(self, s: Structure, forces: bool = True):
-        x = structures_input(self.model.h, [s], self.device)
-        o = self.model.compute(x, forces)
+        e = neighbor_list(s, self.model.h.cutoff)
+        off = np.concatenate([[0], np.cumsum(np.bincount(e.centre, minlength=len(s.positions)))])
+        return self.compute_edges(s.numbers, off, e.neigh, e.shift, s.positions, s.cell, forces)
+
+    def set_neighbors(self, numbers, offsets, neighbors, shifts=None):
+        """An engine's full list: atom i's neighbours neighbors[offsets[i]:offsets[i+1]],
+        each with an optional integer lattice shift [E, 3]."""
+        h = self.model.h
+        offsets = np.asarray(offsets, dtype=np.int64)
+        N = len(offsets) - 1
+        E = int(offsets[-1])
+        neigh = np.asarray(neighbors, dtype=np.int64)[:E]
+        center = np.repeat(np.arange(N), np.diff(offsets))
+        sh = np.zeros((E, 3), dtype=np.int64) if shifts is None else np.asarray(shifts, dtype=np.int64).reshape(E, 3)
+        index = {(int(i), int(j), *map(int, t)): k for k, (i, j, t) in enumerate(zip(center, neigh, sh))}
+        rev = np.array([index.get((int(j), int(i), *map(int, -t)), -1) for i, j, t in zip(center, neigh, sh)],
+                       dtype=np.int32)
+        sp = species_index(numbers, h.atomic_types)
+        t = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt).to(self.device)
+        f64 = dict(dtype=torch.float64, device=self.device)
+        self._x = ModelInput(N, E, int(np.diff(offsets).max()) if N else 0, t(np.array([0, N]), torch.int32),
+                             t(sp, torch.int32), t(offsets, torch.int32), t(center, torch.int32),
+                             t(sp[neigh], torch.int32), t(rev, torch.int32), torch.empty(E, 3, **f64),
+                             torch.empty(E, **f64), torch.empty(E, **f64),
+                             torch.empty(E, dtype=torch.float32, device=self.device))
+        self._neigh = t(neigh, torch.int32)
+        self._shift = None if shifts is None else t(sh, torch.int32)
+        self._out = None
+
+    def compute_step(self, positions, cell=None, forces: bool = True, edge_gradients: bool = False):
+        x = self._x
+        if x is None:
+            raise RuntimeError("compute_step before set_neighbors")
+        if self._shift is not None and cell is None:
+            raise ValueError("the list has shifts, so compute_step needs the cell")
+        h = self.model.h
+        pos = torch.as_tensor(np.ascontiguousarray(positions, dtype=np.float64)).to(self.device)
+        dc = None if cell is None else torch.as_tensor(np.ascontiguousarray(cell, dtype=np.float64)).to(self.device)
+        p = lambda t: None if t is None or t.numel() == 0 else t.data_ptr()
+        _lib.check(_lib.load().pet_edge_geometry(x.n_edges, p(x.center), p(self._neigh), p(self._shift), p(pos),
+                                                 p(dc) if self._shift is not None else None, h.cutoff,
+                                                 h.cutoff_width, CUTOFF_KINDS[h.cutoff_function], p(x.vec),
+                                                 p(x.dist), p(x.pcut), p(x.cut), _stream()), "pet_edge_geometry")
+        o = self.model.compute(x, forces, edge_gradients)
         torch.cuda.synchronize()
         res = {"energy": float(o["energy"][0]), "per_atom": o["per_atom"].cpu().numpy()}
         if forces:
             res["forces"] = o["forces"].cpu().numpy()
             res["virial"] = o["virial"][0].cpu().numpy()
+            if edge_gradients:
+                res["edge_gradient"] = o["edge_grad"].cpu().numpy()
         return res
+
+    def compute_edges(self, numbers, offsets, neighbors, shifts, positions, cell=None, forces: bool = True,
+                      edge_gradients: bool = False):
+        self.set_neighbors(numbers, offsets, neighbors, shifts)
+        return self.compute_step(positions, cell, forces, edge_gradients)
 
 
 def ef_flops(h: Hypers, n_atoms: int, n_edges: int, sum_cnt2: float) -> dict:

@@ -137,3 +137,61 @@ def test_from_checkpoint(device, tmp_path):
     torch.cuda.synchronize()
     for k in a:
         assert torch.equal(a[k], b[k]), k
+
+
+def test_edge_geometry_kernel(device):
+    """pet_edge_geometry against numpy (vectors, lengths) and the oracle's
+    cutoff factor (fp32 transcendentals)."""
+    import oracle
+    from pet_kokkos_amd import _lib
+    from pet_kokkos_amd.forces import CUTOFF_KINDS
+    s = systems.water_box(2, 6.2, seed=9)
+    e = systems.neighbor_list(s, 5.0)
+    E = len(e.centre)
+    t = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt).to(device)
+    vec = torch.empty(E, 3, dtype=torch.float64, device=device)
+    dist, pcut = torch.empty(E, dtype=torch.float64, device=device), torch.empty(E, dtype=torch.float64, device=device)
+    cut = torch.empty(E, dtype=torch.float32, device=device)
+    c, nb, sh, pos, cell = (t(e.centre, torch.int32), t(e.neigh, torch.int32), t(e.shift, torch.int32),
+                            t(s.positions, torch.float64), t(s.cell.reshape(-1), torch.float64))
+    for kind in ("cosine", "bump", "smooth"):
+        _lib.check(_lib.load().pet_edge_geometry(E, c.data_ptr(), nb.data_ptr(), sh.data_ptr(), pos.data_ptr(),
+                                                 cell.data_ptr(), 4.5, 0.5, CUTOFF_KINDS[kind], vec.data_ptr(),
+                                                 dist.data_ptr(), pcut.data_ptr(), cut.data_ptr(), 0), "geometry")
+        torch.cuda.synchronize()
+        assert np.abs(vec.cpu().numpy() - e.vec).max() < 1e-12
+        assert np.abs(dist.cpu().numpy() - e.dist).max() < 1e-12
+        assert np.all(pcut.cpu().numpy() == 4.5)
+        ref, _ = oracle.cutoff(e.dist, 4.5, 0.5, CUTOFF_KINDS[kind])
+        got = cut.cpu().numpy().astype(np.float64)
+        assert np.abs(got - ref.astype(np.float32)).max() <= 2e-7, kind
+        assert np.any(got == 0.0) and np.any((got > 0) & (got < 1)), kind  # the list reaches past the cutoff
+
+
+def test_session_steps_match_fresh_evaluations(device):
+    """set_neighbors with a list 1 A past the cutoff, then compute_step on moved
+    atoms, against fresh evaluations with an exact-cutoff list."""
+    h = weights.MODELS["tiny"]
+    w = weights.random_weights(h, 16)
+    comp = weights.random_composition(h)
+    m = PetModel(h, w, comp)
+    s = systems.water_box(2, 6.2, seed=10)
+    e = systems.neighbor_list(s, h.cutoff + 1.0)
+    off = np.concatenate([[0], np.cumsum(np.bincount(e.centre, minlength=len(s.positions)))])
+    calc = Calculator(m, device)
+    calc.set_neighbors(s.numbers, off, e.neigh, e.shift)
+    rng = np.random.default_rng(0)
+    pos = s.positions.copy()
+    for step in range(3):
+        r = calc.compute_step(pos, s.cell, edge_gradients=True)
+        fresh = Calculator(m, device).compute(systems.Structure(pos.copy(), s.cell, s.numbers))
+        assert abs(r["energy"] - fresh["energy"]) <= 1e-6 * abs(fresh["energy"]), step
+        assert np.abs(r["forces"] - fresh["forces"]).max() <= 1e-5 * np.abs(fresh["forces"]).max(), step
+        assert np.abs(r["virial"] - fresh["virial"]).max() <= 1e-5 * np.abs(fresh["virial"]).max(), step
+        # forces are the fold of the edge gradients (F_i = sum_i's g - sum_into-i g)
+        g = r["edge_gradient"]
+        f = np.zeros_like(r["forces"])
+        np.add.at(f, np.repeat(np.arange(len(pos)), np.diff(off)), g)
+        np.add.at(f, e.neigh, -g)
+        assert np.abs(f - r["forces"]).max() <= 1e-9 * np.abs(f).max()
+        pos = pos + rng.normal(0.0, 0.05, pos.shape)
