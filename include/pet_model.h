@@ -1,9 +1,11 @@
 /* pet_model.h -- the whole PET energy / forces evaluation on gfx950 over a C ABI.
  *
  * The caller of the attention path: peterspackman/pet-kokkos's PetModel with
- * the feedforward featurizer (PreLN, RMSNorm, SwiGLU, d_node != d_pet), its
- * forward pass ff_pass / ff_layer and analytic backward ff_layer_bwd
- * (src/feedforward.cpp:34-411), the readout and energy assembly
+ * either featurizer it implements -- feedforward (PreLN, RMSNorm, SwiGLU,
+ * d_node != d_pet: ff_pass / ff_layer / ff_layer_bwd, src/feedforward.cpp:34-411)
+ * or residual (PostLN, LayerNorm, SiLU, d_node == d_pet, a readout after every
+ * GNN layer: residual_pass / residual_layer, src/residual.cpp:13-251) -- with
+ * its analytic backward, the readout and energy assembly
  * (src/model.cpp:656-780, src/ops.cpp:406-425) and forces_and_virial
  * (src/forces.cpp:345-386) for a fixed cutoff. Every kernel is this library's
  * (the attention, norms, activations, gathers, folds); the dense layers go to
@@ -47,6 +49,7 @@ typedef struct pet_model_hypers {
   double cutoff_width;       /* the smooth cutoff's width */
   double attention_temperature;
   double energy_scale;       /* per-atom energy = energy_scale * net + composition[species] */
+  int featurizer;            /* 0 feedforward, 1 residual (pet::FeaturizerType) */
 } pet_model_hypers;
 
 /* One checkpoint tensor, row-major float64 on the host: cols = 0 for a vector. */
@@ -60,7 +63,8 @@ typedef struct pet_model pet_model;
 
 /* Replaces PetModel::PetModel / load_all (src/model.cpp:61-112, :180-344):
  * uploads, folds compress.0 into its geometry matrix, bias, species table and
- * input_edge block, and interleaves each SwiGLU w_in to (v_j, g_j) rows.
+ * input_edge block, and (feedforward) interleaves each SwiGLU w_in to (v_j, g_j)
+ * rows. The tensors a featurizer needs are those load_all reads for it.
  * composition [n_species] (may be null: zeros). Uses the current device. */
 PET_ATTN_API int pet_model_create(const pet_model_hypers* hypers, const pet_model_tensor* tensors, int n_tensors,
                                   const double* composition, pet_model** out);

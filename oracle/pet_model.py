@@ -2,7 +2,7 @@
 (energy, and by autograd the edge gradients that forces and virial fold from).
 
 A restatement in torch (CPU, float64 by default) of the reference's
-feedforward-featurizer pass, written from the weights as the checkpoint stores
+feedforward- and residual-featurizer passes, written from the weights as the checkpoint stores
 them: compress.0 unfolded (the reference folds its constant blocks at load,
 src/model.cpp:236-262) and each SwiGLU w_in in metatrain's [value | gate] row
 order (the reference interleaves them at load, :211-222). So the fold and the
@@ -13,6 +13,9 @@ has no CPU path.
 What each part follows (file:line in the reference tree):
   pass          PetModel::ff_pass            src/feedforward.cpp:338-411
   GNN layer     PetModel::ff_layer           src/feedforward.cpp:34-198
+  residual      residual_pass / residual_layer  src/residual.cpp:13-133 (PostLN,
+                LayerNorm, SiLU MLP, a readout after every layer, message
+                passing input_edge = (input_edge + out_edge(reverse)) / 2)
   compress      compress_fwd + compress.2    src/ops.cpp:326-371, src/feedforward.cpp:64-66
   attention     softmax(sc q.k + log cf)     src/attention.cpp:205-266 (sc :1525)
   norms         norm_rows                    src/ops.hpp:376-407, eps :195-196
@@ -23,13 +26,12 @@ What each part follows (file:line in the reference tree):
   cutoff        cosine / bump / smooth       include/pet/cutoff.hpp:17-35
 
 Pins (tests/test_oracle_model.py): the attention against the pinned C oracle,
-the norms against torch's, edge gradients against central differences of the
-energy, rotation/translation/permutation invariance, the additivity of two
-structures far apart, and the fold and interleave against a direct evaluation
-of the folded form. The model's forward composition itself (which layer feeds
-which) has no golden vector here -- the reference's golden files need
-published weights that are absent -- so its parity to the reference is
-"parity unpinned" beyond these structural checks.
+the norms against torch's, edge gradients and forces against central
+differences of the energy, permutation and translation invariance, supercell
+extensivity, fp32 against fp64; for both featurizers. The model's forward
+composition itself (which layer feeds which) has no golden vector here -- the
+reference's golden files need published weights that are absent -- so its
+parity to the reference is "parity unpinned" beyond these structural checks.
 """
 from __future__ import annotations
 
@@ -150,14 +152,51 @@ def evaluate(h, weights: dict, species: np.ndarray, pk, composition=None, energy
     x4 = torch.cat([v, dist[:, None]], 1)
     scale = 1.0 / (math.sqrt(h.head_dim) * h.attention_temperature)
 
-    node = w["node_embedders.0.weight"][sp]
-    input_edge = w["edge_embedder.weight"][nsp]
-    for L in range(G):
+    center = torch.as_tensor(pk.center[:E], dtype=torch.int64)
+
+    def head(x, side, i):
+        k = f"{side}_heads.energy.{i}"
+        y = silu(linear(silu(linear(x, w[k + ".0.weight"], w[k + ".0.bias"])), w[k + ".2.weight"], w[k + ".2.bias"]))
+        last = f"{side}_last_layers.energy.{i}.energy___0"
+        return linear(y, w[last + ".weight"], w[last + ".bias"])[:, 0]
+
+    def readout(node_feat, edge_feat, i):
+        """net of read-out i, in double (readout_accumulate, src/ops.cpp:406-418)."""
+        return head(node_feat, "node", i).to(torch.float64).index_add(
+            0, center, (cut * head(edge_feat, "edge", i)).to(torch.float64))
+
+    def compress(L, input_edge):
         g = f"gnn_layers.{L}"
         edge_emb = linear(x4, w[g + ".edge_embedder.weight"], w[g + ".edge_embedder.bias"])
         blocks = [edge_emb, input_edge] if L == 0 else [edge_emb, w[g + ".neighbor_embedder.weight"][nsp], input_edge]
         cpre = silu(linear(torch.cat(blocks, 1), w[g + ".compress.0.weight"], w[g + ".compress.0.bias"]))
-        edge_cur = linear(cpre, w[g + ".compress.2.weight"], w[g + ".compress.2.bias"])
+        return linear(cpre, w[g + ".compress.2.weight"], w[g + ".compress.2.bias"])
+
+    input_edge = w["edge_embedder.weight"][nsp]
+    if getattr(h, "residual", False):
+        net = torch.zeros(N, dtype=torch.float64)
+        for L in range(G):
+            g = f"gnn_layers.{L}"
+            tokens = torch.cat([w[f"node_embedders.{L}.weight"][sp], compress(L, input_edge)], 0)
+            for a in range(A):
+                t = f"{g}.trans.layers.{a}"
+                qkv = linear(tokens, w[t + ".attention.input_linear.weight"], w[t + ".attention.input_linear.bias"])
+                s1 = linear(attention(qkv, cf_seq, tix, h.num_heads, scale), w[t + ".attention.output_linear.weight"],
+                            w[t + ".attention.output_linear.bias"]) + tokens
+                tok_a = norm(s1, w[t + ".norm_attention.weight"], w[t + ".norm_attention.bias"])
+                hmid = silu(linear(tok_a, w[t + ".mlp.w_in.weight"], w[t + ".mlp.w_in.bias"]))
+                s2 = linear(hmid, w[t + ".mlp.w_out.weight"], w[t + ".mlp.w_out.bias"]) + tok_a
+                tokens = norm(s2, w[t + ".norm_mlp.weight"], w[t + ".norm_mlp.bias"])
+            net = net + readout(tokens[:N], tokens[N:], L)
+            if L + 1 < G:
+                back = torch.where((rev >= 0)[:, None], tokens[N:][rev.clamp(min=0)], torch.zeros_like(tokens[N:]))
+                input_edge = 0.5 * (input_edge + back)
+        return _finish(net, sp, h, composition, energy_scale, grad, v)
+
+    node = w["node_embedders.0.weight"][sp]
+    for L in range(G):
+        g = f"gnn_layers.{L}"
+        edge_cur = compress(L, input_edge)
         node_cur = node
         for a in range(A):
             t = f"{g}.trans.layers.{a}"
@@ -179,16 +218,10 @@ def evaluate(h, weights: dict, species: np.ndarray, pk, composition=None, energy
                       w[f"combination_mlps.{L}.2.weight"], w[f"combination_mlps.{L}.2.bias"])
         input_edge = input_edge + edge_cur + comb
 
-    def head(x, side, Dname):
-        k = f"{side}_heads.energy.0"
-        y = silu(linear(silu(linear(x, w[k + ".0.weight"], w[k + ".0.bias"])), w[k + ".2.weight"], w[k + ".2.bias"]))
-        last = f"{side}_last_layers.energy.0.energy___0"
-        return linear(y, w[last + ".weight"], w[last + ".bias"])[:, 0]
+    return _finish(readout(node, input_edge, 0), sp, h, composition, energy_scale, grad, v)
 
-    node_pred = head(node, "node", "Dn")
-    edge_pred = head(input_edge, "edge", "D")
-    center = torch.as_tensor(pk.center[:E], dtype=torch.int64)
-    net = node_pred.to(torch.float64).index_add(0, center, (cut * edge_pred).to(torch.float64))
+
+def _finish(net, sp, h, composition, energy_scale, grad, v):
     comp = torch.zeros(h.n_species, dtype=torch.float64) if composition is None else \
         torch.as_tensor(composition, dtype=torch.float64)
     per_atom = energy_scale * net + comp[sp]

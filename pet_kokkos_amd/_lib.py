@@ -62,7 +62,8 @@ class ModelHypers(ctypes.Structure):
     """pet_model_hypers (include/pet_model.h)."""
     _fields_ = [(n, ctypes.c_int) for n in ("d_pet", "d_node", "d_head", "num_heads", "num_gnn_layers",
                                              "num_attention_layers", "n_species", "cutoff_function")] + \
-               [(n, ctypes.c_double) for n in ("cutoff_width", "attention_temperature", "energy_scale")]
+               [(n, ctypes.c_double) for n in ("cutoff_width", "attention_temperature", "energy_scale")] + \
+               [("featurizer", ctypes.c_int)]
 
 
 class ModelTensor(ctypes.Structure):

@@ -1,4 +1,4 @@
-"""The reference's converted checkpoint: <model>.json (hyperparameters, the
+"""The reference's converted checkpoint, for either featurizer: <model>.json (hyperparameters, the
 species map, composition energies, energy scale) and <model>.safetensors (the
 weights under metatrain's names), as peterspackman/pet-kokkos's
 tools/convert_pet.py:341-420 writes them and src/checkpoint.cpp:12-141 reads
@@ -39,12 +39,21 @@ def load(json_path: str, safetensors_path: str) -> Checkpoint:
     with open(json_path) as f:
         j = json.load(f)
     h = j["hypers"]
-    if h.get("featurizer_type") != "feedforward":
-        _refuse(f"featurizer_type {h.get('featurizer_type')!r} (only 'feedforward')")
-    if h.get("normalization") != "RMSNorm" or h.get("activation") != "SwiGLU" or h.get("transformer_type") != "PreLN":
-        _refuse("a feedforward featurizer other than PreLN + RMSNorm + SwiGLU")
-    if int(h["d_node"]) == int(h["d_pet"]):
-        _refuse("the feedforward featurizer without an expanded central token (d_node == d_pet)")
+    feat = h.get("featurizer_type")
+    if feat == "feedforward":
+        if h.get("normalization") != "RMSNorm" or h.get("activation") != "SwiGLU" or \
+                h.get("transformer_type") != "PreLN":
+            _refuse("a feedforward featurizer other than PreLN + RMSNorm + SwiGLU")
+        if int(h["d_node"]) == int(h["d_pet"]):
+            _refuse("the feedforward featurizer without an expanded central token (d_node == d_pet)")
+    elif feat == "residual":
+        if h.get("normalization") != "LayerNorm" or h.get("activation") != "SiLU" or \
+                h.get("transformer_type") != "PostLN":
+            _refuse("a residual featurizer other than PostLN + LayerNorm + SiLU")
+        if int(h["d_node"]) != int(h["d_pet"]):
+            _refuse("the residual featurizer with an expanded central token (d_node != d_pet)")
+    else:
+        _refuse(f"featurizer_type {feat!r}")
     if h.get("num_neighbors_adaptive") is not None:
         _refuse("the adaptive cutoff")
     for flag in ("zbl", "long_range_enabled", "system_conditioning"):
@@ -54,8 +63,9 @@ def load(json_path: str, safetensors_path: str) -> Checkpoint:
         pass  # extra heads; the energy path ignores them
     if h.get("cutoff_function") not in CUTOFF_NAMES:
         _refuse(f"cutoff_function {h.get('cutoff_function')!r}")
-    if int(h.get("num_readout_layers", 1)) != 1:
-        _refuse("num_readout_layers != 1")
+    readouts = int(h["num_gnn_layers"]) if feat == "residual" else 1
+    if int(h.get("num_readout_layers", readouts)) != readouts:
+        _refuse(f"num_readout_layers != {readouts} for the {feat} featurizer")
     s2i = [int(x) for x in j["species_to_index"]]
     n_species = int(j["n_species"])
     types = [0] * n_species
@@ -67,7 +77,8 @@ def load(json_path: str, safetensors_path: str) -> Checkpoint:
                 num_gnn_layers=int(h["num_gnn_layers"]), num_attention_layers=int(h["num_attention_layers"]),
                 cutoff=float(h["cutoff"]), cutoff_width=float(h["cutoff_width"]),
                 cutoff_function=CUTOFF_NAMES[h["cutoff_function"]],
-                attention_temperature=float(h.get("attention_temperature", 1.0)), atomic_types=tuple(types))
+                attention_temperature=float(h.get("attention_temperature", 1.0)), atomic_types=tuple(types),
+                featurizer=feat)
     if int(h.get("head_dim", hy.head_dim)) != hy.head_dim:
         raise ValueError("checkpoint: head_dim != d_pet / num_heads")
     w = {k: np.asarray(v, dtype=np.float64) for k, v in load_file(safetensors_path).items()}
@@ -88,8 +99,10 @@ def save(prefix: str, h: Hypers, weights: dict, composition, energy_scale: float
         "hypers": {"d_pet": h.d_pet, "d_head": h.d_head, "d_node": h.d_node, "d_feedforward": h.d_feedforward,
                    "num_heads": h.num_heads, "head_dim": h.head_dim,
                    "num_attention_layers": h.num_attention_layers, "num_gnn_layers": h.num_gnn_layers,
-                   "num_readout_layers": 1, "normalization": "RMSNorm", "activation": "SwiGLU",
-                   "transformer_type": "PreLN", "featurizer_type": "feedforward",
+                   "num_readout_layers": h.num_gnn_layers if h.residual else 1,
+                   "normalization": "LayerNorm" if h.residual else "RMSNorm",
+                   "activation": "SiLU" if h.residual else "SwiGLU",
+                   "transformer_type": "PostLN" if h.residual else "PreLN", "featurizer_type": h.featurizer,
                    "attention_temperature": h.attention_temperature, "cutoff": h.cutoff,
                    "cutoff_width": h.cutoff_width, "cutoff_function": inv[h.cutoff_function],
                    "num_neighbors_adaptive": None, "adaptive_cutoff_method": "grid",

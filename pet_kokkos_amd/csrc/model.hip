@@ -14,11 +14,13 @@
 // into the pass that produces their operands.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "../../include/pet_model.h"
@@ -200,33 +202,76 @@ __global__ void concat_bwd_kernel(float* __restrict__ edge_adj, const float* __r
   }
 }
 
-// net[n] = node_pred[n] + sum over n's edges of cut * edge_pred, in double and
-// in edge order (readout_accumulate, src/ops.cpp:406-418); then per_atom =
-// scale * net + composition[species] (assemble_energy, :420-425).
-__global__ void readout_kernel(double* __restrict__ per_atom, const float* __restrict__ node_pred,
+// net[n] (=, or += for acc, in fp32) node_pred[n] + the sum over n's edges
+// of cut * edge_pred, in double and in edge order (readout_accumulate,
+// src/ops.cpp:406-418).
+__global__ void readout_kernel(float* __restrict__ net, const float* __restrict__ node_pred,
                                const float* __restrict__ edge_pred, const int* __restrict__ off,
-                               const float* __restrict__ cut, const int* __restrict__ species,
-                               const double* __restrict__ comp, double scale, int N) {
+                               const float* __restrict__ cut, int acc, int N) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= N) return;
   double s = node_pred[n];
   for (int k = off[n]; k < off[n + 1]; ++k) s += double(cut[k]) * double(edge_pred[k]);
-  const float net = float(s);
-  per_atom[n] = scale * double(net) + comp[species[n]];
+  net[n] = acc ? float(double(net[n]) + s) : float(s);
+}
+
+// per_atom = scale * net + composition[species] (assemble_energy, src/ops.cpp:420-425)
+__global__ void assemble_kernel(double* __restrict__ per_atom, const float* __restrict__ net,
+                                const int* __restrict__ species, const double* __restrict__ comp, double scale,
+                                int N) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n < N) per_atom[n] = scale * double(net[n]) + comp[species[n]];
 }
 
 // The readout's adjoint seeds (readout_bwd, src/model.cpp:749-767): node_pred's
-// is 1, edge_pred's the edge's cutoff factor, and cutoff_adj = edge_pred.
+// is 1, edge_pred's the edge's cutoff factor, and cutoff_adj (+)= edge_pred.
 __global__ void readout_seed_kernel(float* __restrict__ npa, float* __restrict__ epa, float* __restrict__ cutoff_adj,
-                                    const float* __restrict__ cut, const float* __restrict__ epred, int N, int E) {
+                                    const float* __restrict__ cut, const float* __restrict__ epred, int acc, int N,
+                                    int E) {
   GRID_LOOP(i, int64_t(N) + E) {
     if (i < N) {
       npa[i] = 1.0f;
     } else {
       const int64_t k = i - N;
       epa[k] = cut[k];
-      cutoff_adj[k] = epred[k];
+      cutoff_adj[k] = acc ? cutoff_adj[k] + epred[k] : epred[k];
     }
+  }
+}
+
+// out = a + b per row
+__global__ void bias_add_kernel(float* __restrict__ out, const float* __restrict__ a, const float* __restrict__ b,
+                                int64_t R, int W) {
+  GRID_LOOP(i, R * W) out[i] = a[i] + b[i % W];
+}
+
+__global__ void copy_kernel(float* __restrict__ out, const float* __restrict__ a, int64_t n) {
+  GRID_LOOP(i, n) out[i] = a[i];
+}
+
+// out = s * a
+__global__ void scale_kernel(float* __restrict__ out, const float* __restrict__ a, float s, int64_t n) {
+  GRID_LOOP(i, n) out[i] = s * a[i];
+}
+
+// The residual featurizer's message passing (src/residual.cpp:122-131):
+// input_edge[k] = 0.5 (input_edge[k] + out_edge[reverse k]), 0 for no reverse.
+__global__ void message_kernel(float* __restrict__ ie, const float* __restrict__ oe, const int* __restrict__ rev,
+                               int64_t E, int D) {
+  GRID_LOOP(i, E * D) {
+    const int64_t k = i / D;
+    const int d = int(i - k * D), r = rev[k];
+    ie[i] = 0.5f * (ie[i] + (r >= 0 ? oe[int64_t(r) * D + d] : 0.0f));
+  }
+}
+
+// Its backward's reverse share (src/residual.cpp:183-190): efa[k] += 0.5 ie_adj[reverse k].
+__global__ void message_bwd_kernel(float* __restrict__ efa, const float* __restrict__ ie_adj,
+                                   const int* __restrict__ rev, int64_t E, int D) {
+  GRID_LOOP(i, E * D) {
+    const int64_t k = i / D;
+    const int d = int(i - k * D), r = rev[k];
+    efa[i] += r >= 0 ? 0.5f * ie_adj[int64_t(r) * D + d] : 0.0f;
   }
 }
 
@@ -427,24 +472,11 @@ struct Pass {
 
   // One GNN layer forward (ff_layer, src/feedforward.cpp:34-198, every save kept).
   void layer_fwd(int L, float*& node, float* input_edge, Layer& sv) {
-    const std::string c0 = g(L) + ".compress.0";
     sv.cpre = md.f(int64_t(E) * D);
     sv.b.resize(A);
     for (int a = 0; a < A; ++a) sv.b[a].tok = md.f(int64_t(T) * D);
     float* out_edge = md.f(int64_t(E) * D);
-    {
-      auto scope = md.ws.mark();
-      float* cact = md.f(int64_t(E) * D);
-      if (L > 0) ok(gemm_nt(cact, D, input_edge, D, md.p(c0 + "@in"), E, D, D, 0.0f, st));
-      if (E) {
-        hipLaunchKernelGGL(compress_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, sv.cpre, cact, L > 0 ? 1 : 0,
-                           md.p(c0 + "@b"), md.p(c0 + "@tab"), e.neigh_species, md.p(c0 + "@x4"), e.vec, e.dist,
-                           int64_t(E), D);
-        launched();
-      }
-      linear(md, sv.b[0].tok + int64_t(N) * D, cact, E, D, g(L) + ".compress.2", st);
-      md.ws.release(scope);
-    }
+    compress_fwd(L, input_edge, sv.cpre, sv.b[0].tok + int64_t(N) * D);
     float* node_cur = node;
     const float* edge_cur = sv.b[0].tok + int64_t(N) * D;
     for (int a = 0; a < A; ++a) {
@@ -581,11 +613,91 @@ struct Pass {
       md.ws.release(s2);
     }
     // edge_adj is et's: back through compress.2 and compress.0's fold
+    compress_bwd(L, edge_adj, sv.cpre, x4_adj, ie_adj);
+    md.ws.release(scope);
+  }
+
+  // One read-out (src/model.cpp:656-691): two SiLU layers and a last linear a
+  // side, from node rows (width Dn) and edge rows (width D); net (fp32) = its
+  // node prediction + sum of cut * edge predictions, or += for acc
+  // (readout_accumulate, src/ops.cpp:406-418). Keeps the pre-activations.
+  struct Readout {
+    float *nh0, *nh1, *eh0, *eh1, *npred, *epred;
+  };
+  Readout readout_fwd(int i, const float* node_rows, const float* edge_rows, float* net, bool acc) {
+    const std::string si = std::to_string(i), nh = "node_heads.energy." + si, eh = "edge_heads.energy." + si;
+    Readout r{md.f(int64_t(N) * Dh), md.f(int64_t(N) * Dh), md.f(int64_t(E) * Dh), md.f(int64_t(E) * Dh), md.f(N),
+              md.f(E)};
+    auto scope = md.ws.mark();
+    float* x = md.f(std::max<int64_t>(int64_t(N), int64_t(E)) * Dh);
+    linear_pre(md, r.nh0, node_rows, N, Dn, nh + ".0", st);
+    silu(md, x, r.nh0, N, nh + ".0", st);
+    linear_pre(md, r.nh1, x, N, Dh, nh + ".2", st);
+    silu(md, x, r.nh1, N, nh + ".2", st);
+    linear(md, r.npred, x, N, Dh, "node_last_layers.energy." + si + ".energy___0", st);
+    linear_pre(md, r.eh0, edge_rows, E, D, eh + ".0", st);
+    silu(md, x, r.eh0, E, eh + ".0", st);
+    linear_pre(md, r.eh1, x, E, Dh, eh + ".2", st);
+    silu(md, x, r.eh1, E, eh + ".2", st);
+    linear(md, r.epred, x, E, Dh, "edge_last_layers.energy." + si + ".energy___0", st);
+    md.ws.release(scope);
+    if (N) {
+      hipLaunchKernelGGL(readout_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st, net, r.npred, r.epred,
+                         e.off, e.cut, acc ? 1 : 0, N);
+      launched();
+    }
+    return r;
+  }
+  // Its backward (readout_bwd, src/model.cpp:749-780): node_adj [N, Dn] and
+  // edge_adj [E, D] written, cutoff_adj written (or added to, acc).
+  void readout_bwd(int i, const Readout& r, float* node_adj, float* edge_adj, float* cutoff_adj, bool acc) {
+    const std::string si = std::to_string(i), nh = "node_heads.energy." + si, eh = "edge_heads.energy." + si;
+    auto scope = md.ws.mark();
+    float *npa = md.f(N), *epa = md.f(E), *a1 = md.f(std::max<int64_t>(N, E) * Dh),
+          *a0 = md.f(std::max<int64_t>(N, E) * Dh);
+    if (N + E) {
+      hipLaunchKernelGGL(readout_seed_kernel, grid_for(int64_t(N) + E), dim3(256), 0, st, npa, epa, cutoff_adj,
+                         e.cut, r.epred, acc ? 1 : 0, N, E);
+      launched();
+    }
+    linear_bwd(md, a1, npa, N, "node_last_layers.energy." + si + ".energy___0", 0.0f, st);
+    silu_bwd(md, a1, r.nh1, N, nh + ".2", st);
+    linear_bwd(md, a0, a1, N, nh + ".2", 0.0f, st);
+    silu_bwd(md, a0, r.nh0, N, nh + ".0", st);
+    linear_bwd(md, node_adj, a0, N, nh + ".0", 0.0f, st);
+    linear_bwd(md, a1, epa, E, "edge_last_layers.energy." + si + ".energy___0", 0.0f, st);
+    silu_bwd(md, a1, r.eh1, E, eh + ".2", st);
+    linear_bwd(md, a0, a1, E, eh + ".2", 0.0f, st);
+    silu_bwd(md, a0, r.eh0, E, eh + ".0", st);
+    linear_bwd(md, edge_adj, a0, E, eh + ".0", 0.0f, st);
+    md.ws.release(scope);
+  }
+
+  // compress.0 (folded) and compress.2 of layer L into et [E, D] (ld D); the
+  // pre-activation kept in cpre.
+  void compress_fwd(int L, const float* input_edge, float* cpre, float* et) {
     const std::string c0 = g(L) + ".compress.0";
-    float* ga = md.f(int64_t(E) * D);
-    linear_bwd(md, ga, edge_adj, E, g(L) + ".compress.2", 0.0f, st);
+    auto scope = md.ws.mark();
+    float* cact = md.f(int64_t(E) * D);
+    if (L > 0) ok(gemm_nt(cact, D, input_edge, D, md.p(c0 + "@in"), E, D, D, 0.0f, st));
     if (E) {
-      hipLaunchKernelGGL(compress_bwd_kernel, dim3(unsigned((E + 3) / 4)), dim3(256), 0, st, ga, sv.cpre,
+      hipLaunchKernelGGL(compress_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, cpre, cact, L > 0 ? 1 : 0,
+                         md.p(c0 + "@b"), md.p(c0 + "@tab"), e.neigh_species, md.p(c0 + "@x4"), e.vec, e.dist,
+                         int64_t(E), D);
+      launched();
+    }
+    linear(md, et, cact, E, D, g(L) + ".compress.2", st);
+    md.ws.release(scope);
+  }
+  // Its backward from et_adj (compress_bwd, src/ops.cpp:373-404): x4_adj +=,
+  // and past layer 0 ie_adj += the input_edge block's share.
+  void compress_bwd(int L, const float* et_adj, const float* cpre, float* x4_adj, float* ie_adj) {
+    const std::string c0 = g(L) + ".compress.0";
+    auto scope = md.ws.mark();
+    float* ga = md.f(int64_t(E) * D);
+    linear_bwd(md, ga, et_adj, E, g(L) + ".compress.2", 0.0f, st);
+    if (E) {
+      hipLaunchKernelGGL(compress_bwd_kernel, dim3(unsigned((E + 3) / 4)), dim3(256), 0, st, ga, cpre,
                          md.p(c0 + "@x4"), x4_adj, E, D);
       launched();
     }
@@ -593,82 +705,180 @@ struct Pass {
     md.ws.release(scope);
   }
 
+  // What one residual GNN layer keeps (the reference's ResidualSaves, every
+  // wide activation kept): per block qkv, merged, ml, s1 = attention + tokens,
+  // s2 = mlp + LayerNorm(s1), and the MLP's pre-activation.
+  struct RBlock {
+    float *qkv, *merged, *ml, *s1, *s2, *pre;
+  };
+  struct RLayer {
+    float *tokens, *cpre;
+    std::vector<RBlock> b;
+    Readout ro;
+  };
+
+  // residual_layer (src/residual.cpp:13-60): tokens = [node_L ; et], then A
+  // PostLN blocks tokens = LN(s2), s2 = LN(s1) + mlp(LN(s1)), s1 = tokens +
+  // attention(tokens), in place.
+  void residual_layer_fwd(int L, const float* input_edge, RLayer& sv) {
+    sv.tokens = md.f(int64_t(T) * D), sv.cpre = md.f(int64_t(E) * D);
+    if (N) {
+      hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(N) * D), dim3(256), 0, st, sv.tokens,
+                         md.p("node_embedders." + std::to_string(L) + ".weight"), e.species, int64_t(N), D);
+      launched();
+    }
+    compress_fwd(L, input_edge, sv.cpre, sv.tokens + int64_t(N) * D);
+    sv.b.resize(A);
+    const int F = md.ew;
+    for (int a = 0; a < A; ++a) {
+      const std::string tl = t(L, a);
+      RBlock& b = sv.b[a];
+      b.qkv = md.f(int64_t(T) * 3 * D), b.merged = md.f(int64_t(T) * D), b.ml = md.f(int64_t(N) * md.h.num_heads * S * 2);
+      b.s1 = md.f(int64_t(T) * D), b.s2 = md.f(int64_t(T) * D), b.pre = md.f(int64_t(T) * F);
+      auto scope = md.ws.mark();
+      linear(md, b.qkv, sv.tokens, T, D, tl + ".attention.input_linear", st);
+      ok(pet_attn_fwd(&sh, b.qkv, 3 * D, e.off, cf_seq, S, b.merged, D, b.ml, st));
+      // s1 = tokens + b_out, then += merged W_out^T
+      hipLaunchKernelGGL(bias_add_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, b.s1, sv.tokens,
+                         md.p(tl + ".attention.output_linear.bias"), int64_t(T), D);
+      launched();
+      linear_acc(md, b.s1, b.merged, T, D, tl + ".attention.output_linear", st);
+      float* tok_a = md.f(int64_t(T) * D);
+      norm(md, tok_a, b.s1, T, D, tl + ".norm_attention", true, st);
+      // s2 = tok_a + b_out, then += silu(tok_a W_in^T + b_in) W_out^T
+      linear_pre(md, b.pre, tok_a, T, D, tl + ".mlp.w_in", st);
+      float* hm = md.f(int64_t(T) * F);
+      silu(md, hm, b.pre, T, tl + ".mlp.w_in", st);
+      hipLaunchKernelGGL(bias_add_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, b.s2, tok_a,
+                         md.p(tl + ".mlp.w_out.bias"), int64_t(T), D);
+      launched();
+      linear_acc(md, b.s2, hm, T, F, tl + ".mlp.w_out", st);
+      norm(md, sv.tokens, b.s2, T, D, tl + ".norm_mlp", true, st);
+      md.ws.release(scope);
+    }
+  }
+
+  // Its backward (residual_pass, src/residual.cpp:180-226): tokens_adj is the
+  // layer's output tokens' adjoint (overwritten); returns the adjoint of the
+  // tokens the layer began with.
+  float* residual_layer_bwd(int L, const RLayer& sv, float* tokens_adj, float* cf_seq_adj) {
+    const int F = md.ew;
+    for (int a = A - 1; a >= 0; --a) {
+      const std::string tl = t(L, a);
+      const RBlock& b = sv.b[a];
+      auto scope = md.ws.mark();
+      // tokens = LN(s2): s2_adj; tok_a_adj = s2_adj (the residual) + the MLP's input adjoint
+      float* s2_adj = md.f(int64_t(T) * D);
+      float* tok_a_adj = md.f(int64_t(T) * D);
+      ok(pet_norm_rows_bwd(T, D, s2_adj, D, 0.0f, tokens_adj, D, b.s2, D, md.p(tl + ".norm_mlp.weight"), 1, st));
+      hipLaunchKernelGGL(copy_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, tok_a_adj, s2_adj, int64_t(T) * D);
+      launched();
+      float* h_adj = md.f(int64_t(T) * F);
+      linear_bwd(md, h_adj, s2_adj, T, tl + ".mlp.w_out", 0.0f, st);
+      silu_bwd(md, h_adj, b.pre, T, tl + ".mlp.w_in", st);
+      linear_bwd(md, tok_a_adj, h_adj, T, tl + ".mlp.w_in", 1.0f, st);
+      // tok_a = LN(s1): s1_adj into tokens_adj (consumed); the attention's input
+      // adjoint then accumulates onto it (s1 = tokens + attention(tokens))
+      ok(pet_norm_rows_bwd(T, D, tokens_adj, D, 0.0f, tok_a_adj, D, b.s1, D, md.p(tl + ".norm_attention.weight"), 1,
+                           st));
+      float* dmerged = md.f(int64_t(T) * D);
+      float* qkv_adj = md.f(int64_t(T) * 3 * D);
+      float* cfh = md.f(int64_t(N) * md.h.num_heads * S);
+      linear_bwd(md, dmerged, tokens_adj, T, tl + ".attention.output_linear", 0.0f, st);
+      ok(pet_attn_bwd(&sh, b.qkv, 3 * D, e.off, dmerged, D, b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh,
+                      cf_seq_adj, S, st));
+      linear_bwd(md, tokens_adj, qkv_adj, T, tl + ".attention.input_linear", 1.0f, st);
+      md.ws.release(scope);
+    }
+    return tokens_adj;
+  }
+
   void run(bool grad, double* energy, double* per_atom_out, double* forces, double* virial, double* edge_grad_out) {
     md.ws.reset();
     cf_seq = md.f(int64_t(N) * S);
     ok(pet_attn_cf_seq(&sh, e.off, e.cut, cf_seq, S, st));
-    float* node = md.f(int64_t(N) * Dn);
     float* input_edge = md.f(int64_t(E) * D);
-    if (N) {
-      hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(N) * Dn), dim3(256), 0, st, node,
-                         md.p("node_embedders.0.weight"), e.species, int64_t(N), Dn);
-      launched();
-    }
     if (E) {
       hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge,
                          md.p("edge_embedder.weight"), e.neigh_species, int64_t(E), D);
       launched();
     }
-    std::vector<Layer> sv(G);
-    for (int L = 0; L < G; ++L) layer_fwd(L, node, input_edge, sv[L]);
-
-    // readout (src/model.cpp:656-691): two SiLU layers and a last linear a side
-    float *nh0 = md.f(int64_t(N) * Dh), *nh1 = md.f(int64_t(N) * Dh), *eh0 = md.f(int64_t(E) * Dh),
-          *eh1 = md.f(int64_t(E) * Dh), *npred = md.f(N), *epred = md.f(E);
-    {
-      auto scope = md.ws.mark();
-      float* x = md.f(std::max<int64_t>(int64_t(N), int64_t(E)) * Dh);
-      linear_pre(md, nh0, node, N, Dn, "node_heads.energy.0.0", st);
-      silu(md, x, nh0, N, "node_heads.energy.0.0", st);
-      linear_pre(md, nh1, x, N, Dh, "node_heads.energy.0.2", st);
-      silu(md, x, nh1, N, "node_heads.energy.0.2", st);
-      linear(md, npred, x, N, Dh, "node_last_layers.energy.0.energy___0", st);
-      linear_pre(md, eh0, input_edge, E, D, "edge_heads.energy.0.0", st);
-      silu(md, x, eh0, E, "edge_heads.energy.0.0", st);
-      linear_pre(md, eh1, x, E, Dh, "edge_heads.energy.0.2", st);
-      silu(md, x, eh1, E, "edge_heads.energy.0.2", st);
-      linear(md, epred, x, E, Dh, "edge_last_layers.energy.0.energy___0", st);
-      md.ws.release(scope);
+    float* net = md.f(N);
+    const bool residual = md.h.featurizer == 1;
+    std::vector<Layer> sv(residual ? 0 : G);
+    std::vector<RLayer> rv(residual ? G : 0);
+    Readout ro{};
+    if (residual) {
+      // residual_pass (src/residual.cpp:62-133): a read-out after every layer,
+      // then input_edge = (input_edge + out_edge(reverse)) / 2
+      for (int L = 0; L < G; ++L) {
+        residual_layer_fwd(L, input_edge, rv[L]);
+        const float* edge_out = rv[L].tokens + int64_t(N) * D;
+        rv[L].ro = readout_fwd(L, rv[L].tokens, edge_out, net, L > 0);
+        if (L + 1 < G && E) {
+          hipLaunchKernelGGL(message_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge, edge_out,
+                             e.reverse, int64_t(E), D);
+          launched();
+        }
+      }
+    } else {
+      float* node = md.f(int64_t(N) * Dn);
+      if (N) {
+        hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(N) * Dn), dim3(256), 0, st, node,
+                           md.p("node_embedders.0.weight"), e.species, int64_t(N), Dn);
+        launched();
+      }
+      for (int L = 0; L < G; ++L) layer_fwd(L, node, input_edge, sv[L]);
+      ro = readout_fwd(0, node, input_edge, net, false);
     }
     double* per_atom = per_atom_out ? per_atom_out : reinterpret_cast<double*>(md.f(2 * int64_t(N)));
     if (N) {
-      hipLaunchKernelGGL(readout_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st, per_atom, npred, epred,
-                         e.off, e.cut, e.species, md.comp, md.h.energy_scale, N);
+      hipLaunchKernelGGL(assemble_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st, per_atom, net,
+                         e.species, md.comp, md.h.energy_scale, N);
       launched();
     }
     if (energy) ok(pet_sum_by_structure(e.n_struct, 1, e.struct_off, per_atom, energy, 0, st));
     if (!grad) return;
 
-    // backward (ff_pass, src/feedforward.cpp:396-410)
     float* x4_adj = md.f(int64_t(E) * 4);
     float* cf_seq_adj = md.f(int64_t(N) * S);
     float* cutoff_adj = md.f(E);
-    float* node_adj = md.f(int64_t(N) * Dn);
-    float* ie_adj = md.f(int64_t(E) * D);
     fill0(x4_adj, int64_t(E) * 4, st);
     fill0(cf_seq_adj, int64_t(N) * S, st);
-    {
-      auto scope = md.ws.mark();
-      float *npa = md.f(N), *epa = md.f(E), *a1 = md.f(std::max<int64_t>(N, E) * Dh),
-            *a0 = md.f(std::max<int64_t>(N, E) * Dh);
-      if (N + E) {
-        hipLaunchKernelGGL(readout_seed_kernel, grid_for(int64_t(N) + E), dim3(256), 0, st, npa, epa, cutoff_adj,
-                           e.cut, epred, N, E);
-        launched();
+    if (residual) {
+      // each layer's tokens' adjoint from its read-out; ie_adj that of the next
+      // layer's input_edge (src/residual.cpp:156-226)
+      std::vector<float*> tadj(G);
+      for (int L = 0; L < G; ++L) {
+        tadj[L] = md.f(int64_t(T) * D);
+        readout_bwd(L, rv[L].ro, tadj[L], tadj[L] + int64_t(N) * D, cutoff_adj, L > 0);
       }
-      linear_bwd(md, a1, npa, N, "node_last_layers.energy.0.energy___0", 0.0f, st);
-      silu_bwd(md, a1, nh1, N, "node_heads.energy.0.2", st);
-      linear_bwd(md, a0, a1, N, "node_heads.energy.0.2", 0.0f, st);
-      silu_bwd(md, a0, nh0, N, "node_heads.energy.0.0", st);
-      linear_bwd(md, node_adj, a0, N, "node_heads.energy.0.0", 0.0f, st);
-      linear_bwd(md, a1, epa, E, "edge_last_layers.energy.0.energy___0", 0.0f, st);
-      silu_bwd(md, a1, eh1, E, "edge_heads.energy.0.2", st);
-      linear_bwd(md, a0, a1, E, "edge_heads.energy.0.2", 0.0f, st);
-      silu_bwd(md, a0, eh0, E, "edge_heads.energy.0.0", st);
-      linear_bwd(md, ie_adj, a0, E, "edge_heads.energy.0.0", 0.0f, st);
-      md.ws.release(scope);
+      float* ie_adj = md.f(int64_t(E) * D);
+      float* ie_next = md.f(int64_t(E) * D);
+      for (int L = G - 1; L >= 0; --L) {
+        float* efa = tadj[L] + int64_t(N) * D;
+        if (L + 1 < G && E) {  // the message's reverse share: efa += ie_adj(rev) / 2
+          hipLaunchKernelGGL(message_bwd_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, efa, ie_adj, e.reverse,
+                             int64_t(E), D);
+          launched();
+        }
+        float* tok_adj = residual_layer_bwd(L, rv[L], tadj[L], cf_seq_adj);
+        // the message's own share: ie_next = ie_adj / 2 (0 past the last layer)
+        if (E) {
+          hipLaunchKernelGGL(scale_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, ie_next, ie_adj,
+                             L + 1 < G ? 0.5f : 0.0f, int64_t(E) * D);
+          launched();
+        }
+        compress_bwd(L, tok_adj + int64_t(N) * D, rv[L].cpre, x4_adj, ie_next);
+        std::swap(ie_adj, ie_next);
+      }
+    } else {
+      // backward (ff_pass, src/feedforward.cpp:396-410)
+      float* node_adj = md.f(int64_t(N) * Dn);
+      float* ie_adj = md.f(int64_t(E) * D);
+      readout_bwd(0, ro, node_adj, ie_adj, cutoff_adj, false);
+      for (int L = G - 1; L >= 0; --L) layer_bwd(L, sv[L], node_adj, ie_adj, x4_adj, cf_seq_adj);
     }
-    for (int L = G - 1; L >= 0; --L) layer_bwd(L, sv[L], node_adj, ie_adj, x4_adj, cf_seq_adj);
 
     // forces_and_virial (src/forces.cpp:345-386)
     double* grad_e = edge_grad_out ? edge_grad_out : reinterpret_cast<double*>(md.f(6 * int64_t(E)));
@@ -758,8 +968,13 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
   const pet_model_hypers& h = *hy;
   if (h.d_pet < 1 || h.d_node < 1 || h.d_head < 1 || h.num_heads < 1 || h.d_pet % h.num_heads ||
       h.num_gnn_layers < 1 || h.num_attention_layers < 1 || h.n_species < 1 || h.cutoff_function < 0 ||
-      h.cutoff_function > 2 || !(h.cutoff_width > 0.0) || !(h.attention_temperature > 0.0) || h.d_node == h.d_pet)
+      h.cutoff_function > 2 || !(h.cutoff_width > 0.0) || !(h.attention_temperature > 0.0) ||
+      h.featurizer < 0 || h.featurizer > 1)
     return PET_ATTN_EINVAL;
+  // the two families (src/model.cpp:326-336): feedforward with an expanded
+  // central token (d_node != d_pet), residual without (d_node == d_pet)
+  const bool residual = h.featurizer == 1;
+  if (residual != (h.d_node == h.d_pet)) return PET_ATTN_EINVAL;
   const int hd = h.d_pet / h.num_heads;
   if (hd % 16 || hd > 128) return PET_ATTN_EHEADDIM;
   auto md = new pet_model();
@@ -778,8 +993,8 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
       if (it == ld.in.end()) throw Error{PET_MODEL_EMISSING};
       return it->second->rows;
     };
-    md->ew = rows_of(t0 + ".mlp.w_in.weight"), md->cw = rows_of(t0 + ".center_mlp.w_in.weight");
-    if (md->ew % 2 || md->cw % 2) throw Error{PET_MODEL_ESHAPE};
+    md->ew = rows_of(t0 + ".mlp.w_in.weight"), md->cw = residual ? 0 : rows_of(t0 + ".center_mlp.w_in.weight");
+    if (!residual && (md->ew % 2 || md->cw % 2)) throw Error{PET_MODEL_ESHAPE};
     for (int L = 0; L < h.num_gnn_layers; ++L) {
       const std::string g = "gnn_layers." + std::to_string(L), ls = std::to_string(L);
       ld.fold(L);
@@ -790,6 +1005,13 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
         ld.linear(tl + ".attention.output_linear", D, D);
         ld.copy(tl + ".norm_attention.weight", D, 0);
         ld.copy(tl + ".norm_mlp.weight", D, 0);
+        if (residual) {  // PostLN with LayerNorm, a SiLU MLP
+          ld.copy(tl + ".norm_attention.bias", D, 0);
+          ld.copy(tl + ".norm_mlp.bias", D, 0);
+          ld.linear(tl + ".mlp.w_in", md->ew, D);
+          ld.linear(tl + ".mlp.w_out", D, md->ew);
+          continue;
+        }
         ld.swiglu_in(tl + ".mlp.w_in", md->ew, D);
         ld.linear(tl + ".mlp.w_out", D, md->ew / 2);
         ld.linear(tl + ".center_contraction", D, Dn);
@@ -798,19 +1020,24 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
         ld.swiglu_in(tl + ".center_mlp.w_in", md->cw, Dn);
         ld.linear(tl + ".center_mlp.w_out", Dn, md->cw / 2);
       }
+      if (residual) continue;
       ld.copy("combination_norms." + ls + ".weight", 2 * D, 0);
       ld.copy("combination_norms." + ls + ".bias", 2 * D, 0);
       ld.linear("combination_mlps." + ls + ".0", 2 * D, 2 * D);
       ld.linear("combination_mlps." + ls + ".2", D, 2 * D);
     }
     ld.copy("edge_embedder.weight", ns, D);
-    ld.copy("node_embedders.0.weight", ns, Dn);
-    ld.linear("node_heads.energy.0.0", Dh, Dn);
-    ld.linear("node_heads.energy.0.2", Dh, Dh);
-    ld.linear("edge_heads.energy.0.0", Dh, D);
-    ld.linear("edge_heads.energy.0.2", Dh, Dh);
-    ld.linear("node_last_layers.energy.0.energy___0", 1, Dh);
-    ld.linear("edge_last_layers.energy.0.energy___0", 1, Dh);
+    // a read-out after every layer (residual) or once (feedforward)
+    for (int i = 0; i < (residual ? h.num_gnn_layers : 1); ++i) {
+      const std::string si = std::to_string(i);
+      ld.copy("node_embedders." + si + ".weight", ns, Dn);
+      ld.linear("node_heads.energy." + si + ".0", Dh, Dn);
+      ld.linear("node_heads.energy." + si + ".2", Dh, Dh);
+      ld.linear("edge_heads.energy." + si + ".0", Dh, D);
+      ld.linear("edge_heads.energy." + si + ".2", Dh, Dh);
+      ld.linear("node_last_layers.energy." + si + ".energy___0", 1, Dh);
+      ld.linear("edge_last_layers.energy." + si + ".energy___0", 1, Dh);
+    }
 
     size_t total = 0;
     std::vector<size_t> at;
@@ -851,7 +1078,7 @@ int pet_model_compute(pet_model* md, const pet_model_edges* e, int forces, doubl
   if (forces && (!forces_out || (virial && (!e->struct_off || e->n_struct < 1)))) return PET_ATTN_EINVAL;
   if (e->max_neighbors + 1 > pet_attn_max_slots(md->hd)) return PET_ATTN_ESLOTS;
   if (edge_grad && md->h.energy_scale != 1.0) return PET_ATTN_EINVAL;
-  if (int64_t(e->n_atoms) + e->n_edges >= (int64_t(1) << 31) / std::max(3 * md->h.d_pet, md->ew))
+  if (int64_t(e->n_atoms) + e->n_edges >= (int64_t(1) << 31) / std::max(std::max(3 * md->h.d_pet, md->ew), md->cw))
     return PET_ATTN_EINDEX;
   try {
     Pass p(*md, *e, reinterpret_cast<hipStream_t>(stream));

@@ -98,7 +98,7 @@ class PetModel:
         lib = _lib.load()
         hy = _lib.ModelHypers(h.d_pet, h.d_node, h.d_head, h.num_heads, h.num_gnn_layers, h.num_attention_layers,
                               h.n_species, CUTOFF_KINDS[h.cutoff_function], h.cutoff_width, h.attention_temperature,
-                              energy_scale)
+                              energy_scale, 1 if h.residual else 0)
         keep = [np.ascontiguousarray(v, dtype=np.float64) for v in weights.values()]
         arr = (_lib.ModelTensor * len(keep))()
         for i, (name, v) in enumerate(zip(weights.keys(), keep)):

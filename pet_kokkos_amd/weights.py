@@ -9,9 +9,9 @@ the benchmark models are random-init with exactly those names and shapes
 value rows [0, F) then the gate rows [F, 2F); ``compress.0`` unfolded, its
 input columns [edge_emb | neighbour/edge embedding | input_edge]).
 
-Only the feedforward featurizer (PreLN, RMSNorm, SwiGLU, d_node != d_pet) is
-described: the family the reference implements for that featurizer
-(src/model.cpp:326-332).
+Both featurizers the reference implements (src/model.cpp:326-340): the
+feedforward one (PreLN, RMSNorm, SwiGLU, d_node != d_pet) and the residual one
+(PostLN, LayerNorm, SiLU, d_node == d_pet, a readout after every GNN layer).
 """
 from __future__ import annotations
 
@@ -36,6 +36,11 @@ class Hypers:
     cutoff_function: str = "cosine"  # bump | cosine | smooth
     attention_temperature: float = 1.0
     atomic_types: tuple = (1, 6, 8)
+    featurizer: str = "feedforward"  # or "residual"
+
+    @property
+    def residual(self) -> bool:
+        return self.featurizer == "residual"
 
     @property
     def head_dim(self) -> int:
@@ -52,8 +57,9 @@ class Hypers:
 
     @property
     def edge_width(self) -> int:
-        """mlp.w_in's rows: SwiGLU over d_feedforward (tools/roofline.py:112)."""
-        return 2 * self.d_feedforward
+        """mlp.w_in's rows: SwiGLU over d_feedforward (tools/roofline.py:112),
+        d_feedforward for the residual featurizer's SiLU MLP."""
+        return self.d_feedforward if self.residual else 2 * self.d_feedforward
 
 
 # The E+F workloads: configs[1] (water-648) and configs[4] (batch of 32). The
@@ -64,8 +70,13 @@ class Hypers:
 MODELS = {
     "c2": Hypers(d_pet=128, d_node=256, d_head=128, d_feedforward=512, num_heads=4),
     "c5": Hypers(d_pet=512, d_node=1024, d_head=128, d_feedforward=1024, num_heads=8),
-    # a small model for the tests
+    # small models for the tests
     "tiny": Hypers(d_pet=64, d_node=128, d_head=32, d_feedforward=128, num_heads=4),
+    "tiny-residual": Hypers(d_pet=64, d_node=64, d_head=32, d_feedforward=128, num_heads=4,
+                            featurizer="residual"),
+    # the residual family at configs[1]'s shape
+    "c2-residual": Hypers(d_pet=128, d_node=128, d_head=128, d_feedforward=512, num_heads=4,
+                          featurizer="residual"),
 }
 
 
@@ -87,7 +98,9 @@ def random_weights(h: Hypers, seed: int = 0) -> dict[str, np.ndarray]:
             w[name + ".bias"] = 0.1 * rng.standard_normal(width)
 
     w["edge_embedder.weight"] = rng.standard_normal((ns, D))
-    w["node_embedders.0.weight"] = rng.standard_normal((ns, Dn))
+    R = h.num_gnn_layers if h.residual else 1  # readouts
+    for i in range(R):
+        w[f"node_embedders.{i}.weight"] = rng.standard_normal((ns, Dn))
     for L in range(h.num_gnn_layers):
         g = f"gnn_layers.{L}"
         lin(g + ".edge_embedder", D, 4)
@@ -99,24 +112,29 @@ def random_weights(h: Hypers, seed: int = 0) -> dict[str, np.ndarray]:
             t = f"{g}.trans.layers.{a}"
             lin(t + ".attention.input_linear", 3 * D, D)
             lin(t + ".attention.output_linear", D, D)
-            norm(t + ".norm_attention", D)
-            norm(t + ".norm_mlp", D)
+            norm(t + ".norm_attention", D, bias=h.residual)
+            norm(t + ".norm_mlp", D, bias=h.residual)
             lin(t + ".mlp.w_in", h.edge_width, D)
-            lin(t + ".mlp.w_out", D, h.edge_width // 2)
+            lin(t + ".mlp.w_out", D, h.d_feedforward)
+            if h.residual:
+                continue
             lin(t + ".center_contraction", D, Dn)
             lin(t + ".center_expansion", Dn, D)
             norm(t + ".norm_center_features", Dn)
             lin(t + ".center_mlp.w_in", h.center_width, Dn)
             lin(t + ".center_mlp.w_out", Dn, h.center_width // 2)
+        if h.residual:
+            continue
         norm(f"combination_norms.{L}", 2 * D, bias=True)
         lin(f"combination_mlps.{L}.0", 2 * D, 2 * D)
         lin(f"combination_mlps.{L}.2", D, 2 * D)
-    lin("node_heads.energy.0.0", Dh, Dn)
-    lin("node_heads.energy.0.2", Dh, Dh)
-    lin("edge_heads.energy.0.0", Dh, D)
-    lin("edge_heads.energy.0.2", Dh, Dh)
-    lin("node_last_layers.energy.0.energy___0", 1, Dh)
-    lin("edge_last_layers.energy.0.energy___0", 1, Dh)
+    for i in range(R):
+        lin(f"node_heads.energy.{i}.0", Dh, Dn)
+        lin(f"node_heads.energy.{i}.2", Dh, Dh)
+        lin(f"edge_heads.energy.{i}.0", Dh, D)
+        lin(f"edge_heads.energy.{i}.2", Dh, Dh)
+        lin(f"node_last_layers.energy.{i}.energy___0", 1, Dh)
+        lin(f"edge_last_layers.energy.{i}.energy___0", 1, Dh)
     return w
 
 

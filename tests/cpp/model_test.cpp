@@ -5,7 +5,7 @@
 //   model_test DIR
 //
 // reads DIR/hypers.txt (d_pet d_node d_head heads gnn_layers attention_layers
-// n_species cutoff_function cutoff_width temperature energy_scale cutoff),
+// n_species cutoff_function cutoff_width temperature energy_scale cutoff featurizer),
 // DIR/manifest.txt ("name rows cols" a tensor, cols 0 for a vector) with
 // DIR/weights.f64 (the tensors back to back), DIR/composition.f64,
 // DIR/s2i.txt (species_to_index) and DIR/system.txt (N, the cell's 9 numbers,
@@ -34,7 +34,8 @@ int main(int argc, char** argv) {
   pet_model_hypers h{};
   double cutoff = 0;
   if (!(hf >> h.d_pet >> h.d_node >> h.d_head >> h.num_heads >> h.num_gnn_layers >> h.num_attention_layers >>
-        h.n_species >> h.cutoff_function >> h.cutoff_width >> h.attention_temperature >> h.energy_scale >> cutoff))
+        h.n_species >> h.cutoff_function >> h.cutoff_width >> h.attention_temperature >> h.energy_scale >> cutoff >>
+        h.featurizer))
     fail("hypers.txt");
   std::ifstream mf(dir + "/manifest.txt");
   FILE* wf = std::fopen((dir + "/weights.f64").c_str(), "rb");

@@ -11,8 +11,9 @@ import pytest
 from pet_kokkos_amd import checkpoint, weights
 
 
-def test_round_trip(tmp_path):
-    h = weights.MODELS["tiny"]
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
+def test_round_trip(tmp_path, name):
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 3)
     comp = weights.random_composition(h)
     jp, sp = checkpoint.save(str(tmp_path / "m"), h, w, comp, energy_scale=1.5)
@@ -29,7 +30,8 @@ def test_round_trip(tmp_path):
 
 
 @pytest.mark.parametrize("edit", [
-    lambda h: h.update(featurizer_type="residual"),
+    lambda h: h.update(featurizer_type="residual"),  # with RMSNorm / SwiGLU / PreLN and d_node != d_pet
+    lambda h: h.update(featurizer_type="other"),
     lambda h: h.update(normalization="LayerNorm"),
     lambda h: h.update(num_neighbors_adaptive=30.0),
     lambda h: h.update(zbl=True),

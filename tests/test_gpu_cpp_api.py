@@ -101,7 +101,8 @@ def test_cpp_layer_and_forces_api(tmp_path):
     assert (tmp_path / "graph.ok").exists(), "pet::GraphCache: a captured or replayed run differed from the eager one"
 
 
-def test_cpp_model_calculator(tmp_path):
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
+def test_cpp_model_calculator(tmp_path, name):
     """pet::PetModel + pet::Calculator (include/pet/model.hpp) from C++: the
     C++ host neighbour list, the model's energy / forces / virial against the
     CPU oracle, a repeat bit for bit, and forces against a central difference
@@ -113,7 +114,7 @@ def test_cpp_model_calculator(tmp_path):
 
     if not os.path.exists(B.CPP_TEST3):
         pytest.fail(f"{B.CPP_TEST3} is not built (python -m pet_kokkos_amd.build)")
-    h = weights.MODELS["tiny"]
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 21)
     comp = weights.random_composition(h)
     s = systems.water_box(2, 6.2, seed=8)
@@ -121,7 +122,7 @@ def test_cpp_model_calculator(tmp_path):
     with open(tmp_path / "hypers.txt", "w") as f:
         f.write(f"{h.d_pet} {h.d_node} {h.d_head} {h.num_heads} {h.num_gnn_layers} {h.num_attention_layers} "
                 f"{h.n_species} {CUTOFF_KINDS[h.cutoff_function]} {h.cutoff_width} {h.attention_temperature} 1.0 "
-                f"{h.cutoff}\n")
+                f"{h.cutoff} {1 if h.residual else 0}\n")
     with open(tmp_path / "manifest.txt", "w") as f, open(tmp_path / "weights.f64", "wb") as g:
         for k, v in w.items():
             f.write(f"{k} {v.shape[0]} {v.shape[1] if v.ndim == 2 else 0}\n")

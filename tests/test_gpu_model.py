@@ -1,5 +1,6 @@
-"""The whole PET evaluation on the GPU (libpet_attn.so's pet_model_compute)
-against the CPU oracle (oracle/pet_model.py, float64, autograd forces).
+"""The whole PET evaluation on the GPU (libpet_attn.so's pet_model_compute),
+both featurizers, against the CPU oracle (oracle/pet_model.py, float64,
+autograd forces).
 
 The library folds compress.0 and interleaves the SwiGLU weights itself and
 runs an analytic backward; the oracle evaluates the unfolded model and
@@ -66,12 +67,13 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
 @pytest.mark.parametrize("case", list(CASES))
-def test_model_matches_oracle(case, device):
-    h = weights.MODELS["tiny"]
+def test_model_matches_oracle(case, name, device):
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 11)
     comp = weights.random_composition(h)
-    print(f"[model] tiny {case}", flush=True)
+    print(f"[model] {name} {case}", flush=True)
     m = PetModel(h, w, comp)
     x = structures_input(h, CASES[case](), device)
     got = m.compute(x, forces=True, edge_grad=True)
@@ -79,8 +81,9 @@ def test_model_matches_oracle(case, device):
     compare(got, oracle_of(h, w, comp, x))
 
 
-def test_model_repeats_bitwise(device):
-    h = weights.MODELS["tiny"]
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
+def test_model_repeats_bitwise(name, device):
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 12)
     m = PetModel(h, w, weights.random_composition(h))
     x = structures_input(h, CASES["batch-3"](), device)
@@ -104,12 +107,14 @@ def test_energy_only_matches_forces_run(device):
     assert torch.equal(e0, e1)
 
 
-def test_c2_model_water_648(device):
-    """configs[1]'s model (d 128, 4 heads, 2 x 2 layers, FFN 512) on 648-atom water."""
-    h = weights.MODELS["c2"]
+@pytest.mark.parametrize("name", ["c2", "c2-residual"])
+def test_c2_model_water_648(name, device):
+    """configs[1]'s model shape (d 128, 4 heads, 2 x 2 layers, FFN 512) on
+    648-atom water, in either featurizer."""
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 0)
     comp = weights.random_composition(h)
-    print("[model] c2 water-648", flush=True)
+    print(f"[model] {name} water-648", flush=True)
     m = PetModel(h, w, comp)
     x = structures_input(h, [systems.water_box(6, 18.6, seed=0)], device)
     got = m.compute(x, forces=True)
@@ -129,11 +134,12 @@ def test_calculator(device):
     assert np.abs(r["forces"] - ref["forces"]).max() <= 1e-5 * np.abs(ref["forces"]).max()
 
 
-def test_from_checkpoint(device, tmp_path):
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
+def test_from_checkpoint(name, device, tmp_path):
     """A model read from the converted-checkpoint files evaluates bit for bit
     as one built from the same (float32-rounded) weights."""
     from pet_kokkos_amd import checkpoint
-    h = weights.MODELS["tiny"]
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 15)
     comp = weights.random_composition(h)
     jp, sp = checkpoint.save(str(tmp_path / "m"), h, w, comp, energy_scale=1.25)
@@ -239,10 +245,11 @@ def test_other_cutoff_functions(kind, device):
     compare(got, oracle_of(h, w, comp, x))
 
 
-def test_isolated_atom_and_empty_neighbourhoods(device):
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
+def test_isolated_atom_and_empty_neighbourhoods(name, device):
     """An atom with no neighbour within the cutoff (one token) next to a
     molecule, and a structure of one isolated atom."""
-    h = weights.MODELS["tiny"]
+    h = weights.MODELS[name]
     w = weights.random_weights(h, 18)
     comp = weights.random_composition(h)
     m = PetModel(h, w, comp)

@@ -71,7 +71,8 @@ def _model_create(tensors, **over):
     h = weights.MODELS["tiny"]
     hy = dict(d_pet=h.d_pet, d_node=h.d_node, d_head=h.d_head, num_heads=h.num_heads,
               num_gnn_layers=h.num_gnn_layers, num_attention_layers=h.num_attention_layers, n_species=h.n_species,
-              cutoff_function=1, cutoff_width=0.5, attention_temperature=1.0, energy_scale=1.0)
+              cutoff_function=1, cutoff_width=0.5, attention_temperature=1.0, energy_scale=1.0,
+              featurizer=0)
     hy.update(over)
     keep = [np.ascontiguousarray(v, dtype=np.float64) for v in tensors.values()]
     arr = (_lib.ModelTensor * max(1, len(keep)))()
@@ -93,6 +94,8 @@ def test_model_create_rejects_before_the_device():
     bad["gnn_layers.0.compress.2.weight"] = np.zeros((3, 3))
     assert _model_create(bad)[0] == 21  # PET_MODEL_ESHAPE
     assert _model_create(w, d_node=64)[0] == _lib.EINVAL  # the feedforward family needs d_node != d_pet
+    assert _model_create(w, featurizer=1)[0] == _lib.EINVAL  # the residual family needs d_node == d_pet
+    assert _model_create(w, featurizer=2)[0] == _lib.EINVAL
     assert _model_create(w, num_heads=3)[0] == _lib.EINVAL  # d_pet not a multiple of the heads
     assert _model_create(w, num_heads=8)[0] == _lib.EHEADDIM  # head_dim 8
     assert "missing" in _lib.strerror(20)

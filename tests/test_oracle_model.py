@@ -13,7 +13,8 @@ vectors), so the oracle is pinned by:
   translation    moving every atom leaves energy and forces unchanged;
   fold           forces from the edge gradients against central differences
                  of the energy in atom positions;
-  fp32 / fp64    the two precisions agree to fp32 rounding.
+  fp32 / fp64    the two precisions agree to fp32 rounding;
+for both featurizers (feedforward and residual).
 
 The order in which the layers are composed has no independent vector here:
 beyond these checks the model's parity with the reference is unpinned.
@@ -30,6 +31,7 @@ from pet_kokkos_amd import systems, weights
 from pet_kokkos_amd.model import species_index
 
 H = weights.MODELS["tiny"]
+FAMILIES = ["tiny", "tiny-residual"]
 
 
 def setup(s: systems.Structure, h=H, seed=0):
@@ -46,7 +48,7 @@ def small_water(seed=0):
 
 def test_attention_matches_c_oracle():
     s = small_water()
-    w, pk, sp = setup(s)
+    w, pk, sp = setup(s, H)
     tix = om.TokenIndex(pk.off)
     rng = np.random.default_rng(3)
     N, E = len(sp), int(pk.off[-1])
@@ -69,9 +71,11 @@ def test_norms_match_torch():
     assert torch.allclose(om.norm(x, w, b), torch.nn.functional.layer_norm(x, (48,), w, b, eps=om.LN_EPS), atol=1e-13)
 
 
-def test_edge_grad_central_differences():
+@pytest.mark.parametrize("name", FAMILIES)
+def test_edge_grad_central_differences(name):
+    H = weights.MODELS[name]
     s = small_water(1)
-    w, pk, sp = setup(s)
+    w, pk, sp = setup(s, H)
     comp = weights.random_composition(H)
     _, eg = om.evaluate(H, w, sp, pk, comp)
     rng = np.random.default_rng(0)
@@ -89,10 +93,12 @@ def test_edge_grad_central_differences():
             assert abs(fd - eg[k, c]) < 1e-6 * max(1.0, abs(eg[k, c])), (k, c, fd, eg[k, c])
 
 
-def test_forces_central_differences():
+@pytest.mark.parametrize("name", FAMILIES)
+def test_forces_central_differences(name):
+    H = weights.MODELS[name]
     """forces = -dE/dr, by the fold of the edge gradients."""
     s = small_water(2)
-    w, pk, sp = setup(s)
+    w, pk, sp = setup(s, H)
     _, eg = om.evaluate(H, w, sp, pk)
     f, _ = om.fold_forces(len(sp), pk, eg)
     hstep = 1e-5
@@ -102,32 +108,36 @@ def test_forces_central_differences():
             for sgn in (1, -1):
                 s2 = systems.Structure(s.positions.copy(), s.cell, s.numbers)
                 s2.positions[a, c] += sgn * hstep
-                w2, pk2, sp2 = setup(s2)
+                w2, pk2, sp2 = setup(s2, H)
                 pa, _ = om.evaluate(H, w, sp2, pk2, grad=False)
                 vals.append(pa.sum())
             assert abs(-(vals[0] - vals[1]) / (2 * hstep) - f[a, c]) < 1e-6 * max(1.0, abs(f[a, c]))
     assert np.abs(f.sum(0)).max() < 1e-10
 
 
-def test_permutation_and_translation():
+@pytest.mark.parametrize("name", FAMILIES)
+def test_permutation_and_translation(name):
+    H = weights.MODELS[name]
     s = small_water(3)
-    w, pk, sp = setup(s)
+    w, pk, sp = setup(s, H)
     pa, eg = om.evaluate(H, w, sp, pk)
     f, _ = om.fold_forces(len(sp), pk, eg)
     perm = np.random.default_rng(1).permutation(len(sp))
     s2 = systems.Structure(s.positions[perm] + np.array([0.3, -1.1, 2.0]), s.cell, s.numbers[perm])
-    _, pk2, sp2 = setup(s2)
+    _, pk2, sp2 = setup(s2, H)
     pa2, eg2 = om.evaluate(H, w, sp2, pk2)
     f2, _ = om.fold_forces(len(sp2), pk2, eg2)
     assert np.abs(pa2 - pa[perm]).max() < 1e-10
     assert np.abs(f2 - f[perm]).max() < 1e-9
 
 
-def test_supercell_extensive():
+@pytest.mark.parametrize("name", FAMILIES)
+def test_supercell_extensive(name):
+    H = weights.MODELS[name]
     cell = systems.diamond(1, jitter=0.0)
     sup = systems.diamond(2, jitter=0.0)
-    w, pk, sp = setup(cell)
-    w, pk2, sp2 = setup(sup)
+    w, pk, sp = setup(cell, H)
+    w, pk2, sp2 = setup(sup, H)
     pa, _ = om.evaluate(H, w, sp, pk, grad=False)
     pa2, _ = om.evaluate(H, w, sp2, pk2, grad=False)
     # each supercell atom has the environment of its image in the cell (the two
@@ -136,9 +146,11 @@ def test_supercell_extensive():
     assert np.ptp(pa) > 1e-3
 
 
-def test_fp32_close_to_fp64():
+@pytest.mark.parametrize("name", FAMILIES)
+def test_fp32_close_to_fp64(name):
+    H = weights.MODELS[name]
     s = small_water(4)
-    w, pk, sp = setup(s)
+    w, pk, sp = setup(s, H)
     pa64, eg64 = om.evaluate(H, w, sp, pk)
     pa32, eg32 = om.evaluate(H, w, sp, pk, dtype=torch.float32)
     assert abs(pa32.sum() - pa64.sum()) < 1e-5 * abs(pa64.sum())
