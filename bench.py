@@ -158,8 +158,8 @@ def other_configs(device, reps):
 
 def time_ef(device, reps, cpu: bool):
     """Energy+forces evaluations of the whole model (pet_model_compute): C2
-    (configs[1], 648-atom water, d 128 / 4 heads / 2 x 2 layers / FFN 512)
-    and C5 (configs[4], 32 structures, d 512 / 8 heads of 64). ms per
+    (configs[1], 648-atom water, d 128 / 4 heads / 2 x 2 layers / FFN 512) in
+    both featurizers, and C5 (configs[4], 32 structures, d 512 / 8 heads of 64). ms per
     evaluation with inputs resident, the contraction roofline of its FLOPs
     (dense fp32 on the matrix cores: a lower bound that leaves out the
     HBM-bound elementwise passes) and, for C2, the CPU oracle (float32 torch on
@@ -170,7 +170,7 @@ def time_ef(device, reps, cpu: bool):
     from pet_kokkos_amd.model import PetModel, ef_flops, ef_workload, structures_input
 
     res = {}
-    for name in ("c2", "c5"):
+    for name in ("c2", "c2-residual", "c5"):
         h, w, comp, sts = ef_workload(name)
         m = PetModel(h, w, comp)
         x = structures_input(h, sts, device)
@@ -180,11 +180,12 @@ def time_ef(device, reps, cpu: bool):
         o = m.compute(x, True)
         e_ms = _timed(lambda: m.compute(x, False, out=o), n) / 1e3
         ef_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
-        r = dict(structures=len(sts), atoms=x.n_atoms, edges=x.n_edges, d_pet=h.d_pet, heads=h.num_heads,
+        r = dict(featurizer=h.featurizer, structures=len(sts), atoms=x.n_atoms, edges=x.n_edges, d_pet=h.d_pet,
+                 heads=h.num_heads,
                  ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
                  ef_bound_ms=fl["forces"] / PEAK_FP32_MFMA * 1e3, ef_frac_of_roofline=fl["forces"] / PEAK_FP32_MFMA
                  * 1e3 / ef_ms, workspace_gb=m.workspace_bytes / 1e9)
-        if name == "c2" and cpu:
+        if name in ("c2", "c2-residual") and cpu:
             from oracle import pet_model as om
             sp = x.species.cpu().numpy()
             om.evaluate(h, w, sp, x.host, comp, dtype=torch.float32)
@@ -199,8 +200,9 @@ def time_ef(device, reps, cpu: bool):
         res[name] = r
         del m, x, o
         torch.cuda.empty_cache()
-    res["note"] = ("random-init PET-shaped models (feedforward featurizer: RMSNorm, SwiGLU, d_node 2 d_pet, "
-                   "d_head 128); neighbour list built on the host beforehand and not timed")
+    res["note"] = ("random-init PET-shaped models: feedforward featurizer (RMSNorm, SwiGLU, d_node 2 d_pet, "
+                   "d_head 128) for c2 and c5, residual featurizer (LayerNorm, SiLU, d_node d_pet) for "
+                   "c2-residual; neighbour list built on the host beforehand and not timed")
     return res
 
 

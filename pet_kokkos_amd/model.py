@@ -229,24 +229,31 @@ def ef_flops(h: Hypers, n_atoms: int, n_edges: int, sum_cnt2: float) -> dict:
     N, E, T = n_atoms, n_edges, n_atoms + n_edges
     D, Dn, Dh, cw, ew = h.d_pet, h.d_node, h.d_head, h.center_width, h.edge_width
     g = 0.0
+    blocks = h.num_gnn_layers * h.num_attention_layers
+    if h.residual:  # per block QKV, output, the MLP over all tokens; a read-out a layer
+        for L in range(h.num_gnn_layers):
+            g += (E * D * D if L else 0) + E * D * D
+            g += h.num_attention_layers * (T * 3 * D * D + T * D * D + T * ew * D + T * D * ew)
+            g += N * Dh * Dn + N * Dh * Dh + N * Dh + E * Dh * D + E * Dh * Dh + E * Dh
+        return dict(energy=2.0 * g + blocks * 4.0 * sum_cnt2 * D, forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D)
     for L in range(h.num_gnn_layers):
         g += (E * D * D if L else 0) + E * D * D  # compress.0's input_edge block, compress.2
         g += h.num_attention_layers * (N * D * Dn + T * 3 * D * D + T * D * D + N * Dn * D + N * cw * Dn
                                        + N * Dn * cw // 2 + E * ew * D + E * D * ew // 2)
         g += E * 2 * D * 2 * D + E * D * 2 * D  # combination MLP
     g += N * Dh * Dn + N * Dh * Dh + N * Dh + E * Dh * D + E * Dh * Dh + E * Dh  # readout
-    blocks = h.num_gnn_layers * h.num_attention_layers
     return dict(energy=2.0 * g + blocks * 4.0 * sum_cnt2 * D,
                 forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D)
 
 
 def ef_workload(name: str, seed: int = 0):
     """(hypers, weights, composition, structures) of an energy+forces workload:
-    "c2" configs[1] (648-atom water), "c5" configs[4] (32 structures,
-    diamond-64 and water-648 alternating, each seeded by its index)."""
+    "c2" configs[1] (648-atom water), "c2-residual" the same with the residual
+    featurizer, "c5" configs[4] (32 structures, diamond-64 and water-648
+    alternating, each seeded by its index)."""
     from . import systems, weights
     h = weights.MODELS[name]
-    if name == "c2":
+    if name in ("c2", "c2-residual"):
         sts = [systems.water_box(6, 18.6, seed=seed)]
     elif name == "c5":
         sts = [systems.diamond(2, jitter=0.01, seed=seed + k) if k % 2 == 0 else

@@ -32,7 +32,7 @@ def main(argv=None):
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--rows", action="store_true",
                     help="also run the token norm (forward, backward) and the forces' edge term and fold each step")
-    ap.add_argument("--model", choices=["c2", "c5"], help="profile whole energy+forces evaluations instead")
+    ap.add_argument("--model", choices=["c2", "c2-residual", "c5"], help="profile whole energy+forces evaluations instead")
     args = ap.parse_args(argv)
     device = torch.device("cuda", 0)
     if args.model:
