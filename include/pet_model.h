@@ -99,6 +99,20 @@ PET_ATTN_API int pet_model_compute(pet_model* model, const pet_model_edges* edge
                                    double* per_atom, double* forces_out, double* virial, double* edge_grad,
                                    void* stream);
 
+/* A dense layer on the fp32 matrix cores with its neighbours fused:
+ *   v = (A W^T)[i][j] (A [M, K] ld lda, W [N, K] ld ldw, K a multiple of 16,
+ *       A and W 16-byte aligned, lda and ldw multiples of 4),
+ *   v *= row_scale[i], v += bias[j], v += beta * cin[i][j] (each when non-null),
+ *   pre[i][j] = v (when non-null), then C[i][j] = v (act 0), silu(v) (act 1), or
+ *   for act 2 (SwiGLU, W's rows interleaved value/gate) C[i][j/2] = v_j sigmoid(v_{j+1})
+ *   for even j. cin may be C itself (a residual accumulated in place). A fixed
+ *   summation order: results repeat bit for bit.
+ * Replaces the reference's fused GEMMs (src/fused_gemm_hip.cpp: linear_fused,
+ * silu_in_fused, swiglu_in_fused; src/ops.hpp:84-96). */
+PET_ATTN_API int pet_linear_fused(int M, int N, int K, const float* A, int64_t lda, const float* W, int64_t ldw,
+                                  float* C, int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                  int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
+
 /* Bytes of device workspace the model holds now (its high-water mark). */
 PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
 

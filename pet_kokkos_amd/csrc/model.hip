@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -34,6 +35,10 @@ int gemm_nn(float* in_adj, int64_t ldi, const float* out_adj, int64_t ldo, const
 int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, const float* out_adj, int64_t ldg,
                            const float* in, int64_t ldi, const float* weight, int ln, int n_node, float beta_node,
                            float beta_edge, const int* live_off, hipStream_t st);
+// gemm.hip: C = epilogue(A B^T)
+int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                      int64_t ldc, const float* row_scale, const float* bias, const float* cin, int64_t ldcin,
+                      float beta, float* pre, int64_t ldpre, int act, hipStream_t st);
 
 namespace pet_model_impl {
 
@@ -377,6 +382,20 @@ struct pet_model {
 
 namespace {
 
+// Which forward dense layers take this library's fused GEMM (gemm.hip) instead
+// of rocBLAS: 0 none (the default), 1 all, 2 those with at most 4096 rows.
+// Measured on MI355X (C2 / C2-residual / C5 energy+forces, ms): 3.45 / 2.67 /
+// 281 with rocBLAS, 3.50 / 2.68 / 281 with mode 2, 3.96 / 3.00 / 311 with mode
+// 1: its main loop reaches 72% of the fp32 matrix peak at K = 1024 where
+// rocBLAS reaches 90%. PET_MODEL_GEMM selects, read once.
+bool own_gemm(int M, int K) {
+  static const int mode = [] {
+    const char* v = std::getenv("PET_MODEL_GEMM");
+    return v ? std::atoi(v) : 0;
+  }();
+  return K % 16 == 0 && (mode == 1 || (mode == 2 && M <= 4096));
+}
+
 // out[M, Nout] = in W^T + b (b may be null)
 void linear(pet_model& md, float* out, const float* in, int M, int K, const std::string& key, hipStream_t st,
             bool bias = true) {
@@ -384,6 +403,10 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   if (M == 0) return;
   const float* b = bias ? md.p(key + ".bias") : nullptr;
+  if (own_gemm(M, K)) {
+    ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
+    return;
+  }
   hipLaunchKernelGGL(fill_rows_kernel, grid_for(int64_t(M) * W.rows), dim3(256), 0, st, out, b, int64_t(M), W.rows);
   launched();
   ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
@@ -392,7 +415,13 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
 void linear_acc(pet_model& md, float* out, const float* in, int M, int K, const std::string& key, hipStream_t st) {
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
-  if (M) ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
+  if (M == 0) return;
+  if (own_gemm(M, K)) {
+    ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, nullptr, out, W.rows, 1.f, nullptr, 0, 0,
+                         st));
+    return;
+  }
+  ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
 }
 // in_adj[M, K] = out_adj W + beta in_adj
 void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const std::string& key, float beta,
@@ -404,7 +433,13 @@ void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const
 void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const std::string& key, hipStream_t st) {
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
-  if (M) ok(gemm_nt(z, W.rows, in, K, W.p, M, W.rows, K, 0.0f, st));
+  if (M == 0) return;
+  if (own_gemm(M, K)) {
+    ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, z, W.rows, nullptr, nullptr, nullptr, 0, 0.f, nullptr, 0, 0,
+                         st));
+    return;
+  }
+  ok(gemm_nt(z, W.rows, in, K, W.p, M, W.rows, K, 0.0f, st));
 }
 // out = silu(z + b) of linear_pre's z under `key`
 void silu(pet_model& md, float* out, const float* z, int64_t R, const std::string& key, hipStream_t st) {
