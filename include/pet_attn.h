@@ -108,6 +108,23 @@ PET_ATTN_API int pet_attn_bwd(const pet_attn_shape* shape, const float* qkv, int
 
 /* ---- runs of atoms: the kernels of attention_chunked / _bwd_chunked ------ */
 
+/* pet_attn_fwd / pet_attn_bwd on qkv given as raw + transform: the attention
+ * reads qkv[r][j] * row_scale[r] + bias[j] (row_scale [T] and bias [3D] each
+ * may be NULL), so a QKV projection can leave its row scale and bias to the
+ * attention: with qkv = tokens (W_in diag(norm_w))^T and row_scale = 1/rms(token),
+ * this is the RMSNorm + input linear + attention of the reference's layer
+ * without the normed tokens or a bias pass in memory. qkv_adj is the adjoint of
+ * the transformed qkv. No counterpart in the reference (its attention reads a
+ * finished qkv); the fused QKV projection's consumer (src/feedforward.cpp:107-123). */
+PET_ATTN_API int pet_attn_fwd_xf(const pet_attn_shape* shape, const float* qkv, int64_t ldq, const float* row_scale,
+                                 const float* bias, const int* off, const float* cf_seq, int64_t ldc, float* merged,
+                                 int64_t ldm, float* ml, void* stream);
+PET_ATTN_API int pet_attn_bwd_xf(const pet_attn_shape* shape, const float* qkv, int64_t ldq, const float* row_scale,
+                                 const float* bias, const int* off, const float* dmerged, int64_t ldg,
+                                 const float* merged, int64_t ldm, const float* ml, const float* cf_seq, int64_t ldc,
+                                 float* qkv_adj, int64_t lda, float* cfh, float* cf_seq_adj, int64_t ldca,
+                                 void* stream);
+
 /* The forward of atoms [n0, n1) only, whose token rows come as a chunk qkv
  * [Tc, 3D]: the run's own rows first (atom n at row n - n0), then its edges'
  * (edge k at row (n1 - n0) + k - e0), e0 = off[n0], Tc = (n1 - n0) +

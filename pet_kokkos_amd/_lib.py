@@ -20,6 +20,8 @@ EXPORTS = (
     "pet_attn_zero_dead",
     "pet_attn_fwd",
     "pet_attn_bwd",
+    "pet_attn_fwd_xf",
+    "pet_attn_bwd_xf",
     "pet_attention",
     "pet_attention_bwd_workspace",
     "pet_attention_bwd",
@@ -113,6 +115,11 @@ def load() -> ctypes.CDLL:
     lib.pet_attn_bwd.restype = ctypes.c_int
     lib.pet_attn_bwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P]
     lib.pet_attn_fwd_run.restype = ctypes.c_int
+    lib.pet_attn_fwd_xf.restype = ctypes.c_int
+    lib.pet_attn_fwd_xf.argtypes = [sp, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _P]
+    lib.pet_attn_bwd_xf.restype = ctypes.c_int
+    lib.pet_attn_bwd_xf.argtypes = [sp, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P,
+                                    _I64, _P]
     lib.pet_attn_fwd_run.argtypes = [sp, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
     lib.pet_attn_bwd_run.restype = ctypes.c_int
     lib.pet_attn_bwd_run.argtypes = [sp, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P,

@@ -109,6 +109,34 @@ __device__ __forceinline__ void gmem_get(const float* p, float* out) {
   }
 }
 
+// An affine map of qkv applied as it is loaded: row r's values scaled by
+// rs[r], then column j's bias b[j] added (either may be null). With qkv the
+// product of raw tokens and the input linear whose weight has the RMSNorm
+// weight folded in, rs = 1/rms(token) and b the linear's bias make it
+// norm(tokens) W^T + b without the normed tokens or the bias pass ever
+// touching memory: the QKV projection's epilogue, fused into its consumer.
+struct QkvXf {
+  const float* rs = nullptr;
+  const float* b = nullptr;
+};
+template <int W, bool XF>
+__device__ __forceinline__ void qkv_get(const float* qkv, int64_t ldq, size_t r, int col, const QkvXf& xf,
+                                        float* out) {
+  gmem_get<W>(qkv + r * ldq + col, out);
+  if constexpr (!XF) return;
+  if (xf.rs) {
+    const float sc = xf.rs[r];
+#pragma unroll
+    for (int t = 0; t < W; ++t) out[t] *= sc;
+  }
+  if (xf.b) {
+    float bb[W];
+    gmem_get<W>(xf.b + col, bb);
+#pragma unroll
+    for (int t = 0; t < W; ++t) out[t] += bb[t];
+  }
+}
+
 // One work item, an (atom, head), of a run of atoms [n0, n1). The atom's
 // tokens are rows of two matrices: the whole token matrix (merged, and the
 // per-slot arrays), and the run's chunk (qkv, dO, qkv_adj), which holds the
@@ -267,12 +295,12 @@ __device__ __forceinline__ void fwd_store(const Atom& at, const FwdOut<HD>& out,
 
 // One item per workgroup: the item's K, V and q loaded into registers and
 // staged in LDS, one barrier, then its forward.
-template <int HD, int MAXT>
+template <int HD, int MAXT, bool XF = false>
 __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                         const int* __restrict__ off, int N, int n0, int64_t eb,
                                                         int S, int H, float sc, const float* __restrict__ cf_seq,
                                                         int64_t ldc, float* __restrict__ merged, int64_t ldm,
-                                                        float* __restrict__ ml) {
+                                                        float* __restrict__ ml, QkvXf xf) {
   constexpr int W = HD / 4, P = Lds<HD>::P;
   extern __shared__ float lds[];
   const int NW = blockDim.x >> 6, R = NW * 16, D = H * HD;
@@ -290,9 +318,9 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
     const bool real = i < at.cnt;
     if (real) {
       const size_t r = at.row(i);
-      gmem_get<W>(qkv + r * ldq + at.h * HD + g * W, q);
-      gmem_get<W>(qkv + r * ldq + D + at.h * HD + g * W, k);
-      gmem_get<W>(qkv + r * ldq + 2 * D + at.h * HD + g * W, v);
+      qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
+      qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
+      qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
     } else {
 #pragma unroll
       for (int t = 0; t < W; ++t) q[t] = k[t] = v[t] = 0.f;
@@ -414,11 +442,11 @@ struct BwdOut {
 };
 
 // One item's backward from the staged Q, K, dO (and V) and log cf.
-template <int HD>
+template <int HD, bool XF>
 __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const float* Ks, const float* Gs,
                                          const float* Vs, const float* lcf, float* Tb, int nbuf, int vlds,
                                          const float* oo, float mi, float li, const float* __restrict__ qkv,
-                                         int64_t ldq, int H, float sc, BwdOut<HD>& out) {
+                                         int64_t ldq, const QkvXf& xf, int H, float sc, BwdOut<HD>& out) {
   constexpr int W = HD / 4, DT = HD / 16, P = Lds<HD>::P, TP = Lds<HD>::TP, TILE = 16 * TP;
   const int NW = blockDim.x >> 6, D = H * HD;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
@@ -460,7 +488,7 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
       if (v_staged)
         lds_get<W>(Vs + (16 * J + c) * P + g * W, v);
       else if (16 * J + c < at.cnt)
-        gmem_get<W>(qkv + at.row(16 * J + c) * ldq + 2 * D + at.h * HD + g * W, v);  // chunk rows
+        qkv_get<W, XF>(qkv, ldq, at.row(16 * J + c), 2 * D + at.h * HD + g * W, xf, v);  // chunk rows
       else
 #pragma unroll
         for (int t = 0; t < W; ++t) v[t] = 0.f;
@@ -559,7 +587,7 @@ __device__ __forceinline__ void bwd_store(const Atom& at, const BwdOut<HD>& out,
 
 // One item per workgroup: the item's slices, its own rows' O and statistics
 // loaded into registers, staged in LDS, one barrier, then its backward.
-template <int HD, int MAXT>
+template <int HD, int MAXT, bool XF = false>
 __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                         const int* __restrict__ off, int N, int n0, int64_t eb,
                                                         int S, int H, float sc, const float* __restrict__ dmerged,
@@ -567,7 +595,7 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
                                                         const float* __restrict__ ml,
                                                         const float* __restrict__ cf_seq, int64_t ldc,
                                                         float* __restrict__ qkv_adj, int64_t lda,
-                                                        float* __restrict__ cfh, int nbuf, int vlds) {
+                                                        float* __restrict__ cfh, int nbuf, int vlds, QkvXf xf) {
   constexpr int W = HD / 4, P = Lds<HD>::P;
   extern __shared__ float lds[];
   const int NW = blockDim.x >> 6, R = NW * 16, D = H * HD;
@@ -590,10 +618,10 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
     const bool real = i < at.cnt;
     if (real) {
       const size_t r = at.row(i);
-      gmem_get<W>(qkv + r * ldq + at.h * HD + g * W, q);
-      gmem_get<W>(qkv + r * ldq + D + at.h * HD + g * W, k);
+      qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
+      qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
       gmem_get<W>(dmerged + r * ldg + at.h * HD + g * W, go);
-      if (vlds) gmem_get<W>(qkv + r * ldq + 2 * D + at.h * HD + g * W, v);
+      if (vlds) qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
       gmem_get<W>(merged + at.grow(i) * ldm + at.h * HD + g * W, oo);  // the whole's rows
       const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
       mi = m2[0], li = m2[1];
@@ -613,7 +641,7 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
     if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
   }
   BwdOut<HD> out;
-  bwd_item<HD>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, H, sc, out);
+  bwd_item<HD, XF>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, xf, H, sc, out);
   bwd_store<HD>(at, out, S, H, sc, qkv_adj, lda, cfh);
 }
 
@@ -694,7 +722,7 @@ void allow_lds(K k, size_t bytes) {
 // The forward over atoms [n0, n1), qkv a chunk whose edge 0 is row eb.
 template <int HD>
 int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
-               const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, hipStream_t st) {
+               const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st) {
   const int NW = waves_for(sh.slots);
   const size_t bytes = sizeof(float) * Lds<HD>::fwd_floats(NW);
   if (bytes > size_t(max_lds_bytes())) return PET_ATTN_ESLOTS;
@@ -704,17 +732,19 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   if constexpr (HD <= 64) {
     const int threads = 64 * ((sh.slots + 63) / 64);
     const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
-    if (choice == 3 && threads <= 256 && vb <= size_t(max_lds_bytes())) {
+    if (choice == 3 && !xf.rs && !xf.b && threads <= 256 && vb <= size_t(max_lds_bytes())) {
       allow_lds(attn_fwd_valu_kernel<HD>, vb);
       hipLaunchKernelGGL(attn_fwd_valu_kernel<HD>, dim3(unsigned(items)), dim3(threads), vb, st, qkv, ldq, off,
                          sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml);
       return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
     }
   }
-  auto k = NW <= 8 ? attn_fwd_kernel<HD, 512> : attn_fwd_kernel<HD, 1024>;
+  const bool x = xf.rs || xf.b;
+  auto k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true> : attn_fwd_kernel<HD, 512, false>)
+                   : (x ? attn_fwd_kernel<HD, 1024, true> : attn_fwd_kernel<HD, 1024, false>);
   allow_lds(k, bytes);
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
-                     sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml);
+                     sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -740,9 +770,11 @@ int resident_wgs(const void* k, int NW, size_t lds) {
 template <int HD>
 int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
                const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
-               const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, hipStream_t st) {
+               const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st) {
   const int NW = waves_for(sh.slots);
-  auto k = NW <= 8 ? attn_bwd_kernel<HD, 512> : attn_bwd_kernel<HD, 1024>;
+  const bool x = xf.rs || xf.b;
+  auto k = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true> : attn_bwd_kernel<HD, 512, false>)
+                   : (x ? attn_bwd_kernel<HD, 1024, true> : attn_bwd_kernel<HD, 1024, false>);
   // The fullest layout that fits (V staged and two tile buffers, else V from
   // global memory, else also one tile buffer) -- unless it leaves one
   // workgroup a CU and a leaner one fits more: then the leaner. Measured on
@@ -779,7 +811,7 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   allow_lds(k, bytes);
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
                      sh.slots, sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh,
-                     nbuf, vlds);
+                     nbuf, vlds, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -856,8 +888,11 @@ int pet_attn_max_slots(int head_dim) {
   return e < 0 ? -e : 0;
 }
 
-int pet_attn_fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
-                     const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, void* stream) {
+}  // extern "C"
+
+namespace {
+int fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
+            const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, void* stream) {
   if (int e = check_shape(sh)) return e;
   if (int e = check_run(sh, n0, n1, e0)) return e;
   const int64_t D = int64_t(sh->heads) * sh->head_dim;
@@ -868,13 +903,13 @@ int pet_attn_fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const flo
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t eb = int64_t(n1 - n0) - e0;
   return with_head_dim(sh->head_dim, [&](auto hd) {
-    return launch_fwd<decltype(hd)::value>(*sh, n0, n1, eb, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, st);
+    return launch_fwd<decltype(hd)::value>(*sh, n0, n1, eb, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, xf, st);
   });
 }
 
-int pet_attn_bwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
-                     const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
-                     const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, void* stream) {
+int bwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
+            const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml, const float* cf_seq,
+            int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, void* stream) {
   if (int e = check_shape(sh)) return e;
   if (int e = check_run(sh, n0, n1, e0)) return e;
   const int64_t D = int64_t(sh->heads) * sh->head_dim;
@@ -888,8 +923,46 @@ int pet_attn_bwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const flo
   const int64_t eb = int64_t(n1 - n0) - e0;
   return with_head_dim(sh->head_dim, [&](auto hd) {
     return launch_bwd<decltype(hd)::value>(*sh, n0, n1, eb, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq,
-                                           ldc, qkv_adj, lda, cfh, st);
+                                           ldc, qkv_adj, lda, cfh, xf, st);
   });
+}
+
+int fwd_whole(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int* off, const float* cf_seq,
+              int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, void* stream) {
+  if (int e = check_shape(sh)) return e;
+  if (sh->n_atoms == 0) return PET_ATTN_OK;
+  // the whole matrix is the run of every atom: own rows first, edge 0 at row N
+  if (int e = fwd_run(sh, 0, sh->n_atoms, 0, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, xf, stream)) return e;
+  return zero_dead(merged, ldm, sh->heads * sh->head_dim, *sh, off, reinterpret_cast<hipStream_t>(stream));
+}
+
+int bwd_whole(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int* off, const float* dmerged,
+              int64_t ldg, const float* merged, int64_t ldm, const float* ml, const float* cf_seq, int64_t ldc,
+              float* qkv_adj, int64_t lda, float* cfh, float* cf_seq_adj, int64_t ldca, QkvXf xf, void* stream) {
+  if (int e = check_shape(sh)) return e;
+  if (sh->n_atoms == 0) return PET_ATTN_OK;
+  if (!cf_seq_adj || ldca < sh->slots) return PET_ATTN_EINVAL;
+  if (int e = bwd_run(sh, 0, sh->n_atoms, 0, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda,
+                      cfh, xf, stream))
+    return e;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int e = cf_adjoint(*sh, cfh, cf_seq, ldc, cf_seq_adj, ldca, st)) return e;
+  return zero_dead(qkv_adj, lda, 3 * sh->heads * sh->head_dim, *sh, off, st);
+}
+}  // namespace
+
+extern "C" {
+
+int pet_attn_fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
+                     const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, void* stream) {
+  return fwd_run(sh, n0, n1, e0, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, QkvXf{}, stream);
+}
+
+int pet_attn_bwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
+                     const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
+                     const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, void* stream) {
+  return bwd_run(sh, n0, n1, e0, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh,
+                 QkvXf{}, stream);
 }
 
 int pet_attn_cf_adjoint(const pet_attn_shape* sh, const float* cfh, const float* cf_seq, int64_t ldc,
@@ -907,25 +980,28 @@ int pet_attn_zero_dead(const pet_attn_shape* sh, float* x, int64_t ld, int width
 
 int pet_attn_fwd(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int* off, const float* cf_seq,
                  int64_t ldc, float* merged, int64_t ldm, float* ml, void* stream) {
-  if (int e = check_shape(sh)) return e;
-  if (sh->n_atoms == 0) return PET_ATTN_OK;
-  // the whole matrix is the run of every atom: own rows first, edge 0 at row N
-  if (int e = pet_attn_fwd_run(sh, 0, sh->n_atoms, 0, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, stream)) return e;
-  return zero_dead(merged, ldm, sh->heads * sh->head_dim, *sh, off, reinterpret_cast<hipStream_t>(stream));
+  return fwd_whole(sh, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, QkvXf{}, stream);
 }
 
 int pet_attn_bwd(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int* off, const float* dmerged,
                  int64_t ldg, const float* merged, int64_t ldm, const float* ml, const float* cf_seq, int64_t ldc,
                  float* qkv_adj, int64_t lda, float* cfh, float* cf_seq_adj, int64_t ldca, void* stream) {
-  if (int e = check_shape(sh)) return e;
-  if (sh->n_atoms == 0) return PET_ATTN_OK;
-  if (!cf_seq_adj || ldca < sh->slots) return PET_ATTN_EINVAL;
-  if (int e = pet_attn_bwd_run(sh, 0, sh->n_atoms, 0, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc,
-                               qkv_adj, lda, cfh, stream))
-    return e;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (int e = cf_adjoint(*sh, cfh, cf_seq, ldc, cf_seq_adj, ldca, st)) return e;
-  return zero_dead(qkv_adj, lda, 3 * sh->heads * sh->head_dim, *sh, off, st);
+  return bwd_whole(sh, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, cf_seq_adj, ldca,
+                   QkvXf{}, stream);
+}
+
+int pet_attn_fwd_xf(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const float* row_scale,
+                    const float* bias, const int* off, const float* cf_seq, int64_t ldc, float* merged, int64_t ldm,
+                    float* ml, void* stream) {
+  return fwd_whole(sh, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, QkvXf{row_scale, bias}, stream);
+}
+
+int pet_attn_bwd_xf(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const float* row_scale,
+                    const float* bias, const int* off, const float* dmerged, int64_t ldg, const float* merged,
+                    int64_t ldm, const float* ml, const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda,
+                    float* cfh, float* cf_seq_adj, int64_t ldca, void* stream) {
+  return bwd_whole(sh, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, cf_seq_adj, ldca,
+                   QkvXf{row_scale, bias}, stream);
 }
 
 }  // extern "C"

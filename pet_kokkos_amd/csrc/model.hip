@@ -35,6 +35,8 @@ int gemm_nn(float* in_adj, int64_t ldi, const float* out_adj, int64_t ldo, const
 int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, const float* out_adj, int64_t ldg,
                            const float* in, int64_t ldi, const float* weight, int ln, int n_node, float beta_node,
                            float beta_edge, const int* live_off, hipStream_t st);
+// rows.hip: RMSNorm's row factors
+int pet_rows_rms_inv(int rows, int width, const float* in, int64_t ldi, float* inv, hipStream_t st);
 // gemm.hip: C = epilogue(A B^T)
 int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                       int64_t ldc, const float* row_scale, const float* bias, const float* cin, int64_t ldcin,
@@ -481,7 +483,7 @@ void fill0(float* x, int64_t n, hipStream_t st) {
 // What one GNN layer keeps for its backward (the reference's LayerSaves,
 // include/pet/model.hpp:183-198), every block's wide activations included.
 struct Block {
-  float *tok, *qkv, *merged, *ml, *eps, *node_res, *pre_c, *pre_e;
+  float *tok, *inv, *qkv, *merged, *ml, *eps, *node_res, *pre_c, *pre_e;
 };
 struct Layer {
   float *cpre, *concat, *cph;
@@ -518,17 +520,19 @@ struct Pass {
       const std::string tl = t(L, a);
       Block& b = sv.b[a];
       b.qkv = md.f(int64_t(T) * 3 * D), b.merged = md.f(int64_t(T) * D), b.ml = md.f(int64_t(N) * md.h.num_heads * S * 2);
-      b.eps = md.f(int64_t(E) * D), b.node_res = md.f(int64_t(N) * Dn);
+      b.eps = md.f(int64_t(E) * D), b.node_res = md.f(int64_t(N) * Dn), b.inv = md.f(T);
       b.pre_c = md.f(int64_t(N) * md.cw), b.pre_e = md.f(int64_t(E) * md.ew);
       float* node_next = md.f(int64_t(N) * Dn);
       float* edge_next = a + 1 < A ? sv.b[a + 1].tok + int64_t(N) * D : out_edge;
       auto scope = md.ws.mark();
       linear(md, b.tok, node_cur, N, Dn, tl + ".center_contraction", st);
-      float* normed = md.f(int64_t(T) * D);
-      norm(md, normed, b.tok, T, D, tl + ".norm_attention", false, st);
-      linear(md, b.qkv, normed, T, D, tl + ".attention.input_linear", st);
-      ok(pet_attn_fwd(&sh, b.qkv, 3 * D, e.off, cf_seq, S, b.merged, D, b.ml, st));
-      float* attn_out = normed;  // normed is consumed
+      // the fused QKV projection: qkv = tok (W_in diag(norm weight))^T, the
+      // attention applying 1/rms and the bias as it loads it
+      ok(pet_rows_rms_inv(T, D, b.tok, D, b.inv, st));
+      linear_pre(md, b.qkv, b.tok, T, D, tl + ".attention.input_linear@fold", st);
+      ok(pet_attn_fwd_xf(&sh, b.qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, cf_seq, S,
+                         b.merged, D, b.ml, st));
+      float* attn_out = md.f(int64_t(T) * D);
       linear(md, attn_out, b.merged, T, D, tl + ".attention.output_linear", st);
       float* node_exp = md.f(int64_t(N) * Dn);
       linear(md, node_exp, attn_out, N, D, tl + ".center_expansion", st);
@@ -638,8 +642,8 @@ struct Pass {
       float* cfh = md.f(int64_t(N) * md.h.num_heads * S);
       float* in_adj = dmerged;
       linear_bwd(md, dmerged, tok_adj, T, tl + ".attention.output_linear", 0.0f, st);
-      ok(pet_attn_bwd(&sh, b.qkv, 3 * D, e.off, dmerged, D, b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh,
-                      cf_seq_adj, S, st));
+      ok(pet_attn_bwd_xf(&sh, b.qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, dmerged, D,
+                         b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh, cf_seq_adj, S, st));
       linear_bwd(md, in_adj, qkv_adj, T, tl + ".attention.input_linear", 0.0f, st);
       // through the norm: atom rows set (input_node's adjoint), edge rows onto edge_adj
       ok(pet_rows_norm_bwd_sink(T, D, tok_adj, D, in_adj, D, b.tok, D, md.p(tl + ".norm_attention.weight"), 0, N,
@@ -771,8 +775,10 @@ struct Pass {
       b.qkv = md.f(int64_t(T) * 3 * D), b.merged = md.f(int64_t(T) * D), b.ml = md.f(int64_t(N) * md.h.num_heads * S * 2);
       b.s1 = md.f(int64_t(T) * D), b.s2 = md.f(int64_t(T) * D), b.pre = md.f(int64_t(T) * F);
       auto scope = md.ws.mark();
-      linear(md, b.qkv, sv.tokens, T, D, tl + ".attention.input_linear", st);
-      ok(pet_attn_fwd(&sh, b.qkv, 3 * D, e.off, cf_seq, S, b.merged, D, b.ml, st));
+      // qkv without its bias, which the attention adds as it loads it
+      linear_pre(md, b.qkv, sv.tokens, T, D, tl + ".attention.input_linear", st);
+      ok(pet_attn_fwd_xf(&sh, b.qkv, 3 * D, nullptr, md.p(tl + ".attention.input_linear.bias"), e.off, cf_seq, S,
+                         b.merged, D, b.ml, st));
       // s1 = tokens + b_out, then += merged W_out^T
       hipLaunchKernelGGL(bias_add_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, b.s1, sv.tokens,
                          md.p(tl + ".attention.output_linear.bias"), int64_t(T), D);
@@ -820,8 +826,8 @@ struct Pass {
       float* qkv_adj = md.f(int64_t(T) * 3 * D);
       float* cfh = md.f(int64_t(N) * md.h.num_heads * S);
       linear_bwd(md, dmerged, tokens_adj, T, tl + ".attention.output_linear", 0.0f, st);
-      ok(pet_attn_bwd(&sh, b.qkv, 3 * D, e.off, dmerged, D, b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh,
-                      cf_seq_adj, S, st));
+      ok(pet_attn_bwd_xf(&sh, b.qkv, 3 * D, nullptr, md.p(tl + ".attention.input_linear.bias"), e.off, dmerged, D,
+                         b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh, cf_seq_adj, S, st));
       linear_bwd(md, tokens_adj, qkv_adj, T, tl + ".attention.input_linear", 1.0f, st);
       md.ws.release(scope);
     }
@@ -964,6 +970,15 @@ struct Loader {
     put(p + ".weight", F2, K, w);
     put(p + ".bias", F2, 1, bi);
   }
+  // a linear's weight with the RMSNorm weight before it folded into its columns
+  // (key@fold): norm(x) W^T = (1/rms(x)) x (W diag(w))^T
+  void fold_norm(const std::string& lin, const std::string& nrm, int rows, int cols) {
+    const pet_model_tensor &W = get(lin + ".weight", rows, cols), &w = get(nrm + ".weight", cols, 0);
+    std::vector<double> f(size_t(rows) * cols);
+    for (int r = 0; r < rows; ++r)
+      for (int c = 0; c < cols; ++c) f[size_t(r) * cols + c] = W.data[size_t(r) * cols + c] * w.data[c];
+    put(lin + "@fold.weight", rows, cols, f);
+  }
   // compress.0 folded (src/model.cpp:236-262): its input is [edge_emb(x4) |
   // species table | input_edge], edge_emb linear in x4 = (v, |v|).
   void fold(int L) {
@@ -1047,6 +1062,7 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
           ld.linear(tl + ".mlp.w_out", D, md->ew);
           continue;
         }
+        ld.fold_norm(tl + ".attention.input_linear", tl + ".norm_attention", 3 * D, D);
         ld.swiglu_in(tl + ".mlp.w_in", md->ew, D);
         ld.linear(tl + ".mlp.w_out", D, md->ew / 2);
         ld.linear(tl + ".center_contraction", D, Dn);

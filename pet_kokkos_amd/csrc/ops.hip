@@ -126,6 +126,8 @@ using namespace pet_attn;
 int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, const float* out_adj, int64_t ldg,
                            const float* in, int64_t ldi, const float* weight, int ln, int n_node, float beta_node,
                            float beta_edge, const int* live_off, hipStream_t st);
+int pet_rows_rms_inv(int rows, int width, const float* in, int64_t ldi, float* inv, hipStream_t st);
+int pet_rows_fold_cols(float* out, const float* w, const float* s, int rows, int cols, hipStream_t st);
 
 namespace {
 
@@ -144,6 +146,51 @@ int layer_input(const pet_attn_shape* sh, float* normed, float* qkv, const float
     beta = 1.0f;
   }
   return gemm_nt(qkv, 3 * D, normed, D, w_in, T, 3 * D, D, beta, st);
+}
+
+// The fused QKV projection for an RMSNorm: inv = 1/rms(tokens), wf = w_in with
+// the norm weight folded into its columns, qkv = tokens wf^T (no bias, no
+// normed tokens); the attention applies inv and b_in as it loads qkv.
+int layer_input_rms(const pet_attn_shape* sh, float* inv, float* wf, float* qkv, const float* tokens, int64_t ldt,
+                    const float* norm_w, const float* w_in, hipStream_t st) {
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  if (int e = pet_rows_rms_inv(T, D, tokens, ldt, inv, st)) return e;
+  if (int e = pet_rows_fold_cols(wf, w_in, norm_w, 3 * D, D, st)) return e;
+  return gemm_nt(qkv, 3 * D, tokens, ldt, wf, T, 3 * D, D, 0.0f, st);
+}
+
+// out = merged w_out^T + b_out
+int output_linear(const pet_attn_shape* sh, float* out, int64_t ldo, const float* merged, const float* w_out,
+                  const float* b_out, hipStream_t st) {
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  float beta = 0.0f;
+  if (b_out) {
+    const int64_t total = int64_t(T) * D;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(fill_bias_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, out, ldo,
+                       b_out, T, D);
+    if (hipGetLastError() != hipSuccess) return PET_ATTN_ELAUNCH;
+    beta = 1.0f;
+  }
+  return gemm_nt(out, ldo, merged, D, w_out, T, D, D, beta, st);
+}
+
+// attention_bwd with qkv given raw + (rs, b) (pet_attn_bwd_xf), workspace as
+// pet_attention_bwd's.
+int attention_bwd_xf(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int d_in, float* cf_seq_adj, int64_t ldca,
+                     const float* out_adj, int64_t ldo, const float* qkv, int64_t ldq, const float* rs,
+                     const float* b, const float* cf_seq, int64_t ldc, const float* w_in, const float* w_out,
+                     const int* off, const float* merged, const float* ml, float beta, char* ws, hipStream_t st) {
+  const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  float* dmerged = reinterpret_cast<float*>(ws);
+  float* qkv_adj = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
+  float* cfh = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D) +
+                                        align256(sizeof(float) * size_t(T) * 3 * D));
+  if (int e = gemm_nn(dmerged, D, out_adj, ldo, w_out, T, D, D, 0.0f, st)) return e;
+  if (int e = pet_attn_bwd_xf(sh, qkv, ldq, rs, b, off, dmerged, D, merged, D, ml, cf_seq, ldc, qkv_adj, 3 * D, cfh,
+                              cf_seq_adj, ldca, st))
+    return e;
+  return gemm_nn(in_adj, ldi, qkv_adj, 3 * D, w_in, T, 3 * D, d_in, beta, st);
 }
 
 }  // namespace
@@ -189,17 +236,9 @@ int pet_attention_bwd(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int 
   if (!workspace || workspace_bytes < pet_attention_bwd_workspace(sh)) return PET_ATTN_EWORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
   if (T == 0) return PET_ATTN_OK;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  float* dmerged = reinterpret_cast<float*>(ws);
-  float* qkv_adj = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
-  float* cfh = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D) +
-                                        align256(sizeof(float) * size_t(T) * 3 * D));
-  if (int e = gemm_nn(dmerged, D, out_adj, ldo, w_out, T, D, D, 0.0f, st)) return e;
-  if (int e = pet_attn_bwd(sh, qkv, ldq, off, dmerged, D, merged, D, ml, cf_seq, ldc, qkv_adj, 3 * D, cfh,
-                           cf_seq_adj, ldca, stream))
-    return e;
-  return gemm_nn(in_adj, ldi, qkv_adj, 3 * D, w_in, T, 3 * D, d_in, beta, st);
+  return attention_bwd_xf(sh, in_adj, ldi, d_in, cf_seq_adj, ldca, out_adj, ldo, qkv, ldq, nullptr, nullptr, cf_seq,
+                          ldc, w_in, w_out, off, merged, ml, beta, static_cast<char*>(workspace),
+                          reinterpret_cast<hipStream_t>(stream));
 }
 
 size_t pet_attention_chunked_workspace(const pet_attn_shape* sh, const int* off_host, int chunk) {
@@ -283,10 +322,12 @@ int pet_attention_bwd_chunked(const pet_attn_shape* sh, float* in_adj, int64_t l
   return PET_ATTN_OK;
 }
 
+// [T, D] normed tokens (or their adjoint) | [T, 3D] qkv | [T] 1/rms | [3D, D] folded w_in | the backward's
 size_t pet_attention_layer_workspace(const pet_attn_shape* sh) {
   if (!sh) return 0;
   const size_t D = size_t(sh->heads) * sh->head_dim, T = size_t(sh->n_rows);
-  return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) + pet_attention_bwd_workspace(sh);
+  return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) + align256(sizeof(float) * T) +
+         align256(sizeof(float) * 3 * D * D) + pet_attention_bwd_workspace(sh);
 }
 
 int pet_attention_layer(const pet_attn_shape* sh, float* out, int64_t ldo, const float* tokens, int64_t ldt,
@@ -301,8 +342,16 @@ int pet_attention_layer(const pet_attn_shape* sh, float* out, int64_t ldo, const
   if (T == 0) return PET_ATTN_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  const size_t a0 = align256(sizeof(float) * size_t(T) * D), a1 = align256(sizeof(float) * size_t(T) * 3 * D),
+               a2 = align256(sizeof(float) * size_t(T));
   float* normed = reinterpret_cast<float*>(ws);
-  float* qkv = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
+  float* qkv = reinterpret_cast<float*>(ws + a0);
+  if (!norm_b) {  // RMSNorm: the fused projection, norm and bias applied by the attention
+    float *inv = reinterpret_cast<float*>(ws + a0 + a1), *wf = reinterpret_cast<float*>(ws + a0 + a1 + a2);
+    if (int e = layer_input_rms(sh, inv, wf, qkv, tokens, ldt, norm_w, w_in, st)) return e;
+    if (int e = pet_attn_fwd_xf(sh, qkv, 3 * D, inv, b_in, off, cf_seq, ldc, merged, D, ml, stream)) return e;
+    return output_linear(sh, out, ldo, merged, w_out, b_out, st);
+  }
   if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) return e;
   return pet_attention(sh, out, ldo, qkv, 3 * D, cf_seq, ldc, w_out, b_out, off, merged, ml, stream);
 }
@@ -320,13 +369,24 @@ int pet_attention_layer_bwd(const pet_attn_shape* sh, float* tokens_adj, int64_t
   if (T == 0) return PET_ATTN_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  const size_t a0 = align256(sizeof(float) * size_t(T) * D), a1 = align256(sizeof(float) * size_t(T) * 3 * D);
+  const size_t a0 = align256(sizeof(float) * size_t(T) * D), a1 = align256(sizeof(float) * size_t(T) * 3 * D),
+               a2 = align256(sizeof(float) * size_t(T)), a3 = align256(sizeof(float) * 3 * size_t(D) * D);
   float* normed = reinterpret_cast<float*>(ws);
   float* qkv = reinterpret_cast<float*>(ws + a0);
-  if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) return e;
+  float* inv = nullptr;
+  const float* bq = nullptr;
+  if (!norm_b) {  // RMSNorm: the fused projection (as the forward's)
+    inv = reinterpret_cast<float*>(ws + a0 + a1);
+    if (int e = layer_input_rms(sh, inv, reinterpret_cast<float*>(ws + a0 + a1 + a2), qkv, tokens, ldt, norm_w, w_in,
+                                st))
+      return e;
+    bq = b_in;
+  } else if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) {
+    return e;
+  }
   // the normed tokens' adjoint overwrites them: the backward reads only qkv
-  if (int e = pet_attention_bwd(sh, normed, D, D, cf_seq_adj, ldca, out_adj, ldo, qkv, 3 * D, cf_seq, ldc, w_in,
-                                w_out, off, merged, ml, 0.0f, ws + a0 + a1, workspace_bytes - a0 - a1, stream))
+  if (int e = attention_bwd_xf(sh, normed, D, D, cf_seq_adj, ldca, out_adj, ldo, qkv, 3 * D, inv, bq, cf_seq, ldc,
+                               w_in, w_out, off, merged, ml, 0.0f, ws + a0 + a1 + a2 + a3, st))
     return e;
   return pet_rows_norm_bwd_sink(T, D, tokens_adj, lda, normed, D, tokens, ldt, norm_w, norm_b != nullptr,
                                 sh->n_atoms, 0.0f, 1.0f, off, st);

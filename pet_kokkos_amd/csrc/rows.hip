@@ -144,6 +144,32 @@ __global__ void cf_seq_kernel(int N, int S, const int* __restrict__ off, const f
   cf_seq[int64_t(n) * ldc + s] = s == 0 ? 1.0f : s < cnt ? cut[e0 + s - 1] : 0.0f;
 }
 
+// inv[r] = 1 / sqrt(mean(in[r]^2) + eps): RMSNorm's row factor, the same
+// reductions and arithmetic as norm_fwd_kernel's.
+template <int V>
+__global__ void __launch_bounds__(256) rms_inv_kernel(int rows, int width, const float* __restrict__ in, int64_t ldi,
+                                                      float* __restrict__ inv) {
+  const int r = blockIdx.x * 4 + int(threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float* x_row = in + int64_t(r) * ldi;
+  float v = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int d = l + 64 * j;
+    const float x = d < width ? x_row[d] : 0.0f;
+    if (d < width) v += x * x;
+  }
+  v = wave_sum(v);
+  if (l == 0) inv[r] = 1.0f / sqrtf(v / width + kRmsEps);
+}
+
+// out[o][d] = w[o][d] * s[d]: a norm weight folded into the linear after it.
+__global__ void fold_cols_kernel(float* __restrict__ out, const float* __restrict__ w, const float* __restrict__ s,
+                                 int rows, int cols) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < int64_t(rows) * cols) out[i] = w[i] * s[i % cols];
+}
+
 }  // namespace pet_rows
 
 using namespace pet_rows;
@@ -163,6 +189,23 @@ int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, cons
                        out_adj, ldg, in, ldi, weight, ln, n_node, beta_node, beta_edge, live_off);
     return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
   });
+}
+
+int pet_rows_rms_inv(int rows, int width, const float* in, int64_t ldi, float* inv, hipStream_t st) {
+  if (rows < 0 || width < 1 || !in || !inv || ldi < width) return PET_ATTN_EINVAL;
+  if (rows == 0) return PET_ATTN_OK;
+  return with_lanes(width, [&](auto vc) {
+    constexpr int V = decltype(vc)::value;
+    hipLaunchKernelGGL(rms_inv_kernel<V>, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, st, rows, width, in, ldi, inv);
+    return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
+  });
+}
+
+int pet_rows_fold_cols(float* out, const float* w, const float* s, int rows, int cols, hipStream_t st) {
+  const int64_t n = int64_t(rows) * cols;
+  if (n == 0) return PET_ATTN_OK;
+  hipLaunchKernelGGL(fold_cols_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, out, w, s, rows, cols);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
 extern "C" {
