@@ -170,6 +170,178 @@ __global__ void fold_cols_kernel(float* __restrict__ out, const float* __restric
   if (i < int64_t(rows) * cols) out[i] = w[i] * s[i % cols];
 }
 
+// ---- the vectorised row passes ----------------------------------------------
+//
+// For a width that is a multiple of 4 (rows 16-byte aligned): LPR lanes a row
+// (16, 32 or 64: 64 / LPR rows a wavefront), lane t of a row holding float4
+// chunks t + LPR j, j < C4, so every load is a 16-byte one and a narrow row
+// (128 floats: two a wavefront) does not leave half a wavefront idle. The
+// row's sums are a butterfly over its LPR lanes; the arithmetic per value is
+// that of the scalar kernels above.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <int LPR, int C4>
+__global__ void __launch_bounds__(256) norm_fwd4_kernel(int rows, int width, float* __restrict__ out, int64_t ldo,
+                                                        const float* __restrict__ in, int64_t ldi,
+                                                        const float* __restrict__ weight,
+                                                        const float* __restrict__ bias) {
+  constexpr int RPW = 64 / LPR;
+  const int l = threadIdx.x & 63, t = l % LPR;
+  const int r = (blockIdx.x * 4 + int(threadIdx.x >> 6)) * RPW + l / LPR;
+  if (r >= rows) return;  // whole row groups exit together: the butterflies stay within live lanes
+  const bool ln = bias != nullptr;
+  const int w4 = width >> 2;
+  const float4* x_row = reinterpret_cast<const float4*>(in + int64_t(r) * ldi);
+  float4 x[C4];
+#pragma unroll
+  for (int j = 0; j < C4; ++j) {
+    const int q = t + LPR * j;
+    x[j] = q < w4 ? x_row[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float mu = 0.0f;
+  if (ln) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < C4; ++j) s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    mu = row_sum<LPR>(s) / width;
+  }
+  float v = 0.0f;
+#pragma unroll
+  for (int j = 0; j < C4; ++j)
+    if (t + LPR * j < w4) {
+      const float a = x[j].x - mu, b = x[j].y - mu, c = x[j].z - mu, d = x[j].w - mu;
+      v += (a * a + b * b) + (c * c + d * d);
+    }
+  v = row_sum<LPR>(v);
+  const float inv = 1.0f / sqrtf(v / width + (ln ? kLnEps : kRmsEps));
+  float4* o_row = reinterpret_cast<float4*>(out + int64_t(r) * ldo);
+  const float4* w4p = reinterpret_cast<const float4*>(weight);
+  const float4* b4p = reinterpret_cast<const float4*>(bias);
+#pragma unroll
+  for (int j = 0; j < C4; ++j) {
+    const int q = t + LPR * j;
+    if (q < w4) {
+      const float4 wq = w4p[q], bq = ln ? b4p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      o_row[q] = make_float4((x[j].x - mu) * inv * wq.x + bq.x, (x[j].y - mu) * inv * wq.y + bq.y,
+                             (x[j].z - mu) * inv * wq.z + bq.z, (x[j].w - mu) * inv * wq.w + bq.w);
+    }
+  }
+}
+
+template <int LPR, int C4>
+__global__ void __launch_bounds__(256) norm_bwd4_kernel(int rows, int width, float* __restrict__ in_adj, int64_t lda,
+                                                        const float* __restrict__ out_adj, int64_t ldg,
+                                                        const float* __restrict__ in, int64_t ldi,
+                                                        const float* __restrict__ weight, int ln, int n_node,
+                                                        float beta_node, float beta_edge,
+                                                        const int* __restrict__ live_off) {
+  constexpr int RPW = 64 / LPR;
+  const int l = threadIdx.x & 63, t = l % LPR;
+  const int r = (blockIdx.x * 4 + int(threadIdx.x >> 6)) * RPW + l / LPR;
+  if (r >= rows) return;
+  if (live_off && r >= n_node + live_off[n_node]) return;  // a capacity's dead row: no sink
+  const float beta = r < n_node ? beta_node : beta_edge;
+  const int w4 = width >> 2;
+  const float4* x_row = reinterpret_cast<const float4*>(in + int64_t(r) * ldi);
+  const float4* g_row = reinterpret_cast<const float4*>(out_adj + int64_t(r) * ldg);
+  const float4* w4p = reinterpret_cast<const float4*>(weight);
+  float4 x[C4], ga[C4], wq[C4];
+#pragma unroll
+  for (int j = 0; j < C4; ++j) {
+    const int q = t + LPR * j;
+    const bool in_range = q < w4;
+    x[j] = in_range ? x_row[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    ga[j] = in_range ? g_row[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    wq[j] = in_range ? w4p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float mu = 0.0f;
+  if (ln) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < C4; ++j) s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    mu = row_sum<LPR>(s) / width;
+  }
+  float sq = 0.0f, sg = 0.0f, sgx = 0.0f;
+  auto acc1 = [&](float xv, float g, float w) {
+    const float xc = xv - mu, gw = g * w;
+    sq += xc * xc;
+    sg += gw;
+    sgx += gw * xc;
+  };
+#pragma unroll
+  for (int j = 0; j < C4; ++j)
+    if (t + LPR * j < w4) {  // a masked chunk's zeros would add mu^2 to the variance
+      acc1(x[j].x, ga[j].x, wq[j].x), acc1(x[j].y, ga[j].y, wq[j].y);
+      acc1(x[j].z, ga[j].z, wq[j].z), acc1(x[j].w, ga[j].w, wq[j].w);
+    }
+  sq = row_sum<LPR>(sq), sg = row_sum<LPR>(sg), sgx = row_sum<LPR>(sgx);
+  const float inv = 1.0f / sqrtf(sq / width + (ln ? kLnEps : kRmsEps));
+  const float mg = ln ? sg / width : 0.0f, mgx = sgx * inv / width;
+  auto grad = [&](float xv, float g, float w) {
+    const float a = fmaf(g, w, -mg), b = mul_rn(xv - mu, inv);
+    return mul_rn(inv, fmaf(-b, mgx, a));
+  };
+  float4* a_row = reinterpret_cast<float4*>(in_adj + int64_t(r) * lda);
+#pragma unroll
+  for (int j = 0; j < C4; ++j) {
+    const int q = t + LPR * j;
+    if (q < w4) {
+      float4 gq = make_float4(grad(x[j].x, ga[j].x, wq[j].x), grad(x[j].y, ga[j].y, wq[j].y),
+                              grad(x[j].z, ga[j].z, wq[j].z), grad(x[j].w, ga[j].w, wq[j].w));
+      if (beta != 0.0f) {
+        const float4 o = a_row[q];
+        gq = make_float4(beta * o.x + gq.x, beta * o.y + gq.y, beta * o.z + gq.z, beta * o.w + gq.w);
+      }
+      a_row[q] = gq;
+    }
+  }
+}
+
+template <int LPR, int C4>
+__global__ void __launch_bounds__(256) rms_inv4_kernel(int rows, int width, const float* __restrict__ in, int64_t ldi,
+                                                       float* __restrict__ inv) {
+  constexpr int RPW = 64 / LPR;
+  const int l = threadIdx.x & 63, t = l % LPR;
+  const int r = (blockIdx.x * 4 + int(threadIdx.x >> 6)) * RPW + l / LPR;
+  if (r >= rows) return;
+  const int w4 = width >> 2;
+  const float4* x_row = reinterpret_cast<const float4*>(in + int64_t(r) * ldi);
+  float v = 0.0f;
+#pragma unroll
+  for (int j = 0; j < C4; ++j) {
+    const int q = t + LPR * j;
+    if (q < w4) {
+      const float4 x = x_row[q];
+      v += (x.x * x.x + x.y * x.y) + (x.z * x.z + x.w * x.w);
+    }
+  }
+  v = row_sum<LPR>(v);
+  if (t == 0) inv[r] = 1.0f / sqrtf(v / width + kRmsEps);
+}
+
+// f(lpr, c4) for a vectorisable width (a multiple of 4, <= 2048), rows a
+// workgroup = 4 * 64 / lpr; -1 if the width does not vectorise.
+template <class F>
+int with_vec(int width, F&& f) {
+  const int w4 = width / 4;
+  if (width % 4 || w4 < 1 || w4 > 512) return -1;
+  using std::integral_constant;
+  if (w4 <= 16) return f(integral_constant<int, 16>{}, integral_constant<int, 1>{});
+  if (w4 <= 32) return f(integral_constant<int, 32>{}, integral_constant<int, 1>{});
+  if (w4 <= 64) return f(integral_constant<int, 64>{}, integral_constant<int, 1>{});
+  if (w4 <= 128) return f(integral_constant<int, 64>{}, integral_constant<int, 2>{});
+  if (w4 <= 256) return f(integral_constant<int, 64>{}, integral_constant<int, 4>{});
+  return f(integral_constant<int, 64>{}, integral_constant<int, 8>{});
+}
+inline bool aligned16(const void* p, int64_t ld) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0;
+}
+
 }  // namespace pet_rows
 
 using namespace pet_rows;
@@ -183,6 +355,16 @@ int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, cons
   if (rows < 0 || width < 1) return PET_ATTN_EINVAL;
   if (!in_adj || !out_adj || !in || !weight || lda < width || ldg < width || ldi < width) return PET_ATTN_EINVAL;
   if (rows == 0) return PET_ATTN_OK;
+  if (aligned16(in_adj, lda) && aligned16(out_adj, ldg) && aligned16(in, ldi) && aligned16(weight, 4)) {
+    const int e = with_vec(width, [&](auto lc, auto cc) {
+      constexpr int LPR = decltype(lc)::value, C4 = decltype(cc)::value, RPB = 4 * (64 / LPR);
+      hipLaunchKernelGGL((norm_bwd4_kernel<LPR, C4>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, rows,
+                         width, in_adj, lda, out_adj, ldg, in, ldi, weight, ln, n_node, beta_node, beta_edge,
+                         live_off);
+      return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
+    });
+    if (e >= 0) return e;
+  }
   return with_lanes(width, [&](auto vc) {
     constexpr int V = decltype(vc)::value;
     hipLaunchKernelGGL(norm_bwd_kernel<V>, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, st, rows, width, in_adj, lda,
@@ -194,6 +376,15 @@ int pet_rows_norm_bwd_sink(int rows, int width, float* in_adj, int64_t lda, cons
 int pet_rows_rms_inv(int rows, int width, const float* in, int64_t ldi, float* inv, hipStream_t st) {
   if (rows < 0 || width < 1 || !in || !inv || ldi < width) return PET_ATTN_EINVAL;
   if (rows == 0) return PET_ATTN_OK;
+  if (aligned16(in, ldi)) {
+    const int e = with_vec(width, [&](auto lc, auto cc) {
+      constexpr int LPR = decltype(lc)::value, C4 = decltype(cc)::value, RPB = 4 * (64 / LPR);
+      hipLaunchKernelGGL((rms_inv4_kernel<LPR, C4>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, rows,
+                         width, in, ldi, inv);
+      return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
+    });
+    if (e >= 0) return e;
+  }
   return with_lanes(width, [&](auto vc) {
     constexpr int V = decltype(vc)::value;
     hipLaunchKernelGGL(rms_inv_kernel<V>, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, st, rows, width, in, ldi, inv);
@@ -226,6 +417,15 @@ int pet_norm_rows(int rows, int width, float* out, int64_t ldo, const float* in,
   if (rows < 0 || width < 1 || !out || !in || !weight || ldo < width || ldi < width) return PET_ATTN_EINVAL;
   if (rows == 0) return PET_ATTN_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (aligned16(out, ldo) && aligned16(in, ldi) && aligned16(weight, 4) && (!bias || aligned16(bias, 4))) {
+    const int e = with_vec(width, [&](auto lc, auto cc) {
+      constexpr int LPR = decltype(lc)::value, C4 = decltype(cc)::value, RPB = 4 * (64 / LPR);
+      hipLaunchKernelGGL((norm_fwd4_kernel<LPR, C4>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, rows,
+                         width, out, ldo, in, ldi, weight, bias);
+      return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
+    });
+    if (e >= 0) return e;
+  }
   return with_lanes(width, [&](auto vc) {
     constexpr int V = decltype(vc)::value;
     hipLaunchKernelGGL(norm_fwd_kernel<V>, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, st, rows, width, out, ldo,
