@@ -50,6 +50,54 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// ---- fp32 products on the bf16 matrix cores ---------------------------------
+// An fp32 x splits exactly into three bf16 values, x = x0 + x1 + x2 (each the
+// truncated high half of an fp32: x0 takes x's leading 8 significand bits, x1
+// the next 8 of the remainder, x2 what is left, at most 8 bits). A product
+// a.b over k is then the sum of the six part products a_i.b_j with i + j <= 2,
+// each exact in the fp32 accumulator; the three dropped are below 2^-24
+// |a||b| (the "bf16x6" scheme, Henry, Tang & Heinecke, arXiv:1904.06376).
+// gfx950's 16x16x32 bf16 MFMA issues in ~22 cycles against 32 for the 16x16x4
+// fp32 one, so a k = 32 product takes 6 x 22 cycles instead of 8 x 32, at a
+// measured error of 1.0e-7 of sum |a_k b_k| (fp32 MFMA: 1.9e-7). Operand
+// layout as the fp32 instruction's, with k in 8-element groups: lane (c, g)
+// holds row / column c, k = 8g .. 8g + 7, two bf16 a register.
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma_bf(const u4& a, const u4& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ void split3(float x, float& h0, float& h1, float& h2) {
+  h0 = __uint_as_float(__float_as_uint(x) & 0xffff0000u);
+  const float r1 = x - h0;  // exact
+  h1 = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+  h2 = r1 - h1;  // exact, and at most 8 significant bits: its low half is zero
+}
+// Two bf16 in a register: x's high half low, y's high half high.
+__device__ __forceinline__ unsigned pack_hi(float x, float y) {
+  return __builtin_amdgcn_perm(__float_as_uint(y), __float_as_uint(x), 0x07060302u);
+}
+// Eight consecutive floats as three operand registers, part p in out[p].
+__device__ __forceinline__ void split8(const float* x, u4* out) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float a0, a1, a2, b0, b1, b2;
+    split3(x[2 * j], a0, a1, a2);
+    split3(x[2 * j + 1], b0, b1, b2);
+    out[0][j] = pack_hi(a0, b0), out[1][j] = pack_hi(a1, b1), out[2][j] = pack_hi(a2, b2);
+  }
+}
+// c += a.b from split operands, the small products first.
+__device__ __forceinline__ f4 mfma6(const u4* a, const u4* b, f4 c) {
+  c = mfma_bf(a[1], b[1], c);
+  c = mfma_bf(a[0], b[2], c);
+  c = mfma_bf(a[2], b[0], c);
+  c = mfma_bf(a[0], b[1], c);
+  c = mfma_bf(a[1], b[0], c);
+  return mfma_bf(a[0], b[0], c);
+}
+
 constexpr float kOff = -1e30f;  // the log cf of a key no query sees
 __device__ __forceinline__ bool is_off(float lc) { return lc < -1e29f; }
 
@@ -181,12 +229,19 @@ template <int HD>
 struct Lds {
   static constexpr int P = HD + 4;   // row pitch of staged slices
   static constexpr int TP = 16 + 4;  // row pitch of a 16 x 16 tile
-  static size_t fwd_floats(int NW) { return size_t(2) * NW * 16 * P + NW * 16; }
+  // split K rows (forward scores on the bf16 matrix cores): per 8-dim group
+  // its three parts, 8 bf16 each, then a 16-byte pad (rows 16-lane
+  // conflict-free); in 4-byte words
+  static constexpr int KP6 = 3 * HD / 2 + 4;
+  static size_t fwd_floats(int NW, bool spl = false) {
+    return size_t(spl ? KP6 + P : 2 * P) * NW * 16 + NW * 16;
+  }
   // nbuf tile buffers: 2 lets a step's producers write while the last step's
   // owners still read (one barrier a step); 1 needs two barriers a step.
   // vlds: V staged too (else its rows come from global memory).
-  static size_t bwd_floats(int NW, int nbuf, bool vlds) {
-    return size_t(vlds ? 4 : 3) * NW * 16 * P + NW * 16 + size_t(nbuf) * NW * 2 * 16 * TP;
+  // spl: V staged as split rows (pitch KP6) for dP^T on the bf16 matrix cores
+  static size_t bwd_floats(int NW, int nbuf, bool vlds, bool spl = false) {
+    return (size_t(3) * P + (vlds ? (spl ? KP6 : P) : 0)) * NW * 16 + NW * 16 + size_t(nbuf) * NW * 2 * 16 * TP;
   }
 };
 
@@ -200,10 +255,10 @@ struct FwdOut {
 };
 
 // One item's forward from the staged K, V and log cf: wave w, query block w.
-template <int HD>
+template <int HD, bool SPL>
 __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const float* Vs, const float* lcf,
-                                         const float* q, float sc, FwdOut<HD>& out) {
-  constexpr int W = HD / 4, DT = HD / 16, P = Lds<HD>::P;
+                                         const float* q, const u4* qs, float sc, FwdOut<HD>& out) {
+  constexpr int W = HD / 4, DT = HD / 16, P = Lds<HD>::P, KP6 = Lds<HD>::KP6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const int i = 16 * w + c;  // this lane's query slot
   if (w >= at.nb) {  // slots past the atom's tokens: only the workgroup barrier
@@ -216,11 +271,22 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
   for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
   // S^T of key block J: s[r] = query i against key 16J + 4g + r.
   auto scores = [&](int J) {
-    float k[W];
-    lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
     f4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (SPL) {
+      const unsigned* kb = reinterpret_cast<const unsigned*>(Ks) + (16 * J + c) * KP6 + g * (W / 8) * 12;
 #pragma unroll
-    for (int t = 0; t < W; ++t) s = mfma(k[t], q[t], s);
+      for (int kc = 0; kc < W / 8; ++kc) {
+        u4 a[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) a[p] = *reinterpret_cast<const u4*>(kb + kc * 12 + 4 * p);
+        s = mfma6(a, qs + 3 * kc, s);
+      }
+    } else {
+      float k[W];
+      lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
+#pragma unroll
+      for (int t = 0; t < W; ++t) s = mfma(k[t], q[t], s);
+    }
     return s;
   };
   // Online softmax and PV of key block J from its scores s.
@@ -295,17 +361,18 @@ __device__ __forceinline__ void fwd_store(const Atom& at, const FwdOut<HD>& out,
 
 // One item per workgroup: the item's K, V and q loaded into registers and
 // staged in LDS, one barrier, then its forward.
-template <int HD, int MAXT, bool XF = false>
+template <int HD, int MAXT, bool XF = false, bool SPL = false>
 __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                         const int* __restrict__ off, int N, int n0, int64_t eb,
                                                         int S, int H, float sc, const float* __restrict__ cf_seq,
                                                         int64_t ldc, float* __restrict__ merged, int64_t ldm,
                                                         float* __restrict__ ml, QkvXf xf) {
-  constexpr int W = HD / 4, P = Lds<HD>::P;
+  static_assert(!SPL || HD % 32 == 0, "split scores take 32-dim products");
+  constexpr int W = HD / 4, P = Lds<HD>::P, KP6 = Lds<HD>::KP6;
   extern __shared__ float lds[];
   const int NW = blockDim.x >> 6, R = NW * 16, D = H * HD;
   float* Ks = lds;
-  float* Vs = Ks + R * P;
+  float* Vs = Ks + R * (SPL ? KP6 : P);
   float* lcf = Vs + R * P;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, i = 16 * w + (l & 15);
   const Atom at(off, blockIdx.x, H, N, S, n0, eb);
@@ -313,6 +380,7 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
   // (c, g) the slice of row 16w + c it also loads q from -- and its keys' cf;
   // the workgroup barrier is inside fwd_item, after the wave's own block.
   float q[W];
+  u4 qs[SPL ? 3 * (W / 8) : 1];
   if (w < at.nb) {
     float k[W], v[W];
     const bool real = i < at.cnt;
@@ -326,16 +394,28 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
       for (int t = 0; t < W; ++t) q[t] = k[t] = v[t] = 0.f;
     }
     const float pcf = real && g == 0 ? cf_seq[size_t(at.n) * ldc + i] : 0.f;
-    float* o = Ks + i * P + g * W;
+    if constexpr (SPL) {
+      unsigned* o = reinterpret_cast<unsigned*>(Ks) + i * KP6 + g * (W / 8) * 12;
+#pragma unroll
+      for (int kc = 0; kc < W / 8; ++kc) {
+        u4 kp[3];
+        split8(k + 8 * kc, kp);
+        split8(q + 8 * kc, qs + 3 * kc);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *reinterpret_cast<u4*>(o + kc * 12 + 4 * p) = kp[p];
+      }
+    }
+    float* ok = Ks + i * P + g * W;  // fp32 K rows (unsplit)
+    float* ov = Vs + i * P + g * W;
 #pragma unroll
     for (int t = 0; t < W; t += 4) {
-      *reinterpret_cast<float4*>(o + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
-      *reinterpret_cast<float4*>(o + (Vs - Ks) + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+      if constexpr (!SPL) *reinterpret_cast<float4*>(ok + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
+      *reinterpret_cast<float4*>(ov + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
     }
     if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
   }
   FwdOut<HD> out;
-  fwd_item<HD>(at, Ks, Vs, lcf, q, sc, out);
+  fwd_item<HD, SPL>(at, Ks, Vs, lcf, q, qs, sc, out);
   fwd_store<HD>(at, out, S, H, merged, ldm, ml);
 }
 
@@ -442,12 +522,12 @@ struct BwdOut {
 };
 
 // One item's backward from the staged Q, K, dO (and V) and log cf.
-template <int HD, bool XF>
+template <int HD, bool XF, bool SPL>
 __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const float* Ks, const float* Gs,
                                          const float* Vs, const float* lcf, float* Tb, int nbuf, int vlds,
                                          const float* oo, float mi, float li, const float* __restrict__ qkv,
                                          int64_t ldq, const QkvXf& xf, int H, float sc, BwdOut<HD>& out) {
-  constexpr int W = HD / 4, DT = HD / 16, P = Lds<HD>::P, TP = Lds<HD>::TP, TILE = 16 * TP;
+  constexpr int W = HD / 4, DT = HD / 16, P = Lds<HD>::P, TP = Lds<HD>::TP, TILE = 16 * TP, KP6 = Lds<HD>::KP6;
   const int NW = blockDim.x >> 6, D = H * HD;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bool active = w < at.nb;
@@ -455,8 +535,12 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
   // The wave's own q and dO rows: held in registers across the steps, or at
   // head_dim 64 and up re-read from LDS in each step (32+ fewer registers,
   // which is what lets two workgroups share a CU there).
+  // With SPL (V staged as split rows) dP^T runs on the bf16 matrix cores
+  // from dO split once here.
   constexpr bool QG_LDS = HD >= 64;
-  float q[QG_LDS ? 1 : W], go[QG_LDS ? 1 : W], dqi = 0.f;
+  static_assert(!SPL || (!QG_LDS && HD % 32 == 0), "split dP^T: head_dim 32");
+  float q[QG_LDS ? 1 : W], go[QG_LDS || SPL ? 1 : W], dqi = 0.f;
+  u4 gos[SPL ? 3 * (W / 8) : 1];
   if (active) {
     float qa[W], ga[W];
     lds_get<W>(Qs + i * P + g * W, qa);
@@ -465,9 +549,16 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
 #pragma unroll
     for (int t = 0; t < W; ++t) d += ga[t] * oo[t];
     dqi = sum_g(d);  // Dq = dO . O of query i
+    if constexpr (SPL) {
+#pragma unroll
+      for (int kc = 0; kc < W / 8; ++kc) split8(ga + 8 * kc, gos + 3 * kc);
+    }
     if constexpr (!QG_LDS) {
 #pragma unroll
-      for (int t = 0; t < W; ++t) q[t] = qa[t], go[t] = ga[t];
+      for (int t = 0; t < W; ++t) {
+        q[t] = qa[t];
+        if constexpr (!SPL) go[t] = ga[t];
+      }
     }
   }
   f4 dq[DT], dk[DT], dv[DT];
@@ -482,7 +573,20 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
     int J = w + s;
     if (J >= nb) J -= nb;
     f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-    {
+    if constexpr (SPL) {  // V staged split: v_staged holds
+      float k[W];
+      lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
+      const unsigned* vb = reinterpret_cast<const unsigned*>(Vs) + (16 * J + c) * KP6 + g * (W / 8) * 12;
+#pragma unroll
+      for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st);
+#pragma unroll
+      for (int kc = 0; kc < W / 8; ++kc) {
+        u4 a[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) a[p] = *reinterpret_cast<const u4*>(vb + kc * 12 + 4 * p);
+        dp = mfma6(a, gos + 3 * kc, dp);
+      }
+    } else {
       float k[W], v[W];
       lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
       if (v_staged)
@@ -587,7 +691,7 @@ __device__ __forceinline__ void bwd_store(const Atom& at, const BwdOut<HD>& out,
 
 // One item per workgroup: the item's slices, its own rows' O and statistics
 // loaded into registers, staged in LDS, one barrier, then its backward.
-template <int HD, int MAXT, bool XF = false>
+template <int HD, int MAXT, bool XF = false, bool SPL = false>
 __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                         const int* __restrict__ off, int N, int n0, int64_t eb,
                                                         int S, int H, float sc, const float* __restrict__ dmerged,
@@ -596,14 +700,14 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
                                                         const float* __restrict__ cf_seq, int64_t ldc,
                                                         float* __restrict__ qkv_adj, int64_t lda,
                                                         float* __restrict__ cfh, int nbuf, int vlds, QkvXf xf) {
-  constexpr int W = HD / 4, P = Lds<HD>::P;
+  constexpr int W = HD / 4, P = Lds<HD>::P, KP6 = Lds<HD>::KP6;
   extern __shared__ float lds[];
   const int NW = blockDim.x >> 6, R = NW * 16, D = H * HD;
   float* Qs = lds;
   float* Ks = Qs + R * P;
   float* Gs = Ks + R * P;
-  float* Vs = Gs + R * P;  // when vlds
-  float* lcf = Vs + (vlds ? R * P : 0);
+  float* Vs = Gs + R * P;  // when vlds: fp32 rows, or split rows with SPL (which needs vlds)
+  float* lcf = Vs + (vlds ? R * (SPL ? KP6 : P) : 0);
   float* Tb = lcf + R;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, i = 16 * w + (l & 15);
   const Atom at(off, blockIdx.x, H, N, S, n0, eb);
@@ -636,12 +740,23 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
       *reinterpret_cast<float4*>(o + t) = make_float4(q[t], q[t + 1], q[t + 2], q[t + 3]);
       *reinterpret_cast<float4*>(o + (Ks - Qs) + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
       *reinterpret_cast<float4*>(o + (Gs - Qs) + t) = make_float4(go[t], go[t + 1], go[t + 2], go[t + 3]);
-      if (vlds) *reinterpret_cast<float4*>(o + (Vs - Qs) + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+      if (!SPL && vlds)
+        *reinterpret_cast<float4*>(o + (Vs - Qs) + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+    }
+    if constexpr (SPL) {
+      unsigned* ov = reinterpret_cast<unsigned*>(Vs) + i * KP6 + g * (W / 8) * 12;
+#pragma unroll
+      for (int kc = 0; kc < W / 8; ++kc) {
+        u4 vp[3];
+        split8(v + 8 * kc, vp);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *reinterpret_cast<u4*>(ov + kc * 12 + 4 * p) = vp[p];
+      }
     }
     if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
   }
   BwdOut<HD> out;
-  bwd_item<HD, XF>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, xf, H, sc, out);
+  bwd_item<HD, XF, SPL>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, xf, H, sc, out);
   bwd_store<HD>(at, out, S, H, sc, qkv_adj, lda, cfh);
 }
 
@@ -711,41 +826,18 @@ int env_int(const char* name) {
   const char* v = std::getenv(name);
   return v ? std::atoi(v) : 0;
 }
+// PET_ATTN_SPLIT=0 turns the split-fp32 bf16 products off; read at every
+// launch, so that a process can compare both paths.
+bool split_enabled() {
+  const char* v = std::getenv("PET_ATTN_SPLIT");
+  return !v || std::atoi(v) != 0;
+}
 
 template <class K>
 void allow_lds(K k, size_t bytes) {
   if (bytes > 65536)
     (void) hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(bytes));
-}
-
-// The forward over atoms [n0, n1), qkv a chunk whose edge 0 is row eb.
-template <int HD>
-int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
-               const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st) {
-  const int NW = waves_for(sh.slots);
-  const size_t bytes = sizeof(float) * Lds<HD>::fwd_floats(NW);
-  if (bytes > size_t(max_lds_bytes())) return PET_ATTN_ESLOTS;
-  const int64_t items = int64_t(n1 - n0) * sh.heads;
-  if (items == 0) return PET_ATTN_OK;
-  static const int choice = env_int("PET_ATTN_FWD");  // 3: the vector-ALU kernel, for comparison
-  if constexpr (HD <= 64) {
-    const int threads = 64 * ((sh.slots + 63) / 64);
-    const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
-    if (choice == 3 && !xf.rs && !xf.b && threads <= 256 && vb <= size_t(max_lds_bytes())) {
-      allow_lds(attn_fwd_valu_kernel<HD>, vb);
-      hipLaunchKernelGGL(attn_fwd_valu_kernel<HD>, dim3(unsigned(items)), dim3(threads), vb, st, qkv, ldq, off,
-                         sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml);
-      return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
-    }
-  }
-  const bool x = xf.rs || xf.b;
-  auto k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true> : attn_fwd_kernel<HD, 512, false>)
-                   : (x ? attn_fwd_kernel<HD, 1024, true> : attn_fwd_kernel<HD, 1024, false>);
-  allow_lds(k, bytes);
-  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
-                     sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
-  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
 // Workgroups of kernel k (NW waves, lds bytes of LDS) one CU holds at once,
@@ -764,6 +856,59 @@ int resident_wgs(const void* k, int NW, size_t lds) {
   const size_t gran = (lds + 2047) / 2048 * 2048;
   const int by_lds = gran ? int(163840 / gran) : 8;
   return std::max(1, std::min(by_vgpr, by_lds));
+}
+
+// The forward over atoms [n0, n1), qkv a chunk whose edge 0 is row eb.
+template <int HD>
+int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+               const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st) {
+  const int NW = waves_for(sh.slots);
+  size_t bytes = sizeof(float) * Lds<HD>::fwd_floats(NW);
+  if (bytes > size_t(max_lds_bytes())) return PET_ATTN_ESLOTS;
+  // scores on the bf16 matrix cores (split fp32) where head_dim is a multiple
+  // of 32 and the split K rows fit as many workgroups a CU; PET_ATTN_SPLIT=0
+  // keeps every product on the fp32 matrix cores
+  const size_t sbytes = sizeof(float) * Lds<HD>::fwd_floats(NW, true);
+  bool spl = false;
+  if constexpr (HD % 32 == 0) {
+    if (split_enabled() && sbytes <= size_t(max_lds_bytes())) {
+      const void* plain = reinterpret_cast<const void*>(attn_fwd_kernel<HD, 512, false, false>);
+      const void* split = reinterpret_cast<const void*>(attn_fwd_kernel<HD, 512, false, true>);
+      spl = resident_wgs(split, NW, sbytes) >= resident_wgs(plain, NW, bytes);
+    }
+  }
+  if (spl) bytes = sbytes;
+  const int64_t items = int64_t(n1 - n0) * sh.heads;
+  if (items == 0) return PET_ATTN_OK;
+  static const int choice = env_int("PET_ATTN_FWD");  // 3: the vector-ALU kernel, for comparison
+  if constexpr (HD <= 64) {
+    const int threads = 64 * ((sh.slots + 63) / 64);
+    const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
+    if (choice == 3 && !xf.rs && !xf.b && threads <= 256 && vb <= size_t(max_lds_bytes())) {
+      allow_lds(attn_fwd_valu_kernel<HD>, vb);
+      hipLaunchKernelGGL(attn_fwd_valu_kernel<HD>, dim3(unsigned(items)), dim3(threads), vb, st, qkv, ldq, off,
+                         sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml);
+      return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+    }
+  }
+  const bool x = xf.rs || xf.b;
+  using KT = decltype(&attn_fwd_kernel<HD, 512, false, false>);
+  KT k;
+  if constexpr (HD % 32 == 0) {
+    if (spl)
+      k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true, true> : attn_fwd_kernel<HD, 512, false, true>)
+                  : (x ? attn_fwd_kernel<HD, 1024, true, true> : attn_fwd_kernel<HD, 1024, false, true>);
+    else
+      k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true> : attn_fwd_kernel<HD, 512, false>)
+                  : (x ? attn_fwd_kernel<HD, 1024, true> : attn_fwd_kernel<HD, 1024, false>);
+  } else {
+    k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true> : attn_fwd_kernel<HD, 512, false>)
+                : (x ? attn_fwd_kernel<HD, 1024, true> : attn_fwd_kernel<HD, 1024, false>);
+  }
+  allow_lds(k, bytes);
+  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
+                     sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
 // The backward over atoms [n0, n1); qkv, dmerged and qkv_adj are the chunk's.
@@ -808,6 +953,18 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   }
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
+  // dP^T on the bf16 matrix cores (V staged split) at head_dim 32 when V is
+  // staged and the split rows keep as many workgroups a CU
+  if constexpr (HD == 32) {
+    const size_t sb = sizeof(float) * Lds<HD>::bwd_floats(NW, nbuf, true, true);
+    if (vlds && split_enabled() && sb <= cap) {
+      auto ks = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true, true> : attn_bwd_kernel<HD, 512, false, true>)
+                        : (x ? attn_bwd_kernel<HD, 1024, true, true> : attn_bwd_kernel<HD, 1024, false, true>);
+      if (resident_wgs(reinterpret_cast<const void*>(ks), NW, sb) >=
+          resident_wgs(reinterpret_cast<const void*>(k), NW, bytes))
+        k = ks, bytes = sb;
+    }
+  }
   allow_lds(k, bytes);
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
                      sh.slots, sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh,
