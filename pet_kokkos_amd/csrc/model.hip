@@ -19,6 +19,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -282,6 +283,114 @@ __global__ void message_bwd_kernel(float* __restrict__ efa, const float* __restr
   }
 }
 
+// ---- the same passes, 4 floats a thread ---------------------------------------
+// For a width W with W / 4 dividing 256 (the model's widths) and 16-byte
+// aligned rows: thread t of a workgroup keeps the column slice t % (W / 4) and
+// steps over rows 256 / (W / 4) at a time, so every access is a 16-byte one and
+// no index needs a 64-bit division. The arithmetic per value is the scalar
+// kernels': the results are the same bits.
+#define ROWS4_LOOP(r, c, R, W4)                  \
+  const int c = int(threadIdx.x) % (W4);         \
+  const int rpb_ = 256 / (W4);                   \
+  for (int64_t r = int64_t(blockIdx.x) * rpb_ + int(threadIdx.x) / (W4); r < (R); r += int64_t(gridDim.x) * rpb_)
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+__global__ void fill_rows4_kernel(float4* __restrict__ out, const float4* __restrict__ b, int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) out[r * W4 + c] = b ? b[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+__global__ void residual4_kernel(float4* __restrict__ s, float4* __restrict__ out, const float4* __restrict__ a,
+                                 const float4* __restrict__ cc, const float4* __restrict__ b, int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) {
+    const int64_t i = r * W4 + c;
+    const float4 v = add4(a[i], cc[i]);
+    if (s) s[i] = v;
+    out[i] = add4(v, b[c]);
+  }
+}
+__global__ void add_bias4_kernel(float4* __restrict__ x, const float4* __restrict__ b, int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) x[r * W4 + c] = add4(x[r * W4 + c], b[c]);
+}
+__global__ void bias_add4_kernel(float4* __restrict__ out, const float4* __restrict__ a, const float4* __restrict__ b,
+                                 int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) out[r * W4 + c] = add4(a[r * W4 + c], b[c]);
+}
+__device__ __forceinline__ float silu1(float z, float b) {
+  const float v = z + b;
+  return v * sig_fast(v);
+}
+__global__ void silu4_kernel(float4* __restrict__ out, const float4* __restrict__ z, const float4* __restrict__ b,
+                             int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) {
+    const float4 x = z[r * W4 + c], bb = b[c];
+    out[r * W4 + c] = make_float4(silu1(x.x, bb.x), silu1(x.y, bb.y), silu1(x.z, bb.z), silu1(x.w, bb.w));
+  }
+}
+__device__ __forceinline__ float silu_bwd1(float g, float pre, float b) {
+  const float x = pre + b, sg = sig_fast(x);
+  return g * (sg * (1.0f + x * (1.0f - sg)));
+}
+__global__ void silu_bwd4_kernel(float4* __restrict__ g, const float4* __restrict__ pre, const float4* __restrict__ b,
+                                 int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) {
+    const int64_t i = r * W4 + c;
+    const float4 gg = g[i], x = pre[i], bb = b[c];
+    g[i] = make_float4(silu_bwd1(gg.x, x.x, bb.x), silu_bwd1(gg.y, x.y, bb.y), silu_bwd1(gg.z, x.z, bb.z),
+                       silu_bwd1(gg.w, x.w, bb.w));
+  }
+}
+// h has F4 float4 a row; pre and b hold (v, g) pairs, two float4 per h float4
+__global__ void swiglu4_kernel(float4* __restrict__ h, const float4* __restrict__ pre, const float4* __restrict__ b,
+                               int64_t R, int F4) {
+  ROWS4_LOOP(r, c, R, F4) {
+    const float4 p0 = pre[r * 2 * F4 + 2 * c], p1 = pre[r * 2 * F4 + 2 * c + 1], b0 = b[2 * c], b1 = b[2 * c + 1];
+    h[r * F4 + c] = make_float4((p0.x + b0.x) * sig_fast(p0.y + b0.y), (p0.z + b0.z) * sig_fast(p0.w + b0.w),
+                                (p1.x + b1.x) * sig_fast(p1.y + b1.y), (p1.z + b1.z) * sig_fast(p1.w + b1.w));
+  }
+}
+__device__ __forceinline__ float2 swiglu_bwd1(float g, float pv, float pg, float bv, float bg) {
+  const float v = pv + bv, sg = sig_fast(pg + bg);
+  return make_float2(g * sg, g * v * sg * (1.0f - sg));
+}
+__global__ void swiglu_bwd4_kernel(float4* __restrict__ pre_adj, const float4* __restrict__ h_adj,
+                                   const float4* __restrict__ pre, const float4* __restrict__ b, int64_t R, int F4) {
+  ROWS4_LOOP(r, c, R, F4) {
+    const float4 g = h_adj[r * F4 + c];
+    const float4 p0 = pre[r * 2 * F4 + 2 * c], p1 = pre[r * 2 * F4 + 2 * c + 1], b0 = b[2 * c], b1 = b[2 * c + 1];
+    const float2 a = swiglu_bwd1(g.x, p0.x, p0.y, b0.x, b0.y), bq = swiglu_bwd1(g.y, p0.z, p0.w, b0.z, b0.w);
+    const float2 cq = swiglu_bwd1(g.z, p1.x, p1.y, b1.x, b1.y), d = swiglu_bwd1(g.w, p1.z, p1.w, b1.z, b1.w);
+    pre_adj[r * 2 * F4 + 2 * c] = make_float4(a.x, a.y, bq.x, bq.y);
+    pre_adj[r * 2 * F4 + 2 * c + 1] = make_float4(cq.x, cq.y, d.x, d.y);
+  }
+}
+__global__ void copy4_kernel(float4* __restrict__ out, const float4* __restrict__ a, int64_t n4) {
+  GRID_LOOP(i, n4) out[i] = a[i];
+}
+__global__ void scale4_kernel(float4* __restrict__ out, const float4* __restrict__ a, float s, int64_t n4) {
+  GRID_LOOP(i, n4) {
+    const float4 v = a[i];
+    out[i] = make_float4(s * v.x, s * v.y, s * v.z, s * v.w);
+  }
+}
+__global__ void fill04_kernel(float4* __restrict__ x, int64_t n4) {
+  GRID_LOOP(i, n4) x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// W / 4 divides 256 and every pointer (null allowed) is 16-byte aligned
+inline bool rows4_ok(int W, std::initializer_list<const void*> ps) {
+  if (W <= 0 || W % 4 || 256 % (W / 4)) return false;
+  for (const void* p : ps)
+    if (!al16(p)) return false;
+  return true;
+}
+inline dim3 grid_rows4(int64_t R, int W4) {
+  const int64_t b = (R + 256 / W4 - 1) / (256 / W4);
+  return dim3(unsigned(b < 8192 ? (b > 0 ? b : 1) : 8192));
+}
+inline float4* v4(float* p) { return reinterpret_cast<float4*>(p); }
+inline const float4* v4(const float* p) { return reinterpret_cast<const float4*>(p); }
+
 inline dim3 grid_for(int64_t n) {
   const int64_t b = (n + 255) / 256;
   return dim3(unsigned(b < 8192 ? (b > 0 ? b : 1) : 8192));
@@ -409,7 +518,11 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
-  hipLaunchKernelGGL(fill_rows_kernel, grid_for(int64_t(M) * W.rows), dim3(256), 0, st, out, b, int64_t(M), W.rows);
+  if (rows4_ok(W.rows, {out, b}))
+    hipLaunchKernelGGL(fill_rows4_kernel, grid_rows4(M, W.rows / 4), dim3(256), 0, st, v4(out), v4(b), int64_t(M),
+                       W.rows / 4);
+  else
+    hipLaunchKernelGGL(fill_rows_kernel, grid_for(int64_t(M) * W.rows), dim3(256), 0, st, out, b, int64_t(M), W.rows);
   launched();
   ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
 }
@@ -447,36 +560,99 @@ void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const st
 void silu(pet_model& md, float* out, const float* z, int64_t R, const std::string& key, hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
   if (R == 0) return;
-  hipLaunchKernelGGL(silu_kernel, grid_for(R * b.rows), dim3(256), 0, st, out, z, b.p, R, b.rows);
+  if (rows4_ok(b.rows, {out, z, b.p}))
+    hipLaunchKernelGGL(silu4_kernel, grid_rows4(R, b.rows / 4), dim3(256), 0, st, v4(out), v4(z), v4(b.p), R,
+                       b.rows / 4);
+  else
+    hipLaunchKernelGGL(silu_kernel, grid_for(R * b.rows), dim3(256), 0, st, out, z, b.p, R, b.rows);
   launched();
 }
 void silu_bwd(pet_model& md, float* g, const float* z, int64_t R, const std::string& key, hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
   if (R == 0) return;
-  hipLaunchKernelGGL(silu_bwd_kernel, grid_for(R * b.rows), dim3(256), 0, st, g, z, b.p, R, b.rows);
+  if (rows4_ok(b.rows, {g, z, b.p}))
+    hipLaunchKernelGGL(silu_bwd4_kernel, grid_rows4(R, b.rows / 4), dim3(256), 0, st, v4(g), v4(z), v4(b.p), R,
+                       b.rows / 4);
+  else
+    hipLaunchKernelGGL(silu_bwd_kernel, grid_for(R * b.rows), dim3(256), 0, st, g, z, b.p, R, b.rows);
   launched();
 }
 // h = swiglu(z + b) of linear_pre's z under `key` (a .w_in)
 void swiglu(pet_model& md, float* h, const float* z, int64_t R, const std::string& key, hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
   if (R == 0) return;
-  hipLaunchKernelGGL(swiglu_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st, h,
-                     reinterpret_cast<const float2*>(z), reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
+  if (b.rows % 2 == 0 && rows4_ok(b.rows / 2, {h, z, b.p}))
+    hipLaunchKernelGGL(swiglu4_kernel, grid_rows4(R, b.rows / 8), dim3(256), 0, st, v4(h), v4(z), v4(b.p), R,
+                       b.rows / 8);
+  else
+    hipLaunchKernelGGL(swiglu_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st, h,
+                       reinterpret_cast<const float2*>(z), reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
   launched();
 }
 void swiglu_bwd(pet_model& md, float* z_adj, const float* h_adj, const float* z, int64_t R, const std::string& key,
                 hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
   if (R == 0) return;
-  hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st, reinterpret_cast<float2*>(z_adj),
-                     h_adj, reinterpret_cast<const float2*>(z), reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
+  if (b.rows % 2 == 0 && rows4_ok(b.rows / 2, {z_adj, h_adj, z, b.p}))
+    hipLaunchKernelGGL(swiglu_bwd4_kernel, grid_rows4(R, b.rows / 8), dim3(256), 0, st, v4(z_adj), v4(h_adj), v4(z),
+                       v4(b.p), R, b.rows / 8);
+  else
+    hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st,
+                       reinterpret_cast<float2*>(z_adj), h_adj, reinterpret_cast<const float2*>(z),
+                       reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
+  launched();
+}
+// The elementwise passes: the float4 kernels where the width and alignment allow.
+void residual_pass(float* sv, float* out, const float* a, const float* c, const float* b, int64_t R, int W,
+                   hipStream_t st) {
+  if (R == 0) return;
+  if (rows4_ok(W, {sv, out, a, c, b}))
+    hipLaunchKernelGGL(residual4_kernel, grid_rows4(R, W / 4), dim3(256), 0, st, v4(sv), v4(out), v4(a), v4(c), v4(b),
+                       R, W / 4);
+  else
+    hipLaunchKernelGGL(residual_kernel, grid_for(R * W), dim3(256), 0, st, sv, out, a, c, b, R, W);
+  launched();
+}
+void add_bias_pass(float* x, const float* b, int64_t R, int W, hipStream_t st) {
+  if (R == 0) return;
+  if (rows4_ok(W, {x, b}))
+    hipLaunchKernelGGL(add_bias4_kernel, grid_rows4(R, W / 4), dim3(256), 0, st, v4(x), v4(b), R, W / 4);
+  else
+    hipLaunchKernelGGL(add_bias_kernel, grid_for(R * W), dim3(256), 0, st, x, b, R, W);
+  launched();
+}
+void bias_add_pass(float* out, const float* a, const float* b, int64_t R, int W, hipStream_t st) {
+  if (R == 0) return;
+  if (rows4_ok(W, {out, a, b}))
+    hipLaunchKernelGGL(bias_add4_kernel, grid_rows4(R, W / 4), dim3(256), 0, st, v4(out), v4(a), v4(b), R, W / 4);
+  else
+    hipLaunchKernelGGL(bias_add_kernel, grid_for(R * W), dim3(256), 0, st, out, a, b, R, W);
+  launched();
+}
+void copy_pass(float* out, const float* a, int64_t n, hipStream_t st) {
+  if (n == 0) return;
+  if (n % 4 == 0 && al16(out) && al16(a))
+    hipLaunchKernelGGL(copy4_kernel, grid_for(n / 4), dim3(256), 0, st, v4(out), v4(a), n / 4);
+  else
+    hipLaunchKernelGGL(copy_kernel, grid_for(n), dim3(256), 0, st, out, a, n);
+  launched();
+}
+void scale_pass(float* out, const float* a, float sc, int64_t n, hipStream_t st) {
+  if (n == 0) return;
+  if (n % 4 == 0 && al16(out) && al16(a))
+    hipLaunchKernelGGL(scale4_kernel, grid_for(n / 4), dim3(256), 0, st, v4(out), v4(a), sc, n / 4);
+  else
+    hipLaunchKernelGGL(scale_kernel, grid_for(n), dim3(256), 0, st, out, a, sc, n);
   launched();
 }
 void norm(pet_model& md, float* out, const float* in, int R, int W, const std::string& key, bool ln, hipStream_t st) {
   ok(pet_norm_rows(R, W, out, W, in, W, md.p(key + ".weight"), ln ? md.p(key + ".bias") : nullptr, st));
 }
 void fill0(float* x, int64_t n, hipStream_t st) {
-  hipLaunchKernelGGL(fill0_kernel, grid_for(n), dim3(256), 0, st, x, n);
+  if (n % 4 == 0 && al16(x))
+    hipLaunchKernelGGL(fill04_kernel, grid_for(n / 4), dim3(256), 0, st, v4(x), n / 4);
+  else
+    hipLaunchKernelGGL(fill0_kernel, grid_for(n), dim3(256), 0, st, x, n);
   launched();
 }
 
@@ -538,14 +714,12 @@ struct Pass {
       linear(md, node_exp, attn_out, N, D, tl + ".center_expansion", st);
       // eps = attention's edge rows + edge_cur; edge_next = eps + mlp's output bias
       if (E) {
-        hipLaunchKernelGGL(residual_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, b.eps, edge_next,
-                           attn_out + int64_t(N) * D, edge_cur, md.p(tl + ".mlp.w_out.bias"), int64_t(E), D);
-        launched();
+        residual_pass(b.eps, edge_next, attn_out + int64_t(N) * D, edge_cur, md.p(tl + ".mlp.w_out.bias"),
+                      int64_t(E), D, st);
       }
       if (N) {
-        hipLaunchKernelGGL(residual_kernel, grid_for(int64_t(N) * Dn), dim3(256), 0, st, b.node_res, node_next,
-                           node_cur, node_exp, md.p(tl + ".center_mlp.w_out.bias"), int64_t(N), Dn);
-        launched();
+        residual_pass(b.node_res, node_next, node_cur, node_exp, md.p(tl + ".center_mlp.w_out.bias"), int64_t(N),
+                      Dn, st);
       }
       // node_next += center_mlp(norm(node_res)); edge_next += mlp(norm(eps))
       float* nn = node_exp;  // consumed
@@ -579,9 +753,7 @@ struct Pass {
     linear_pre(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
     silu(md, cn, sv.cph, E, "combination_mlps." + ls + ".0", st);
     if (E) {
-      hipLaunchKernelGGL(add_bias_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge,
-                         md.p("combination_mlps." + ls + ".2.bias"), int64_t(E), D);
-      launched();
+      add_bias_pass(input_edge, md.p("combination_mlps." + ls + ".2.bias"), int64_t(E), D, st);
     }
     linear_acc(md, input_edge, cn, E, 2 * D, "combination_mlps." + ls + ".2", st);
     md.ws.release(scope);
@@ -780,9 +952,7 @@ struct Pass {
       ok(pet_attn_fwd_xf(&sh, b.qkv, 3 * D, nullptr, md.p(tl + ".attention.input_linear.bias"), e.off, cf_seq, S,
                          b.merged, D, b.ml, st));
       // s1 = tokens + b_out, then += merged W_out^T
-      hipLaunchKernelGGL(bias_add_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, b.s1, sv.tokens,
-                         md.p(tl + ".attention.output_linear.bias"), int64_t(T), D);
-      launched();
+      bias_add_pass(b.s1, sv.tokens, md.p(tl + ".attention.output_linear.bias"), int64_t(T), D, st);
       linear_acc(md, b.s1, b.merged, T, D, tl + ".attention.output_linear", st);
       float* tok_a = md.f(int64_t(T) * D);
       norm(md, tok_a, b.s1, T, D, tl + ".norm_attention", true, st);
@@ -790,9 +960,7 @@ struct Pass {
       linear_pre(md, b.pre, tok_a, T, D, tl + ".mlp.w_in", st);
       float* hm = md.f(int64_t(T) * F);
       silu(md, hm, b.pre, T, tl + ".mlp.w_in", st);
-      hipLaunchKernelGGL(bias_add_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, b.s2, tok_a,
-                         md.p(tl + ".mlp.w_out.bias"), int64_t(T), D);
-      launched();
+      bias_add_pass(b.s2, tok_a, md.p(tl + ".mlp.w_out.bias"), int64_t(T), D, st);
       linear_acc(md, b.s2, hm, T, F, tl + ".mlp.w_out", st);
       norm(md, sv.tokens, b.s2, T, D, tl + ".norm_mlp", true, st);
       md.ws.release(scope);
@@ -812,8 +980,7 @@ struct Pass {
       float* s2_adj = md.f(int64_t(T) * D);
       float* tok_a_adj = md.f(int64_t(T) * D);
       ok(pet_norm_rows_bwd(T, D, s2_adj, D, 0.0f, tokens_adj, D, b.s2, D, md.p(tl + ".norm_mlp.weight"), 1, st));
-      hipLaunchKernelGGL(copy_kernel, grid_for(int64_t(T) * D), dim3(256), 0, st, tok_a_adj, s2_adj, int64_t(T) * D);
-      launched();
+      copy_pass(tok_a_adj, s2_adj, int64_t(T) * D, st);
       float* h_adj = md.f(int64_t(T) * F);
       linear_bwd(md, h_adj, s2_adj, T, tl + ".mlp.w_out", 0.0f, st);
       silu_bwd(md, h_adj, b.pre, T, tl + ".mlp.w_in", st);
@@ -906,9 +1073,7 @@ struct Pass {
         float* tok_adj = residual_layer_bwd(L, rv[L], tadj[L], cf_seq_adj);
         // the message's own share: ie_next = ie_adj / 2 (0 past the last layer)
         if (E) {
-          hipLaunchKernelGGL(scale_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, ie_next, ie_adj,
-                             L + 1 < G ? 0.5f : 0.0f, int64_t(E) * D);
-          launched();
+          scale_pass(ie_next, ie_adj, L + 1 < G ? 0.5f : 0.0f, int64_t(E) * D, st);
         }
         compress_bwd(L, tok_adj + int64_t(N) * D, rv[L].cpre, x4_adj, ie_next);
         std::swap(ie_adj, ie_next);
