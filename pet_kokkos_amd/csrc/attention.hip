@@ -100,6 +100,10 @@ __device__ __forceinline__ f4 mfma6(const u4* a, const u4* b, f4 c) {
 
 constexpr float kOff = -1e30f;  // the log cf of a key no query sees
 __device__ __forceinline__ bool is_off(float lc) { return lc < -1e29f; }
+// The running max's start in the matrix-core forward: above kOff, so a key
+// with log cf kOff has exp(x - max) = 0 exactly whatever keys came before,
+// without a test per key (x = s sc + kOff rounds to kOff for any real score).
+constexpr float kFloor = -1e29f;
 
 // Over the four lanes that share c (g = 0..3): gfx950's lane-swap
 // instructions exchange rows of 32 and of 16 lanes in registers, no LDS. Both
@@ -265,7 +269,7 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
     lds_barrier();
     return;
   }
-  float mx = kOff, sum = 0.f;
+  float mx = kFloor, sum = 0.f;
   f4 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
@@ -296,14 +300,14 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
     float x[4], bm = kOff;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      x[r] = is_off(lc[r]) ? kOff : s[r] * sc + lc[r];
+      x[r] = s[r] * sc + lc[r];
       bm = fmaxf(bm, x[r]);
     }
     const float nm = fmaxf(mx, max_g(bm));
     const float alpha = __expf(mx - nm);
     float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = is_off(lc[r]) ? 0.f : __expf(x[r] - nm);
+    for (int r = 0; r < 4; ++r) p[r] = __expf(x[r] - nm);
     sum = sum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     mx = nm;
 #pragma unroll
@@ -338,7 +342,7 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
   // else a query on an edge at its cutoff: zeros
   out.live = i < at.cnt && (i == 0 || !is_off(lcf[i]));
   out.invl = out.live && tot > 0.f ? 1.0f / tot : 0.f;
-  out.mx = out.live ? mx : kOff;
+  out.mx = out.live && tot > 0.f ? mx : kOff;  // no live key: the max never left kFloor
 #pragma unroll
   for (int t = 0; t < DT; ++t) out.acc[t] = acc[t];
 }
@@ -566,6 +570,9 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
   for (int t = 0; t < DT; ++t) dq[t] = dk[t] = dv[t] = f4{0.f, 0.f, 0.f, 0.f};
   float cfa = 0.f;
   const int nb = at.nb;
+  // A query with no live key (li = 0) or a key with log cf kOff gets an
+  // exponent near -1e30, so exp gives 0 exactly without a test per key.
+  const float mie = li > 0.f ? mi : 1e30f;
   // Phase 1 of step s: tile (query block w, key block J = (w + s) mod nb):
   // S^T and dP^T, then A and dS, the dQ share, and A, dS left in LDS.
   auto phase1 = [&](int s, bool v_staged) {
@@ -611,7 +618,7 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
     lds_get<4>(lcf + 16 * J + 4 * g, lc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {  // query i, key 16J + 4g + r
-      a[r] = li > 0.f && !is_off(lc[r]) ? __expf(st[r] * sc + lc[r] - mi) * li : 0.f;
+      a[r] = __expf(st[r] * sc + lc[r] - mie) * li;
       ds[r] = a[r] * (dp[r] - dqi);
     }
     // dQ^T += K^T dS^T over the tile's keys.
