@@ -74,6 +74,11 @@ MODELS = {
     "tiny": Hypers(d_pet=64, d_node=128, d_head=32, d_feedforward=128, num_heads=4),
     "tiny-residual": Hypers(d_pet=64, d_node=64, d_head=32, d_feedforward=128, num_heads=4,
                             featurizer="residual"),
+    # widths whose quarter does not divide 256 and a head_dim of 16: the
+    # library's scalar fallbacks of its row passes, and masked norm lanes
+    "odd": Hypers(d_pet=48, d_node=72, d_head=40, d_feedforward=36, num_heads=3),
+    "odd-residual": Hypers(d_pet=48, d_node=48, d_head=40, d_feedforward=36, num_heads=3,
+                           featurizer="residual"),
     # the residual family at configs[1]'s shape
     "c2-residual": Hypers(d_pet=128, d_node=128, d_head=128, d_feedforward=512, num_heads=4,
                           featurizer="residual"),

@@ -81,6 +81,22 @@ def test_model_matches_oracle(case, name, device):
     compare(got, oracle_of(h, w, comp, x))
 
 
+@pytest.mark.parametrize("name", ["odd", "odd-residual"])
+def test_odd_widths_match_oracle(name, device):
+    # d 48 in 3 heads of 16, FFN 36, d_node 72, read-out width 40: the row
+    # passes take their scalar kernels (a width's quarter not dividing 256) and
+    # the norms their masked vector lanes
+    h = weights.MODELS[name]
+    w = weights.random_weights(h, 14)
+    comp = weights.random_composition(h)
+    print(f"[model] {name} batch-3", flush=True)
+    m = PetModel(h, w, comp)
+    x = structures_input(h, CASES["batch-3"](), device)
+    got = m.compute(x, forces=True, edge_grad=True)
+    torch.cuda.synchronize()
+    compare(got, oracle_of(h, w, comp, x))
+
+
 @pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
 def test_model_repeats_bitwise(name, device):
     h = weights.MODELS[name]
