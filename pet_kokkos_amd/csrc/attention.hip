@@ -522,6 +522,9 @@ __global__ void __launch_bounds__(256) attn_fwd_valu_kernel(const float* __restr
 }
 
 // ---- backward --------------------------------------------------------------
+// a * b for small non-negative indices (a row index times a pitch): the
+// full-rate 24-bit multiply instead of the quarter-rate 32-bit one.
+__device__ __forceinline__ int mul24(int a, int b) { return int(__umul24(unsigned(a), unsigned(b))); }
 // A lane's share of one item's backward result, held until it is stored.
 template <int HD>
 struct BwdOut {
@@ -577,17 +580,18 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
   // A query with no live key (li = 0) or a key with log cf kOff gets an
   // exponent near -1e30, so exp gives 0 exactly without a test per key.
   const float mie = li > 0.f ? mi : 1e30f;
+  float* const Tb1 = Tb + mul24(NW * 2, TILE);  // the second tile buffer
   // Phase 1 of step s: tile (query block w, key block J = (w + s) mod nb):
   // S^T and dP^T, then A and dS, the dQ share, and A, dS left in LDS.
   auto phase1 = [&](int s, bool v_staged) {
-    float* tb = Tb + (nbuf == 2 ? (s & 1) : 0) * (NW * 2 * TILE);
+    float* tb = nbuf == 2 && (s & 1) ? Tb1 : Tb;
     int J = w + s;
     if (J >= nb) J -= nb;
     f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
     if constexpr (SPL) {  // V staged split: v_staged holds
       float k[W];
-      lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
-      const unsigned* vb = reinterpret_cast<const unsigned*>(Vs) + (16 * J + c) * KP6 + g * (W / 8) * 12;
+      lds_get<W>(Ks + mul24(16 * J + c, P) + g * W, k);
+      const unsigned* vb = reinterpret_cast<const unsigned*>(Vs) + mul24(16 * J + c, KP6) + g * (W / 8) * 12;
 #pragma unroll
       for (int t = 0; t < W; ++t) st = mfma(k[t], q[t], st);
 #pragma unroll
@@ -599,9 +603,9 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
       }
     } else {
       float k[W], v[W];
-      lds_get<W>(Ks + (16 * J + c) * P + g * W, k);
+      lds_get<W>(Ks + mul24(16 * J + c, P) + g * W, k);
       if (v_staged)
-        lds_get<W>(Vs + (16 * J + c) * P + g * W, v);
+        lds_get<W>(Vs + mul24(16 * J + c, P) + g * W, v);
       else if (16 * J + c < at.cnt)
         qkv_get<W, XF>(qkv, ldq, at.row(16 * J + c), 2 * D + at.h * HD + g * W, xf, v);  // chunk rows
       else
@@ -629,28 +633,28 @@ __device__ __forceinline__ void bwd_item(const Atom& at, const float* Qs, const 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float kk[DT];
-      lds_get<DT>(Ks + (16 * J + 4 * g + r) * P + c * DT, kk);
+      lds_get<DT>(Ks + mul24(16 * J + 4 * g + r, P) + c * DT, kk);
 #pragma unroll
       for (int t = 0; t < DT; ++t) dq[t] = mfma(kk[t], ds[r], dq[t]);
     }
-    float* ta = tb + (2 * w) * TILE;
+    float* ta = tb + mul24(2 * w, TILE);
     *reinterpret_cast<float4*>(ta + c * TP + 4 * g) = make_float4(a[0], a[1], a[2], a[3]);
     *reinterpret_cast<float4*>(ta + TILE + c * TP + 4 * g) = make_float4(ds[0], ds[1], ds[2], ds[3]);
   };
   // Phase 2 of step s: key block w's tile from query block Ip = (w - s) mod nb:
   // dK^T += Q^T dS, dV^T += dO^T A, and the key's dS summed.
   auto phase2 = [&](int s) {
-    const float* tb = Tb + (nbuf == 2 ? (s & 1) : 0) * (NW * 2 * TILE);
+    const float* tb = nbuf == 2 && (s & 1) ? Tb1 : Tb;
     int Ip = w - s;
     if (Ip < 0) Ip += nb;
-    const float* ta = tb + (2 * Ip) * TILE;
+    const float* ta = tb + mul24(2 * Ip, TILE);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float av = ta[(4 * g + r) * TP + c], dsv = ta[TILE + (4 * g + r) * TP + c];
       cfa += dsv;
       float qq[DT], gg[DT];
-      lds_get<DT>(Qs + (16 * Ip + 4 * g + r) * P + c * DT, qq);
-      lds_get<DT>(Gs + (16 * Ip + 4 * g + r) * P + c * DT, gg);
+      lds_get<DT>(Qs + mul24(16 * Ip + 4 * g + r, P) + c * DT, qq);
+      lds_get<DT>(Gs + mul24(16 * Ip + 4 * g + r, P) + c * DT, gg);
 #pragma unroll
       for (int t = 0; t < DT; ++t) dk[t] = mfma(qq[t], dsv, dk[t]), dv[t] = mfma(gg[t], av, dv[t]);
     }
