@@ -269,10 +269,6 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
     lds_barrier();
     return;
   }
-  // In base 2: the scores scaled by sc log2(e) and the staged log cf in log2,
-  // so each exponent is exp2 of a difference (the hardware exp) with no
-  // multiply; the saved max goes back to natural units.
-  const float sc2 = sc * 1.44269504088896341f;
   float mx = kFloor, sum = 0.f;
   f4 acc[DT];
 #pragma unroll
@@ -304,14 +300,14 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
     float x[4], bm = kOff;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      x[r] = s[r] * sc2 + lc[r];
+      x[r] = s[r] * sc + lc[r];
       bm = fmaxf(bm, x[r]);
     }
     const float nm = fmaxf(mx, max_g(bm));
-    const float alpha = __builtin_amdgcn_exp2f(mx - nm);
+    const float alpha = __expf(mx - nm);
     float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - nm);
+    for (int r = 0; r < 4; ++r) p[r] = __expf(x[r] - nm);
     sum = sum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     mx = nm;
 #pragma unroll
@@ -346,7 +342,7 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
   // else a query on an edge at its cutoff: zeros
   out.live = i < at.cnt && (i == 0 || !is_off(lcf[i]));
   out.invl = out.live && tot > 0.f ? 1.0f / tot : 0.f;
-  out.mx = out.live && tot > 0.f ? mx * 0.693147180559945309f : kOff;  // no live key: the max never left kFloor
+  out.mx = out.live && tot > 0.f ? mx : kOff;  // no live key: the max never left kFloor
 #pragma unroll
   for (int t = 0; t < DT; ++t) out.acc[t] = acc[t];
 }
@@ -420,7 +416,7 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
       if constexpr (!SPL) *reinterpret_cast<float4*>(ok + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
       *reinterpret_cast<float4*>(ov + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
     }
-    if (g == 0) lcf[i] = pcf > 0.f ? __log2f(pcf) : kOff;  // base 2 (fwd_item)
+    if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
   }
   FwdOut<HD> out;
   fwd_item<HD, SPL>(at, Ks, Vs, lcf, q, qs, sc, out);
