@@ -39,6 +39,9 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/pet_attn.h"
 
@@ -844,11 +847,30 @@ bool split_enabled() {
   return !v || std::atoi(v) != 0;
 }
 
+// Per-kernel facts the launchers consult on every call, looked up once: the
+// compiled VGPR count, and (per device) the dynamic LDS limit already raised.
+std::mutex g_kernel_mu;
+int kernel_vgprs(const void* k) {
+  static std::map<const void*, int> vgprs;
+  std::lock_guard<std::mutex> lock(g_kernel_mu);
+  auto it = vgprs.find(k);
+  if (it != vgprs.end()) return it->second;
+  hipFuncAttributes fa{};
+  const int v = hipFuncGetAttributes(&fa, k) == hipSuccess ? fa.numRegs : -1;
+  vgprs[k] = v;
+  return v;
+}
 template <class K>
 void allow_lds(K k, size_t bytes) {
-  if (bytes > 65536)
-    (void) hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               int(bytes));
+  if (bytes <= 65536) return;
+  static std::map<std::pair<int, const void*>, size_t> raised;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  const void* kp = reinterpret_cast<const void*>(k);
+  std::lock_guard<std::mutex> lock(g_kernel_mu);
+  size_t& have = raised[{dev, kp}];
+  if (have >= bytes) return;
+  if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) == hipSuccess) have = bytes;
 }
 
 // Workgroups of kernel k (NW waves, lds bytes of LDS) one CU holds at once,
@@ -859,9 +881,9 @@ void allow_lds(K k, size_t bytes) {
 // LDS goes in 2 KB granules of 160 KB. (The runtime's occupancy query counts
 // more than fit for 5-wave workgroups.)
 int resident_wgs(const void* k, int NW, size_t lds) {
-  hipFuncAttributes fa{};
-  if (hipFuncGetAttributes(&fa, k) != hipSuccess) return 1;
-  const int vg = std::max(8, (fa.numRegs + 7) / 8 * 8);
+  const int regs = kernel_vgprs(k);
+  if (regs < 0) return 1;
+  const int vg = std::max(8, (regs + 7) / 8 * 8);
   const int c = std::min(8, 512 / vg);
   const int by_vgpr = NW % 4 ? (4 * c - 4) / NW : 4 * c / NW;
   const size_t gran = (lds + 2047) / 2048 * 2048;
