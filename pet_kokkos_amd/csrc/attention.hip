@@ -102,6 +102,13 @@ __device__ __forceinline__ f4 mfma6(const u4* a, const u4* b, f4 c) {
 }
 
 constexpr float kOff = -1e30f;  // the log cf of a key no query sees
+// log cf of a key with cf > 0: the hardware log2 times ln 2 (the fast log of
+// the reference's device path), held above -104 (log of the smallest
+// subnormal) so that a subnormal cf, which the hardware log flushes, stays a
+// live key.
+__device__ __forceinline__ float log_cf(float cf) {
+  return fmaxf(__builtin_amdgcn_logf(cf) * 0.693147180559945309f, -104.f);
+}
 __device__ __forceinline__ bool is_off(float lc) { return lc < -1e29f; }
 // The running max's start in the matrix-core forward: above kOff, so a key
 // with log cf kOff has exp(x - max) = 0 exactly whatever keys came before,
@@ -323,24 +330,53 @@ __device__ __forceinline__ void fwd_item(const Atom& at, const float* Ks, const 
       for (int t = 0; t < DT; ++t) acc[t] = mfma(v[t], p[r], acc[t]);  // O^T: dim (4g + r') DT + t, query i
     }
   };
+  // Two key blocks at a time: one max, one rescale of acc and sum for 32
+  // keys instead of 16.
+  auto block2 = [&](int J0, const f4& s0, int J1, const f4& s1) {
+    float lc[8];
+    lds_get<4>(lcf + 16 * J0 + 4 * g, lc);
+    lds_get<4>(lcf + 16 * J1 + 4 * g, lc + 4);
+    float x[8], bm = kOff;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = s0[r] * sc + lc[r];
+      x[4 + r] = s1[r] * sc + lc[4 + r];
+      bm = fmaxf(bm, fmaxf(x[r], x[4 + r]));
+    }
+    const float nm = fmaxf(mx, max_g(bm));
+    const float alpha = __expf(mx - nm);
+    float p[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) p[r] = __expf(x[r] - nm);
+    sum = sum * alpha + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+    mx = nm;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v[DT];
+        lds_get<DT>(Vs + (16 * (h ? J1 : J0) + 4 * g + r) * P + c * DT, v);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) acc[t] = mfma(v[t], p[4 * h + r], acc[t]);
+      }
+  };
   // The wave's own key block first: it is all the wave itself staged, so it
   // runs before the workgroup barrier, under the other waves' loads. Then the
-  // others in the order w + 1, w + 2, ... (mod nb), the next block's scores
-  // issued before this block's softmax and PV, the last block peeled.
+  // others in the order w + 1, w + 2, ... (mod nb), two at a time (their two
+  // score products independent), an odd one last.
   block(w, scores(w));
   lds_barrier();
-  if (at.nb > 1) {
-    int J = w + 1 < at.nb ? w + 1 : 0;
-    f4 s = scores(J);
-    for (int t = 2; t < at.nb; ++t) {
-      const int Jn = J + 1 < at.nb ? J + 1 : 0;
-      const f4 sn = scores(Jn);
-      block(J, s);
-      s = sn;
-      J = Jn;
-    }
-    block(J, s);
+  auto next = [&](int j) { return j + 1 < at.nb ? j + 1 : 0; };
+  int rem = at.nb - 1, J0 = next(w);
+  for (; rem >= 2; rem -= 2) {
+    const int J1 = next(J0);
+    const f4 s0 = scores(J0), s1 = scores(J1);
+    block2(J0, s0, J1, s1);
+    J0 = next(J1);
   }
+  if (rem == 1) block(J0, scores(J0));
   const float tot = sum_g(sum);
   // else a query on an edge at its cutoff: zeros
   out.live = i < at.cnt && (i == 0 || !is_off(lcf[i]));
@@ -369,7 +405,9 @@ __device__ __forceinline__ void fwd_store(const Atom& at, const FwdOut<HD>& out,
 // One item per workgroup: the item's K, V and q loaded into registers and
 // staged in LDS, one barrier, then its forward.
 template <int HD, int MAXT, bool XF = false, bool SPL = false>
-__global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict__ qkv, int64_t ldq,
+// At head_dim <= 32 the forward is held to 64 VGPRs (eight waves a SIMD: five
+// 5-wave workgroups a CU), which it fits without spilling.
+__global__ void __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(HD <= 32 ? 8 : 1))) attn_fwd_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                         const int* __restrict__ off, int N, int n0, int64_t eb,
                                                         int S, int H, float sc, const float* __restrict__ cf_seq,
                                                         int64_t ldc, float* __restrict__ merged, int64_t ldm,
@@ -419,7 +457,7 @@ __global__ void __launch_bounds__(MAXT) attn_fwd_kernel(const float* __restrict_
       if constexpr (!SPL) *reinterpret_cast<float4*>(ok + t) = make_float4(k[t], k[t + 1], k[t + 2], k[t + 3]);
       *reinterpret_cast<float4*>(ov + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
     }
-    if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
+    if (g == 0) lcf[i] = pcf > 0.f ? log_cf(pcf) : kOff;
   }
   FwdOut<HD> out;
   fwd_item<HD, SPL>(at, Ks, Vs, lcf, q, qs, sc, out);
@@ -456,7 +494,7 @@ __global__ void __launch_bounds__(256) attn_fwd_valu_kernel(const float* __restr
   const int i = threadIdx.x;
   if (i < at.cnt) {
     const float cv = cf_seq[size_t(at.n) * ldc + i];
-    lcf[i] = cv > 0.f ? __logf(cv) : kOff;
+    lcf[i] = cv > 0.f ? log_cf(cv) : kOff;
   }
   float q[HD], acc[HD];
   if (i < at.cnt) gmem_get<HD>(qkv + at.row(i) * ldq + at.h * HD, q);
@@ -767,7 +805,7 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
         for (int p = 0; p < 3; ++p) *reinterpret_cast<u4*>(ov + kc * 12 + 4 * p) = vp[p];
       }
     }
-    if (g == 0) lcf[i] = pcf > 0.f ? __logf(pcf) : kOff;
+    if (g == 0) lcf[i] = pcf > 0.f ? log_cf(pcf) : kOff;
   }
   BwdOut<HD> out;
   bwd_item<HD, XF, SPL>(at, Qs, Ks, Gs, Vs, lcf, Tb, nbuf, vlds, oo, mi, li, qkv, ldq, xf, H, sc, out);
