@@ -169,37 +169,40 @@ def time_ef(device, reps, cpu: bool):
 
     from pet_kokkos_amd.model import PetModel, ef_flops, ef_workload, structures_input
 
-    res = {}
+    res, cpu_cases = {}, []
+    # every GPU timing first, the CPU oracles after: a host thread pool left
+    # spinning by an oracle run would slow the launches of the next timing
     for name in ("c2", "c2-residual", "c5"):
         h, w, comp, sts = ef_workload(name)
         m = PetModel(h, w, comp)
         x = structures_input(h, sts, device)
         cnt = np.diff(x.host.off).astype(np.float64) + 1
         fl = ef_flops(h, x.n_atoms, x.n_edges, float((cnt * cnt).sum()))
-        n = max(3, reps // (2 if name == "c2" else 20))
+        n = max(3, reps // (5 if name != "c5" else 20))
         o = m.compute(x, True)
         e_ms = _timed(lambda: m.compute(x, False, out=o), n) / 1e3
         ef_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
-        r = dict(featurizer=h.featurizer, structures=len(sts), atoms=x.n_atoms, edges=x.n_edges, d_pet=h.d_pet,
-                 heads=h.num_heads,
-                 ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
-                 ef_bound_ms=fl["forces"] / PEAK_FP32_MFMA * 1e3, ef_frac_of_roofline=fl["forces"] / PEAK_FP32_MFMA
-                 * 1e3 / ef_ms, workspace_gb=m.workspace_bytes / 1e9)
+        res[name] = dict(featurizer=h.featurizer, structures=len(sts), atoms=x.n_atoms, edges=x.n_edges,
+                         d_pet=h.d_pet, heads=h.num_heads, ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
+                         ef_bound_ms=fl["forces"] / PEAK_FP32_MFMA * 1e3,
+                         ef_frac_of_roofline=fl["forces"] / PEAK_FP32_MFMA * 1e3 / ef_ms,
+                         workspace_gb=m.workspace_bytes / 1e9)
         if name in ("c2", "c2-residual") and cpu:
-            from oracle import pet_model as om
-            sp = x.species.cpu().numpy()
-            om.evaluate(h, w, sp, x.host, comp, dtype=torch.float32)
+            cpu_cases.append((name, h, w, comp, x.species.cpu().numpy(), x.host))
+        del m, x, o
+        torch.cuda.empty_cache()
+    if cpu_cases:
+        from oracle import pet_model as om
+        for name, h, w, comp, sp, host in cpu_cases:
+            om.evaluate(h, w, sp, host, comp, dtype=torch.float32)
             t = []
             for _ in range(2):
                 c0 = time.perf_counter()
-                om.evaluate(h, w, sp, x.host, comp, dtype=torch.float32)
+                om.evaluate(h, w, sp, host, comp, dtype=torch.float32)
                 t.append(time.perf_counter() - c0)
-            r["cpu_ms"] = min(t) * 1e3
-            r["cpu_note"] = (f"oracle/pet_model.py in float32 torch on {torch.get_num_threads()} host threads, "
-                             "forces by autograd, best of 2 after a warmup")
-        res[name] = r
-        del m, x, o
-        torch.cuda.empty_cache()
+            res[name]["cpu_ms"] = min(t) * 1e3
+            res[name]["cpu_note"] = (f"oracle/pet_model.py in float32 torch on {torch.get_num_threads()} host "
+                                     "threads, forces by autograd, best of 2 after a warmup")
     res["note"] = ("random-init PET-shaped models: feedforward featurizer (RMSNorm, SwiGLU, d_node 2 d_pet, "
                    "d_head 128) for c2 and c5, residual featurizer (LayerNorm, SiLU, d_node d_pet) for "
                    "c2-residual; neighbour list built on the host beforehand and not timed")
