@@ -999,7 +999,7 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   // the fullest holds one workgroup a CU and V-from-global with one buffer two
   // (C5 backward 3853 -> 3244 us). PET_ATTN_BWD_VLDS (1 staged, 2 not) and
   // PET_ATTN_BWD_NBUF (1, 2) force a layout where it fits.
-  static const int force_v = env_int("PET_ATTN_BWD_VLDS"), force_b = env_int("PET_ATTN_BWD_NBUF");
+  const int force_v = env_int("PET_ATTN_BWD_VLDS"), force_b = env_int("PET_ATTN_BWD_NBUF");  // read per launch
   const size_t cap = size_t(max_lds_bytes());
   const int layouts[3][2] = {{1, 2}, {0, 2}, {0, 1}};  // (vlds, nbuf), fullest first
   int best = -1, best_res = 0;

@@ -191,6 +191,23 @@ def test_split_products_as_accurate_as_fp32(device, hd, monkeypatch):
         assert not np.array_equal(out["0"][2], out["1"][2])
 
 
+@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("vlds,nbuf", [(1, 2), (1, 1), (2, 2), (2, 1)])
+@pytest.mark.parametrize("split", ["1", "0"])
+def test_backward_layouts(device, hd, vlds, nbuf, split, monkeypatch):
+    # Every LDS layout of the backward, forced (PET_ATTN_BWD_VLDS: 1 V staged,
+    # 2 from global memory; PET_ATTN_BWD_NBUF: tile buffers), with the split
+    # dP (V staged split, head_dim 32) and without: the pipelined two-buffer
+    # step loop and the two-barrier one-buffer loop, on ragged atoms.
+    monkeypatch.setenv("PET_ATTN_BWD_VLDS", str(vlds))
+    monkeypatch.setenv("PET_ATTN_BWD_NBUF", str(nbuf))
+    monkeypatch.setenv("PET_ATTN_SPLIT", split)
+    counts = [0, 15, 16, 31, 47, 5, 60, 33, 70]
+    tk, qkv, dm = random_case(counts, 2, hd, seed=200 + hd + 10 * vlds + nbuf, cf_kind="random")
+    check_against_oracle(device, f"backward layout vlds {vlds} nbuf {nbuf} split {split} hd {hd}", tk.off,
+                         tk.cf_seq, qkv, dm, 2, hd)
+
+
 def test_cf_adjoint_accumulates(device):
     tk, qkv, dm = random_case([12, 40, 7], 2, 32, seed=6)
     start = np.random.default_rng(0).standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
