@@ -500,10 +500,8 @@ namespace {
 // 1: its main loop reaches 72% of the fp32 matrix peak at K = 1024 where
 // rocBLAS reaches 90%. PET_MODEL_GEMM selects, read once.
 bool own_gemm(int M, int K) {
-  static const int mode = [] {
-    const char* v = std::getenv("PET_MODEL_GEMM");
-    return v ? std::atoi(v) : 0;
-  }();
+  const char* v = std::getenv("PET_MODEL_GEMM");  // read per call: a process may compare both
+  const int mode = v ? std::atoi(v) : 0;
   return K % 16 == 0 && (mode == 1 || (mode == 2 && M <= 4096));
 }
 

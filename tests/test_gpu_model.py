@@ -98,6 +98,22 @@ def test_odd_widths_match_oracle(name, device):
 
 
 @pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
+def test_model_on_the_fused_dense_layer(name, device, monkeypatch):
+    # PET_MODEL_GEMM=1: every dense layer with K a multiple of 16 on the
+    # library's fused GEMM (pet_linear_fused's kernel) instead of rocBLAS
+    monkeypatch.setenv("PET_MODEL_GEMM", "1")
+    h = weights.MODELS[name]
+    w = weights.random_weights(h, 15)
+    comp = weights.random_composition(h)
+    print(f"[model] {name} batch-3 on the fused dense layer", flush=True)
+    m = PetModel(h, w, comp)
+    x = structures_input(h, CASES["batch-3"](), device)
+    got = m.compute(x, forces=True, edge_grad=True)
+    torch.cuda.synchronize()
+    compare(got, oracle_of(h, w, comp, x))
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
 def test_model_repeats_bitwise(name, device):
     h = weights.MODELS[name]
     w = weights.random_weights(h, 12)
