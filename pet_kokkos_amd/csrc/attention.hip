@@ -429,15 +429,13 @@ __global__ void __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(HD <=
   if (w < at.nb) {
     float k[W], v[W];
     const bool real = i < at.cnt;
-    if (real) {
-      const size_t r = at.row(i);
-      qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
-      qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
-      qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
-    } else {
-#pragma unroll
-      for (int t = 0; t < W; ++t) q[t] = k[t] = v[t] = 0.f;
-    }
+    // A padded slot (i >= cnt) loads the atom's own row instead of zeros: its
+    // values are finite (and cached), its key's log cf is kOff so its weight
+    // is exactly 0, and its query's results are not stored; no branch.
+    const size_t r = at.row(real ? i : 0);
+    qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
+    qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
+    qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
     const float pcf = real && g == 0 ? cf_seq[size_t(at.n) * ldc + i] : 0.f;
     if constexpr (SPL) {
       unsigned* o = reinterpret_cast<unsigned*>(Ks) + i * KP6 + g * (W / 8) * 12;
