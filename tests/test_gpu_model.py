@@ -242,6 +242,30 @@ def test_session_steps_match_fresh_evaluations(device):
         pos = pos + rng.normal(0.0, 0.05, pos.shape)
 
 
+def test_session_steps_replayed_as_a_graph(device):
+    """Calculator(graph=True): from the third step on a list each step is one
+    graph replay; its results are the bits of the eager steps."""
+    h = weights.MODELS["tiny"]
+    w = weights.random_weights(h, 17)
+    m = PetModel(h, w, weights.random_composition(h))
+    s = systems.water_box(2, 6.2, seed=11)
+    e = systems.neighbor_list(s, h.cutoff + 1.0)
+    off = np.concatenate([[0], np.cumsum(np.bincount(e.centre, minlength=len(s.positions)))])
+    eager, graph = Calculator(m, device), Calculator(m, device, graph=True)
+    for c in (eager, graph):
+        c.set_neighbors(s.numbers, off, e.neigh, e.shift)
+    rng = np.random.default_rng(1)
+    pos = s.positions.copy()
+    for step in range(6):
+        a = eager.compute_step(pos, s.cell, edge_gradients=True)
+        b = graph.compute_step(pos, s.cell, edge_gradients=True)
+        assert a["energy"] == b["energy"], step
+        for k in ("per_atom", "forces", "virial", "edge_gradient"):
+            assert np.array_equal(a[k], b[k]), (step, k)
+        pos = pos + rng.normal(0.0, 0.05, pos.shape)
+    assert graph._graphs is not None and not graph._graphs.broken
+
+
 def test_c5_model_small_batch(device):
     """configs[4]'s model shape (d 512, 8 heads of 64, 2 x 2 layers) on a small
     batch: the head_dim-64 attention kernels and wide norms inside the model."""
