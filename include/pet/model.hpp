@@ -22,12 +22,14 @@
 #include <cmath>
 #include <cstdint>
 #include <map>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
 #include <vector>
 
 #include "../pet_model.h"
+#include "graph.hpp"
 
 namespace pet {
 
@@ -204,10 +206,21 @@ struct EdgeListView {
 // drift past the cutoff weigh nothing); compute_edges() is both at once. Edge
 // geometry is always made on the device (pet_edge_geometry). Device buffers
 // are kept between calls and grown when a structure needs more.
+//
+// With graph = true (and a non-null stream: capture needs one; on the null
+// stream the steps stay eager), compute_step replays its device work -- edge
+// geometry and the whole evaluation -- as one HIP graph per output set from the
+// third step on a list (pet::GraphCache): positions are copied into the buffer
+// the graph reads, the results are the bits of an eager step, and a small
+// structure's step loses most of its launch cost. set_neighbors drops the
+// recorded graphs.
 class Calculator {
  public:
-  Calculator(PetModel& model, double cutoff, std::vector<int> species_to_index, hipStream_t stream = nullptr)
-      : model_(model), cutoff_(cutoff), s2i_(std::move(species_to_index)), stream_(stream) {}
+  Calculator(PetModel& model, double cutoff, std::vector<int> species_to_index, hipStream_t stream = nullptr,
+             bool graph = false)
+      : model_(model), cutoff_(cutoff), s2i_(std::move(species_to_index)), stream_(stream) {
+    if (graph) graphs_ = std::make_unique<GraphCache>(stream);
+  }
   Calculator(const Calculator&) = delete;
   Calculator& operator=(const Calculator&) = delete;
   ~Calculator() {
@@ -286,8 +299,12 @@ class Calculator {
     d_.vec = buf<double>("vec", 3 * size_t(E)), d_.dist = buf<double>("dist", E), d_.pcut = buf<double>("pcut", E);
     d_.cut = buf<float>("cut", E);
     model_check(hipStreamSynchronize(stream_) == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH, "synchronize");
+    if (graphs_) graphs_->clear();
     have_list_ = true;
   }
+
+  // Whether the step graphs fell back to eager work for good (a failed capture).
+  bool graph_broken() const { return graphs_ && graphs_->broken(); }
 
   // One step on the list set_neighbors holds, with the atoms' positions in its
   // order (Calculator::compute_step, include/pet/calculator.hpp:228-230).
@@ -299,18 +316,29 @@ class Calculator {
     const int N = d_.n_atoms, E = d_.n_edges;
     double* pos = buf<double>("pos", 3 * size_t(N));
     double* dcell = buf<double>("cell", 9);
-    copy_in(pos, positions, 3 * size_t(N));
-    if (cell) copy_in(dcell, cell, 9);
-    model_check(pet_edge_geometry(E, d_.center, neigh_, shift_, pos, shift_ ? dcell : nullptr, cutoff_,
-                                  h.cutoff_width, h.cutoff_function, const_cast<double*>(d_.vec),
-                                  const_cast<double*>(d_.dist), const_cast<double*>(d_.pcut),
-                                  const_cast<float*>(d_.cut), stream_),
-                "edge geometry");
     DeviceOut o;
     o.energy = buf<double>("energy", 1), o.per_atom = buf<double>("per_atom", N);
     if (forces) o.forces = buf<double>("forces", 3 * size_t(N)), o.virial = buf<double>("virial", 9);
     if (forces && edge_gradient) o.edge_grad = buf<double>("edge_grad", 3 * size_t(E));
-    model_.compute(d_, forces, o, stream_);
+    copy_in(pos, positions, 3 * size_t(N));
+    if (cell) copy_in(dcell, cell, 9);
+    auto work = [&] {
+      model_check(pet_edge_geometry(E, d_.center, neigh_, shift_, pos, shift_ ? dcell : nullptr, cutoff_,
+                                    h.cutoff_width, h.cutoff_function, const_cast<double*>(d_.vec),
+                                    const_cast<double*>(d_.dist), const_cast<double*>(d_.pcut),
+                                    const_cast<float*>(d_.cut), stream_),
+                  "edge geometry");
+      model_.compute(d_, forces, o, stream_);
+    };
+    if (graphs_) {
+      // every buffer the recorded work reads or writes, by address
+      const GraphCache::Key key{std::uintptr_t(forces), std::uintptr_t(pos), std::uintptr_t(dcell),
+                                std::uintptr_t(o.energy), std::uintptr_t(o.per_atom), std::uintptr_t(o.forces),
+                                std::uintptr_t(o.virial), std::uintptr_t(o.edge_grad), std::uintptr_t(d_.vec)};
+      graphs_->run(key, work);
+    } else {
+      work();
+    }
     EnergyResult r;
     r.per_atom.resize(N);
     copy_out(&r.total, o.energy, 1);
@@ -378,6 +406,7 @@ class Calculator {
   const int* neigh_ = nullptr;
   const int* shift_ = nullptr;
   bool have_list_ = false;
+  std::unique_ptr<GraphCache> graphs_;
 };
 
 }  // namespace pet

@@ -12,7 +12,10 @@
 // then "Z x y z" an atom). Writes DIR/result.f64 = [energy, per_atom (N),
 // forces (3N), virial (9)], DIR/repeat.ok when a second evaluation gives the
 // same bits, and DIR/fd.f64 = [central difference of the energy in atom 0's x
-// (step 1e-3 A, energy-only runs), the force's x].
+// (step 1e-3 A, energy-only runs), the force's x], and DIR/graph.ok when
+// compute_step on a Calculator with graph = true (a stream of its own) gives
+// the bits of an eager Calculator's on the same list, step after step, with
+// and without forces and edge gradients.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -93,6 +96,41 @@ int main(int argc, char** argv) {
     FILE* ff = std::fopen((dir + "/fd.f64").c_str(), "wb");
     std::fwrite(fd, sizeof(double), 2, ff);
     std::fclose(ff);
+
+    hipStream_t st = nullptr;
+    if (hipStreamCreate(&st) != hipSuccess) fail("hipStreamCreate");
+    {
+      const auto& hy = model.hypers();
+      const pet::HostEdges e = pet::build_edges(s, cutoff, hy.cutoff_width, hy.cutoff_function);
+      std::vector<int> z(s.numbers), nb(e.neigh);
+      std::vector<double> pos(3 * size_t(N)), cell(9);
+      for (int n = 0; n < N; ++n)
+        for (int c = 0; c < 3; ++c) pos[3 * size_t(n) + c] = s.positions[n][c];
+      for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) cell[3 * r + c] = s.cell[r][c];
+      pet::EdgeListView v;
+      v.n_atoms = N, v.positions = pos.data(), v.atomic_numbers = z.data(), v.offsets = e.off.data();
+      v.neighbors = nb.data(), v.shifts = e.shift.data(), v.cell = cell.data();
+      pet::Calculator eager(model, cutoff, s2i, st), graph(model, cutoff, s2i, st, true);
+      eager.set_neighbors(v), graph.set_neighbors(v);
+      bool same = true;
+      auto eq = [](const std::vector<double>& a, const std::vector<double>& b) {
+        return a.size() == b.size() && std::memcmp(a.data(), b.data(), sizeof(double) * a.size()) == 0;
+      };
+      for (int k = 0; k < 10; ++k) {
+        // small displacements, so the list stays the one set_neighbors holds
+        for (size_t i = 0; i < pos.size(); ++i) pos[i] += 1e-3 * double((i * 7 + k * 3) % 5) - 2e-3;
+        const bool f = k % 5 != 4, eg = k % 2 == 0;
+        std::vector<double> ga, gb;
+        const pet::EnergyResult a = eager.compute_step(pos.data(), cell.data(), f, f && eg ? &ga : nullptr);
+        const pet::EnergyResult b = graph.compute_step(pos.data(), cell.data(), f, f && eg ? &gb : nullptr);
+        same = same && std::memcmp(&a.total, &b.total, sizeof(double)) == 0 && eq(a.per_atom, b.per_atom) &&
+               eq(a.forces, b.forces) && std::memcmp(a.virial, b.virial, sizeof a.virial) == 0 && eq(ga, gb);
+      }
+      if (graph.graph_broken()) fail("graph capture fell back to eager work");
+      if (same) std::fclose(std::fopen((dir + "/graph.ok").c_str(), "wb"));
+    }
+    (void) hipStreamDestroy(st);
   } catch (const std::exception& e) {
     fail(e.what());
   }

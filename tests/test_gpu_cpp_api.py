@@ -106,7 +106,8 @@ def test_cpp_model_calculator(tmp_path, name):
     """pet::PetModel + pet::Calculator (include/pet/model.hpp) from C++: the
     C++ host neighbour list, the model's energy / forces / virial against the
     CPU oracle, a repeat bit for bit, and forces against a central difference
-    of the energy."""
+    of the energy, and compute_step replayed as a HIP graph giving the bits of
+    eager steps."""
     from oracle import pet_model as om
     from pet_kokkos_amd import weights
     from pet_kokkos_amd.forces import CUTOFF_KINDS
@@ -151,3 +152,4 @@ def test_cpp_model_calculator(tmp_path, name):
     assert os.path.exists(tmp_path / "repeat.ok")
     fd, f0 = np.fromfile(tmp_path / "fd.f64", dtype=np.float64)
     assert abs(fd - f0) <= 1e-2 + 1e-3 * abs(f0), (fd, f0)
+    assert (tmp_path / "graph.ok").exists(), "Calculator(graph = true): a replayed step differed from an eager one"
