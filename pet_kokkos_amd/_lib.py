@@ -43,6 +43,8 @@ EXPORTS = (
     "pet_model_compute",
     "pet_model_workspace_bytes",
     "pet_linear_fused",
+    "pet_linear_split_weights",
+    "pet_linear_fused_split",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX = range(9)
@@ -176,6 +178,10 @@ def load() -> ctypes.CDLL:
     lib.pet_model_compute.argtypes = [_P, ctypes.POINTER(ModelEdges), _I, _P, _P, _P, _P, _P, _P]
     lib.pet_linear_fused.restype = ctypes.c_int
     lib.pet_linear_fused.argtypes = [_I, _I, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
+    lib.pet_linear_split_weights.restype = ctypes.c_int
+    lib.pet_linear_split_weights.argtypes = [_P, _I, _I, _I64, _P, _P]
+    lib.pet_linear_fused_split.restype = ctypes.c_int
+    lib.pet_linear_fused_split.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_model_workspace_bytes.restype = ctypes.c_size_t
     lib.pet_model_workspace_bytes.argtypes = [_P]
     _lib = lib

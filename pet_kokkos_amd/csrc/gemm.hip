@@ -24,12 +24,19 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "../../include/pet_model.h"
+#include "split_bf16.h"
 
 namespace pet_gemm {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
+using pet_split::f4;
+using pet_split::mfma6;
+using pet_split::pack_hi;
+using pet_split::split3;
+using pet_split::split8;
+using pet_split::u4;
 
 __device__ __forceinline__ f4 mfma(float a, float b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -46,6 +53,36 @@ struct Epi {
   int64_t ldpre = 0;
   int act = 0;                       // 0 none, 1 SiLU, 2 SwiGLU (C has N/2 columns)
 };
+
+// The epilogue, shared by the kernels: lane (c, g) of tile (a, b) holds rows
+// 4g + r, column c of the wave's (BM/2) x (BN/2) share.
+template <int BM, int BN>
+__device__ __forceinline__ void epilogue(const f4 (&acc)[BM / 32][BN / 32], int m0, int n0, int wm, int wn, int c,
+                                         int g, int M, int N, float* C, int64_t ldc, const Epi& epi) {
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const int j = n0 + wn * WN + 16 * b + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = m0 + wm * WM + 16 * a + 4 * g + r;
+        float v = acc[a][b][r];
+        if (epi.row_scale && i < M) v *= epi.row_scale[i];
+        if (epi.bias && j < N) v += epi.bias[j];
+        if (epi.cin && i < M && j < N) v += epi.beta * epi.cin[int64_t(i) * epi.ldcin + j];
+        if (epi.pre && i < M && j < N) epi.pre[int64_t(i) * epi.ldpre + j] = v;
+        if (epi.act == 2) {
+          // SwiGLU: columns 2c' (value) and 2c'+1 (gate) sit in lanes c and c + 1
+          const float gate = __shfl_down(v, 1, 16);
+          if ((c & 1) == 0 && i < M && j < N) C[int64_t(i) * ldc + j / 2] = v * sig_fast(gate);
+        } else if (i < M && j < N) {
+          C[int64_t(i) * ldc + j] = epi.act == 1 ? v * sig_fast(v) : v;
+        }
+      }
+    }
+}
 
 template <int BM, int BN, int BK = 32>
 __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const float* __restrict__ A, int64_t lda,
@@ -126,29 +163,122 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
     }
   }
 
-  // epilogue: lane (c, g) of tile (a, b) holds rows 4g + r, column c
+  epilogue<BM, BN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+}
+
+// The same product with the fp32 matrix cores' work moved to the bf16 ones:
+// B comes split once (pet_linear_split_weights: per row, per 8-element k
+// group, its three bf16 parts, 48 bytes), A is split as each k step of 32 is
+// staged, and a 16 x 16 x 32 step is the six part products of split_bf16.h
+// (6 x ~22 cycles against 8 x 32 on the fp32 instruction, at fp32's error).
+// 64 x 64 or 128 x 64 tiles of 4 waves (2 x 2), k steps of 32 through LDS
+// (the next step's slices loaded into registers under the current step's
+// products): a row's step is 4 groups x 3 parts x 16 bytes plus a 16-byte pad
+// (13 u4, so a 16-lane column of 128-bit reads is conflict-free), 26 / 39 KB
+// a workgroup. K a multiple of 32. Measured against torch's GEMM at the
+// model's shapes: even at K = 128 (27318 x 128 x 128: 16.1 against 20.0 us),
+// ahead at 26670 x 1024 x 128 (75 against 86 us) and 131072 x 1536 x 512
+// (1402 against 1458 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
+template <int BM, int BN>
+__global__ void __launch_bounds__(256) gemm_nt_split_kernel(int M, int N, int K, const float* __restrict__ A,
+                                                            int64_t lda, const u4* __restrict__ Bs, float* C,
+                                                            int64_t ldc, Epi epi) {
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16, RP = 13;
+  constexpr int AQ = BM * 8, AL = (AQ + 255) / 256;   // float4 of a step's A slice, a thread's share
+  constexpr int BQ = BN * 12, BL = (BQ + 255) / 256;  // u4 of a step's B slice
+  __shared__ u4 As[BM * RP], Bt[BN * RP];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  const int wm = w >> 1, wn = w & 1;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, KG = K / 8;
+
+  f4 acc[TM][TN];
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      const int j = n0 + wn * WN + 16 * b + c;
+    for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // A: thread t's float4 slots q = t + 256 u, row q / 8, k 4 (q % 8) .. ;
+  // B: u4 slots q, row q / 12, part (q % 12) of the row's step
+  float4 ra[AL];
+  u4 rb[BL];
+  auto load = [&](int k0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = m0 + wm * WM + 16 * a + 4 * g + r;
-        float v = acc[a][b][r];
-        if (epi.row_scale && i < M) v *= epi.row_scale[i];
-        if (epi.bias && j < N) v += epi.bias[j];
-        if (epi.cin && i < M && j < N) v += epi.beta * epi.cin[int64_t(i) * epi.ldcin + j];
-        if (epi.pre && i < M && j < N) epi.pre[int64_t(i) * epi.ldpre + j] = v;
-        if (epi.act == 2) {
-          // SwiGLU: columns 2c' (value) and 2c'+1 (gate) sit in lanes c and c + 1
-          const float gate = __shfl_down(v, 1, 16);
-          if ((c & 1) == 0 && i < M && j < N) C[int64_t(i) * ldc + j / 2] = v * sig_fast(gate);
-        } else if (i < M && j < N) {
-          C[int64_t(i) * ldc + j] = epi.act == 1 ? v * sig_fast(v) : v;
-        }
+    for (int u = 0; u < AL; ++u) {
+      const int q = tid + 256 * u, i = m0 + q / 8;
+      ra[u] = q < AQ && i < M ? *reinterpret_cast<const float4*>(A + int64_t(i) * lda + k0 + 4 * (q % 8))
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < BL; ++u) {
+      const int q = tid + 256 * u, j = n0 + q / 12;
+      rb[u] = q < BQ && j < N ? Bs[(int64_t(j) * KG + k0 / 8) * 3 + q % 12] : u4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int u = 0; u < AL; ++u) {
+      const int q = tid + 256 * u;
+      if (q < AQ) {
+        // the float4 is half of k group (q % 8) / 2: its parts go to that half of each part's 16 bytes
+        float h[3][4];
+        split3(ra[u].x, h[0][0], h[1][0], h[2][0]);
+        split3(ra[u].y, h[0][1], h[1][1], h[2][1]);
+        split3(ra[u].z, h[0][2], h[1][2], h[2][2]);
+        split3(ra[u].w, h[0][3], h[1][3], h[2][3]);
+        unsigned* dst = reinterpret_cast<unsigned*>(&As[(q / 8) * RP + ((q % 8) / 2) * 3]) + 2 * (q & 1);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          *reinterpret_cast<uint2*>(dst + 4 * p) = make_uint2(pack_hi(h[p][0], h[p][1]), pack_hi(h[p][2], h[p][3]));
       }
     }
+#pragma unroll
+    for (int u = 0; u < BL; ++u) {
+      const int q = tid + 256 * u;
+      if (q < BQ) Bt[(q / 12) * RP + q % 12] = rb[u];
+    }
+  };
+
+  const int steps = K / 32;
+  load(0);
+  store();
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    if (s + 1 < steps) load((s + 1) * 32);
+    u4 av[TM][3], bv[TN][3];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) av[a][p] = As[(wm * WM + 16 * a + c) * RP + 3 * g + p];
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) bv[b][p] = Bt[(wn * WN + 16 * b + c) * RP + 3 * g + p];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b) acc[a][b] = mfma6(av[a], bv[b], acc[a][b]);
+    if (s + 1 < steps) {
+      __syncthreads();  // every wave is done with the step's slices
+      store();
+      __syncthreads();
+    }
+  }
+  epilogue<BM, BN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+}
+
+// W [N, K] (ld ldw) as split rows: out[(n K/8 + j) 3 + p] = part p of k group j.
+__global__ void split_rows_kernel(const float* __restrict__ W, int N, int K, int64_t ldw, u4* __restrict__ out) {
+  const int KG = K / 8;
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= int64_t(N) * KG) return;
+  const int n = int(t / KG), j = int(t % KG);
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = W[int64_t(n) * ldw + 8 * j + e];
+  u4 parts[3];
+  split8(x, parts);
+#pragma unroll
+  for (int p = 0; p < 3; ++p) out[t * 3 + p] = parts[p];
 }
 
 }  // namespace pet_gemm
@@ -190,5 +320,51 @@ extern "C" int pet_linear_fused(int M, int N, int K, const float* A, int64_t lda
                            (cin && ldcin < N) || (pre && ldpre < N) || act < 0 || act > 2))
     return PET_ATTN_EINVAL;
   return pet_gemm_nt_fused(M, N, K, A, lda, W, ldw, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
+                           reinterpret_cast<hipStream_t>(stream));
+}
+
+int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
+                      const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                      float* pre, int64_t ldpre, int act, hipStream_t st) {
+  if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
+  if (M == 0 || N == 0) return PET_ATTN_OK;
+  if (K % 32 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15))
+    return PET_ATTN_EALIGN;
+  if (act == 2 && N % 2) return PET_ATTN_EINVAL;
+  Epi e;
+  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
+  e.act = act;
+  auto go = [&](auto kern, int bm, int bn) {
+    hipLaunchKernelGGL(kern, dim3(unsigned((N + bn - 1) / bn), unsigned((M + bm - 1) / bm)), dim3(256), 0, st, M, N,
+                       K, A, lda, static_cast<const u4*>(Bs), C, ldc, e);
+  };
+  // measured on MI355X: 128 x 64 tiles where there are many (131072 x 1536 x
+  // 512: 1402 us against 1535 for 64 x 64), 64 x 64 otherwise (27318 x 128 x
+  // 128: 16.1 against 18.4 us); one LDS buffer beat two in every shape
+  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
+  if (t128 >= 2048)
+    go(gemm_nt_split_kernel<128, 64>, 128, 64);
+  else
+    go(gemm_nt_split_kernel<64, 64>, 64, 64);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+extern "C" int pet_linear_split_weights(const float* W, int N, int K, int64_t ldw, void* out, void* stream) {
+  if (N < 0 || K < 0 || K % 32 || ldw < K || ((N > 0 && K > 0) && (!W || !out))) return PET_ATTN_EINVAL;
+  if (reinterpret_cast<uintptr_t>(out) & 15) return PET_ATTN_EALIGN;
+  const int64_t n = int64_t(N) * (K / 8);
+  if (n == 0) return PET_ATTN_OK;
+  hipLaunchKernelGGL(split_rows_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), W, N, K, ldw, static_cast<u4*>(out));
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+extern "C" int pet_linear_fused_split(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit, float* C,
+                                      int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                      int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream) {
+  if ((M > 0 && N > 0) && (!A || !Wsplit || !C || ldc < (act == 2 ? N / 2 : N) || lda < K ||
+                           (cin && ldcin < N) || (pre && ldpre < N) || act < 0 || act > 2))
+    return PET_ATTN_EINVAL;
+  return pet_gemm_nt_split(M, N, K, A, lda, Wsplit, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
                            reinterpret_cast<hipStream_t>(stream));
 }

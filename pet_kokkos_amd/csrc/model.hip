@@ -42,6 +42,9 @@ int pet_rows_rms_inv(int rows, int width, const float* in, int64_t ldi, float* i
 int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                       int64_t ldc, const float* row_scale, const float* bias, const float* cin, int64_t ldcin,
                       float beta, float* pre, int64_t ldpre, int act, hipStream_t st);
+int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
+                      const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                      float* pre, int64_t ldpre, int act, hipStream_t st);
 
 namespace pet_model_impl {
 
@@ -469,13 +472,16 @@ struct pet_model {
   pet_model_hypers h{};
   int hd = 0, cw = 0, ew = 0;  // head_dim, center / edge MLP pre-activation widths
   std::unordered_map<std::string, Mat> m;
+  std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
   void* weights = nullptr;
+  void* wsplit = nullptr;
   double* comp = nullptr;
   Arena ws;
 
   ~pet_model() {
-    if (weights || comp || ws.bytes()) (void) hipDeviceSynchronize();
+    if (weights || wsplit || comp || ws.bytes()) (void) hipDeviceSynchronize();
     if (weights) (void) hipFree(weights);
+    if (wsplit) (void) hipFree(wsplit);
     if (comp) (void) hipFree(comp);
   }
   const Mat& w(const std::string& name) const {
@@ -505,6 +511,28 @@ bool own_gemm(int M, int K) {
   return K % 16 == 0 && (mode == 1 || (mode == 2 && M <= 4096));
 }
 
+// out[M, N] = in W^T + beta out, W a model matrix [N, K]: rocBLAS fp32, or
+// this library's split-product kernel (gemm.hip) where W has a split copy (K a
+// multiple of 32) and in is 16-byte aligned rows -- by default for the large
+// products (M N K >= 2^32), every one with PET_MODEL_GEMM=3, none with
+// PET_MODEL_GEMM=0. Measured on MI355X (energy+forces, ms, same process):
+// C2 2.98 / 2.15 (residual) with rocBLAS, the same by default (no C2 product is
+// that large), 3.59 / 2.40 with all split; C5 275 with rocBLAS, 267 by
+// default, 267 with all split.
+int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int N,
+           int K, float beta, hipStream_t st) {
+  const char* v = std::getenv("PET_MODEL_GEMM");  // read per call: a process may compare both
+  const int mode = v ? std::atoi(v) : 4;
+  const bool big = double(M) * N * K >= 4294967296.0;
+  if ((mode == 3 || (mode == 4 && big)) && ldi % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
+    auto it = md.split.find(W);
+    if (it != md.split.end())
+      return pet_gemm_nt_split(M, N, K, in, ldi, it->second, out, ldo, nullptr, nullptr, beta != 0.f ? out : nullptr,
+                               ldo, beta, nullptr, 0, 0, st);
+  }
+  return gemm_nt(out, ldo, in, ldi, W, M, N, K, beta, st);
+}
+
 // out[M, Nout] = in W^T + b (b may be null)
 void linear(pet_model& md, float* out, const float* in, int M, int K, const std::string& key, hipStream_t st,
             bool bias = true) {
@@ -522,7 +550,7 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
   else
     hipLaunchKernelGGL(fill_rows_kernel, grid_for(int64_t(M) * W.rows), dim3(256), 0, st, out, b, int64_t(M), W.rows);
   launched();
-  ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
+  ok(gemm_w(md, out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
 }
 // out += in W^T (the caller has put residual + bias in out)
 void linear_acc(pet_model& md, float* out, const float* in, int M, int K, const std::string& key, hipStream_t st) {
@@ -534,13 +562,13 @@ void linear_acc(pet_model& md, float* out, const float* in, int M, int K, const 
                          st));
     return;
   }
-  ok(gemm_nt(out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
+  ok(gemm_w(md, out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
 }
 // in_adj[M, K] = out_adj W + beta in_adj
 void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const std::string& key, float beta,
                 hipStream_t st) {
   const Mat& WT = md.w(key + ".weight^T");  // [K, Nout]: out_adj W = out_adj (W^T)^T
-  if (M) ok(gemm_nt(in_adj, WT.rows, out_adj, WT.cols, WT.p, M, WT.rows, WT.cols, beta, st));
+  if (M) ok(gemm_w(md, in_adj, WT.rows, out_adj, WT.cols, WT.p, M, WT.rows, WT.cols, beta, st));
 }
 // z[M, Nout] = in W^T, no bias: the pre-activation an activation pass reads with its bias
 void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const std::string& key, hipStream_t st) {
@@ -552,7 +580,7 @@ void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const st
                          st));
     return;
   }
-  ok(gemm_nt(z, W.rows, in, K, W.p, M, W.rows, K, 0.0f, st));
+  ok(gemm_w(md, z, W.rows, in, K, W.p, M, W.rows, K, 0.0f, st));
 }
 // out = silu(z + b) of linear_pre's z under `key`
 void silu(pet_model& md, float* out, const float* z, int64_t R, const std::string& key, hipStream_t st) {
@@ -888,7 +916,7 @@ struct Pass {
     const std::string c0 = g(L) + ".compress.0";
     auto scope = md.ws.mark();
     float* cact = md.f(int64_t(E) * D);
-    if (L > 0) ok(gemm_nt(cact, D, input_edge, D, md.p(c0 + "@in"), E, D, D, 0.0f, st));
+    if (L > 0) ok(gemm_w(md, cact, D, input_edge, D, md.p(c0 + "@in"), E, D, D, 0.0f, st));
     if (E) {
       hipLaunchKernelGGL(compress_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, cpre, cact, L > 0 ? 1 : 0,
                          md.p(c0 + "@b"), md.p(c0 + "@tab"), e.neigh_species, md.p(c0 + "@x4"), e.vec, e.dist,
@@ -910,7 +938,7 @@ struct Pass {
                          md.p(c0 + "@x4"), x4_adj, E, D);
       launched();
     }
-    if (L > 0 && E) ok(gemm_nt(ie_adj, D, ga, D, md.p(c0 + "@in^T"), E, D, D, 1.0f, st));
+    if (L > 0 && E) ok(gemm_w(md, ie_adj, D, ga, D, md.p(c0 + "@in^T"), E, D, D, 1.0f, st));
     md.ws.release(scope);
   }
 
@@ -1278,6 +1306,22 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
                                 ld.shapes[i].second};
     }
     if (hipMemcpy(md->weights, host.data(), total, hipMemcpyHostToDevice) != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
+    // split-row copies (6 bytes an element) of the matrices whose K is a
+    // multiple of 32, for the split-product dense layers
+    size_t stotal = 0;
+    std::vector<std::pair<const Mat*, size_t>> sat;
+    for (auto& [n, mt] : md->m)
+      if (mt.cols > 0 && mt.cols % 32 == 0)
+        sat.push_back({&mt, stotal}), stotal += (size_t(6) * mt.rows * mt.cols + 255) & ~size_t(255);
+    if (stotal) {
+      if (hipMalloc(&md->wsplit, stotal) != hipSuccess) throw Error{PET_MODEL_EMEMORY};
+      for (auto& [mt, o] : sat) {
+        void* dst = static_cast<char*>(md->wsplit) + o;
+        ok(pet_linear_split_weights(mt->p, mt->rows, mt->cols, mt->cols, dst, nullptr));
+        md->split[mt->p] = dst;
+      }
+      if (hipDeviceSynchronize() != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
+    }
     std::vector<double> comp(ns, 0.0);
     if (composition) comp.assign(composition, composition + ns);
     if (hipMalloc(&md->comp, sizeof(double) * ns) != hipSuccess) throw Error{PET_MODEL_EMEMORY};

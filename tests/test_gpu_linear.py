@@ -2,7 +2,10 @@
 matrix products of the same fp32 inputs, for every epilogue: a row scale (the
 RMSNorm fold), a bias, a residual accumulated in place, the kept
 pre-activation, SiLU and SwiGLU. Tolerance 1e-5 of the largest output
-magnitude (fp32 sums over K <= 1024); runs repeat bit for bit."""
+magnitude (fp32 sums over K <= 1024); runs repeat bit for bit. The same for
+its split-product form (pet_linear_fused_split over weights split by
+pet_linear_split_weights), whose split is checked exactly: three bf16 parts
+that sum to each weight."""
 from __future__ import annotations
 
 import numpy as np
@@ -14,10 +17,28 @@ from pet_kokkos_amd import _lib
 pytestmark = pytest.mark.gpu
 
 
-def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
+def split_weights(W):
+    N, K = W.shape
+    out = torch.empty(N * K * 3, dtype=torch.int16, device=W.device)
+    _lib.check(_lib.load().pet_linear_split_weights(W.data_ptr(), N, K, W.stride(0), out.data_ptr(),
+                                                    torch.cuda.current_stream().cuda_stream),
+               "pet_linear_split_weights")
+    return out
+
+
+def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, split=False):
     M, K = A.shape
     N = W.shape[0]
     p = lambda t: None if t is None else t.data_ptr()
+    if split:
+        Ws = split_weights(W)
+        _lib.check(_lib.load().pet_linear_fused_split(M, N, K, p(A), A.stride(0), Ws.data_ptr(), p(C), C.stride(0),
+                                                      p(row_scale), p(bias), p(cin),
+                                                      0 if cin is None else cin.stride(0), beta, p(pre),
+                                                      0 if pre is None else pre.stride(0), act,
+                                                      torch.cuda.current_stream().cuda_stream),
+                   "pet_linear_fused_split")
+        return
     _lib.check(_lib.load().pet_linear_fused(M, N, K, p(A), A.stride(0), p(W), W.stride(0), p(C), C.stride(0),
                                             p(row_scale), p(bias), p(cin), 0 if cin is None else cin.stride(0),
                                             beta, p(pre), 0 if pre is None else pre.stride(0), act,
@@ -28,23 +49,27 @@ SHAPES = [(1, 16, 16), (37, 40, 32), (300, 128, 128), (2049, 96, 256), (5000, 38
           (129, 64, 1024)]
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
 @pytest.mark.parametrize("M,N,K", SHAPES)
-def test_plain_and_bias(M, N, K, device):
+def test_plain_and_bias(M, N, K, split, device):
+    if split and K % 32:
+        pytest.skip("the split form needs K a multiple of 32")
     g = torch.Generator(device=device).manual_seed(M + N + K)
     A = torch.randn(M, K, device=device, generator=g)
     W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
     b = torch.randn(N, device=device, generator=g)
     C = torch.empty(M, N, device=device)
-    linear_fused(A, W, C, bias=b)
+    linear_fused(A, W, C, bias=b, split=split)
     ref = (A.double() @ W.double().T + b.double()).cpu().numpy()
     got = C.cpu().numpy()
     assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
     C2 = torch.empty_like(C)
-    linear_fused(A, W, C2, bias=b)
+    linear_fused(A, W, C2, bias=b, split=split)
     assert torch.equal(C, C2)
 
 
-def test_epilogues(device):
+@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
+def test_epilogues(split, device):
     M, N, K = 777, 256, 128
     g = torch.Generator(device=device).manual_seed(5)
     A = torch.randn(M, K, device=device, generator=g)
@@ -55,19 +80,19 @@ def test_epilogues(device):
     base = (A.double() @ W.double().T) * rs.double()[:, None] + b.double()
     # residual in place: C = base + 1.0 * C
     C = R.clone()
-    linear_fused(A, W, C, row_scale=rs, bias=b, cin=C, beta=1.0)
+    linear_fused(A, W, C, row_scale=rs, bias=b, cin=C, beta=1.0, split=split)
     ref = base + R.double()
     assert (C.double() - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
     # SiLU with the pre-activation kept
     C = torch.empty(M, N, device=device)
     pre = torch.empty(M, N, device=device)
-    linear_fused(A, W, C, row_scale=rs, bias=b, pre=pre, act=1)
+    linear_fused(A, W, C, row_scale=rs, bias=b, pre=pre, act=1, split=split)
     assert (pre.double() - base).abs().max().item() <= 1e-5 * base.abs().max().item()
     ref = base * torch.sigmoid(base)
     assert (C.double() - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
     # SwiGLU: columns (2c, 2c + 1) = (value, gate) -> column c
     C = torch.empty(M, N // 2, device=device)
-    linear_fused(A, W, C, bias=b, pre=pre, act=2)
+    linear_fused(A, W, C, bias=b, pre=pre, act=2, split=split)
     z = A.double() @ W.double().T + b.double()
     ref = z[:, 0::2] * torch.sigmoid(z[:, 1::2])
     assert (C.double() - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
@@ -80,3 +105,24 @@ def test_rejects(device):
     C = torch.zeros(8, 8, device=device)
     with pytest.raises(_lib.PetAttnError):
         linear_fused(A, W, C)  # K not a multiple of 16
+
+
+def test_split_weights_exact(device):
+    """Each weight's three parts are bf16 values (an fp32 with a zero low half)
+    that sum to it exactly, part 0 carrying its leading bits, laid out per row
+    and 8-element k group as parts 0, 1, 2."""
+    N, K = 48, 64
+    g = torch.Generator(device=device).manual_seed(3)
+    W = torch.randn(N, K, device=device, generator=g) * torch.logspace(-20, 20, K, device=device)
+    Ws = split_weights(W).cpu().numpy().view(np.uint16).reshape(N, K // 8, 3, 8)
+    parts = (Ws.astype(np.uint32) << 16).view(np.float32)  # [N, K/8, 3, 8]
+    w = W.cpu().numpy().reshape(N, K // 8, 8)
+    assert np.array_equal(parts[:, :, 0, :] + parts[:, :, 1, :] + parts[:, :, 2, :], w)
+    assert np.array_equal(parts[:, :, 0, :], (w.view(np.uint32) & 0xFFFF0000).view(np.float32))
+    assert np.all(np.abs(parts[:, :, 1, :]) <= np.abs(w) * 2.0 ** -7)
+
+
+def test_split_rejects(device):
+    W = torch.zeros(8, 48, device=device)
+    with pytest.raises(_lib.PetAttnError):
+        split_weights(W)  # K not a multiple of 32

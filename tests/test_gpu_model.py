@@ -97,20 +97,27 @@ def test_odd_widths_match_oracle(name, device):
     compare(got, oracle_of(h, w, comp, x))
 
 
+@pytest.mark.parametrize("mode", ["1", "3"], ids=["fp32", "split"])
 @pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
-def test_model_on_the_fused_dense_layer(name, device, monkeypatch):
-    # PET_MODEL_GEMM=1: every dense layer with K a multiple of 16 on the
-    # library's fused GEMM (pet_linear_fused's kernel) instead of rocBLAS
-    monkeypatch.setenv("PET_MODEL_GEMM", "1")
+def test_model_on_the_fused_dense_layer(name, mode, device, monkeypatch):
+    # PET_MODEL_GEMM=1: every forward dense layer with K a multiple of 16 on the
+    # library's fused GEMM (pet_linear_fused's kernel) instead of rocBLAS;
+    # PET_MODEL_GEMM=3: every dense layer with K a multiple of 32 on its
+    # split-product form (pet_linear_fused_split's kernel), backward included
+    monkeypatch.setenv("PET_MODEL_GEMM", mode)
     h = weights.MODELS[name]
     w = weights.random_weights(h, 15)
     comp = weights.random_composition(h)
-    print(f"[model] {name} batch-3 on the fused dense layer", flush=True)
+    print(f"[model] {name} batch-3 on the fused dense layer, PET_MODEL_GEMM={mode}", flush=True)
     m = PetModel(h, w, comp)
     x = structures_input(h, CASES["batch-3"](), device)
     got = m.compute(x, forces=True, edge_grad=True)
     torch.cuda.synchronize()
     compare(got, oracle_of(h, w, comp, x))
+    again = m.compute(x, forces=True, edge_grad=True)
+    torch.cuda.synchronize()
+    for k in got:
+        assert torch.equal(got[k], again[k]), k
 
 
 @pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
