@@ -54,8 +54,25 @@ struct Epi {
   int act = 0;                       // 0 none, 1 SiLU, 2 SwiGLU (C has N/2 columns)
 };
 
-// The epilogue, shared by the kernels: lane (c, g) of tile (a, b) holds rows
-// 4g + r, column c of the wave's (BM/2) x (BN/2) share.
+// The epilogue of one result element v at (i, j), shared by the kernels. Every
+// lane of the wave calls it together (SwiGLU pairs neighbouring lanes):
+// (i, j) may lie outside the result, which is then left alone.
+__device__ __forceinline__ void epi_elem(float v, int i, int j, int c, int M, int N, float* C, int64_t ldc,
+                                         const Epi& epi) {
+  if (epi.row_scale && i < M) v *= epi.row_scale[i];
+  if (epi.bias && j < N) v += epi.bias[j];
+  if (epi.cin && i < M && j < N) v += epi.beta * epi.cin[int64_t(i) * epi.ldcin + j];
+  if (epi.pre && i < M && j < N) epi.pre[int64_t(i) * epi.ldpre + j] = v;
+  if (epi.act == 2) {
+    // SwiGLU: columns 2c' (value) and 2c'+1 (gate) sit in lanes c and c + 1
+    const float gate = __shfl_down(v, 1, 16);
+    if ((c & 1) == 0 && i < M && j < N) C[int64_t(i) * ldc + j / 2] = v * sig_fast(gate);
+  } else if (i < M && j < N) {
+    C[int64_t(i) * ldc + j] = epi.act == 1 ? v * sig_fast(v) : v;
+  }
+}
+// The tile kernels' epilogue: lane (c, g) of tile (a, b) holds rows 4g + r,
+// column c of the wave's (BM/2) x (BN/2) share.
 template <int BM, int BN>
 __device__ __forceinline__ void epilogue(const f4 (&acc)[BM / 32][BN / 32], int m0, int n0, int wm, int wn, int c,
                                          int g, int M, int N, float* C, int64_t ldc, const Epi& epi) {
@@ -63,25 +80,10 @@ __device__ __forceinline__ void epilogue(const f4 (&acc)[BM / 32][BN / 32], int 
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      const int j = n0 + wn * WN + 16 * b + c;
+    for (int b = 0; b < TN; ++b)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = m0 + wm * WM + 16 * a + 4 * g + r;
-        float v = acc[a][b][r];
-        if (epi.row_scale && i < M) v *= epi.row_scale[i];
-        if (epi.bias && j < N) v += epi.bias[j];
-        if (epi.cin && i < M && j < N) v += epi.beta * epi.cin[int64_t(i) * epi.ldcin + j];
-        if (epi.pre && i < M && j < N) epi.pre[int64_t(i) * epi.ldpre + j] = v;
-        if (epi.act == 2) {
-          // SwiGLU: columns 2c' (value) and 2c'+1 (gate) sit in lanes c and c + 1
-          const float gate = __shfl_down(v, 1, 16);
-          if ((c & 1) == 0 && i < M && j < N) C[int64_t(i) * ldc + j / 2] = v * sig_fast(gate);
-        } else if (i < M && j < N) {
-          C[int64_t(i) * ldc + j] = epi.act == 1 ? v * sig_fast(v) : v;
-        }
-      }
-    }
+      for (int r = 0; r < 4; ++r)
+        epi_elem(acc[a][b][r], m0 + wm * WM + 16 * a + 4 * g + r, n0 + wn * WN + 16 * b + c, c, M, N, C, ldc, epi);
 }
 
 template <int BM, int BN, int BK = 32>
@@ -292,6 +294,7 @@ int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const fl
                 int64_t ldpre, int act, hipStream_t st) {
   if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
+  if (K == 0) return PET_ATTN_EINVAL;
   if (K % 16 || lda % 4 || ldb % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(B) & 15))
     return PET_ATTN_EALIGN;
   if (act == 2 && N % 2) return PET_ATTN_EINVAL;
@@ -328,6 +331,7 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
                       float* pre, int64_t ldpre, int act, hipStream_t st) {
   if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
+  if (K == 0) return PET_ATTN_EINVAL;
   if (K % 32 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15))
     return PET_ATTN_EALIGN;
   if (act == 2 && N % 2) return PET_ATTN_EINVAL;

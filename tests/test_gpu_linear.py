@@ -105,6 +105,8 @@ def test_rejects(device):
     C = torch.zeros(8, 8, device=device)
     with pytest.raises(_lib.PetAttnError):
         linear_fused(A, W, C)  # K not a multiple of 16
+    with pytest.raises(_lib.PetAttnError):
+        linear_fused(torch.zeros(8, 0, device=device), torch.zeros(8, 0, device=device), C)  # K = 0
 
 
 def test_split_weights_exact(device):
