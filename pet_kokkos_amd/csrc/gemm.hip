@@ -72,11 +72,11 @@ __device__ __forceinline__ void epi_elem(float v, int i, int j, int c, int M, in
   }
 }
 // The tile kernels' epilogue: lane (c, g) of tile (a, b) holds rows 4g + r,
-// column c of the wave's (BM/2) x (BN/2) share.
-template <int BM, int BN>
-__device__ __forceinline__ void epilogue(const f4 (&acc)[BM / 32][BN / 32], int m0, int n0, int wm, int wn, int c,
+// column c of the wave's WM x WN share.
+template <int WM, int WN>
+__device__ __forceinline__ void epilogue(const f4 (&acc)[WM / 16][WN / 16], int m0, int n0, int wm, int wn, int c,
                                          int g, int M, int N, float* C, int64_t ldc, const Epi& epi) {
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+  constexpr int TM = WM / 16, TN = WN / 16;
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
     }
   }
 
-  epilogue<BM, BN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
 }
 
 // The same product with the fp32 matrix cores' work moved to the bf16 ones:
@@ -173,24 +173,26 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
 // group, its three bf16 parts, 48 bytes), A is split as each k step of 32 is
 // staged, and a 16 x 16 x 32 step is the six part products of split_bf16.h
 // (6 x ~22 cycles against 8 x 32 on the fp32 instruction, at fp32's error).
-// 64 x 64 or 128 x 64 tiles of 4 waves (2 x 2), k steps of 32 through LDS
+// 64 x 64 or 128 x 64 tiles of 4 waves (2 x 2), 128 x 128 of 8 (2 x 4), k steps of 32 through LDS
 // (the next step's slices loaded into registers under the current step's
 // products): a row's step is 4 groups x 3 parts x 16 bytes plus a 16-byte pad
-// (13 u4, so a 16-lane column of 128-bit reads is conflict-free), 26 / 39 KB
+// (13 u4, so a 16-lane column of 128-bit reads is conflict-free), 26 / 52 KB
 // a workgroup. K a multiple of 32. Measured against torch's GEMM at the
 // model's shapes: even at K = 128 (27318 x 128 x 128: 16.1 against 20.0 us),
 // ahead at 26670 x 1024 x 128 (75 against 86 us) and 131072 x 1536 x 512
-// (1402 against 1458 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
-template <int BM, int BN>
-__global__ void __launch_bounds__(256) gemm_nt_split_kernel(int M, int N, int K, const float* __restrict__ A,
-                                                            int64_t lda, const u4* __restrict__ Bs, float* C,
-                                                            int64_t ldc, Epi epi) {
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16, RP = 13;
-  constexpr int AQ = BM * 8, AL = (AQ + 255) / 256;   // float4 of a step's A slice, a thread's share
-  constexpr int BQ = BN * 12, BL = (BQ + 255) / 256;  // u4 of a step's B slice
+// (1200 against 1555 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
+// WGM x WGN waves down and across a tile (64 WGM WGN threads).
+template <int BM, int BN, int WGM = 2, int WGN = 2>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, int N, int K,
+                                                                       const float* __restrict__ A, int64_t lda,
+                                                                       const u4* __restrict__ Bs, float* C,
+                                                                       int64_t ldc, Epi epi) {
+  constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 13;
+  constexpr int AQ = BM * 8, AL = (AQ + T - 1) / T;   // float4 of a step's A slice, a thread's share
+  constexpr int BQ = BN * 12, BL = (BQ + T - 1) / T;  // u4 of a step's B slice
   __shared__ u4 As[BM * RP], Bt[BN * RP];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WGN, wn = w % WGN;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, KG = K / 8;
 
   f4 acc[TM][TN];
@@ -206,20 +208,20 @@ __global__ void __launch_bounds__(256) gemm_nt_split_kernel(int M, int N, int K,
   auto load = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < AL; ++u) {
-      const int q = tid + 256 * u, i = m0 + q / 8;
+      const int q = tid + T * u, i = m0 + q / 8;
       ra[u] = q < AQ && i < M ? *reinterpret_cast<const float4*>(A + int64_t(i) * lda + k0 + 4 * (q % 8))
                               : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int u = 0; u < BL; ++u) {
-      const int q = tid + 256 * u, j = n0 + q / 12;
+      const int q = tid + T * u, j = n0 + q / 12;
       rb[u] = q < BQ && j < N ? Bs[(int64_t(j) * KG + k0 / 8) * 3 + q % 12] : u4{0u, 0u, 0u, 0u};
     }
   };
   auto store = [&]() {
 #pragma unroll
     for (int u = 0; u < AL; ++u) {
-      const int q = tid + 256 * u;
+      const int q = tid + T * u;
       if (q < AQ) {
         // the float4 is half of k group (q % 8) / 2: its parts go to that half of each part's 16 bytes
         float h[3][4];
@@ -235,7 +237,7 @@ __global__ void __launch_bounds__(256) gemm_nt_split_kernel(int M, int N, int K,
     }
 #pragma unroll
     for (int u = 0; u < BL; ++u) {
-      const int q = tid + 256 * u;
+      const int q = tid + T * u;
       if (q < BQ) Bt[(q / 12) * RP + q % 12] = rb[u];
     }
   };
@@ -265,7 +267,7 @@ __global__ void __launch_bounds__(256) gemm_nt_split_kernel(int M, int N, int K,
       __syncthreads();
     }
   }
-  epilogue<BM, BN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
 }
 
 // W [N, K] (ld ldw) as split rows: out[(n K/8 + j) 3 + p] = part p of k group j.
@@ -338,18 +340,22 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
   Epi e;
   e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
   e.act = act;
-  auto go = [&](auto kern, int bm, int bn) {
-    hipLaunchKernelGGL(kern, dim3(unsigned((N + bn - 1) / bn), unsigned((M + bm - 1) / bm)), dim3(256), 0, st, M, N,
-                       K, A, lda, static_cast<const u4*>(Bs), C, ldc, e);
+  auto go = [&](auto kern, int bm, int bn, int threads) {
+    hipLaunchKernelGGL(kern, dim3(unsigned((N + bn - 1) / bn), unsigned((M + bm - 1) / bm)), dim3(threads), 0, st, M,
+                       N, K, A, lda, static_cast<const u4*>(Bs), C, ldc, e);
   };
-  // measured on MI355X: 128 x 64 tiles where there are many (131072 x 1536 x
-  // 512: 1402 us against 1535 for 64 x 64), 64 x 64 otherwise (27318 x 128 x
-  // 128: 16.1 against 18.4 us); one LDS buffer beat two in every shape
+  // measured on MI355X: 128 x 128 tiles of 8 waves where there are many
+  // (131072 x 1536 x 512: 1200-1213 us against 1394-1418 for 128 x 64 and
+  // 1535 for 64 x 64; 256 x 128 and 128 x 256 tiles of 16 waves were no
+  // faster), 64 x 64 otherwise (27318 x 128 x 128: 16.1 against 18.4 us); one
+  // LDS buffer beat two in every shape
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
-  if (t128 >= 2048)
-    go(gemm_nt_split_kernel<128, 64>, 128, 64);
+  if (N >= 128 && t128 >= 2048)
+    go(gemm_nt_split_kernel<128, 128, 2, 4>, 128, 128, 512);
+  else if (t128 >= 2048)
+    go(gemm_nt_split_kernel<128, 64>, 128, 64, 256);
   else
-    go(gemm_nt_split_kernel<64, 64>, 64, 64);
+    go(gemm_nt_split_kernel<64, 64>, 64, 64, 256);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 

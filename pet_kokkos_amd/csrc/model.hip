@@ -517,8 +517,8 @@ bool own_gemm(int M, int K) {
 // products (M N K >= 2^32), every one with PET_MODEL_GEMM=3, none with
 // PET_MODEL_GEMM=0. Measured on MI355X (energy+forces, ms, same process):
 // C2 2.98 / 2.15 (residual) with rocBLAS, the same by default (no C2 product is
-// that large), 3.59 / 2.40 with all split; C5 275 with rocBLAS, 267 by
-// default, 267 with all split.
+// that large), 3.59 / 2.40 with all split; C5 276-279 with rocBLAS, 244 by
+// default and with all split.
 int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int N,
            int K, float beta, hipStream_t st) {
   const char* v = std::getenv("PET_MODEL_GEMM");  // read per call: a process may compare both

@@ -45,8 +45,9 @@ def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=Non
                                             torch.cuda.current_stream().cuda_stream), "pet_linear_fused")
 
 
+# the last two are large enough for the split form's 128 x 128 and 128 x 64 tiles
 SHAPES = [(1, 16, 16), (37, 40, 32), (300, 128, 128), (2049, 96, 256), (5000, 384, 128), (1000, 1024, 512),
-          (129, 64, 1024)]
+          (129, 64, 1024), (16385, 1024, 64), (131071, 96, 64)]
 
 
 @pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
