@@ -173,15 +173,15 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
 // group, its three bf16 parts, 48 bytes), A is split as each k step of 32 is
 // staged, and a 16 x 16 x 32 step is the six part products of split_bf16.h
 // (6 x ~22 cycles against 8 x 32 on the fp32 instruction, at fp32's error).
-// 64 x 64 or 128 x 64 tiles of 4 waves (2 x 2), 128 x 128 of 8 (2 x 4), k steps of 32 through LDS
-// (the next step's slices loaded into registers under the current step's
-// products): a row's step is 4 groups x 3 parts x 16 bytes plus a 16-byte pad
-// (13 u4, so a 16-lane column of 128-bit reads is conflict-free), 26 / 52 KB
-// a workgroup. K a multiple of 32. Measured against torch's GEMM at the
-// model's shapes: even at K = 128 (27318 x 128 x 128: 16.1 against 20.0 us),
-// ahead at 26670 x 1024 x 128 (75 against 86 us) and 131072 x 1536 x 512
-// (1200 against 1555 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
-// WGM x WGN waves down and across a tile (64 WGM WGN threads).
+// Tiles of WGM x WGN waves (64 WGM WGN threads): 64 x 64 or 128 x 64 of 2 x 2,
+// 128 x 128 of 2 x 4. K steps of 32 go through one LDS buffer, the next
+// step's slices loaded into registers under the current step's products. A
+// row's step is 4 groups x 3 parts x 16 bytes plus a 16-byte pad (13 u4, so a
+// 16-lane column of 128-bit reads is conflict-free): 26 / 39 / 52 KB a
+// workgroup. K a multiple of 32. Measured against torch's GEMM at the model's
+// shapes: even at K = 128 (27318 x 128 x 128: 16.1 against 20.0 us), ahead at
+// 26670 x 1024 x 128 (75 against 86 us) and 131072 x 1536 x 512 (1200 against
+// 1555 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
 template <int BM, int BN, int WGM = 2, int WGN = 2>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, int N, int K,
                                                                        const float* __restrict__ A, int64_t lda,
