@@ -15,7 +15,11 @@
 // (step 1e-3 A, energy-only runs), the force's x], and DIR/graph.ok when
 // compute_step on a Calculator with graph = true (a stream of its own) gives
 // the bits of an eager Calculator's on the same list, step after step, with
-// and without forces and edge gradients.
+// and without forces and edge gradients, and DIR/linear.ok when
+// pet::linear_fused (include/pet/linear.hpp) on plain and on split weights
+// agrees with a host double product within 1e-5 of its largest magnitude.
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -23,6 +27,7 @@
 #include <string>
 #include <vector>
 
+#include "pet/linear.hpp"
 #include "pet/model.hpp"
 
 static void fail(const std::string& what) {
@@ -131,6 +136,41 @@ int main(int argc, char** argv) {
       if (same) std::fclose(std::fopen((dir + "/graph.ok").c_str(), "wb"));
     }
     (void) hipStreamDestroy(st);
+
+    {  // the dense layer: out = in W^T + b + out
+      const int M = 300, Nw = 64, K = 96;
+      std::vector<float> A(size_t(M) * K), W(size_t(Nw) * K), b(Nw), C0(size_t(M) * Nw);
+      unsigned x = 12345u;
+      auto rnd = [&x] { return (x = x * 1664525u + 1013904223u, float(int(x >> 9) - (1 << 22)) / float(1 << 22)); };
+      for (float& v : A) v = rnd();
+      for (float& v : W) v = rnd();
+      for (float& v : b) v = rnd();
+      for (float& v : C0) v = rnd();
+      float *dA, *dW, *db, *dC;
+      if (hipMalloc(&dA, A.size() * 4) || hipMalloc(&dW, W.size() * 4) || hipMalloc(&db, b.size() * 4) ||
+          hipMalloc(&dC, C0.size() * 4))
+        fail("hipMalloc");
+      (void) hipMemcpy(dA, A.data(), A.size() * 4, hipMemcpyHostToDevice);
+      (void) hipMemcpy(dW, W.data(), W.size() * 4, hipMemcpyHostToDevice);
+      (void) hipMemcpy(db, b.data(), b.size() * 4, hipMemcpyHostToDevice);
+      double worst = 0, big = 0;
+      const pet::SplitWeights ws(dW, Nw, K, K);
+      for (const pet::DenseWeight& dw : {pet::plain_weight(dW, Nw, K, K), ws.weight()}) {
+        (void) hipMemcpy(dC, C0.data(), C0.size() * 4, hipMemcpyHostToDevice);
+        pet::linear_fused(dC, Nw, dA, K, M, dw, db, 1.0f);
+        std::vector<float> C(C0.size());
+        (void) hipMemcpy(C.data(), dC, C.size() * 4, hipMemcpyDeviceToHost);
+        for (int i = 0; i < M; ++i)
+          for (int j = 0; j < Nw; ++j) {
+            double ref = double(b[j]) + double(C0[size_t(i) * Nw + j]);
+            for (int k = 0; k < K; ++k) ref += double(A[size_t(i) * K + k]) * double(W[size_t(j) * K + k]);
+            worst = std::max(worst, std::fabs(ref - double(C[size_t(i) * Nw + j])));
+            big = std::max(big, std::fabs(ref));
+          }
+      }
+      (void) hipFree(dA), (void) hipFree(dW), (void) hipFree(db), (void) hipFree(dC);
+      if (worst <= 1e-5 * big) std::fclose(std::fopen((dir + "/linear.ok").c_str(), "wb"));
+    }
   } catch (const std::exception& e) {
     fail(e.what());
   }

@@ -13,36 +13,17 @@ import pytest
 import torch
 
 from pet_kokkos_amd import _lib
+from pet_kokkos_amd import linear as L
 
 pytestmark = pytest.mark.gpu
 
 
 def split_weights(W):
-    N, K = W.shape
-    out = torch.empty(N * K * 3, dtype=torch.int16, device=W.device)
-    _lib.check(_lib.load().pet_linear_split_weights(W.data_ptr(), N, K, W.stride(0), out.data_ptr(),
-                                                    torch.cuda.current_stream().cuda_stream),
-               "pet_linear_split_weights")
-    return out
+    return L.SplitWeights(W)
 
 
 def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, split=False):
-    M, K = A.shape
-    N = W.shape[0]
-    p = lambda t: None if t is None else t.data_ptr()
-    if split:
-        Ws = split_weights(W)
-        _lib.check(_lib.load().pet_linear_fused_split(M, N, K, p(A), A.stride(0), Ws.data_ptr(), p(C), C.stride(0),
-                                                      p(row_scale), p(bias), p(cin),
-                                                      0 if cin is None else cin.stride(0), beta, p(pre),
-                                                      0 if pre is None else pre.stride(0), act,
-                                                      torch.cuda.current_stream().cuda_stream),
-                   "pet_linear_fused_split")
-        return
-    _lib.check(_lib.load().pet_linear_fused(M, N, K, p(A), A.stride(0), p(W), W.stride(0), p(C), C.stride(0),
-                                            p(row_scale), p(bias), p(cin), 0 if cin is None else cin.stride(0),
-                                            beta, p(pre), 0 if pre is None else pre.stride(0), act,
-                                            torch.cuda.current_stream().cuda_stream), "pet_linear_fused")
+    L.fused(A, split_weights(W) if split else W, C, row_scale, bias, cin, beta, pre, act)
 
 
 # the last two are large enough for the split form's 128 x 128 and 128 x 64 tiles
@@ -117,7 +98,7 @@ def test_split_weights_exact(device):
     N, K = 48, 64
     g = torch.Generator(device=device).manual_seed(3)
     W = torch.randn(N, K, device=device, generator=g) * torch.logspace(-20, 20, K, device=device)
-    Ws = split_weights(W).cpu().numpy().view(np.uint16).reshape(N, K // 8, 3, 8)
+    Ws = split_weights(W).data.cpu().numpy().view(np.uint16).reshape(N, K // 8, 3, 8)
     parts = (Ws.astype(np.uint32) << 16).view(np.float32)  # [N, K/8, 3, 8]
     w = W.cpu().numpy().reshape(N, K // 8, 8)
     assert np.array_equal(parts[:, :, 0, :] + parts[:, :, 1, :] + parts[:, :, 2, :], w)
@@ -129,3 +110,28 @@ def test_split_rejects(device):
     W = torch.zeros(8, 48, device=device)
     with pytest.raises(_lib.PetAttnError):
         split_weights(W)  # K not a multiple of 32
+
+
+def test_reference_named_wrappers(device):
+    """linear_fused / silu_in_fused / swiglu_in_fused, as the reference names
+    them, on both weight forms."""
+    M, N, K = 300, 64, 96
+    g = torch.Generator(device=device).manual_seed(9)
+    A = torch.randn(M, K, device=device, generator=g)
+    W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
+    b = torch.randn(N, device=device, generator=g)
+    z = A.double() @ W.double().T + b.double()
+    tol = lambda ref: 1e-5 * ref.abs().max().item()
+    for w in (W, L.SplitWeights(W)):
+        out = torch.randn(M, N, device=device, generator=g)
+        base = out.double().clone()
+        L.linear_fused(out, A, w, b, beta=1.0)
+        assert (out.double() - (z + base)).abs().max().item() <= tol(z + base)
+        out, pre = torch.empty(M, N, device=device), torch.empty(M, N, device=device)
+        L.silu_in_fused(out, pre, A, w, b)
+        assert (pre.double() - z).abs().max().item() <= tol(z)
+        assert (out.double() - z * torch.sigmoid(z)).abs().max().item() <= tol(z * torch.sigmoid(z))
+        h = torch.empty(M, N // 2, device=device)
+        L.swiglu_in_fused(pre, h, A, w, b)
+        ref = z[:, 0::2] * torch.sigmoid(z[:, 1::2])
+        assert (h.double() - ref).abs().max().item() <= tol(ref)
