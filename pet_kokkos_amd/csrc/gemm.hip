@@ -270,6 +270,22 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
   epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
 }
 
+// W^T as split rows, W [K, N] (ld ldw): out[(n K/8 + j) 3 + p] = part p of
+// column n's k group j.
+__global__ void split_rows_t_kernel(const float* __restrict__ W, int N, int K, int64_t ldw, u4* __restrict__ out) {
+  const int KG = K / 8;
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= int64_t(N) * KG) return;
+  const int n = int(t % N), j = int(t / N);  // consecutive threads, consecutive columns of a row
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = W[int64_t(8 * j + e) * ldw + n];
+  u4 parts[3];
+  split8(x, parts);
+#pragma unroll
+  for (int p = 0; p < 3; ++p) out[(int64_t(n) * KG + j) * 3 + p] = parts[p];
+}
+
 // W [N, K] (ld ldw) as split rows: out[(n K/8 + j) 3 + p] = part p of k group j.
 __global__ void split_rows_kernel(const float* __restrict__ W, int N, int K, int64_t ldw, u4* __restrict__ out) {
   const int KG = K / 8;
@@ -356,6 +372,21 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
     go(gemm_nt_split_kernel<128, 64>, 128, 64, 256);
   else
     go(gemm_nt_split_kernel<64, 64>, 64, 64, 256);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// B [N, K] as split rows, from W = B (transposed false: W [N, K]) or W = B^T
+// (transposed true: W [K, N]); K a multiple of 32, out 16-byte aligned.
+int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st) {
+  if (N < 0 || K < 0 || K % 32 || (reinterpret_cast<uintptr_t>(out) & 15)) return PET_ATTN_EINVAL;
+  const int64_t n = int64_t(N) * (K / 8);
+  if (n == 0) return PET_ATTN_OK;
+  if (transposed)
+    hipLaunchKernelGGL(split_rows_t_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, W, N, K, ldw,
+                       static_cast<u4*>(out));
+  else
+    hipLaunchKernelGGL(split_rows_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, W, N, K, ldw,
+                       static_cast<u4*>(out));
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 

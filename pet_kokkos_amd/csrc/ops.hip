@@ -13,6 +13,12 @@
 
 #include "../../include/pet_attn.h"
 
+// gemm.hip: the split-product dense layer and its weight split
+int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
+                      const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                      float* pre, int64_t ldpre, int act, hipStream_t st);
+int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st);
+
 namespace pet_attn {
 
 // One rocBLAS handle per device, made on first use and kept for the process.
@@ -54,6 +60,30 @@ int gemm_nn(float* in_adj, int64_t ldi, const float* out_adj, int64_t ldo, const
   const rocblas_status s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, K, M, Nout, &one, W, K,
                                          out_adj, rocblas_int(ldo), &beta, in_adj, rocblas_int(ldi));
   return s == rocblas_status_success ? PET_ATTN_OK : PET_ATTN_EBLAS;
+}
+
+// The layer level's dense products on the split-product kernel (gemm.hip:
+// fp32 accuracy on the bf16 matrix cores) where it was measured faster than
+// rocBLAS -- products with M N K >= 2^32, K a multiple of 32 -- and the
+// operands allow (A rows 16-byte aligned); split holds the weight's split
+// rows (6 N K bytes) when the caller has room for them, else null.
+// out[M, N] = A B^T (+ bias) + beta out, B [N, K] given as W = B (W_is_bt
+// false, W [N, K] ld ldw) or W = B^T (true, W [K, N] ld ldw). Returns -1 when
+// the split kernel does not take the product (the caller then runs rocBLAS).
+int split_dense(float* out, int64_t ldo, const float* A, int64_t lda, const float* W, int64_t ldw, bool W_is_bt, int M,
+                int N, int K, const float* bias, float beta, void* split, hipStream_t st) {
+  if (!split || K % 32 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || double(M) * N * K < 4294967296.0)
+    return -1;
+  if (int e = pet_gemm_split_weights(W, N, K, ldw, W_is_bt, split, st)) return e;
+  return pet_gemm_nt_split(M, N, K, A, lda, split, out, ldo, nullptr, bias, beta != 0.f ? out : nullptr, ldo, beta,
+                           nullptr, 0, 0, st);
+}
+// Bytes of split rows the layer level keeps for its four weights: W_in (folded)
+// and W_in^T [3D x D each], W_out and W_out^T [D x D each].
+inline size_t align256s(size_t n) { return (n + 255) & ~size_t(255); }
+size_t layer_split_bytes(int D) {
+  const size_t d = size_t(D);
+  return 2 * align256s(6 * 3 * d * d) + 2 * align256s(6 * d * d);
 }
 
 // out[r][j] = b[j] (or 0 without a bias): the bias the GEMM then accumulates onto.
@@ -152,17 +182,21 @@ int layer_input(const pet_attn_shape* sh, float* normed, float* qkv, const float
 // the norm weight folded into its columns, qkv = tokens wf^T (no bias, no
 // normed tokens); the attention applies inv and b_in as it loads qkv.
 int layer_input_rms(const pet_attn_shape* sh, float* inv, float* wf, float* qkv, const float* tokens, int64_t ldt,
-                    const float* norm_w, const float* w_in, hipStream_t st) {
+                    const float* norm_w, const float* w_in, hipStream_t st, void* split = nullptr) {
   const int D = sh->heads * sh->head_dim, T = sh->n_rows;
   if (int e = pet_rows_rms_inv(T, D, tokens, ldt, inv, st)) return e;
   if (int e = pet_rows_fold_cols(wf, w_in, norm_w, 3 * D, D, st)) return e;
+  const int se = split_dense(qkv, 3 * D, tokens, ldt, wf, D, false, T, 3 * D, D, nullptr, 0.0f, split, st);
+  if (se >= 0) return se;
   return gemm_nt(qkv, 3 * D, tokens, ldt, wf, T, 3 * D, D, 0.0f, st);
 }
 
 // out = merged w_out^T + b_out
 int output_linear(const pet_attn_shape* sh, float* out, int64_t ldo, const float* merged, const float* w_out,
-                  const float* b_out, hipStream_t st) {
+                  const float* b_out, hipStream_t st, void* split = nullptr) {
   const int D = sh->heads * sh->head_dim, T = sh->n_rows;
+  const int se = split_dense(out, ldo, merged, D, w_out, D, false, T, D, D, b_out, 0.0f, split, st);
+  if (se >= 0) return se;
   float beta = 0.0f;
   if (b_out) {
     const int64_t total = int64_t(T) * D;
@@ -180,16 +214,23 @@ int output_linear(const pet_attn_shape* sh, float* out, int64_t ldo, const float
 int attention_bwd_xf(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int d_in, float* cf_seq_adj, int64_t ldca,
                      const float* out_adj, int64_t ldo, const float* qkv, int64_t ldq, const float* rs,
                      const float* b, const float* cf_seq, int64_t ldc, const float* w_in, const float* w_out,
-                     const int* off, const float* merged, const float* ml, float beta, char* ws, hipStream_t st) {
+                     const int* off, const float* merged, const float* ml, float beta, char* ws, hipStream_t st,
+                     void* split_out_t = nullptr, void* split_in_t = nullptr) {
   const int D = sh->heads * sh->head_dim, T = sh->n_rows;
   float* dmerged = reinterpret_cast<float*>(ws);
   float* qkv_adj = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
   float* cfh = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D) +
                                         align256(sizeof(float) * size_t(T) * 3 * D));
-  if (int e = gemm_nn(dmerged, D, out_adj, ldo, w_out, T, D, D, 0.0f, st)) return e;
+  // dmerged = out_adj W_out: B = W_out^T; in_adj = qkv_adj W_in: B = W_in^T
+  int se = split_dense(dmerged, D, out_adj, ldo, w_out, D, true, T, D, D, nullptr, 0.0f, split_out_t, st);
+  if (se > 0) return se;
+  if (se < 0)
+    if (int e = gemm_nn(dmerged, D, out_adj, ldo, w_out, T, D, D, 0.0f, st)) return e;
   if (int e = pet_attn_bwd_xf(sh, qkv, ldq, rs, b, off, dmerged, D, merged, D, ml, cf_seq, ldc, qkv_adj, 3 * D, cfh,
                               cf_seq_adj, ldca, st))
     return e;
+  se = split_dense(in_adj, ldi, qkv_adj, 3 * D, w_in, d_in, true, T, d_in, 3 * D, nullptr, beta, split_in_t, st);
+  if (se >= 0) return se;
   return gemm_nn(in_adj, ldi, qkv_adj, 3 * D, w_in, T, 3 * D, d_in, beta, st);
 }
 
@@ -327,7 +368,7 @@ size_t pet_attention_layer_workspace(const pet_attn_shape* sh) {
   if (!sh) return 0;
   const size_t D = size_t(sh->heads) * sh->head_dim, T = size_t(sh->n_rows);
   return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) + align256(sizeof(float) * T) +
-         align256(sizeof(float) * 3 * D * D) + pet_attention_bwd_workspace(sh);
+         align256(sizeof(float) * 3 * D * D) + pet_attention_bwd_workspace(sh) + layer_split_bytes(int(D));
 }
 
 int pet_attention_layer(const pet_attn_shape* sh, float* out, int64_t ldo, const float* tokens, int64_t ldt,
@@ -346,11 +387,15 @@ int pet_attention_layer(const pet_attn_shape* sh, float* out, int64_t ldo, const
                a2 = align256(sizeof(float) * size_t(T));
   float* normed = reinterpret_cast<float*>(ws);
   float* qkv = reinterpret_cast<float*>(ws + a0);
+  // the split rows of W_in (folded) and W_out, past the backward's workspace
+  char* sp = ws + a0 + a1 + a2 + align256(sizeof(float) * 3 * size_t(D) * D) + pet_attention_bwd_workspace(sh);
+  void* s_in = sp;
+  void* s_out = sp + 2 * align256(6 * 3 * size_t(D) * D);
   if (!norm_b) {  // RMSNorm: the fused projection, norm and bias applied by the attention
     float *inv = reinterpret_cast<float*>(ws + a0 + a1), *wf = reinterpret_cast<float*>(ws + a0 + a1 + a2);
-    if (int e = layer_input_rms(sh, inv, wf, qkv, tokens, ldt, norm_w, w_in, st)) return e;
+    if (int e = layer_input_rms(sh, inv, wf, qkv, tokens, ldt, norm_w, w_in, st, s_in)) return e;
     if (int e = pet_attn_fwd_xf(sh, qkv, 3 * D, inv, b_in, off, cf_seq, ldc, merged, D, ml, stream)) return e;
-    return output_linear(sh, out, ldo, merged, w_out, b_out, st);
+    return output_linear(sh, out, ldo, merged, w_out, b_out, st, s_out);
   }
   if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) return e;
   return pet_attention(sh, out, ldo, qkv, 3 * D, cf_seq, ldc, w_out, b_out, off, merged, ml, stream);
@@ -375,10 +420,15 @@ int pet_attention_layer_bwd(const pet_attn_shape* sh, float* tokens_adj, int64_t
   float* qkv = reinterpret_cast<float*>(ws + a0);
   float* inv = nullptr;
   const float* bq = nullptr;
+  // the split rows of W_in (folded), W_in^T and W_out^T, past the backward's workspace
+  char* sp = ws + a0 + a1 + a2 + a3 + pet_attention_bwd_workspace(sh);
+  void* s_in = sp;
+  void* s_in_t = sp + align256(6 * 3 * size_t(D) * D);
+  void* s_out_t = sp + 2 * align256(6 * 3 * size_t(D) * D) + align256(6 * size_t(D) * D);
   if (!norm_b) {  // RMSNorm: the fused projection (as the forward's)
     inv = reinterpret_cast<float*>(ws + a0 + a1);
     if (int e = layer_input_rms(sh, inv, reinterpret_cast<float*>(ws + a0 + a1 + a2), qkv, tokens, ldt, norm_w, w_in,
-                                st))
+                                st, s_in))
       return e;
     bq = b_in;
   } else if (int e = layer_input(sh, normed, qkv, tokens, ldt, norm_w, norm_b, w_in, b_in, st)) {
@@ -386,7 +436,7 @@ int pet_attention_layer_bwd(const pet_attn_shape* sh, float* tokens_adj, int64_t
   }
   // the normed tokens' adjoint overwrites them: the backward reads only qkv
   if (int e = attention_bwd_xf(sh, normed, D, D, cf_seq_adj, ldca, out_adj, ldo, qkv, 3 * D, inv, bq, cf_seq, ldc,
-                               w_in, w_out, off, merged, ml, 0.0f, ws + a0 + a1 + a2 + a3, st))
+                               w_in, w_out, off, merged, ml, 0.0f, ws + a0 + a1 + a2 + a3, st, s_out_t, s_in_t))
     return e;
   return pet_rows_norm_bwd_sink(T, D, tokens_adj, lda, normed, D, tokens, ldt, norm_w, norm_b != nullptr,
                                 sh->n_atoms, 0.0f, 1.0f, off, st);

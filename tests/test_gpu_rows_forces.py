@@ -159,15 +159,21 @@ def test_sum_by_structure(device):
     assert rel(acc.cpu().numpy(), 2 * ref) <= 1e-12
 
 
+@pytest.mark.parametrize("cfg", ["c1", "c3"])
 @pytest.mark.parametrize("ln", [False, True])
 @pytest.mark.parametrize("dead", [False, True])
-def test_attention_layer_fwd_bwd(device, ln, dead):
+def test_attention_layer_fwd_bwd(device, ln, dead, cfg):
     """tokens -> norm -> qkv -> attention -> out, and back to the tokens'
     adjoint (atom rows set, live edge rows accumulated, dead rows untouched),
-    against the oracle's chain of the same steps."""
-    print(f"[gpu] attention_layer ln {ln} dead {dead}", flush=True)
-    conf, tk = systems.config_tokens("c1")
+    against the oracle's chain of the same steps. At C3 every dense product of
+    the layer is large enough (M N K >= 2^32) for the split-product kernel."""
+    if cfg == "c3" and dead:
+        pytest.skip("dead rows are covered at C1")
+    print(f"[gpu] attention_layer {cfg} ln {ln} dead {dead}", flush=True)
+    conf, tk = systems.config_tokens(cfg)
     H, hd, D = conf.heads, conf.head_dim, conf.d_model
+    if cfg == "c3":
+        assert tk.n_rows * D * D >= 2 ** 32 and D % 32 == 0  # the split kernel takes every product
     inp = systems.attention_inputs(tk, D, H, seed=9)
     rng = np.random.default_rng(11)
     T = tk.n_rows + (7 if dead else 0)
