@@ -102,7 +102,8 @@ def time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device):
         L.attention_layer(ws, "b", o, x, nw, None, w_in, b_in, cf, w_out, b_out, tkd, S, H, hd, 1.0),
         L.attention_layer_bwd(ws, "b", tadj, ca, dm, x, nw, None, w_in, b_in, cf, w_out, tkd, S, H, hd, 1.0)), reps)
     out["layer_note"] = ("attention block of a PET layer: RMSNorm, QKV linear, attention, output linear, and the "
-                         "backward (rebuilt norm and QKV, attention_bwd, norm backward into the token adjoint)")
+                         "backward (rebuilt norm and QKV, attention_bwd, norm backward into the token adjoint); "
+                         "its dense products on the split-product kernel (fp32 accuracy on the bf16 matrix cores)")
     cfgs = systems.CONFIGS[args.config]
     s = systems.build_structure(cfgs.structure, 0)
     pk = systems.packed_edges(len(s.positions), systems.neighbor_list(s, cfgs.cutoff), cfgs.cutoff, cfgs.width)
