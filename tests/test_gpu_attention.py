@@ -250,18 +250,20 @@ def test_strided_views_and_stream(device):
     assert torch.all(mbig[:, D:] == 7.0) and torch.all(qabig[:, 3 * D:] == 7.0)
 
 
+@pytest.mark.parametrize("cfg", ["c1", "c3"])
 @pytest.mark.parametrize("beta", [0.0, 1.0])
-def test_op_level_attention(device, beta):
+def test_op_level_attention(device, beta, cfg):
     # attention()/attention_bwd() with the output and input linears, as the
-    # reference's feedforward (beta 0) and residual (beta 1) featurizers call them.
-    conf, tk = systems.config_tokens("c1")
+    # reference's feedforward (beta 0) and residual (beta 1) featurizers call them,
+    # on C1 and at C3's full size.
+    conf, tk = systems.config_tokens(cfg)
     H, hd, D = conf.heads, conf.head_dim, conf.d_model
     inp = systems.attention_inputs(tk, D, H, seed=5)
     rng = np.random.default_rng(9)
     in_adj0 = rng.standard_normal((tk.n_rows, D)).astype(np.float32)
     cf_adj0 = rng.standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
     temp = 1.3
-    say(f"[gpu] op level beta={beta}")
+    say(f"[gpu] op level {cfg} beta={beta}")
     ws = A.Workspace(device)
     t = A.Tokens(dev(tk.off, device, torch.int32), tk.n_atoms)
     out = torch.empty((tk.n_rows, D), device=device)
