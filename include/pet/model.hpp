@@ -29,7 +29,7 @@
 #include <vector>
 
 #include "../pet_model.h"
-#include "graph.hpp"
+#include "replay.hpp"
 
 namespace pet {
 
@@ -210,7 +210,7 @@ struct EdgeListView {
 // With graph = true (and a non-null stream: capture needs one; on the null
 // stream the steps stay eager), compute_step replays its device work -- edge
 // geometry and the whole evaluation -- as one HIP graph per output set from the
-// third step on a list (pet::GraphCache): positions are copied into the buffer
+// second step on a list (pet::StepRecorder): positions are copied into the buffer
 // the graph reads, the results are the bits of an eager step, and a small
 // structure's step loses most of its launch cost. set_neighbors drops the
 // recorded graphs.
@@ -219,7 +219,7 @@ class Calculator {
   Calculator(PetModel& model, double cutoff, std::vector<int> species_to_index, hipStream_t stream = nullptr,
              bool graph = false)
       : model_(model), cutoff_(cutoff), s2i_(std::move(species_to_index)), stream_(stream) {
-    if (graph) graphs_ = std::make_unique<GraphCache>(stream);
+    if (graph) graphs_ = std::make_unique<StepRecorder>(stream);
   }
   Calculator(const Calculator&) = delete;
   Calculator& operator=(const Calculator&) = delete;
@@ -299,12 +299,14 @@ class Calculator {
     d_.vec = buf<double>("vec", 3 * size_t(E)), d_.dist = buf<double>("dist", E), d_.pcut = buf<double>("pcut", E);
     d_.cut = buf<float>("cut", E);
     model_check(hipStreamSynchronize(stream_) == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH, "synchronize");
-    if (graphs_) graphs_->clear();
+    if (graphs_) graphs_->forget();
     have_list_ = true;
   }
 
-  // Whether the step graphs fell back to eager work for good (a failed capture).
-  bool graph_broken() const { return graphs_ && graphs_->broken(); }
+  // Whether a step's capture failed (that output set then runs eagerly).
+  bool graph_broken() const { return graphs_ && graphs_->counters().refusals > 0; }
+  // The recorder's counters (all zero without graph = true).
+  StepRecorder::Counters graph_counters() const { return graphs_ ? graphs_->counters() : StepRecorder::Counters{}; }
 
   // One step on the list set_neighbors holds, with the atoms' positions in its
   // order (Calculator::compute_step, include/pet/calculator.hpp:228-230).
@@ -332,10 +334,9 @@ class Calculator {
     };
     if (graphs_) {
       // every buffer the recorded work reads or writes, by address
-      const GraphCache::Key key{std::uintptr_t(forces), std::uintptr_t(pos), std::uintptr_t(dcell),
-                                std::uintptr_t(o.energy), std::uintptr_t(o.per_atom), std::uintptr_t(o.forces),
-                                std::uintptr_t(o.virial), std::uintptr_t(o.edge_grad), std::uintptr_t(d_.vec)};
-      graphs_->run(key, work);
+      Signature sig{std::uint64_t(forces)};
+      sig.add(pos).add(dcell).add(o.energy).add(o.per_atom).add(o.forces).add(o.virial).add(o.edge_grad).add(d_.vec);
+      graphs_->launch(sig, work);
     } else {
       work();
     }
@@ -406,7 +407,7 @@ class Calculator {
   const int* neigh_ = nullptr;
   const int* shift_ = nullptr;
   bool have_list_ = false;
-  std::unique_ptr<GraphCache> graphs_;
+  std::unique_ptr<StepRecorder> graphs_;
 };
 
 }  // namespace pet

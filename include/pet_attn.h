@@ -45,16 +45,18 @@ extern "C" {
 enum {
   PET_ATTN_OK = 0,
   PET_ATTN_EINVAL = 1,      /* a null pointer, negative size or leading dimension too small */
-  PET_ATTN_EHEADDIM = 2,    /* head_dim not one the kernels hold (a multiple of 16, <= 128) */
-  PET_ATTN_ESLOTS = 3,      /* slots (S) above pet_attn_max_slots(head_dim) */
-  PET_ATTN_EALIGN = 4,      /* a pointer or leading dimension not a multiple of 4 floats */
+  PET_ATTN_EHEADDIM = 2,    /* head_dim outside 1..128 (the reference's kMaxHeadDim, src/ops.hpp:19) */
+  PET_ATTN_ESLOTS = 3,      /* slots (S) too large for a kernel that holds an atom in LDS (model-level callers) */
+  PET_ATTN_EALIGN = 4,      /* a pointer or leading dimension not a multiple of 4 floats (head_dim a multiple of 4),
+                               or a pointer not 4-byte aligned */
   PET_ATTN_ELAUNCH = 5,     /* a HIP launch or runtime call failed */
   PET_ATTN_EBLAS = 6,       /* the BLAS call of a linear failed */
   PET_ATTN_EWORKSPACE = 7,  /* the workspace is smaller than pet_attention_bwd_workspace() */
   PET_ATTN_EINDEX = 8       /* a row index or element offset that does not fit 2^31 */
 };
 
-/* The most tokens an atom may have (16 waves of 16 queries per workgroup). */
+/* The most tokens an atom may have in the LDS-staged kernels (16 waves of 16
+ * queries per workgroup); larger S runs on the streaming kernels. */
 #define PET_ATTN_MAX_SLOTS 256
 
 typedef struct pet_attn_shape {
@@ -73,12 +75,38 @@ PET_ATTN_API float pet_attn_scale(int head_dim, double temperature);
 
 PET_ATTN_API const char* pet_attn_strerror(int code);
 
-/* The most slots (S) both kernels hold for this head_dim on the current
- * device, their staged rows bounded by its LDS (at most PET_ATTN_MAX_SLOTS);
- * 0 for a head_dim they do not hold. Calls with a larger S return
- * PET_ATTN_ESLOTS. No counterpart in the reference, whose kernels stream
- * 16-token blocks through registers. */
+/* The most slots (S) the LDS-staged kernels hold for this head_dim on the
+ * current device (at most PET_ATTN_MAX_SLOTS); 0 for a head_dim they do not
+ * hold (not a multiple of 16). Calls with a larger S, or such a head_dim, run
+ * on the streaming kernels (keys or queries through LDS in 64-row tiles, any
+ * S, any head_dim 1..128), as the reference computes any S on its flat path
+ * and any head_dim on its generic one (src/attention.cpp:28-39, :195-203). */
 PET_ATTN_API int pet_attn_max_slots(int head_dim);
+
+/* ---- process-wide tuning options ----------------------------------------- */
+
+/* Options that choose among equivalent kernels (all meet the same tolerance;
+ * each choice is bit-repeatable). Defaults need none of them. They are
+ * process-wide, read by each launch (an evaluation reads PET_OPT_MODEL_GEMM
+ * once at its start), and not read from the environment. A HIP graph keeps the
+ * kernels of the options in force when it was recorded. The reference's
+ * counterpart is its process-global GEMM mode (include/pet/gemm.hpp:119-122). */
+enum {
+  PET_OPT_SPLIT = 1,       /* 1 (default): fp32 products split over the bf16 matrix cores where they pay; 0: fp32 MFMA only */
+  PET_OPT_FWD_KERNEL = 2,  /* 0 (default): matrix-core forward; 3: the vector-ALU forward (head_dim <= 64), for comparison */
+  PET_OPT_BWD_VLDS = 3,    /* 0 (default): automatic; 1: V staged in LDS; 2: V read from global memory (where it fits) */
+  PET_OPT_BWD_NBUF = 4,    /* 0 (default): automatic; 1 or 2 backward tile buffers (where it fits) */
+  PET_OPT_MODEL_GEMM = 5,  /* the model's dense layers: 4 (default) split-product kernel for M*N*K >= 2^32, else rocBLAS;
+                              0 rocBLAS only; 1 / 2 the fp32 fused kernel for every / <= 4096-row forward layer;
+                              3 the split-product kernel wherever K is a multiple of 32 */
+  PET_OPT_ATTN_STREAM = 6, /* 0 (default): the LDS-staged kernels where they hold the shape; 1: the streaming kernels always */
+  PET_OPT_COUNT = 7
+};
+
+/* Sets an option; PET_ATTN_EINVAL for an unknown option or a value out of range. */
+PET_ATTN_API int pet_attn_set_option(int option, int value);
+/* The option's value, -1 for an unknown option. */
+PET_ATTN_API int pet_attn_get_option(int option);
 
 /* ---- the core kernels -------------------------------------------------- */
 

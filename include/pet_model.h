@@ -123,6 +123,11 @@ PET_ATTN_API int pet_linear_fused(int M, int N, int K, const float* A, int64_t l
  * for bit. No counterpart in the reference, which runs its dense layers in
  * fp32 (src/fused_gemm_hip.cpp); a faster form of pet_linear_fused. */
 PET_ATTN_API int pet_linear_split_weights(const float* W, int N, int K, int64_t ldw, void* out, void* stream);
+/* The split rows of B = W^T from W [K, N] (ld ldw >= N) without forming W^T:
+ * what pet_linear_split_weights makes of W^T, for the input adjoint of a dense
+ * layer (in_adj = out_adj W, i.e. B = W^T [K_in, N_out]). */
+PET_ATTN_API int pet_linear_split_weights_transposed(const float* W, int N, int K, int64_t ldw, void* out,
+                                                     void* stream);
 PET_ATTN_API int pet_linear_fused_split(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit, float* C,
                                         int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                         int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);

@@ -14,6 +14,8 @@ EXPORTS = (
     "pet_attn_scale",
     "pet_attn_strerror",
     "pet_attn_max_slots",
+    "pet_attn_set_option",
+    "pet_attn_get_option",
     "pet_attn_fwd_run",
     "pet_attn_bwd_run",
     "pet_attn_cf_adjoint",
@@ -44,6 +46,7 @@ EXPORTS = (
     "pet_model_workspace_bytes",
     "pet_linear_fused",
     "pet_linear_split_weights",
+    "pet_linear_split_weights_transposed",
     "pet_linear_fused_split",
 )
 
@@ -111,6 +114,10 @@ def load() -> ctypes.CDLL:
     lib.pet_attn_strerror.argtypes = [ctypes.c_int]
     lib.pet_attn_max_slots.restype = ctypes.c_int
     lib.pet_attn_max_slots.argtypes = [ctypes.c_int]
+    lib.pet_attn_set_option.restype = ctypes.c_int
+    lib.pet_attn_set_option.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.pet_attn_get_option.restype = ctypes.c_int
+    lib.pet_attn_get_option.argtypes = [ctypes.c_int]
     sp = ctypes.POINTER(Shape)
     lib.pet_attn_fwd.restype = ctypes.c_int
     lib.pet_attn_fwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
@@ -180,12 +187,48 @@ def load() -> ctypes.CDLL:
     lib.pet_linear_fused.argtypes = [_I, _I, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_linear_split_weights.restype = ctypes.c_int
     lib.pet_linear_split_weights.argtypes = [_P, _I, _I, _I64, _P, _P]
+    lib.pet_linear_split_weights_transposed.restype = ctypes.c_int
+    lib.pet_linear_split_weights_transposed.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_split.restype = ctypes.c_int
     lib.pet_linear_fused_split.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_model_workspace_bytes.restype = ctypes.c_size_t
     lib.pet_model_workspace_bytes.argtypes = [_P]
     _lib = lib
     return lib
+
+
+OPTIONS = {"split": 1, "fwd_kernel": 2, "bwd_vlds": 3, "bwd_nbuf": 4, "model_gemm": 5, "attn_stream": 6}
+
+
+def set_option(name: str, value: int) -> None:
+    """pet_attn_set_option by name (split, fwd_kernel, bwd_vlds, bwd_nbuf, model_gemm, attn_stream)."""
+    check(load().pet_attn_set_option(OPTIONS[name], int(value)), f"pet_attn_set_option({name}={value})")
+
+
+def get_option(name: str) -> int:
+    return int(load().pet_attn_get_option(OPTIONS[name]))
+
+
+class options:
+    """Context manager: the named options set for the block, restored after.
+
+        with _lib.options(split=0, bwd_vlds=2): ...
+    """
+
+    def __init__(self, **values):
+        self.values = values
+        self.saved = {}
+
+    def __enter__(self):
+        for k, v in self.values.items():
+            self.saved[k] = get_option(k)
+            set_option(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k, v in self.saved.items():
+            set_option(k, v)
+        return False
 
 
 def strerror(code: int) -> str:

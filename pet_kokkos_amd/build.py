@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpet_attn.so")
-SOURCES = ["attention.hip", "ops.hip", "rows.hip", "forces.hip", "model.hip", "gemm.hip"]
+SOURCES = ["attention.hip", "attention_stream.hip", "ops.hip", "rows.hip", "forces.hip", "model.hip", "gemm.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -62,18 +62,34 @@ def build_cpp_test(verbose: bool = False) -> str:
     return CPP_TEST
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into LIB (always recompiles) and return its path."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs,
-           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+def _run(cmd, what: str, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {LIB}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}) building {what}")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source into LIB (always recompiles; one hipcc per
+    source, in parallel, then one link) and return its path."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    cflags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = []
+    for s in SOURCES:
+        obj = os.path.join(objdir, s.replace(".hip", ".o"))
+        jobs.append((obj, [hipcc(), *cflags, "-c", "-I", os.path.join(ROOT, "include"), "-o", obj,
+                           os.path.join(CSRC, s)]))
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(workers) as pool:
+        for f in [pool.submit(_run, cmd, obj, verbose) for obj, cmd in jobs]:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *[o for o, _ in jobs],
+          "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"], LIB, verbose)
     os.replace(tmp, LIB)
     build_cpp_test(verbose)
     return LIB

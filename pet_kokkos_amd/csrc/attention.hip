@@ -35,6 +35,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -44,15 +45,10 @@
 #include <utility>
 
 #include "../../include/pet_attn.h"
+#include "attn_common.h"
 #include "split_bf16.h"
 
 namespace pet_attn {
-
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 // ---- fp32 products on the bf16 matrix cores (split_bf16.h) -------------------
 using pet_split::bf8;
@@ -62,144 +58,6 @@ using pet_split::pack_hi;
 using pet_split::split3;
 using pet_split::split8;
 using pet_split::u4;
-
-constexpr float kOff = -1e30f;  // the log cf of a key no query sees
-// log cf of a key with cf > 0: the hardware log2 times ln 2 (the fast log of
-// the reference's device path), held above -104 (log of the smallest
-// subnormal) so that a subnormal cf, which the hardware log flushes, stays a
-// live key.
-__device__ __forceinline__ float log_cf(float cf) {
-  return fmaxf(__builtin_amdgcn_logf(cf) * 0.693147180559945309f, -104.f);
-}
-__device__ __forceinline__ bool is_off(float lc) { return lc < -1e29f; }
-// The running max's start in the matrix-core forward: above kOff, so a key
-// with log cf kOff has exp(x - max) = 0 exactly whatever keys came before,
-// without a test per key (x = s sc + kOff rounds to kOff for any real score).
-constexpr float kFloor = -1e29f;
-
-// Over the four lanes that share c (g = 0..3): gfx950's lane-swap
-// instructions exchange rows of 32 and of 16 lanes in registers, no LDS. Both
-// lanes of a pair combine the same two values in the same order, so every
-// lane ends with bit-identical results.
-__device__ __forceinline__ float max_g(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float sum_g(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// A workgroup barrier that orders LDS traffic only. __syncthreads() also
-// fences global memory, which on gfx9 means waiting for every outstanding
-// vector-memory load -- the prefetches a barrier is meant to overlap.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// n floats from LDS (p aligned to n floats when n is 2 or 4).
-template <int n>
-__device__ __forceinline__ void lds_get(const float* p, float* out) {
-  if constexpr (n % 4 == 0) {
-#pragma unroll
-    for (int j = 0; j < n; j += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(p + j);
-      out[j] = x.x, out[j + 1] = x.y, out[j + 2] = x.z, out[j + 3] = x.w;
-    }
-  } else if constexpr (n % 2 == 0) {
-#pragma unroll
-    for (int j = 0; j < n; j += 2) {
-      const float2 x = *reinterpret_cast<const float2*>(p + j);
-      out[j] = x.x, out[j + 1] = x.y;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < n; ++j) out[j] = p[j];
-  }
-}
-// n (a multiple of 4) floats from global memory, 16-byte aligned.
-template <int n>
-__device__ __forceinline__ void gmem_get(const float* p, float* out) {
-#pragma unroll
-  for (int j = 0; j < n; j += 4) {
-    const float4 x = *reinterpret_cast<const float4*>(p + j);
-    out[j] = x.x, out[j + 1] = x.y, out[j + 2] = x.z, out[j + 3] = x.w;
-  }
-}
-
-// An affine map of qkv applied as it is loaded: row r's values scaled by
-// rs[r], then column j's bias b[j] added (either may be null). With qkv the
-// product of raw tokens and the input linear whose weight has the RMSNorm
-// weight folded in, rs = 1/rms(token) and b the linear's bias make it
-// norm(tokens) W^T + b without the normed tokens or the bias pass ever
-// touching memory: the QKV projection's epilogue, fused into its consumer.
-struct QkvXf {
-  const float* rs = nullptr;
-  const float* b = nullptr;
-};
-template <int W, bool XF>
-__device__ __forceinline__ void qkv_get(const float* qkv, int64_t ldq, size_t r, int col, const QkvXf& xf,
-                                        float* out) {
-  gmem_get<W>(qkv + r * ldq + col, out);
-  if constexpr (!XF) return;
-  if (xf.rs) {
-    const float sc = xf.rs[r];
-#pragma unroll
-    for (int t = 0; t < W; ++t) out[t] *= sc;
-  }
-  if (xf.b) {
-    float bb[W];
-    gmem_get<W>(xf.b + col, bb);
-#pragma unroll
-    for (int t = 0; t < W; ++t) out[t] += bb[t];
-  }
-}
-
-// One work item, an (atom, head), of a run of atoms [n0, n1). The atom's
-// tokens are rows of two matrices: the whole token matrix (merged, and the
-// per-slot arrays), and the run's chunk (qkv, dO, qkv_adj), which holds the
-// run's own rows first (atom n at n - n0) and then its edges' rows (edge k at
-// eb + k, eb = (n1 - n0) - off[n0]). Unchunked, n0 = 0 and eb = N and the two
-// agree (the chunk layout of the reference's attention_chunked,
-// src/attention.cpp:2055-2070, run_qkv).
-struct Atom {
-  int n, h, N, n0, o0, cnt, nb;
-  int64_t eb;
-  __device__ Atom(const int* off, int item, int H, int N_, int S, int n0_, int64_t eb_) : N(N_), n0(n0_), eb(eb_) {
-    const int a = item / H;
-    h = item - a * H;
-    n = n0 + a;
-    o0 = off[n];
-    const int c = off[n + 1] - o0 + 1;
-    cnt = c < S ? c : S;  // a count above S would be the caller's error; never read past S
-    nb = (cnt + 15) >> 4;
-  }
-  // slot s's row in the run's chunk
-  __device__ size_t row(int s) const { return s == 0 ? size_t(n - n0) : size_t(eb + o0 + s - 1); }
-  // slot s's row in the whole token matrix
-  __device__ size_t grow(int s) const { return s == 0 ? size_t(n) : size_t(N) + size_t(o0) + size_t(s - 1); }
-};
-
-// Element e of a lane's hd/4 slice, from the DT result tiles: e = r * DT + t.
-template <int DT>
-__device__ __forceinline__ float tile_elem(const f4* acc, int e) {
-  return acc[e % DT][e / DT];
-}
-template <int HD>
-__device__ __forceinline__ void store_slice(float* dst, const f4* acc, float f) {
-  constexpr int W = HD / 4, DT = HD / 16;
-#pragma unroll
-  for (int e = 0; e < W; e += 4)
-    *reinterpret_cast<float4*>(dst + e) =
-        make_float4(tile_elem<DT>(acc, e) * f, tile_elem<DT>(acc, e + 1) * f, tile_elem<DT>(acc, e + 2) * f,
-                    tile_elem<DT>(acc, e + 3) * f);
-}
 
 template <int HD>
 struct Lds {
@@ -430,7 +288,7 @@ __global__ void __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(HD <=
 // softmax over the keys four at a time. No padding to 16-token blocks, but each
 // score and each weighted V row is hd fp32 FMAs on the vector ALUs (a wave64
 // instruction every 4 cycles) instead of a quarter of a matrix-core product.
-// Selected by PET_ATTN_FWD=3 (head_dim <= 64); the matrix-core kernel is the
+// Selected by option PET_OPT_FWD_KERNEL 3 (head_dim <= 64); the matrix-core kernel is the
 // default.
 template <int HD>
 __global__ void __launch_bounds__(256) attn_fwd_valu_kernel(const float* __restrict__ qkv, int64_t ldq,
@@ -815,15 +673,18 @@ int max_lds_bytes() {
 int check_shape(const pet_attn_shape* sh) {
   if (!sh) return PET_ATTN_EINVAL;
   if (sh->n_atoms < 0 || sh->n_rows < sh->n_atoms || sh->slots < 1 || sh->heads < 1) return PET_ATTN_EINVAL;
-  if (sh->head_dim < 16 || sh->head_dim > 128 || sh->head_dim % 16 != 0) return PET_ATTN_EHEADDIM;
-  if (sh->slots > PET_ATTN_MAX_SLOTS) return PET_ATTN_ESLOTS;
+  if (sh->head_dim < 1 || sh->head_dim > 128) return PET_ATTN_EHEADDIM;
   const int64_t D = int64_t(sh->heads) * sh->head_dim;
   if (int64_t(sh->n_rows) * 3 * D >= (int64_t(1) << 31) * 4) return PET_ATTN_EINDEX;
   if (int64_t(sh->n_atoms) * sh->heads * sh->slots >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
   return PET_ATTN_OK;
 }
-int check_matrix(const void* p, int64_t ld, int64_t width) {
+// A matrix argument: non-null, rows no narrower than width, and 16-byte
+// aligned rows unless head_dim is not a multiple of 4 (the streaming kernels
+// then load columns one at a time: 4-byte alignment).
+int check_matrix(const void* p, int64_t ld, int64_t width, int head_dim) {
   if (!p || ld < width) return PET_ATTN_EINVAL;
+  if (head_dim % 4 != 0) return (reinterpret_cast<uintptr_t>(p) & 3u) ? PET_ATTN_EALIGN : PET_ATTN_OK;
   if (!aligned16(p) || ld % 4 != 0) return PET_ATTN_EALIGN;
   return PET_ATTN_OK;
 }
@@ -833,17 +694,11 @@ int check_run(const pet_attn_shape* sh, int n0, int n1, int e0) {
 }
 int waves_for(int S) { return (S + 15) / 16; }
 
-// Tuning knobs read once from the environment (0 or unset: automatic).
-int env_int(const char* name) {
-  const char* v = std::getenv(name);
-  return v ? std::atoi(v) : 0;
-}
-// PET_ATTN_SPLIT=0 turns the split-fp32 bf16 products off; read at every
-// launch, so that a process can compare both paths.
-bool split_enabled() {
-  const char* v = std::getenv("PET_ATTN_SPLIT");
-  return !v || std::atoi(v) != 0;
-}
+// Process-wide tuning options (pet_attn_set_option): each an atomic read
+// once per launch, never the environment.
+std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {4}, {0}};
+int option(int o) { return g_options[o].load(std::memory_order_relaxed); }
+bool split_enabled() { return option(PET_OPT_SPLIT) != 0; }
 
 // Per-kernel facts the launchers consult on every call, looked up once: the
 // compiled VGPR count, and (per device) the dynamic LDS limit already raised.
@@ -897,7 +752,7 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   size_t bytes = sizeof(float) * Lds<HD>::fwd_floats(NW);
   if (bytes > size_t(max_lds_bytes())) return PET_ATTN_ESLOTS;
   // scores on the bf16 matrix cores (split fp32) where head_dim is a multiple
-  // of 32 and the split K rows fit as many workgroups a CU; PET_ATTN_SPLIT=0
+  // of 32 and the split K rows fit as many workgroups a CU; option PET_OPT_SPLIT 0
   // keeps every product on the fp32 matrix cores
   const size_t sbytes = sizeof(float) * Lds<HD>::fwd_floats(NW, true);
   bool spl = false;
@@ -911,7 +766,7 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   if (spl) bytes = sbytes;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
-  static const int choice = env_int("PET_ATTN_FWD");  // 3: the vector-ALU kernel, for comparison
+  const int choice = option(PET_OPT_FWD_KERNEL);  // 3: the vector-ALU kernel, for comparison
   if constexpr (HD <= 64) {
     const int threads = 64 * ((sh.slots + 63) / 64);
     const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
@@ -957,9 +812,9 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   // MI355X: at head_dim 32 the fullest is fastest though the leanest would fit
   // a third workgroup (C3 backward 429 us against 466-493 us); at head_dim 64
   // the fullest holds one workgroup a CU and V-from-global with one buffer two
-  // (C5 backward 3853 -> 3244 us). PET_ATTN_BWD_VLDS (1 staged, 2 not) and
-  // PET_ATTN_BWD_NBUF (1, 2) force a layout where it fits.
-  const int force_v = env_int("PET_ATTN_BWD_VLDS"), force_b = env_int("PET_ATTN_BWD_NBUF");  // read per launch
+  // (C5 backward 3853 -> 3244 us). PET_OPT_BWD_VLDS (1 staged, 2 not) and
+  // PET_OPT_BWD_NBUF (1, 2) force a layout where it fits.
+  const int force_v = option(PET_OPT_BWD_VLDS), force_b = option(PET_OPT_BWD_NBUF);
   const size_t cap = size_t(max_lds_bytes());
   const int layouts[3][2] = {{1, 2}, {0, 2}, {0, 1}};  // (vlds, nbuf), fullest first
   int best = -1, best_res = 0;
@@ -1050,8 +905,8 @@ const char* pet_attn_strerror(int code) {
   switch (code) {
     case PET_ATTN_OK: return "ok";
     case PET_ATTN_EINVAL: return "invalid argument (null pointer, negative size or leading dimension too small)";
-    case PET_ATTN_EHEADDIM: return "unsupported head_dim (a multiple of 16, at most 128)";
-    case PET_ATTN_ESLOTS: return "too many slots per atom for the kernels' LDS (see pet_attn_max_slots)";
+    case PET_ATTN_EHEADDIM: return "unsupported head_dim (1 to 128)";
+    case PET_ATTN_ESLOTS: return "too many slots per atom";
     case PET_ATTN_EALIGN: return "a pointer or leading dimension is not a multiple of 4 floats";
     case PET_ATTN_ELAUNCH: return "a HIP launch or runtime call failed";
     case PET_ATTN_EBLAS: return "the BLAS call of a linear failed";
@@ -1063,6 +918,16 @@ const char* pet_attn_strerror(int code) {
     default: return "unknown pet_attn error";
   }
 }
+
+int pet_attn_set_option(int opt, int value) {
+  if (opt <= 0 || opt >= PET_OPT_COUNT) return PET_ATTN_EINVAL;
+  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 4, 1};
+  if (value < lo[opt] || value > hi[opt]) return PET_ATTN_EINVAL;
+  g_options[opt].store(value, std::memory_order_relaxed);
+  return PET_ATTN_OK;
+}
+
+int pet_attn_get_option(int opt) { return opt > 0 && opt < PET_OPT_COUNT ? option(opt) : -1; }
 
 int pet_attn_max_slots(int head_dim) {
   int e = with_head_dim(head_dim, [&](auto hd) {
@@ -1078,6 +943,20 @@ int pet_attn_max_slots(int head_dim) {
 
 }  // extern "C"
 
+namespace pet_attn {
+// The streaming kernels (attention_stream.hip): any S, any head_dim 1..128.
+int stream_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+               const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st);
+int stream_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+               const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
+               const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st);
+// The LDS-staged kernels take head_dim a multiple of 16 and S within their LDS
+// envelope; everything else streams (or everything, with PET_OPT_ATTN_STREAM).
+bool streams(const pet_attn_shape& sh) {
+  return sh.head_dim % 16 != 0 || option(PET_OPT_ATTN_STREAM) != 0 || sh.slots > pet_attn_max_slots(sh.head_dim);
+}
+}  // namespace pet_attn
+
 namespace {
 int fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,
             const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, void* stream) {
@@ -1085,11 +964,12 @@ int fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, 
   if (int e = check_run(sh, n0, n1, e0)) return e;
   const int64_t D = int64_t(sh->heads) * sh->head_dim;
   if (n1 == n0) return PET_ATTN_OK;
-  if (int e = check_matrix(qkv, ldq, 3 * D)) return e;
-  if (int e = check_matrix(merged, ldm, D)) return e;
+  if (int e = check_matrix(qkv, ldq, 3 * D, sh->head_dim)) return e;
+  if (int e = check_matrix(merged, ldm, D, sh->head_dim)) return e;
   if (!off || !cf_seq || ldc < sh->slots) return PET_ATTN_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t eb = int64_t(n1 - n0) - e0;
+  if (streams(*sh)) return stream_fwd(*sh, n0, n1, eb, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, xf, st);
   return with_head_dim(sh->head_dim, [&](auto hd) {
     return launch_fwd<decltype(hd)::value>(*sh, n0, n1, eb, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, xf, st);
   });
@@ -1102,13 +982,16 @@ int bwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, 
   if (int e = check_run(sh, n0, n1, e0)) return e;
   const int64_t D = int64_t(sh->heads) * sh->head_dim;
   if (n1 == n0) return PET_ATTN_OK;
-  if (int e = check_matrix(qkv, ldq, 3 * D)) return e;
-  if (int e = check_matrix(dmerged, ldg, D)) return e;
-  if (int e = check_matrix(merged, ldm, D)) return e;
-  if (int e = check_matrix(qkv_adj, lda, 3 * D)) return e;
+  if (int e = check_matrix(qkv, ldq, 3 * D, sh->head_dim)) return e;
+  if (int e = check_matrix(dmerged, ldg, D, sh->head_dim)) return e;
+  if (int e = check_matrix(merged, ldm, D, sh->head_dim)) return e;
+  if (int e = check_matrix(qkv_adj, lda, 3 * D, sh->head_dim)) return e;
   if (!off || !ml || !cf_seq || !cfh || ldc < sh->slots) return PET_ATTN_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t eb = int64_t(n1 - n0) - e0;
+  if (streams(*sh))
+    return stream_bwd(*sh, n0, n1, eb, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh,
+                      xf, st);
   return with_head_dim(sh->head_dim, [&](auto hd) {
     return launch_bwd<decltype(hd)::value>(*sh, n0, n1, eb, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq,
                                            ldc, qkv_adj, lda, cfh, xf, st);

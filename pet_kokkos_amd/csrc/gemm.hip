@@ -96,7 +96,9 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
   __shared__ float As[2][BM * PK], Bs[2][BN * PK];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
   const int wm = w >> 1, wn = w & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // a 1-D grid of tiles, a row block's column tiles consecutive
+  const int NT = (N + BN - 1) / BN, tile = blockIdx.x;
+  const int m0 = (tile / NT) * BM, n0 = (tile % NT) * BN;
 
   f4 acc[TM][TN];
 #pragma unroll
@@ -197,10 +199,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
   // contiguous run of tiles in row-block order, so a row block's column tiles
   // share an L2 (509730 x 512 x 512: 1547 against 1624 us in launch order).
   // A bijection of the tiles whatever the hardware's order.
-  const int total = gridDim.x * gridDim.y, L = blockIdx.x + gridDim.x * blockIdx.y;
+  // A 1-D grid of all the tiles, tile t = (row block t / NT, column tile t % NT).
+  const int NT = (N + BN - 1) / BN, total = gridDim.x, L = blockIdx.x;
   const int q = total / 8, r = total % 8, x = L % 8;
   const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + L / 8;
-  const int tm = t / gridDim.x, tn = t % gridDim.x;
+  const int tm = t / NT, tn = t % NT;
   const int m0 = tm * BM, n0 = tn * BN, KG = K / 8;
 
   f4 acc[TM][TN];
@@ -329,10 +332,10 @@ int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const fl
   e.act = act;
   auto tiles = [&](int bm, int bn) { return int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const bool k32 = K % 32 == 0;
-  auto go = [&](auto kern, int bm, int bn) {
-    hipLaunchKernelGGL(kern, dim3(unsigned((N + bn - 1) / bn), unsigned((M + bm - 1) / bm)), dim3(256), 0, st, M, N,
-                       K, A, lda, B, ldb, C, ldc, e);
+  auto go = [&](auto kern, int bm, int bn) {  // a 1-D grid: every tile, no extent limit below 2^31 tiles
+    hipLaunchKernelGGL(kern, dim3(unsigned(tiles(bm, bn))), dim3(256), 0, st, M, N, K, A, lda, B, ldb, C, ldc, e);
   };
+  if (tiles(64, 32) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
   if (N > 64 && tiles(128, 128) >= 512)
     k32 ? go(gemm_nt_kernel<128, 128, 32>, 128, 128) : go(gemm_nt_kernel<128, 128, 16>, 128, 128);
   else if (N > 32 && tiles(128, 64) >= 512)
@@ -357,16 +360,18 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
                       float* pre, int64_t ldpre, int act, hipStream_t st) {
   if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
-  if (K == 0 || (M + 63) / 64 > 65535) return PET_ATTN_EINVAL;  // the grid's y extent: row tiles
+  if (K == 0) return PET_ATTN_EINVAL;
+  if (int64_t((M + 63) / 64) * ((N + 63) / 64) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;  // 1-D grid of tiles
   if (K % 32 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15))
     return PET_ATTN_EALIGN;
   if (act == 2 && N % 2) return PET_ATTN_EINVAL;
   Epi e;
   e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
   e.act = act;
-  auto go = [&](auto kern, int bm, int bn, int threads) {
-    hipLaunchKernelGGL(kern, dim3(unsigned((N + bn - 1) / bn), unsigned((M + bm - 1) / bm)), dim3(threads), 0, st, M,
-                       N, K, A, lda, static_cast<const u4*>(Bs), C, ldc, e);
+  auto go = [&](auto kern, int bm, int bn, int threads) {  // a 1-D grid of every tile
+    const int64_t tiles = int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    hipLaunchKernelGGL(kern, dim3(unsigned(tiles)), dim3(threads), 0, st, M, N, K, A, lda,
+                       static_cast<const u4*>(Bs), C, ldc, e);
   };
   // measured on MI355X: 128 x 128 tiles of 8 waves where there are many
   // (131072 x 1536 x 512: 1200-1213 us against 1394-1418 for 128 x 64 and
@@ -406,6 +411,13 @@ extern "C" int pet_linear_split_weights(const float* W, int N, int K, int64_t ld
   hipLaunchKernelGGL(split_rows_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), W, N, K, ldw, static_cast<u4*>(out));
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+extern "C" int pet_linear_split_weights_transposed(const float* W, int N, int K, int64_t ldw, void* out,
+                                                   void* stream) {
+  if (N < 0 || K < 0 || K % 32 || ldw < N || ((N > 0 && K > 0) && (!W || !out))) return PET_ATTN_EINVAL;
+  if (reinterpret_cast<uintptr_t>(out) & 15) return PET_ATTN_EALIGN;
+  return pet_gemm_split_weights(W, N, K, ldw, true, out, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pet_linear_fused_split(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit, float* C,

@@ -471,6 +471,7 @@ using namespace pet_model_impl;
 struct pet_model {
   pet_model_hypers h{};
   int hd = 0, cw = 0, ew = 0;  // head_dim, center / edge MLP pre-activation widths
+  int gemm_mode = 4;           // PET_OPT_MODEL_GEMM for the evaluation in progress
   std::unordered_map<std::string, Mat> m;
   std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
   void* weights = nullptr;
@@ -504,25 +505,23 @@ namespace {
 // Measured on MI355X (C2 / C2-residual / C5 energy+forces, ms): 3.45 / 2.67 /
 // 281 with rocBLAS, 3.50 / 2.68 / 281 with mode 2, 3.96 / 3.00 / 311 with mode
 // 1: its main loop reaches 72% of the fp32 matrix peak at K = 1024 where
-// rocBLAS reaches 90%. PET_MODEL_GEMM selects, read once.
-bool own_gemm(int M, int K) {
-  const char* v = std::getenv("PET_MODEL_GEMM");  // read per call: a process may compare both
-  const int mode = v ? std::atoi(v) : 0;
-  return K % 16 == 0 && (mode == 1 || (mode == 2 && M <= 4096));
+// rocBLAS reaches 90%. The option PET_OPT_MODEL_GEMM selects (md.gemm_mode,
+// read once at the start of each evaluation).
+bool own_gemm(const pet_model& md, int M, int K) {
+  return K % 16 == 0 && (md.gemm_mode == 1 || (md.gemm_mode == 2 && M <= 4096));
 }
 
 // out[M, N] = in W^T + beta out, W a model matrix [N, K]: rocBLAS fp32, or
 // this library's split-product kernel (gemm.hip) where W has a split copy (K a
 // multiple of 32) and in is 16-byte aligned rows -- by default for the large
-// products (M N K >= 2^32), every one with PET_MODEL_GEMM=3, none with
-// PET_MODEL_GEMM=0. Measured on MI355X (energy+forces, ms, same process):
+// products (M N K >= 2^32), every one with PET_OPT_MODEL_GEMM 3, none with
+// PET_OPT_MODEL_GEMM 0. Measured on MI355X (energy+forces, ms, same process):
 // C2 2.98 / 2.15 (residual) with rocBLAS, the same by default (no C2 product is
 // that large), 3.59 / 2.40 with all split; C5 276-279 with rocBLAS, 244 by
 // default and with all split.
 int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int N,
            int K, float beta, hipStream_t st) {
-  const char* v = std::getenv("PET_MODEL_GEMM");  // read per call: a process may compare both
-  const int mode = v ? std::atoi(v) : 4;
+  const int mode = md.gemm_mode;
   const bool big = double(M) * N * K >= 4294967296.0;
   if ((mode == 3 || (mode == 4 && big)) && ldi % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
     auto it = md.split.find(W);
@@ -540,7 +539,7 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   if (M == 0) return;
   const float* b = bias ? md.p(key + ".bias") : nullptr;
-  if (own_gemm(M, K)) {
+  if (own_gemm(md, M, K)) {
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
@@ -557,7 +556,7 @@ void linear_acc(pet_model& md, float* out, const float* in, int M, int K, const 
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   if (M == 0) return;
-  if (own_gemm(M, K)) {
+  if (own_gemm(md, M, K)) {
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, nullptr, out, W.rows, 1.f, nullptr, 0, 0,
                          st));
     return;
@@ -575,7 +574,7 @@ void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const st
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   if (M == 0) return;
-  if (own_gemm(M, K)) {
+  if (own_gemm(md, M, K)) {
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, z, W.rows, nullptr, nullptr, nullptr, 0, 0.f, nullptr, 0, 0,
                          st));
     return;
@@ -1216,8 +1215,12 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
   // central token (d_node != d_pet), residual without (d_node == d_pet)
   const bool residual = h.featurizer == 1;
   if (residual != (h.d_node == h.d_pet)) return PET_ATTN_EINVAL;
+  // any head_dim the attention holds (1..128, the reference's kMaxHeadDim,
+  // src/model.cpp:331-334): multiples of 16 on the LDS-staged kernels, the
+  // rest on the streaming ones
+  if (h.d_pet % h.num_heads) return PET_ATTN_EINVAL;
   const int hd = h.d_pet / h.num_heads;
-  if (hd % 16 || hd > 128) return PET_ATTN_EHEADDIM;
+  if (hd < 1 || hd > 128) return PET_ATTN_EHEADDIM;
   auto md = new pet_model();
   md->h = h, md->hd = hd;
   try {
@@ -1343,12 +1346,12 @@ int pet_model_compute(pet_model* md, const pet_model_edges* e, int forces, doubl
                       double* forces_out, double* virial, double* edge_grad, void* stream) {
   if (!md || !e || e->n_atoms < 0 || e->n_edges < 0 || e->max_neighbors < 0 || e->n_struct < 0) return PET_ATTN_EINVAL;
   if (e->n_atoms == 0) return PET_ATTN_OK;
+  md->gemm_mode = pet_attn_get_option(PET_OPT_MODEL_GEMM);
   if (!e->species || !e->off || (e->n_edges > 0 && (!e->center || !e->neigh_species || !e->reverse || !e->vec ||
                                                     !e->dist || !e->pcut || !e->cut)))
     return PET_ATTN_EINVAL;
   if (energy && (!e->struct_off || e->n_struct < 1)) return PET_ATTN_EINVAL;
   if (forces && (!forces_out || (virial && (!e->struct_off || e->n_struct < 1)))) return PET_ATTN_EINVAL;
-  if (e->max_neighbors + 1 > pet_attn_max_slots(md->hd)) return PET_ATTN_ESLOTS;
   if (edge_grad && md->h.energy_scale != 1.0) return PET_ATTN_EINVAL;
   if (int64_t(e->n_atoms) + e->n_edges >= (int64_t(1) << 31) / std::max(std::max(3 * md->h.d_pet, md->ew), md->cw))
     return PET_ATTN_EINDEX;

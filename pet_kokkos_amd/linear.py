@@ -20,30 +20,78 @@ class SplitWeights:
     """W [N, K] (K a multiple of 32) as its three bf16 parts, N K 6 bytes of
     device memory: made once, then used in place of W by every call."""
 
-    def __init__(self, W: torch.Tensor):
-        N, K = W.shape
+    def __init__(self, W: torch.Tensor, transposed: bool = False):
+        """transposed: the split of W^T, from W [K, N] as it is stored."""
+        _check(W, "W")
+        N, K = (W.shape[1], W.shape[0]) if transposed else W.shape
         self.shape = (N, K)
         self.data = torch.empty(N * K * 3, dtype=torch.int16, device=W.device)
-        _lib.check(_lib.load().pet_linear_split_weights(W.data_ptr(), N, K, W.stride(0), self.data.data_ptr(),
-                                                        torch.cuda.current_stream().cuda_stream),
-                   "pet_linear_split_weights")
+        fn = _lib.load().pet_linear_split_weights_transposed if transposed else _lib.load().pet_linear_split_weights
+        _lib.check(fn(W.data_ptr(), N, K, W.stride(0), self.data.data_ptr(), torch.cuda.current_stream().cuda_stream),
+                   "pet_linear_split_weights" + ("_transposed" if transposed else ""))
+
+
+def _check(t, name, rows=None, cols=None, vector=False, device=None):
+    """A float32 CUDA tensor, unit stride along its last axis, of the stated
+    extents (a row may be longer than `cols` in a 2-D view: the leading
+    dimension is passed)."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: a torch tensor is needed")
+    if t.dtype != torch.float32:
+        raise ValueError(f"{name}: float32 is needed, not {t.dtype}")
+    if not t.is_cuda or (device is not None and t.device != device):
+        raise ValueError(f"{name}: on {t.device}, the operands' device is {device}")
+    if t.dim() != (1 if vector else 2):
+        raise ValueError(f"{name}: {1 if vector else 2}-D is needed, not shape {tuple(t.shape)}")
+    if t.numel() > 1 and t.stride(-1) != 1:
+        raise ValueError(f"{name}: the last axis must be contiguous (stride 1)")
+    if vector:
+        if rows is not None and t.shape[0] < rows:
+            raise ValueError(f"{name}: {t.shape[0]} entries, {rows} needed")
+        return
+    if t.dim() == 2 and t.shape[0] > 1 and t.stride(0) < t.shape[1]:
+        raise ValueError(f"{name}: rows overlap (stride {t.stride(0)} < width {t.shape[1]})")
+    if rows is not None and t.shape[0] < rows:
+        raise ValueError(f"{name}: {t.shape[0]} rows, {rows} needed")
+    if cols is not None and t.shape[1] != cols:
+        raise ValueError(f"{name}: {t.shape[1]} columns, {cols} needed")
 
 
 def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
+    if act not in (0, 1, 2):
+        raise ValueError(f"act {act}: 0 (none), 1 (SiLU) or 2 (SwiGLU)")
+    _check(A, "A")
     M, K = A.shape
+    dev = A.device
+    if isinstance(W, SplitWeights):
+        N, Kw = W.shape
+        if W.data.device != dev:
+            raise ValueError(f"W: on {W.data.device}, A on {dev}")
+    else:
+        _check(W, "W", device=dev)
+        N, Kw = W.shape
+    if Kw != K:
+        raise ValueError(f"A has K = {K}, W has K = {Kw}")
+    if act == 2 and N % 2:
+        raise ValueError("SwiGLU needs an even number of weight rows (value, gate pairs)")
+    _check(C, "C", M, N // 2 if act == 2 else N, device=dev)
+    if row_scale is not None:
+        _check(row_scale, "row_scale", M, vector=True, device=dev)
+    if bias is not None:
+        _check(bias, "bias", N, vector=True, device=dev)
+    if cin is not None:
+        _check(cin, "cin", M, N, device=dev)
+    if pre is not None:
+        _check(pre, "pre", M, N, device=dev)
     p = lambda t: None if t is None else t.data_ptr()
     ld = lambda t: 0 if t is None else t.stride(0)
     st = torch.cuda.current_stream().cuda_stream
     lib = _lib.load()
     if isinstance(W, SplitWeights):
-        N = W.shape[0]
-        if W.shape[1] != K:
-            raise ValueError("A and W disagree on K")
         _lib.check(lib.pet_linear_fused_split(M, N, K, p(A), A.stride(0), W.data.data_ptr(), p(C), C.stride(0),
                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
                    "pet_linear_fused_split")
     else:
-        N = W.shape[0]
         _lib.check(lib.pet_linear_fused(M, N, K, p(A), A.stride(0), p(W), W.stride(0), p(C), C.stride(0),
                                         p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
                    "pet_linear_fused")

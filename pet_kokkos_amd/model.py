@@ -158,7 +158,7 @@ class Calculator:
 
     With ``graph=True`` compute_step replays the step's device work (edge
     geometry and the whole evaluation) as one HIP graph per (forces,
-    edge_gradients) once it has run twice on a list (``GraphCache``): the
+    edge_gradients) from its second step on a list (``StepRecorder``): the
     positions are copied into a buffer the graph reads, the results are the
     same bits as an eager step, and a small structure's step loses most of its
     launch cost (64 atoms: 1.02 -> 0.77 ms). A new list (set_neighbors) drops
@@ -203,8 +203,8 @@ class Calculator:
         self._pos = torch.empty((N, 3), **f64)
         self._cell = torch.empty((3, 3), **f64)
         if self._graph:
-            from .graph import GraphCache
-            self._graphs = GraphCache(keep=4)
+            from .replay import StepRecorder
+            self._graphs = StepRecorder(warm_runs=1, max_live=4)
 
     def compute_step(self, positions, cell=None, forces: bool = True, edge_gradients: bool = False):
         x = self._x
@@ -226,7 +226,7 @@ class Calculator:
                        "pet_edge_geometry")
             return self.model.compute(x, forces, edge_gradients)
 
-        o = self._graphs.run((forces, edge_gradients), step) if self._graphs is not None else step()
+        o = self._graphs.launch((forces, edge_gradients), step) if self._graphs is not None else step()
         torch.cuda.synchronize()
         res = {"energy": float(o["energy"][0]), "per_atom": o["per_atom"].cpu().numpy()}
         if forces:

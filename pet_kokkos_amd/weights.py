@@ -79,6 +79,10 @@ MODELS = {
     "odd": Hypers(d_pet=48, d_node=72, d_head=40, d_feedforward=36, num_heads=3),
     "odd-residual": Hypers(d_pet=48, d_node=48, d_head=40, d_feedforward=36, num_heads=3,
                            featurizer="residual"),
+    # head_dims the LDS-staged attention kernels do not hold (the streaming
+    # kernels): 20 (a multiple of 4) and 10 (not even that; widths of 30)
+    "hd20": Hypers(d_pet=60, d_node=120, d_head=40, d_feedforward=48, num_heads=3),
+    "hd10-residual": Hypers(d_pet=30, d_node=30, d_head=20, d_feedforward=24, num_heads=3, featurizer="residual"),
     # the residual family at configs[1]'s shape
     "c2-residual": Hypers(d_pet=128, d_node=128, d_head=128, d_feedforward=512, num_heads=4,
                           featurizer="residual"),

@@ -9,7 +9,7 @@
 // the edges' cutoff factors, attention_layer, attention_layer_bwd (cf_seq_adj
 // from zero) and forces_and_virial (cosine cutoff, width 0.5, scale -1); writes
 // DIR/{cf,out,tokens_adj,cf_adj}.f32 and DIR/{forces,vir9,grad}.f64; then runs
-// the same chain four more times through a pet::GraphCache on a stream of its
+// the same chain four more times through a pet::StepRecorder on a stream of its
 // own (eager, captured, replayed, replayed) and writes DIR/graph.ok when every
 // run gave the first one's bits.
 #include <cstdio>
@@ -20,7 +20,7 @@
 #include <cstring>
 
 #include "pet/forces.hpp"
-#include "pet/graph.hpp"
+#include "pet/replay.hpp"
 
 template <class T>
 static std::vector<T> read(const std::string& path, size_t n) {
@@ -133,12 +133,12 @@ int main(int argc, char** argv) {
     const auto ref_t = host(tadj, size_t(T) * D);
     const auto ref_c = host(csa, size_t(N) * S);
     const auto ref_f = host(forces.data(), size_t(N) * 3);
-    pet::GraphCache cache(st);
-    const pet::GraphCache::Key key{uintptr_t(tokens), uintptr_t(T), uintptr_t(D)};
+    pet::StepRecorder cache(st);
+    const pet::Signature key{uint64_t(uintptr_t(tokens)), uint64_t(T), uint64_t(D)};
     bool same = true;
     try {
       for (int rep = 0; rep < 4; ++rep) {
-        cache.run(key, [&] {
+        cache.launch(key, [&] {
           // the accumulated outputs start from zero: a fill kernel, no memset node
           hipLaunchKernelGGL(fill0, dim3(256), dim3(256), 0, st, tadj, size_t(T) * D);
           hipLaunchKernelGGL(fill0, dim3(64), dim3(256), 0, st, csa, size_t(N) * S);
@@ -165,7 +165,9 @@ int main(int argc, char** argv) {
       std::fprintf(stderr, "graph: %s\n", e.what());
       return 11;
     }
-    if (same && !cache.broken() && cache.size() == 1) write(dir + "/graph.ok", std::vector<char>{'1'});
+    const auto& n = cache.counters();
+    if (same && n.refusals == 0 && n.records == 1 && n.launches == 3 && n.eager == 1 && cache.live() == 1)
+      write(dir + "/graph.ok", std::vector<char>{'1'});
     (void) hipStreamDestroy(st);
   }
   std::printf("ok\n");

@@ -1,10 +1,14 @@
 """Parity of the HIP attention (through the C ABI) with the CPU oracle and the
 golden vectors, on an MI355X.
 
-Tolerance: every attention output and gradient within
-1e-5 relative of the oracle's fp32 result, measured as
-max|gpu - ref| / max|ref| per tensor (RTOL below); the saved statistics and
-the cf adjoint likewise. Run to run the kernels are bit-identical.
+Tolerance: every element of every attention output and
+gradient within 1e-5 relative of the oracle's fp32 result, with an absolute
+floor tied to the scale of its row (|gpu - ref| <= 1e-5 (|ref| + F_row)), for
+the cf adjoint and the saved max the scale of the terms they are differences
+of (tests/parity.py states the rules and why), and the same against the
+oracle's fp64 twin. Measured on MI355X (C1-C4, the golden vectors): at most
+1.6e-6 against either. Run to run the kernels are
+bit-identical.
 """
 from __future__ import annotations
 
@@ -17,12 +21,12 @@ import pytest
 import torch
 
 import oracle
+from parity import RTOL, attention_errors, row_err
 from pet_kokkos_amd import attention as A
 from pet_kokkos_amd import systems
 
 pytestmark = pytest.mark.gpu
 
-RTOL = 1e-5
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "attn_*.npz")))
 
 
@@ -54,20 +58,17 @@ def gpu_fwd_bwd(device, off, cf_seq, qkv, dm, H, hd, temperature=1.0, dead=False
     return [t.cpu().numpy() for t in (merged, ml, qa, ca, cfh)]
 
 
-def check_against_oracle(device, name, off, cf_seq, qkv, dm, H, hd, temperature=1.0, dead=False, T=None):
+def check_against_oracle(device, name, off, cf_seq, qkv, dm, H, hd, temperature=1.0, dead=False, T=None, f64=True):
     say(f"[gpu] {name}: N={len(off) - 1} T={qkv.shape[0]} S={cf_seq.shape[1]} H={H} hd={hd}")
     m, ml, qa, ca, cfh = gpu_fwd_bwd(device, off, cf_seq, qkv, dm, H, hd, temperature, dead)
-    rm, rml = oracle.attn_fwd(qkv, off, cf_seq, H, hd, temperature, dead=dead)
-    rqa, rca, rcfh = oracle.attn_bwd(qkv, off, dm, rm, rml, cf_seq, H, hd, temperature, dead=dead)
-    errs = dict(merged=rel(m, rm), qkv_adj=rel(qa, rqa), cf_seq_adj=rel(ca, rca), cfh=rel(cfh, rcfh))
-    live = rml[:, 1] > 0
-    assert np.array_equal(ml[:, 1] > 0, live), "live queries differ"
-    assert np.all(ml[~live, 0] == np.float32(-1e30)) and np.all(ml[~live, 1] == 0)
-    errs["ml.max"] = rel(ml[live, 0], rml[live, 0])
-    errs["ml.invl"] = rel(ml[live, 1], rml[live, 1])
-    say("    ", {k: f"{v:.2e}" for k, v in errs.items()})
-    for k, v in errs.items():
-        assert v <= RTOL, f"{name}: {k} off by {v:.3e} relative"
+    sc = oracle.scale(hd, temperature)
+    for dt in ((np.float32, np.float64) if f64 else (np.float32,)):
+        rm, rml = oracle.attn_fwd(qkv, off, cf_seq, H, hd, temperature, dead=dead, dtype=dt)
+        rqa, rca, rcfh = oracle.attn_bwd(qkv, off, dm, rm, rml, cf_seq, H, hd, temperature, dead=dead, dtype=dt)
+        errs = attention_errors(off, cf_seq, qkv, dm, H, hd, m, qa, ca, cfh, (rm, rqa, rca, rcfh), sc, ml, rml)
+        say(f"     vs {np.dtype(dt).name} oracle:", {k: f"{v:.2e}" for k, v in errs.items()})
+        for k, v in errs.items():
+            assert v <= RTOL, f"{name}: {k} off by {v:.3e} (element-wise, floored) against the {np.dtype(dt).name} oracle"
     return m, ml, qa, ca, cfh
 
 
@@ -87,13 +88,11 @@ def test_golden_vectors(device, path):
     H, hd, temp = int(g["heads"]), int(g["head_dim"]), float(g["temperature"])
     say(f"[gpu] golden {os.path.basename(path)}")
     m, ml, qa, ca, cfh = gpu_fwd_bwd(device, g["off"], g["cf_seq"], g["qkv"], g["dmerged"], H, hd, temp)
-    assert rel(m, g["merged"]) <= RTOL
-    assert rel(qa, g["qkv_adj"]) <= RTOL
-    assert rel(cfh, g["cfh"]) <= 10 * RTOL
-    assert rel(ca, g["cf_seq_adj"]) <= 10 * RTOL
-    live = g["ml"][:, 1] > 0
-    assert np.array_equal(ml[:, 1] > 0, live)
-    assert rel(ml[live, 1], g["ml"][live, 1]) <= RTOL
+    errs = attention_errors(g["off"], g["cf_seq"], g["qkv"], g["dmerged"], H, hd, m, qa, ca, cfh,
+                            (g["merged"], g["qkv_adj"], g["cf_seq_adj"], g["cfh"]), float(g["scale"]), ml, g["ml"])
+    say("     vs the fp64 brute force:", {k: f"{v:.2e}" for k, v in errs.items()})
+    for k, v in errs.items():
+        assert v <= RTOL, k
 
 
 @pytest.mark.parametrize("cfg", ["c1", "c2", "c4", "c3", "c5"])
@@ -106,7 +105,7 @@ def test_configs(device, cfg):
         qkv = systems.attention_inputs(tk, conf.d_model, conf.heads, seed=1)["qkv"]
     dm = rng.standard_normal((tk.n_rows, conf.d_model), dtype=np.float32)
     check_against_oracle(device, f"config {cfg} ({conf.name})", tk.off, tk.cf_seq, qkv, dm, conf.heads,
-                         conf.head_dim)
+                         conf.head_dim, f64=cfg != "c5")
 
 
 @pytest.mark.parametrize("hd", [16, 32, 48, 64, 80, 96, 112, 128])
@@ -126,16 +125,14 @@ def test_many_slots(device, hd, top):
     check_against_oracle(device, f"many slots hd {hd} S {tk.slots}", tk.off, tk.cf_seq, qkv, dm, 2, hd)
 
 
-def test_slots_past_capacity_raise(device):
+def test_max_slots(device):
+    # the LDS-staged kernels' envelope; past it (and for head_dims not a
+    # multiple of 16) the streaming kernels run (tests/test_gpu_stream.py)
     lib = A._lib.load()
-    cap = lib.pet_attn_max_slots(128)
     say(f"[gpu] max slots by head_dim: " + ", ".join(f"{h}:{lib.pet_attn_max_slots(h)}" for h in
                                                     (16, 32, 48, 64, 80, 96, 112, 128)))
     assert lib.pet_attn_max_slots(24) == 0
-    assert 64 <= cap < 256
-    tk, qkv, dm = random_case([cap + 5, 3], 1, 128, seed=0)
-    with pytest.raises(RuntimeError):
-        gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 1, 128)
+    assert 64 <= lib.pet_attn_max_slots(128) < 256 and lib.pet_attn_max_slots(16) == 256
 
 
 def test_edge_cases(device):
@@ -169,10 +166,10 @@ def test_bit_identical_repeats(device):
 
 
 @pytest.mark.parametrize("hd", [32, 64, 96, 128])
-def test_split_products_as_accurate_as_fp32(device, hd, monkeypatch):
+def test_split_products_as_accurate_as_fp32(device, hd):
     # Where head_dim is a multiple of 32 the forward's scores run on the bf16
     # matrix cores with each fp32 operand split into three exact bf16 parts;
-    # PET_ATTN_SPLIT=0 keeps them on the fp32 matrix cores. Both must meet the
+    # the option split = 0 keeps them on the fp32 matrix cores. Both must meet the
     # tolerance, and the split one at an error no larger than the fp32 one's
     # order (measured: 1.0e-7 against 1.9e-7 of sum |a b| per product).
     counts = [0, 15, 16, 31, 47, 5, 60, 33, 70, 71]
@@ -180,10 +177,10 @@ def test_split_products_as_accurate_as_fp32(device, hd, monkeypatch):
     rm, rml = oracle.attn_fwd(qkv, tk.off, tk.cf_seq, 2, hd, 1.0)
     out = {}
     for mode in ("0", "1"):
-        monkeypatch.setenv("PET_ATTN_SPLIT", mode)
-        say(f"[gpu] split products hd {hd} PET_ATTN_SPLIT={mode}")
-        out[mode] = check_against_oracle(device, f"split={mode} hd {hd}", tk.off, tk.cf_seq, qkv, dm, 2, hd)
-    e0, e1 = rel(out["0"][0], rm), rel(out["1"][0], rm)
+        say(f"[gpu] split products hd {hd} split={mode}")
+        with A._lib.options(split=int(mode)):
+            out[mode] = check_against_oracle(device, f"split={mode} hd {hd}", tk.off, tk.cf_seq, qkv, dm, 2, hd)
+    e0, e1 = row_err(out["0"][0], rm), row_err(out["1"][0], rm)
     say(f"    merged error: fp32 products {e0:.2e}, split {e1:.2e}")
     assert e1 <= max(4 * e0, 1e-6)
     if hd == 32:  # the split kernels are the ones taken there: their rounding differs
@@ -194,18 +191,16 @@ def test_split_products_as_accurate_as_fp32(device, hd, monkeypatch):
 @pytest.mark.parametrize("hd", [32, 64])
 @pytest.mark.parametrize("vlds,nbuf", [(1, 2), (1, 1), (2, 2), (2, 1)])
 @pytest.mark.parametrize("split", ["1", "0"])
-def test_backward_layouts(device, hd, vlds, nbuf, split, monkeypatch):
-    # Every LDS layout of the backward, forced (PET_ATTN_BWD_VLDS: 1 V staged,
-    # 2 from global memory; PET_ATTN_BWD_NBUF: tile buffers), with the split
+def test_backward_layouts(device, hd, vlds, nbuf, split):
+    # Every LDS layout of the backward, forced (option bwd_vlds: 1 V staged,
+    # 2 from global memory; bwd_nbuf: tile buffers), with the split
     # dP (V staged split, head_dim 32) and without: the pipelined two-buffer
     # step loop and the two-barrier one-buffer loop, on ragged atoms.
-    monkeypatch.setenv("PET_ATTN_BWD_VLDS", str(vlds))
-    monkeypatch.setenv("PET_ATTN_BWD_NBUF", str(nbuf))
-    monkeypatch.setenv("PET_ATTN_SPLIT", split)
     counts = [0, 15, 16, 31, 47, 5, 60, 33, 70]
     tk, qkv, dm = random_case(counts, 2, hd, seed=200 + hd + 10 * vlds + nbuf, cf_kind="random")
-    check_against_oracle(device, f"backward layout vlds {vlds} nbuf {nbuf} split {split} hd {hd}", tk.off,
-                         tk.cf_seq, qkv, dm, 2, hd)
+    with A._lib.options(bwd_vlds=vlds, bwd_nbuf=nbuf, split=int(split)):
+        check_against_oracle(device, f"backward layout vlds {vlds} nbuf {nbuf} split {split} hd {hd}", tk.off,
+                             tk.cf_seq, qkv, dm, 2, hd)
 
 
 def test_cf_adjoint_accumulates(device):
@@ -244,9 +239,9 @@ def test_strided_views_and_stream(device):
     torch.cuda.synchronize()
     rm, rml = oracle.attn_fwd(qkv, tk.off, tk.cf_seq, 2, 32)
     rqa, rca, _ = oracle.attn_bwd(qkv, tk.off, dm, rm, rml, tk.cf_seq, 2, 32)
-    assert rel(m.cpu().numpy(), rm) <= RTOL
-    assert rel(qa.cpu().numpy(), rqa) <= RTOL
-    assert rel(ca.cpu().numpy(), rca) <= RTOL
+    assert row_err(m.cpu().numpy(), rm) <= RTOL
+    assert row_err(qa.cpu().numpy(), rqa) <= RTOL
+    assert row_err(ca.cpu().numpy(), rca) <= RTOL
     assert torch.all(mbig[:, D:] == 7.0) and torch.all(qabig[:, 3 * D:] == 7.0)
 
 
@@ -278,8 +273,8 @@ def test_op_level_attention(device, beta, cfg):
     rout, rm, rml = oracle.attention(inp["qkv"], tk.off, tk.cf_seq, inp["w_out"], inp["b_out"], H, hd, temp)
     rin, rca = oracle.attention_bwd(inp["out_adj"], inp["qkv"], tk.off, tk.cf_seq, inp["w_in"], inp["w_out"], rm, rml,
                                     H, hd, temp, cf_seq_adj=cf_adj0, in_adj=in_adj0, beta=beta)
-    e = dict(out=rel(out.cpu().numpy(), rout), in_adj=rel(in_adj.cpu().numpy(), rin),
-             cf_seq_adj=rel(cf_adj.cpu().numpy(), rca))
+    e = dict(out=row_err(out.cpu().numpy(), rout), in_adj=row_err(in_adj.cpu().numpy(), rin),
+             cf_seq_adj=row_err(cf_adj.cpu().numpy(), rca))
     say("    ", {k: f"{v:.2e}" for k, v in e.items()})
     for k, v in e.items():
         assert v <= RTOL, k

@@ -15,6 +15,8 @@ import pytest
 import torch
 
 import oracle
+from parity import row_err
+from pet_kokkos_amd import _lib
 from pet_kokkos_amd import attention as A
 from pet_kokkos_amd import systems
 
@@ -31,11 +33,17 @@ def run_rows(N, n0, n1, e0, e1):
     return torch.cat([torch.arange(n0, n1), torch.arange(N + e0, N + e1)])
 
 
-@pytest.mark.parametrize("cfg,chunk", [("c1", 37), ("c1", 300), ("c2", 500), ("c4", 4000)])
-def test_runs_bit_identical(device, cfg, chunk):
+@pytest.mark.parametrize("cfg,chunk,stream", [("c1", 37, 0), ("c1", 300, 0), ("c2", 500, 0), ("c4", 4000, 0),
+                                              ("c1", 37, 1), ("c4", 4000, 1)])
+def test_runs_bit_identical(device, cfg, chunk, stream):
+    with _lib.options(attn_stream=stream):
+        _runs_bit_identical(device, cfg, chunk, stream)
+
+
+def _runs_bit_identical(device, cfg, chunk, stream):
     conf, tk = systems.config_tokens(cfg)
     H, hd, D = conf.heads, conf.head_dim, conf.d_model
-    print(f"[gpu] runs {cfg} chunk {chunk}", flush=True)
+    print(f"[gpu] runs {cfg} chunk {chunk} streaming kernels {stream}", flush=True)
     inp = systems.attention_inputs(tk, D, H, seed=4)
     rng = np.random.default_rng(5)
     q = torch.from_numpy(inp["qkv"]).to(device)
@@ -125,6 +133,6 @@ def test_op_level_chunked(device, beta, dead, chunk):
     rout, rm, rml = oracle.attention(qkv_h, tk.off, tk.cf_seq, inp["w_out"], inp["b_out"], H, hd, temp, dead=dead)
     rin, rca = oracle.attention_bwd(out_adj_h, qkv_h, tk.off, tk.cf_seq, inp["w_in"], inp["w_out"], rm, rml, H, hd,
                                     temp, cf_seq_adj=cf_adj0, in_adj=in_adj0, beta=beta, dead=dead)
-    assert rel(o2, rout) <= RTOL and rel(i2, rin) <= RTOL and rel(ca2.cpu().numpy(), rca) <= RTOL
+    assert row_err(o2, rout) <= RTOL and row_err(i2, rin) <= RTOL and row_err(ca2.cpu().numpy(), rca) <= RTOL
     if dead:
         assert np.array_equal(i2[tk.n_rows:], (beta * in_adj0[tk.n_rows:]).astype(np.float32))

@@ -98,7 +98,7 @@ def test_cpp_layer_and_forces_api(tmp_path):
     rf, rv = oracle.fold(N, pk.off, pk.reverse, pk.vec, rg, scale=-1.0)
     assert rel(rd("forces.f64", np.float64, (N, 3)), rf) <= RTOL
     assert rel(rd("vir9.f64", np.float64, (9,)), rv.sum(axis=0)) <= RTOL
-    assert (tmp_path / "graph.ok").exists(), "pet::GraphCache: a captured or replayed run differed from the eager one"
+    assert (tmp_path / "graph.ok").exists(), "pet::StepRecorder: a recorded or replayed run differed from the eager one"
 
 
 @pytest.mark.parametrize("name", ["tiny", "tiny-residual"])

@@ -1,5 +1,5 @@
-"""The path recorded as HIP graphs and replayed (pet_kokkos_amd.graph, the
-role of the reference's GraphCache, include/pet/graph.hpp): every replay gives
+"""The path recorded as HIP graphs and replayed (pet_kokkos_amd.replay, the
+role of the reference's graph cache, include/pet/graph.hpp): every replay gives
 the eager run's bits, with the program's own eager work and synchronisations
 between the replays; the core kernels, the op level with rocBLAS's GEMMs, the
 layer level with the token norm, and the forces' edge term and fold."""
@@ -11,7 +11,7 @@ import torch
 
 from pet_kokkos_amd import attention as A
 from pet_kokkos_amd import forces as F
-from pet_kokkos_amd import graph as G
+from pet_kokkos_amd import replay as G
 from pet_kokkos_amd import layer as L
 from pet_kokkos_amd import systems
 
@@ -72,19 +72,32 @@ def test_graph_replays_are_bit_identical(device):
         return [x.clone() for x in (merged, ml, qa, cfh, out, in_adj, tadj, csa, *res)]
 
     eager = snapshot(work())
-    cache = G.GraphCache()
+    cache = G.StepRecorder()
     key = ("c1", T, D)
-    first = snapshot(cache.run(key, work))  # first sight: eager
+    first = snapshot(cache.launch(key, work))  # warming: eager
     for a, b in zip(eager, first):
         assert torch.equal(a, b)
     for rep in range(4):
-        res = cache.run(key, work)  # captured on the second call, replayed after
+        res = cache.launch(key, work)  # recorded on the second call, replayed after
         got = snapshot(res)
-        assert not cache.broken
+        assert cache.counters.refusals == 0
         for a, b in zip(eager, got):
             assert torch.equal(a, b), f"replay {rep} differs"
         # the program's own eager work between replays
         scratch = torch.randn((T, D), device=device)
         L.norm_rows(scratch, scratch, t["nw"], None)
         torch.cuda.synchronize()
-    assert len(cache._graphs) == 1
+    n = cache.counters
+    assert cache.live == 1 and n.records == 1 and n.eager == 1 and n.launches == 4, n
+
+
+def test_recorder_bounds(device):
+    # past max_live the least recently replayed graph is dropped
+    x = torch.zeros(1024, device=device)
+    cache = G.StepRecorder(warm_runs=0, max_live=2)
+    for k in (1, 2, 1, 3, 1):
+        out = cache.launch(("add", k), lambda k=k: x.add(k))
+        torch.cuda.synchronize()
+        assert torch.all(out == k)
+    n = cache.counters
+    assert n.records == 3 and n.evictions == 1 and cache.live == 2 and n.launches == 5, n

@@ -89,6 +89,60 @@ def test_rejects(device):
         linear_fused(A, W, C)  # K not a multiple of 16
     with pytest.raises(_lib.PetAttnError):
         linear_fused(torch.zeros(8, 0, device=device), torch.zeros(8, 0, device=device), C)  # K = 0
+    A, W = torch.zeros(8, 32, device=device), torch.zeros(8, 32, device=device)
+    with pytest.raises(ValueError):
+        linear_fused(A, W, torch.zeros(7, 8, device=device))  # C too short
+    with pytest.raises(ValueError):
+        linear_fused(A, W, torch.zeros(8, 4, device=device))  # C too narrow
+    with pytest.raises(ValueError):
+        linear_fused(A, W, torch.zeros(8, 8, device=device, dtype=torch.float64))  # not float32
+    with pytest.raises(ValueError):
+        linear_fused(A.double(), W, C)
+    with pytest.raises(ValueError):
+        linear_fused(A, W, torch.zeros(8, 16, device=device)[:, ::2])  # strided columns
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, bias=torch.zeros(7, device=device))  # bias too short
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, row_scale=torch.zeros(3, device=device))
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, pre=torch.zeros(8, 7, device=device), act=1)
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, cin=torch.zeros(4, 8, device=device), beta=1.0)
+    with pytest.raises(ValueError):
+        linear_fused(A, W.cpu(), C)  # not on the device
+    with pytest.raises(ValueError):
+        linear_fused(A, torch.zeros(7, 32, device=device), torch.zeros(8, 4, device=device), act=2)  # odd SwiGLU rows
+    with pytest.raises(ValueError):
+        split_weights(torch.zeros(8, 32, device=device, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
+def test_rows_past_a_2d_grid(split, device):
+    # more 64-row tiles than a grid's y extent (65535) holds: both kernels run
+    # a 1-D grid of tiles
+    M, N, K = 65535 * 64 + 100, 16, 32
+    print(f"[gpu] linear M={M} N={N} K={K} split={split}", flush=True)
+    g = torch.Generator(device=device).manual_seed(21)
+    A = torch.randn(M, K, device=device, generator=g)
+    W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
+    C = torch.empty(M, N, device=device)
+    linear_fused(A, W, C, split=split)
+    ref = A.double() @ W.double().T
+    err = (C.double() - ref).abs().max().item()
+    assert err <= 1e-5 * ref.abs().max().item()
+    assert (C[-1].double() - ref[-1]).abs().max().item() <= 1e-5 * ref.abs().max().item()
+
+
+def test_split_weights_transposed_exact(device):
+    # the layer backward's split of W^T (pet_gemm_split_weights, transposed)
+    # holds the same bytes as the plain split of W^T made contiguous
+    N, K = 96, 64
+    g = torch.Generator(device=device).manual_seed(4)
+    W = torch.randn(K, N, device=device, generator=g) * torch.logspace(-10, 10, N, device=device)
+    a = L.SplitWeights(W, transposed=True).data  # [N, K] split rows of W^T
+    b = split_weights(W.t().contiguous()).data
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
 
 
 def test_split_weights_exact(device):

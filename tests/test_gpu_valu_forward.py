@@ -1,43 +1,37 @@
-"""The vector-ALU forward (attn_fwd_valu_kernel, selected by PET_ATTN_FWD=3,
-kept to compare the matrix-core kernel against) checked against the oracle in
-a process of its own, since the kernel choice is read once per process."""
+"""The vector-ALU forward (attn_fwd_valu_kernel, selected by the option
+fwd_kernel = 3, kept to compare the matrix-core kernel against) checked
+against the oracle element-wise (tests/parity.py's row-floor rule)."""
 from __future__ import annotations
 
-import os
-import subprocess
-import sys
-
+import numpy as np
 import pytest
+import torch
+
+import oracle
+from parity import RTOL, row_err
+from pet_kokkos_amd import _lib
+from pet_kokkos_amd import attention as A
+from pet_kokkos_amd import systems
 
 pytestmark = pytest.mark.gpu
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
-SCRIPT = r"""
-import numpy as np, torch, oracle
-from pet_kokkos_amd import attention as A, systems
-dev = torch.device("cuda", 0)
-for cfg in ("c1", "c4"):
+@pytest.mark.parametrize("cfg", ["c1", "c4"])
+def test_valu_forward_matches_oracle(device, cfg):
+    print(f"[gpu] vector-ALU forward (fwd_kernel=3) {cfg}", flush=True)
     conf, tk = systems.config_tokens(cfg)
     H, hd = conf.heads, conf.head_dim
     qkv = systems.attention_inputs(tk, conf.d_model, H, seed=2)["qkv"]
-    merged, ml = A.attn_fwd(torch.from_numpy(qkv).to(dev), torch.from_numpy(tk.off).to(dev),
-                            torch.from_numpy(tk.cf_seq).to(dev), H, hd)
-    torch.cuda.synchronize()
+    with _lib.options(fwd_kernel=3):
+        merged, ml = A.attn_fwd(torch.from_numpy(qkv).to(device), torch.from_numpy(tk.off).to(device),
+                                torch.from_numpy(tk.cf_seq).to(device), H, hd)
+        torch.cuda.synchronize()
     rm, rml = oracle.attn_fwd(qkv, tk.off, tk.cf_seq, H, hd)
-    em = np.abs(merged.cpu().numpy() - rm).max() / np.abs(rm).max()
+    ml = ml.cpu().numpy()
     live = rml[:, 1] > 0
-    el = np.abs(ml.cpu().numpy()[live] - rml[live]).max() / np.abs(rml[live]).max()
-    assert np.array_equal(ml.cpu().numpy()[~live], rml[~live]), cfg
-    print(cfg, em, el, flush=True)
-    assert em <= 1e-5 and el <= 1e-5, cfg
-print("ok")
-"""
-
-
-def test_valu_forward_matches_oracle():
-    print("[gpu] vector-ALU forward (PET_ATTN_FWD=3) c1, c4", flush=True)
-    env = dict(os.environ, PET_ATTN_FWD="3", PYTHONPATH=ROOT)
-    res = subprocess.run([sys.executable, "-c", SCRIPT], env=env, cwd=ROOT, capture_output=True, text=True,
-                         timeout=240)
-    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stdout + res.stderr
+    assert np.array_equal(ml[~live], rml[~live])
+    em = row_err(merged.cpu().numpy(), rm)
+    el = row_err(np.where(live[:, None], ml, 0).reshape(-1, 2 * tk.slots),
+                 np.where(live[:, None], rml, 0).reshape(-1, 2 * tk.slots))
+    print(f"    merged {em:.2e}, ml {el:.2e}", flush=True)
+    assert em <= RTOL and el <= RTOL

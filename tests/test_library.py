@@ -44,10 +44,13 @@ def test_scale_matches_reference_rounding():
 
 def test_error_codes_without_device():
     lib = _lib.load()
-    sh = _lib.Shape(4, 20, 8, 2, 24, 0, 0.2)  # head_dim 24: not held
-    assert lib.pet_attn_fwd(ctypes.byref(sh), 16, 96, 16, 16, 8, 16, 48, None, None) == _lib.EHEADDIM
-    sh = _lib.Shape(4, 20, 300, 2, 32, 0, 0.2)  # too many slots
-    assert lib.pet_attn_fwd(ctypes.byref(sh), 16, 192, 16, 16, 300, 16, 64, None, None) == _lib.ESLOTS
+    for hd in (0, 129):  # head_dim outside 1..128 (the reference's kMaxHeadDim)
+        sh = _lib.Shape(4, 20, 8, 2, hd, 0, 0.2)
+        assert lib.pet_attn_fwd(ctypes.byref(sh), 16, 6 * max(hd, 1), 16, 16, 8, 16, 48, None, None) == _lib.EHEADDIM
+    sh = _lib.Shape(4, 20, 8, 2, 24, 0, 0.2)  # head_dim 24 (the streaming kernels): its own checks apply
+    assert lib.pet_attn_fwd(ctypes.byref(sh), 16, 100, 16, 16, 8, 16, 48, None, None) == _lib.EINVAL  # ldq < 3D
+    sh = _lib.Shape(4, 20, 8, 2, 10, 0, 0.2)  # head_dim 10: 4-byte alignment suffices, 2 bytes does not
+    assert lib.pet_attn_fwd(ctypes.byref(sh), 18, 60, 16, 16, 8, 16, 20, None, None) == _lib.EALIGN
     sh = _lib.Shape(4, 20, 8, 2, 32, 0, 0.2)
     assert lib.pet_attn_fwd(ctypes.byref(sh), None, 192, 16, 16, 8, 16, 64, None, None) == _lib.EINVAL
     assert lib.pet_attn_fwd(ctypes.byref(sh), 16, 100, 16, 16, 8, 16, 64, None, None) == _lib.EINVAL  # ldq < 3D
@@ -97,7 +100,7 @@ def test_model_create_rejects_before_the_device():
     assert _model_create(w, featurizer=1)[0] == _lib.EINVAL  # the residual family needs d_node == d_pet
     assert _model_create(w, featurizer=2)[0] == _lib.EINVAL
     assert _model_create(w, num_heads=3)[0] == _lib.EINVAL  # d_pet not a multiple of the heads
-    assert _model_create(w, num_heads=8)[0] == _lib.EHEADDIM  # head_dim 8
+    assert _model_create(w, d_pet=258, num_heads=2)[0] == _lib.EHEADDIM  # head_dim 129
     assert "missing" in _lib.strerror(20)
     lib = _lib.load()
     assert lib.pet_model_compute(None, None, 1, None, None, None, None, None, None) == _lib.EINVAL
