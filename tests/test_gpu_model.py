@@ -14,17 +14,19 @@ rounding of the network itself is below it. The oracle run in float32 (a
 second fp32 restatement of the same pass) measures that rounding on each case;
 the tests assert, against the float64 oracle,
 
-    |E_gpu - E_64| <= max(1e-7 |E_64|, 2 |E_32 - E_64|, L1)
+    |E_gpu - E_64| <= max(1e-7 |E_64|, 2 |E_32 - E_64|, 2 L1)
     max|F_gpu - F_64| <= max(1e-5 eV/A,  2 max|F_32 - F_64|)
     per-atom energies, edge gradients, virial: the forces' rule, each with its
     north-star-sized floor (1e-7 of the largest |value|, 1e-5 for forces-like),
 
-L1 = sum_atoms d_a, d_a the float32 oracle's per-atom deviation (at least an
-fp32 ulp of the term): the energy error of an fp32 evaluation whose per-atom
+L1 = sum_atoms d_a, d_a the float32 oracle's per-atom deviation (at least 4
+fp32 ulps of the term): the energy error of an fp32 evaluation whose per-atom
 roundings align, as the float32 oracle's mostly do (its total error is one
 draw of that, at times far below it). That is the north-star bar, or the
 error an fp32 restatement of the reference makes on the same structure where
-fp32 itself cannot meet it. Measured on
+fp32 itself cannot meet it. On C2's water-648 the tests also assert fixed bars
+that the float32 oracle meets as well: energy 5e-7 relative, forces 5e-5
+eV/A. Measured on
 MI355X, C2 water-648: energy 1.2e-7 relative (float32 oracle 3.3e-7), forces
 3.3e-5 eV/A (float32 oracle 2.6e-5); residual family 4.1e-7 (4.2e-7) and
 1.3e-5 (1.7e-5) eV/A. Runs repeat bit for bit.
@@ -78,15 +80,16 @@ def compare(got, ref):
         err = np.abs(g[k] - ref[k])
         e32 = np.abs(r32[k] - ref[k])
         if k == "energy":  # per structure
-            # L1: the structure's per-atom fp32 deviations (each at least an
-            # fp32 ulp of the term) summed with one sign -- the energy error of
-            # an fp32 evaluation whose per-atom roundings align, as the float32
-            # oracle's mostly do (its total error is a single draw of that)
+            # L1: the structure's per-atom fp32 deviations (each at least 4
+            # fp32 ulps of the term: its last layers' roundings) summed with
+            # one sign -- the energy error of an fp32 evaluation whose
+            # per-atom roundings align, as the float32 oracle's mostly do
+            # (its total error is a single draw of that)
             soff = ref["soff"]
             d = np.maximum(np.abs(r32["per_atom"] - ref["per_atom"]),
-                           np.spacing(np.abs(ref["per_atom"]).astype(np.float32)).astype(np.float64))
+                           4 * np.spacing(np.abs(ref["per_atom"]).astype(np.float32)).astype(np.float64))
             l1 = np.array([d[a:b].sum() for a, b in zip(soff[:-1], soff[1:])])
-            bar = np.maximum(np.maximum(FLOORS[k](ref[k]), FP32_FACTOR * e32), l1)
+            bar = np.maximum(np.maximum(FLOORS[k](ref[k]), FP32_FACTOR * e32), FP32_FACTOR * l1)
             print(f"[model] energy: rel err {np.max(err / np.abs(ref[k])):.2e} (float32 oracle "
                   f"{np.max(e32 / np.abs(ref[k])):.2e})", flush=True)
             print(f"[model] energy: abs err {err.max():.2e} against a bar of {bar.min():.2e}..{bar.max():.2e}", flush=True)
@@ -198,7 +201,16 @@ def test_c2_model_water_648(name, device):
     x = structures_input(h, [systems.water_box(6, 18.6, seed=0)], device)
     got = m.compute(x, forces=True)
     torch.cuda.synchronize()
-    compare(got, oracle_of(h, w, comp, x))
+    ref = oracle_of(h, w, comp, x)
+    compare(got, ref)
+    # fixed bars, met by the float32 restatement too (so they are fp32's, not
+    # this library's): energy 5e-7 relative, forces 5e-5 eV/A
+    for name_, e, f in (("gpu", float(got["energy"][0]), got["forces"].cpu().numpy()),
+                        ("float32 oracle", ref["fp32"]["energy"][0], ref["fp32"]["forces"])):
+        de = abs(e - ref["energy"][0]) / abs(ref["energy"][0])
+        df = np.abs(f - ref["forces"]).max()
+        print(f"[model] {name}: {name_} energy {de:.2e} relative, forces {df:.2e} eV/A", flush=True)
+        assert de <= 5e-7 and df <= 5e-5, name_
 
 
 def test_calculator(device):
