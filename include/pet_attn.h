@@ -52,7 +52,8 @@ enum {
   PET_ATTN_ELAUNCH = 5,     /* a HIP launch or runtime call failed */
   PET_ATTN_EBLAS = 6,       /* the BLAS call of a linear failed */
   PET_ATTN_EWORKSPACE = 7,  /* the workspace is smaller than pet_attention_bwd_workspace() */
-  PET_ATTN_EINDEX = 8       /* a row index or element offset that does not fit 2^31 */
+  PET_ATTN_EINDEX = 8,      /* a row index or element offset that does not fit 2^31 */
+  PET_ATTN_ESCRATCH = 9     /* a size above pet_attn_bwd_noalloc's fixed scratch */
 };
 
 /* The most tokens an atom may have in the LDS-staged kernels (16 waves of 16
@@ -133,6 +134,24 @@ PET_ATTN_API int pet_attn_bwd(const pet_attn_shape* shape, const float* qkv, int
                  const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
                  const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh,
                  float* cf_seq_adj, int64_t ldca, void* stream);
+
+/* pet_attn_bwd for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * same kernels and the same results bit for bit, with no cfh argument -- its
+ * N * H * S floats of scratch live in a fixed device array of
+ * PET_ATTN_NOALLOC_MAX_SCRATCH bytes that the library holds on every GPU it
+ * runs on until the process ends. Calls with N * heads * slots * 4 above that
+ * size return PET_ATTN_ESCRATCH and launch nothing. The call allocates
+ * nothing and calls no allocating routine. All calls on one GPU share its
+ * array, so calls that overlap on one GPU (on different streams, or from
+ * several threads) race: order them on one stream. No counterpart in the
+ * reference, whose backward takes its scratch from the Workspace pool
+ * (src/attention.cpp:1814-1907). */
+#define PET_ATTN_NOALLOC_MAX_SCRATCH (32u << 20)
+PET_ATTN_API int pet_attn_bwd_noalloc(const pet_attn_shape* shape, const float* qkv, int64_t ldq, const int* off,
+                                      const float* dmerged, int64_t ldg, const float* merged, int64_t ldm,
+                                      const float* ml, const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda,
+                                      float* cf_seq_adj, int64_t ldca, void* stream);
 
 /* ---- runs of atoms: the kernels of attention_chunked / _bwd_chunked ------ */
 

@@ -22,6 +22,7 @@ EXPORTS = (
     "pet_attn_zero_dead",
     "pet_attn_fwd",
     "pet_attn_bwd",
+    "pet_attn_bwd_noalloc",
     "pet_attn_fwd_xf",
     "pet_attn_bwd_xf",
     "pet_attention",
@@ -50,7 +51,8 @@ EXPORTS = (
     "pet_linear_fused_split",
 )
 
-OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX = range(9)
+OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX, ESCRATCH = range(10)
+NOALLOC_MAX_SCRATCH = 32 << 20  # bytes (PET_ATTN_NOALLOC_MAX_SCRATCH)
 MAX_SLOTS = 256
 
 
@@ -123,6 +125,8 @@ def load() -> ctypes.CDLL:
     lib.pet_attn_fwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
     lib.pet_attn_bwd.restype = ctypes.c_int
     lib.pet_attn_bwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P]
+    lib.pet_attn_bwd_noalloc.restype = ctypes.c_int
+    lib.pet_attn_bwd_noalloc.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _P]
     lib.pet_attn_fwd_run.restype = ctypes.c_int
     lib.pet_attn_fwd_xf.restype = ctypes.c_int
     lib.pet_attn_fwd_xf.argtypes = [sp, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _P]

@@ -912,6 +912,8 @@ const char* pet_attn_strerror(int code) {
     case PET_ATTN_EBLAS: return "the BLAS call of a linear failed";
     case PET_ATTN_EWORKSPACE: return "workspace smaller than the matching *_workspace() size";
     case PET_ATTN_EINDEX: return "an index does not fit 2^31";
+    case PET_ATTN_ESCRATCH:
+      return "N * heads * slots is above pet_attn_bwd_noalloc's scratch (PET_ATTN_NOALLOC_MAX_SCRATCH bytes)";
     case 20: return "a tensor the model's architecture needs is missing";
     case 21: return "a tensor's shape disagrees with the model's hyperparameters";
     case 22: return "a device allocation failed";
@@ -1057,6 +1059,59 @@ int pet_attn_fwd(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const 
 int pet_attn_bwd(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int* off, const float* dmerged,
                  int64_t ldg, const float* merged, int64_t ldm, const float* ml, const float* cf_seq, int64_t ldc,
                  float* qkv_adj, int64_t lda, float* cfh, float* cf_seq_adj, int64_t ldca, void* stream) {
+  return bwd_whole(sh, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, cf_seq_adj, ldca,
+                   QkvXf{}, stream);
+}
+
+}  // extern "C"
+
+// ---- the allocation-free backward ---------------------------------------------
+// pet_attn_bwd_noalloc's cfh scratch: a file-scope device array, one per GPU
+// the library runs on, held until the process ends. Host code never uses the
+// array's name as an address (on the host it is a stand-in symbol): each
+// device's address is looked up once, with that device current, by
+// hipGetSymbolAddress, and kept here.
+namespace pet_attn {
+constexpr int64_t kScratchFloats = PET_ATTN_NOALLOC_MAX_SCRATCH / sizeof(float);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's scratch address (null if it cannot be found).
+float* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch[dev].load(std::memory_order_relaxed);
+  if (p) return p;
+  void* addr = nullptr;
+  if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) {
+    (void) hipGetLastError();
+    return nullptr;
+  }
+  p = static_cast<float*>(addr);
+  g_scratch[dev].store(p, std::memory_order_release);
+  return p;
+}
+}  // namespace pet_attn
+
+extern "C" {
+
+int pet_attn_bwd_noalloc(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int* off,
+                         const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
+                         const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cf_seq_adj,
+                         int64_t ldca, void* stream) {
+  if (int e = check_shape(sh)) return e;
+  // cfh [N, H, S] in the scratch array: every element the backward writes,
+  // nothing read before it is written, so nothing needs clearing
+  if (int64_t(sh->n_atoms) * sh->heads * sh->slots > kScratchFloats) return PET_ATTN_ESCRATCH;
+  if (sh->n_atoms == 0) return PET_ATTN_OK;
+  float* cfh = scratch_ptr();
+  if (!cfh) return PET_ATTN_ELAUNCH;
   return bwd_whole(sh, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, cf_seq_adj, ldca,
                    QkvXf{}, stream);
 }
