@@ -155,3 +155,19 @@ def test_fp32_close_to_fp64(name):
     pa32, eg32 = om.evaluate(H, w, sp, pk, dtype=torch.float32)
     assert abs(pa32.sum() - pa64.sum()) < 1e-5 * abs(pa64.sum())
     assert np.abs(eg32 - eg64).max() < 1e-4 * np.abs(eg64).max()
+
+
+def test_oracle_reduces_to_the_closed_form():
+    """The oracle's composition where the mathematics fixes it: a PET with
+    every block's output layers zeroed (tests/reduced_pet.py) has a closed-form
+    energy -- species-embedding node features, edge features summed over the
+    layers' compress maps, the readout of both."""
+    from pet_kokkos_amd.model import structures_input
+    from reduced_pet import closed_form_energy, reduced_weights
+    h = weights.MODELS["tiny"]
+    w = reduced_weights(h, 31)
+    comp = weights.random_composition(h)
+    for s in (systems.water_box(2, 6.2, seed=3), systems.diamond(1, jitter=0.05, seed=4)):
+        x = structures_input(h, [s], "cpu")
+        pa, _ = om.evaluate(h, w, x.species.numpy(), x.host, comp, grad=False)
+        assert np.abs(pa - closed_form_energy(h, w, comp, s)).max() < 1e-10
