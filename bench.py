@@ -32,7 +32,26 @@ sys.path.insert(0, ROOT)
 
 METRIC = "µs per attention fwd+bwd and ms per E+F eval (1 GPU), % of HBM/MFMA roofline"
 PEAK_FP32_MFMA = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
+PEAK_BF16_MFMA = 2.5e15  # FLOP/s, MI355X dense bf16 matrix
+# an fp32 product as six bf16 products (the split-fp32 scheme): fp32 FLOP/s
+PEAK_SPLIT_FP32 = PEAK_BF16_MFMA / 6
 PEAK_HBM = 8.0e12  # B/s
+
+
+def mixed_seconds(flops, split_share):
+    """Time at the matrix-core ceilings of the instructions that run: the
+    split_share of the FLOPs as split-fp32 products on the bf16 matrix cores
+    (2.5 PFLOP/s / 6), the rest on the fp32 matrix cores (157.3 TFLOP/s)."""
+    return flops * ((1.0 - split_share) / PEAK_FP32_MFMA + split_share / PEAK_SPLIT_FP32)
+
+
+def split_shares(plan):
+    """Shares of the forward's and the backward's FLOPs that run as split
+    products: the forward's scores are half its FLOPs (scores, PV), the
+    backward's dP a fifth (scores, dP, dQ, dK, dV)."""
+    if plan.get("streaming"):
+        return 0.0, 0.0
+    return 0.5 * plan["fwd_split_scores"], 0.2 * plan["bwd_split_dp"]
 
 
 def algorithmic(tk, D, H):
@@ -126,6 +145,7 @@ def other_configs(device, reps):
     with their fraction of the same roofline."""
     import torch
 
+    from pet_kokkos_amd import _lib
     from pet_kokkos_amd import attention as A
     from pet_kokkos_amd import systems
 
@@ -148,10 +168,12 @@ def other_configs(device, reps):
         f_us = _timed(lambda: A.attn_fwd(qkv, off, cf, H, hd, merged=merged, ml=ml), reps)
         b_us = _timed(lambda: A.attn_bwd(qkv, off, dm, merged, ml, cf, H, hd, cf_seq_adj=ca, qkv_adj=qa, cfh=cfh), reps)
         alg = algorithmic(tk, D, H)
-        bound = max((alg["fwd_flops"] + alg["bwd_flops"]) / PEAK_FP32_MFMA,
+        plan = _lib.describe(N, T, S, H, hd)
+        fsh, bsh = split_shares(plan)
+        bound = max(mixed_seconds(alg["fwd_flops"], fsh) + mixed_seconds(alg["bwd_flops"], bsh),
                     (alg["fwd_bytes"] + alg["bwd_bytes"]) / PEAK_HBM) * 1e6
         res[name] = dict(workload=conf.name, atoms=N, tokens=T, head_dim=hd, fwd_us=f_us, bwd_us=b_us,
-                         bound_us=bound, frac_of_roofline=bound / (f_us + b_us))
+                         bound_us=bound, frac_of_roofline=bound / (f_us + b_us), kernel_plan=plan)
         del qkv, dm, merged, ml, qa, cfh, ca
         torch.cuda.empty_cache()
     return res
@@ -180,13 +202,17 @@ def time_ef(device, reps, cpu: bool):
         cnt = np.diff(x.host.off).astype(np.float64) + 1
         fl = ef_flops(h, x.n_atoms, x.n_edges, float((cnt * cnt).sum()))
         n = max(3, reps // (5 if name != "c5" else 20))
+        # contraction bound at the ceilings of the instructions that run: the
+        # large dense products as split-fp32 on the bf16 matrix cores, the rest
+        # (small products, the attention at head_dim 64) on the fp32 ones
+        bound_ms = mixed_seconds(fl["forces"], fl["split"] / fl["forces"]) * 1e3
         o = m.compute(x, True)
         e_ms = _timed(lambda: m.compute(x, False, out=o), n) / 1e3
         ef_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
         res[name] = dict(featurizer=h.featurizer, structures=len(sts), atoms=x.n_atoms, edges=x.n_edges,
                          d_pet=h.d_pet, heads=h.num_heads, ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
-                         ef_bound_ms=fl["forces"] / PEAK_FP32_MFMA * 1e3,
-                         ef_frac_of_roofline=fl["forces"] / PEAK_FP32_MFMA * 1e3 / ef_ms,
+                         ef_bound_ms=bound_ms, ef_frac_of_roofline=bound_ms / ef_ms,
+                         ef_split_share=fl["split"] / fl["forces"],
                          workspace_gb=m.workspace_bytes / 1e9)
         if name in ("c2", "c2-residual") and cpu:
             cpu_cases.append((name, h, w, comp, x.species.cpu().numpy(), x.host))
@@ -215,6 +241,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup-s", type=float, default=2.0, help="warm up for at least this many seconds")
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-op-level", action="store_true", help="skip the op-level (with linears) timing")
@@ -231,6 +258,7 @@ def main():
     import numpy as np
     import torch
 
+    from pet_kokkos_amd import _lib
     from pet_kokkos_amd import attention as A
     from pet_kokkos_amd import systems
 
@@ -265,9 +293,16 @@ def main():
         if ev:
             ev[2].record()
 
+    # W warmup steps, then more until --warmup-s seconds have passed (the
+    # clocks settle; a short warmup left the first timed steps slower)
+    w0 = time.perf_counter()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    while time.perf_counter() - w0 < args.warmup_s:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -284,14 +319,20 @@ def main():
     us_per_step = total_ms * 1e3 / args.steps
     alg = algorithmic(tk, D, H)
     fwd_avg, bwd_avg = statistics.fmean(fwd_us), statistics.fmean(bwd_us)
-    core_flops = alg["fwd_flops"] + alg["bwd_flops"]
+    plan = _lib.describe(N, T, S, H, hd)
+    fsh, bsh = split_shares(plan)
     core_bytes = alg["fwd_bytes"] + alg["bwd_bytes"]
-    bound_us = max(core_flops / PEAK_FP32_MFMA, core_bytes / PEAK_HBM) * 1e6
-    bwd_mfma_bound = alg["bwd_flops"] / PEAK_FP32_MFMA >= alg["bwd_bytes"] / PEAK_HBM
-    if bwd_mfma_bound:
+    # the core's bound at the ceilings of the instructions that run
+    core_mfma_s = mixed_seconds(alg["fwd_flops"], fsh) + mixed_seconds(alg["bwd_flops"], bsh)
+    bound_us = max(core_mfma_s, core_bytes / PEAK_HBM) * 1e6
+    bwd_mfma_s = mixed_seconds(alg["bwd_flops"], bsh)
+    if bwd_mfma_s >= alg["bwd_bytes"] / PEAK_HBM:
+        peak = alg["bwd_flops"] / bwd_mfma_s  # fp32-equivalent FLOP/s of the instruction mix
         achieved = alg["bwd_flops"] / (bwd_avg * 1e-6) / 1e12
         roof = dict(kernel=f"attn_bwd_kernel<{hd}, 512> (+ attn_cf_adjoint_kernel)", bound="mfma", achieved=achieved,
-                    peak=PEAK_FP32_MFMA / 1e12, unit="TFLOP/s", frac=achieved / (PEAK_FP32_MFMA / 1e12))
+                    peak=peak / 1e12, unit="TFLOP/s", frac=achieved / (peak / 1e12),
+                    ceiling=f"fp32 matrix peak 157.3 TFLOP/s for {100 * (1 - bsh):.0f}% of the FLOPs, split-fp32 on "
+                            f"the bf16 matrix cores (2.5 PFLOP/s / 6) for {100 * bsh:.0f}%")
     else:
         achieved = alg["bwd_bytes"] / (bwd_avg * 1e-6) / 1e9
         roof = dict(kernel="attn_bwd_kernel", bound="hbm", achieved=achieved, peak=PEAK_HBM / 1e9, unit="GB/s",
@@ -302,10 +343,14 @@ def main():
         with open(tpath) as f:
             roof["traffic"] = json.load(f).get("hbm_bytes_per_launch")
 
+    steps_us = [a + b for a, b in zip(fwd_us, bwd_us)]
     extra = dict(
         fwd_us=fwd_avg, bwd_us=bwd_avg, fwd_us_min=min(fwd_us), bwd_us_min=min(bwd_us),
-        step_us_median=statistics.median([a + b for a, b in zip(fwd_us, bwd_us)]),
+        fwd_us_median=statistics.median(fwd_us), bwd_us_median=statistics.median(bwd_us),
+        step_us_median=statistics.median(steps_us), step_us_min=min(steps_us),
         core_bound_us=bound_us, core_frac_of_roofline=bound_us / us_per_step,
+        core_bound_fp32_only_us=max((alg["fwd_flops"] + alg["bwd_flops"]) / PEAK_FP32_MFMA, core_bytes / PEAK_HBM) * 1e6,
+        kernel_plan=plan,
         fwd_tflops=alg["fwd_flops"] / (fwd_avg * 1e-6) / 1e12,
         fwd_gbps=alg["fwd_bytes"] / (fwd_avg * 1e-6) / 1e9,
         bwd_gbps=alg["bwd_bytes"] / (bwd_avg * 1e-6) / 1e9,

@@ -109,6 +109,22 @@ PET_ATTN_API int pet_attn_set_option(int option, int value);
 /* The option's value, -1 for an unknown option. */
 PET_ATTN_API int pet_attn_get_option(int option);
 
+/* What pet_attn_fwd / pet_attn_bwd launch for a shape under the current
+ * options, without launching: the streaming kernels, or the LDS-staged ones
+ * with their split products and backward layout (used to price a roofline by
+ * the instructions that run). No counterpart in the reference. */
+typedef struct pet_attn_plan {
+  int streaming;              /* 1: the streaming kernels (the fields below stay 0) */
+  int waves;                  /* waves a workgroup (16 slots each) */
+  int fwd_split_scores;       /* forward scores as split-fp32 products on the bf16 matrix cores */
+  int fwd_valu;               /* the vector-ALU forward (option PET_OPT_FWD_KERNEL 3) */
+  int fwd_lds_bytes, fwd_workgroups_per_cu;
+  int bwd_split_dp;           /* backward dP as split-fp32 products on the bf16 matrix cores */
+  int bwd_v_staged, bwd_tile_buffers;
+  int bwd_lds_bytes, bwd_workgroups_per_cu;
+} pet_attn_plan;
+PET_ATTN_API int pet_attn_describe(const pet_attn_shape* shape, pet_attn_plan* out);
+
 /* ---- the core kernels -------------------------------------------------- */
 
 /* Forward: merged[T, D] (ld ldm) = per-head attention of qkv[T, 3D] (ld ldq);

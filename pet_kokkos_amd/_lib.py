@@ -16,6 +16,7 @@ EXPORTS = (
     "pet_attn_max_slots",
     "pet_attn_set_option",
     "pet_attn_get_option",
+    "pet_attn_describe",
     "pet_attn_fwd_run",
     "pet_attn_bwd_run",
     "pet_attn_cf_adjoint",
@@ -66,6 +67,21 @@ class Shape(ctypes.Structure):
         ("dead", ctypes.c_int),
         ("scale", ctypes.c_float),
     ]
+
+
+class Plan(ctypes.Structure):
+    """pet_attn_plan (include/pet_attn.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("streaming", "waves", "fwd_split_scores", "fwd_valu", "fwd_lds_bytes",
+                                             "fwd_workgroups_per_cu", "bwd_split_dp", "bwd_v_staged",
+                                             "bwd_tile_buffers", "bwd_lds_bytes", "bwd_workgroups_per_cu")]
+
+
+def describe(n_atoms, n_rows, slots, heads, head_dim) -> dict:
+    """pet_attn_describe: what the core kernels run for this shape (no launch)."""
+    sh = Shape(n_atoms, n_rows, slots, heads, head_dim, 0, 1.0)
+    p = Plan()
+    check(load().pet_attn_describe(ctypes.byref(sh), ctypes.byref(p)), "pet_attn_describe")
+    return {n: getattr(p, n) for n, _ in Plan._fields_}
 
 
 class ModelHypers(ctypes.Structure):
@@ -121,6 +137,8 @@ def load() -> ctypes.CDLL:
     lib.pet_attn_get_option.restype = ctypes.c_int
     lib.pet_attn_get_option.argtypes = [ctypes.c_int]
     sp = ctypes.POINTER(Shape)
+    lib.pet_attn_describe.restype = ctypes.c_int
+    lib.pet_attn_describe.argtypes = [sp, ctypes.POINTER(Plan)]
     lib.pet_attn_fwd.restype = ctypes.c_int
     lib.pet_attn_fwd.argtypes = [sp, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P]
     lib.pet_attn_bwd.restype = ctypes.c_int

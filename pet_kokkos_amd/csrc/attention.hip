@@ -744,44 +744,72 @@ int resident_wgs(const void* k, int NW, size_t lds) {
   return std::max(1, std::min(by_vgpr, by_lds));
 }
 
+// Which kernel a launch takes (the LDS-staged kernels; the streaming ones are
+// chosen before, by streams()): its LDS bytes, its split products and, for the
+// backward, its LDS layout. Made by plan_fwd / plan_bwd from the shape and
+// the options, so that a caller can ask (pet_attn_describe) what a launch runs.
+struct Plan {
+  int ok = 0;             // 0: the shape does not fit the staged kernels' LDS
+  size_t bytes = 0;       // dynamic LDS
+  bool split = false;     // forward: the scores; backward: dP, on the bf16 matrix cores
+  bool valu = false;      // forward: the vector-ALU kernel
+  int vlds = 0, nbuf = 0; // backward: V staged, tile buffers
+  int resident = 0;       // workgroups a CU
+};
+
+template <int HD>
+Plan plan_fwd(const pet_attn_shape& sh, bool xf) {
+  Plan p;
+  const int NW = waves_for(sh.slots);
+  const size_t cap = size_t(max_lds_bytes());
+  p.bytes = sizeof(float) * Lds<HD>::fwd_floats(NW);
+  if (p.bytes > cap) return p;
+  p.ok = 1;
+  const void* plain = reinterpret_cast<const void*>(attn_fwd_kernel<HD, 512, false, false>);
+  p.resident = resident_wgs(plain, NW, p.bytes);
+  // scores on the bf16 matrix cores (split fp32) where head_dim is a multiple
+  // of 32 and the split K rows fit as many workgroups a CU; option PET_OPT_SPLIT 0
+  // keeps every product on the fp32 matrix cores
+  if constexpr (HD % 32 == 0) {
+    const size_t sbytes = sizeof(float) * Lds<HD>::fwd_floats(NW, true);
+    if (split_enabled() && sbytes <= cap) {
+      const void* split = reinterpret_cast<const void*>(attn_fwd_kernel<HD, 512, false, true>);
+      const int r = resident_wgs(split, NW, sbytes);
+      if (r >= p.resident) p.split = true, p.bytes = sbytes, p.resident = r;
+    }
+  }
+  if constexpr (HD <= 64) {  // option PET_OPT_FWD_KERNEL 3: the vector-ALU kernel, for comparison
+    const int threads = 64 * ((sh.slots + 63) / 64);
+    const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
+    if (option(PET_OPT_FWD_KERNEL) == 3 && !xf && threads <= 256 && vb <= cap)
+      p.valu = true, p.split = false, p.bytes = vb, p.resident = 0;
+  }
+  return p;
+}
+
 // The forward over atoms [n0, n1), qkv a chunk whose edge 0 is row eb.
 template <int HD>
 int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
                const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st) {
+  const bool x = xf.rs || xf.b;
+  const Plan p = plan_fwd<HD>(sh, x);
+  if (!p.ok) return PET_ATTN_ESLOTS;
   const int NW = waves_for(sh.slots);
-  size_t bytes = sizeof(float) * Lds<HD>::fwd_floats(NW);
-  if (bytes > size_t(max_lds_bytes())) return PET_ATTN_ESLOTS;
-  // scores on the bf16 matrix cores (split fp32) where head_dim is a multiple
-  // of 32 and the split K rows fit as many workgroups a CU; option PET_OPT_SPLIT 0
-  // keeps every product on the fp32 matrix cores
-  const size_t sbytes = sizeof(float) * Lds<HD>::fwd_floats(NW, true);
-  bool spl = false;
-  if constexpr (HD % 32 == 0) {
-    if (split_enabled() && sbytes <= size_t(max_lds_bytes())) {
-      const void* plain = reinterpret_cast<const void*>(attn_fwd_kernel<HD, 512, false, false>);
-      const void* split = reinterpret_cast<const void*>(attn_fwd_kernel<HD, 512, false, true>);
-      spl = resident_wgs(split, NW, sbytes) >= resident_wgs(plain, NW, bytes);
-    }
-  }
-  if (spl) bytes = sbytes;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
-  const int choice = option(PET_OPT_FWD_KERNEL);  // 3: the vector-ALU kernel, for comparison
   if constexpr (HD <= 64) {
-    const int threads = 64 * ((sh.slots + 63) / 64);
-    const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
-    if (choice == 3 && !xf.rs && !xf.b && threads <= 256 && vb <= size_t(max_lds_bytes())) {
-      allow_lds(attn_fwd_valu_kernel<HD>, vb);
-      hipLaunchKernelGGL(attn_fwd_valu_kernel<HD>, dim3(unsigned(items)), dim3(threads), vb, st, qkv, ldq, off,
+    if (p.valu) {
+      const int threads = 64 * ((sh.slots + 63) / 64);
+      allow_lds(attn_fwd_valu_kernel<HD>, p.bytes);
+      hipLaunchKernelGGL(attn_fwd_valu_kernel<HD>, dim3(unsigned(items)), dim3(threads), p.bytes, st, qkv, ldq, off,
                          sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml);
       return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
     }
   }
-  const bool x = xf.rs || xf.b;
   using KT = decltype(&attn_fwd_kernel<HD, 512, false, false>);
   KT k;
   if constexpr (HD % 32 == 0) {
-    if (spl)
+    if (p.split)
       k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true, true> : attn_fwd_kernel<HD, 512, false, true>)
                   : (x ? attn_fwd_kernel<HD, 1024, true, true> : attn_fwd_kernel<HD, 1024, false, true>);
     else
@@ -791,29 +819,27 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
     k = NW <= 8 ? (x ? attn_fwd_kernel<HD, 512, true> : attn_fwd_kernel<HD, 512, false>)
                 : (x ? attn_fwd_kernel<HD, 1024, true> : attn_fwd_kernel<HD, 1024, false>);
   }
-  allow_lds(k, bytes);
-  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
+  allow_lds(k, p.bytes);
+  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), p.bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
                      sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
-// The backward over atoms [n0, n1); qkv, dmerged and qkv_adj are the chunk's.
+// The fullest layout that fits (V staged and two tile buffers, else V from
+// global memory, else also one tile buffer) -- unless it leaves one workgroup
+// a CU and a leaner one fits more: then the leaner. Measured on MI355X: at
+// head_dim 32 the fullest is fastest though the leanest would fit a third
+// workgroup (C3 backward 429 us against 466-493 us); at head_dim 64 the
+// fullest holds one workgroup a CU and V-from-global with one buffer two (C5
+// backward 3853 -> 3244 us). The options PET_OPT_BWD_VLDS (1 staged, 2 not)
+// and PET_OPT_BWD_NBUF (1, 2) force a layout where it fits. dP^T runs on the
+// bf16 matrix cores (V staged split) at head_dim 32 when V is staged and the
+// split rows keep as many workgroups a CU.
 template <int HD>
-int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
-               const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
-               const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st) {
+Plan plan_bwd(const pet_attn_shape& sh) {
+  Plan p;
   const int NW = waves_for(sh.slots);
-  const bool x = xf.rs || xf.b;
-  auto k = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true> : attn_bwd_kernel<HD, 512, false>)
-                   : (x ? attn_bwd_kernel<HD, 1024, true> : attn_bwd_kernel<HD, 1024, false>);
-  // The fullest layout that fits (V staged and two tile buffers, else V from
-  // global memory, else also one tile buffer) -- unless it leaves one
-  // workgroup a CU and a leaner one fits more: then the leaner. Measured on
-  // MI355X: at head_dim 32 the fullest is fastest though the leanest would fit
-  // a third workgroup (C3 backward 429 us against 466-493 us); at head_dim 64
-  // the fullest holds one workgroup a CU and V-from-global with one buffer two
-  // (C5 backward 3853 -> 3244 us). PET_OPT_BWD_VLDS (1 staged, 2 not) and
-  // PET_OPT_BWD_NBUF (1, 2) force a layout where it fits.
+  const void* k = reinterpret_cast<const void*>(attn_bwd_kernel<HD, 512, false>);
   const int force_v = option(PET_OPT_BWD_VLDS), force_b = option(PET_OPT_BWD_NBUF);
   const size_t cap = size_t(max_lds_bytes());
   const int layouts[3][2] = {{1, 2}, {0, 2}, {0, 1}};  // (vlds, nbuf), fullest first
@@ -821,7 +847,7 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   for (int j = 0; j < 3; ++j) {
     const size_t b = sizeof(float) * Lds<HD>::bwd_floats(NW, layouts[j][1], layouts[j][0]);
     if (b > cap) continue;
-    const int res = resident_wgs(reinterpret_cast<const void*>(k), NW, b);
+    const int res = resident_wgs(k, NW, b);
     if (best < 0) {
       best = j, best_res = res;
       if (res > 1) break;  // the fullest that fits holds more than one: keep it
@@ -829,32 +855,48 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
       best = j, best_res = res;
     }
   }
-  if (best < 0) return PET_ATTN_ESLOTS;
-  int vlds = layouts[best][0], nbuf = layouts[best][1];
-  size_t bytes = sizeof(float) * Lds<HD>::bwd_floats(NW, nbuf, vlds);
+  if (best < 0) return p;
+  p.ok = 1;
+  p.vlds = layouts[best][0], p.nbuf = layouts[best][1], p.resident = best_res;
+  p.bytes = sizeof(float) * Lds<HD>::bwd_floats(NW, p.nbuf, p.vlds);
   if (force_v || force_b) {
-    const int v = force_v ? (force_v == 1) : vlds, b = force_b ? force_b : nbuf;
+    const int v = force_v ? (force_v == 1) : p.vlds, b = force_b ? force_b : p.nbuf;
     const size_t fb = sizeof(float) * Lds<HD>::bwd_floats(NW, b, v);
-    if ((b == 1 || b == 2) && fb <= cap) vlds = v, nbuf = b, bytes = fb;
+    if ((b == 1 || b == 2) && fb <= cap) p.vlds = v, p.nbuf = b, p.bytes = fb, p.resident = resident_wgs(k, NW, fb);
   }
-  const int64_t items = int64_t(n1 - n0) * sh.heads;
-  if (items == 0) return PET_ATTN_OK;
-  // dP^T on the bf16 matrix cores (V staged split) at head_dim 32 when V is
-  // staged and the split rows keep as many workgroups a CU
   if constexpr (HD == 32) {
-    const size_t sb = sizeof(float) * Lds<HD>::bwd_floats(NW, nbuf, true, true);
-    if (vlds && split_enabled() && sb <= cap) {
-      auto ks = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true, true> : attn_bwd_kernel<HD, 512, false, true>)
-                        : (x ? attn_bwd_kernel<HD, 1024, true, true> : attn_bwd_kernel<HD, 1024, false, true>);
-      if (resident_wgs(reinterpret_cast<const void*>(ks), NW, sb) >=
-          resident_wgs(reinterpret_cast<const void*>(k), NW, bytes))
-        k = ks, bytes = sb;
+    const size_t sb = sizeof(float) * Lds<HD>::bwd_floats(NW, p.nbuf, true, true);
+    if (p.vlds && split_enabled() && sb <= cap) {
+      const void* ks = reinterpret_cast<const void*>(attn_bwd_kernel<HD, 512, false, true>);
+      const int r = resident_wgs(ks, NW, sb);
+      if (r >= p.resident) p.split = true, p.bytes = sb, p.resident = r;
     }
   }
-  allow_lds(k, bytes);
-  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
+  return p;
+}
+
+// The backward over atoms [n0, n1); qkv, dmerged and qkv_adj are the chunk's.
+template <int HD>
+int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+               const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
+               const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st) {
+  const Plan p = plan_bwd<HD>(sh);
+  if (!p.ok) return PET_ATTN_ESLOTS;
+  const int NW = waves_for(sh.slots);
+  const int64_t items = int64_t(n1 - n0) * sh.heads;
+  if (items == 0) return PET_ATTN_OK;
+  const bool x = xf.rs || xf.b;
+  auto k = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true> : attn_bwd_kernel<HD, 512, false>)
+                   : (x ? attn_bwd_kernel<HD, 1024, true> : attn_bwd_kernel<HD, 1024, false>);
+  if constexpr (HD == 32) {
+    if (p.split)
+      k = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true, true> : attn_bwd_kernel<HD, 512, false, true>)
+                  : (x ? attn_bwd_kernel<HD, 1024, true, true> : attn_bwd_kernel<HD, 1024, false, true>);
+  }
+  allow_lds(k, p.bytes);
+  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), p.bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb,
                      sh.slots, sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh,
-                     nbuf, vlds, xf);
+                     p.nbuf, p.vlds, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -958,6 +1000,26 @@ bool streams(const pet_attn_shape& sh) {
   return sh.head_dim % 16 != 0 || option(PET_OPT_ATTN_STREAM) != 0 || sh.slots > pet_attn_max_slots(sh.head_dim);
 }
 }  // namespace pet_attn
+
+extern "C" int pet_attn_describe(const pet_attn_shape* sh, pet_attn_plan* out) {
+  if (!out) return PET_ATTN_EINVAL;
+  *out = pet_attn_plan{};
+  if (int e = check_shape(sh)) return e;
+  if (streams(*sh)) {
+    out->streaming = 1;
+    return PET_ATTN_OK;
+  }
+  return with_head_dim(sh->head_dim, [&](auto hd) {
+    constexpr int HD = decltype(hd)::value;
+    const Plan f = plan_fwd<HD>(*sh, false), b = plan_bwd<HD>(*sh);
+    out->fwd_split_scores = f.split, out->fwd_valu = f.valu, out->fwd_lds_bytes = int(f.bytes);
+    out->fwd_workgroups_per_cu = f.resident;
+    out->bwd_split_dp = b.split, out->bwd_v_staged = b.vlds, out->bwd_tile_buffers = b.nbuf;
+    out->bwd_lds_bytes = int(b.bytes), out->bwd_workgroups_per_cu = b.resident;
+    out->waves = waves_for(sh->slots);
+    return PET_ATTN_OK;
+  });
+}
 
 namespace {
 int fwd_run(const pet_attn_shape* sh, int n0, int n1, int e0, const float* qkv, int64_t ldq, const int* off,

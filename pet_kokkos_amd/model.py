@@ -242,30 +242,47 @@ class Calculator:
         return self.compute_step(positions, cell, forces, edge_gradients)
 
 
-def ef_flops(h: Hypers, n_atoms: int, n_edges: int, sum_cnt2: float) -> dict:
-    """Algorithmic FLOPs of one evaluation, the reference's accounting
-    (tools/roofline.py:188-260): 2 M N K per dense layer, the attention's
-    4 (forward) and 10 (backward) sum(cnt^2) D per block; the backward's
-    GEMMs are the input adjoints only (forces need no weight gradients), one
-    per forward GEMM."""
+def ef_gemms(h: Hypers, n_atoms: int, n_edges: int) -> list:
+    """The evaluation's dense products as (M, N, K), one per forward layer
+    (the reference's accounting, tools/roofline.py:188-260); an energy+forces
+    evaluation runs each once more as its input adjoint (M K N)."""
     N, E, T = n_atoms, n_edges, n_atoms + n_edges
     D, Dn, Dh, cw, ew = h.d_pet, h.d_node, h.d_head, h.center_width, h.edge_width
-    g = 0.0
-    blocks = h.num_gnn_layers * h.num_attention_layers
+    g = []
+    readout = [(N, Dh, Dn), (N, Dh, Dh), (N, 1, Dh), (E, Dh, D), (E, Dh, Dh), (E, 1, Dh)]
     if h.residual:  # per block QKV, output, the MLP over all tokens; a read-out a layer
         for L in range(h.num_gnn_layers):
-            g += (E * D * D if L else 0) + E * D * D
-            g += h.num_attention_layers * (T * 3 * D * D + T * D * D + T * ew * D + T * D * ew)
-            g += N * Dh * Dn + N * Dh * Dh + N * Dh + E * Dh * D + E * Dh * Dh + E * Dh
-        return dict(energy=2.0 * g + blocks * 4.0 * sum_cnt2 * D, forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D)
+            g += ([(E, D, D)] if L else []) + [(E, D, D)]
+            g += h.num_attention_layers * [(T, 3 * D, D), (T, D, D), (T, ew, D), (T, D, ew)]
+            g += readout
+        return g
     for L in range(h.num_gnn_layers):
-        g += (E * D * D if L else 0) + E * D * D  # compress.0's input_edge block, compress.2
-        g += h.num_attention_layers * (N * D * Dn + T * 3 * D * D + T * D * D + N * Dn * D + N * cw * Dn
-                                       + N * Dn * cw // 2 + E * ew * D + E * D * ew // 2)
-        g += E * 2 * D * 2 * D + E * D * 2 * D  # combination MLP
-    g += N * Dh * Dn + N * Dh * Dh + N * Dh + E * Dh * D + E * Dh * Dh + E * Dh  # readout
+        g += ([(E, D, D)] if L else []) + [(E, D, D)]  # compress.0's input_edge block, compress.2
+        g += h.num_attention_layers * [(N, D, Dn), (T, 3 * D, D), (T, D, D), (N, Dn, D), (N, cw, Dn),
+                                       (N, Dn, cw // 2), (E, ew, D), (E, D, ew // 2)]
+        g += [(E, 2 * D, 2 * D), (E, D, 2 * D)]  # combination MLP
+    return g + readout
+
+
+# The model's dense products with M N K >= 2^32 run on the split-product kernel
+# by default (fp32 accuracy, six bf16 products on the bf16 matrix cores); the
+# rest on rocBLAS fp32.
+SPLIT_THRESHOLD = 2.0 ** 32
+
+
+def ef_flops(h: Hypers, n_atoms: int, n_edges: int, sum_cnt2: float) -> dict:
+    """Algorithmic FLOPs of one evaluation: 2 M N K per dense layer forward and
+    once more for its input adjoint (forces need no weight gradients), the
+    attention's 4 (forward) and 10 (backward) sum(cnt^2) D per block; and the
+    part of the forces FLOPs in dense products large enough for the
+    split-product kernel ("split")."""
+    gm = ef_gemms(h, n_atoms, n_edges)
+    g = float(sum(m * n * k for m, n, k in gm))
+    big = float(sum(m * n * k for m, n, k in gm if float(m) * n * k >= SPLIT_THRESHOLD))
+    blocks = h.num_gnn_layers * h.num_attention_layers
+    D = h.d_pet
     return dict(energy=2.0 * g + blocks * 4.0 * sum_cnt2 * D,
-                forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D)
+                forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D, split=4.0 * big)
 
 
 def ef_workload(name: str, seed: int = 0):
