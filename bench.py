@@ -382,7 +382,17 @@ def main():
         s1.record()
         torch.cuda.synchronize()
         extra["op_level_us"] = s0.elapsed_time(s1) * 1e3 / reps
-        extra["op_level_note"] = "attention()+attention_bwd(): core + W_out fwd, W_out^T and W_in^T GEMMs (rocBLAS)"
+        # its contraction bound: the core's, plus the output linear (2 T D^2)
+        # and the input adjoint (6 T D^2) on the split-product kernel and
+        # dmerged (2 T D^2) on rocBLAS fp32
+        big = T * D * D >= 2 ** 32
+        gemm_s = (mixed_seconds(2.0 * T * D * D, 1.0 if big else 0.0) + mixed_seconds(2.0 * T * D * D, 0.0)
+                  + mixed_seconds(6.0 * T * D * D, 1.0 if big else 0.0))
+        extra["op_level_bound_us"] = (core_mfma_s + gemm_s) * 1e6
+        extra["op_level_frac_of_roofline"] = extra["op_level_bound_us"] / extra["op_level_us"]
+        extra["op_level_note"] = ("attention()+attention_bwd(): core + the output linear (split-product kernel, W_out "
+                                  "split as it is staged, bias in its epilogue), dmerged = out_adj W_out (rocBLAS) and "
+                                  "the input adjoint (split-product kernel, W_in^T split into the workspace)")
 
     if not args.no_rows:
         extra["rows"] = time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device)

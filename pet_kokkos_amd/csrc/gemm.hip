@@ -184,14 +184,18 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
 // shapes: even at K = 128 (27318 x 128 x 128: 16.1 against 20.0 us), ahead at
 // 26670 x 1024 x 128 (75 against 86 us) and 131072 x 1536 x 512 (1200 against
 // 1555 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
-template <int BM, int BN, int WGM = 2, int WGN = 2>
+//
+// BF: B comes as fp32 rows [N, K] (ld ldb) and is split as it is staged, like
+// A (for a caller with no room to keep a split copy: twice the staging VALU).
+template <int BM, int BN, int WGM = 2, int WGN = 2, bool BF = false>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, int N, int K,
                                                                        const float* __restrict__ A, int64_t lda,
                                                                        const u4* __restrict__ Bs, float* C,
-                                                                       int64_t ldc, Epi epi) {
+                                                                       int64_t ldc, Epi epi,
+                                                                       const float* __restrict__ Bf, int64_t ldb) {
   constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 13;
   constexpr int AQ = BM * 8, AL = (AQ + T - 1) / T;   // float4 of a step's A slice, a thread's share
-  constexpr int BQ = BN * 12, BL = (BQ + T - 1) / T;  // u4 of a step's B slice
+  constexpr int BQ = BF ? BN * 8 : BN * 12, BL = (BQ + T - 1) / T;  // B slice: float4 (BF) or u4 slots
   __shared__ u4 As[BM * RP], Bt[BN * RP];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
   const int wm = w / WGN, wn = w % WGN;
@@ -215,7 +219,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
   // A: thread t's float4 slots q = t + 256 u, row q / 8, k 4 (q % 8) .. ;
   // B: u4 slots q, row q / 12, part (q % 12) of the row's step
   float4 ra[AL];
-  u4 rb[BL];
+  u4 rb[BF ? 1 : BL];
+  float4 rbf[BF ? BL : 1];
   auto load = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < AL; ++u) {
@@ -225,31 +230,44 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
     }
 #pragma unroll
     for (int u = 0; u < BL; ++u) {
-      const int q = tid + T * u, j = n0 + q / 12;
-      rb[u] = q < BQ && j < N ? Bs[(int64_t(j) * KG + k0 / 8) * 3 + q % 12] : u4{0u, 0u, 0u, 0u};
+      if constexpr (BF) {
+        const int q = tid + T * u, j = n0 + q / 8;
+        rbf[u] = q < BQ && j < N ? *reinterpret_cast<const float4*>(Bf + int64_t(j) * ldb + k0 + 4 * (q % 8))
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const int q = tid + T * u, j = n0 + q / 12;
+        rb[u] = q < BQ && j < N ? Bs[(int64_t(j) * KG + k0 / 8) * 3 + q % 12] : u4{0u, 0u, 0u, 0u};
+      }
     }
+  };
+  // a float4 of row `row`'s k slots 4 (q % 8) .. into its split row (parts of
+  // k group (q % 8) / 2, half q & 1) of tile X
+  auto store_split = [&](u4* X, int row, int q, const float4& v) {
+    float h[3][4];
+    split3(v.x, h[0][0], h[1][0], h[2][0]);
+    split3(v.y, h[0][1], h[1][1], h[2][1]);
+    split3(v.z, h[0][2], h[1][2], h[2][2]);
+    split3(v.w, h[0][3], h[1][3], h[2][3]);
+    unsigned* dst = reinterpret_cast<unsigned*>(&X[row * RP + ((q % 8) / 2) * 3]) + 2 * (q & 1);
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      *reinterpret_cast<uint2*>(dst + 4 * p) = make_uint2(pack_hi(h[p][0], h[p][1]), pack_hi(h[p][2], h[p][3]));
   };
   auto store = [&]() {
 #pragma unroll
     for (int u = 0; u < AL; ++u) {
+      // the float4 is half of k group (q % 8) / 2: its parts go to that half of each part's 16 bytes
       const int q = tid + T * u;
-      if (q < AQ) {
-        // the float4 is half of k group (q % 8) / 2: its parts go to that half of each part's 16 bytes
-        float h[3][4];
-        split3(ra[u].x, h[0][0], h[1][0], h[2][0]);
-        split3(ra[u].y, h[0][1], h[1][1], h[2][1]);
-        split3(ra[u].z, h[0][2], h[1][2], h[2][2]);
-        split3(ra[u].w, h[0][3], h[1][3], h[2][3]);
-        unsigned* dst = reinterpret_cast<unsigned*>(&As[(q / 8) * RP + ((q % 8) / 2) * 3]) + 2 * (q & 1);
-#pragma unroll
-        for (int p = 0; p < 3; ++p)
-          *reinterpret_cast<uint2*>(dst + 4 * p) = make_uint2(pack_hi(h[p][0], h[p][1]), pack_hi(h[p][2], h[p][3]));
-      }
+      if (q < AQ) store_split(As, q / 8, q, ra[u]);
     }
 #pragma unroll
     for (int u = 0; u < BL; ++u) {
       const int q = tid + T * u;
-      if (q < BQ) Bt[(q / 12) * RP + q % 12] = rb[u];
+      if constexpr (BF) {
+        if (q < BQ) store_split(Bt, q / 8, q, rbf[u]);
+      } else {
+        if (q < BQ) Bt[(q / 12) * RP + q % 12] = rb[u];
+      }
     }
   };
 
@@ -371,7 +389,7 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
   auto go = [&](auto kern, int bm, int bn, int threads) {  // a 1-D grid of every tile
     const int64_t tiles = int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     hipLaunchKernelGGL(kern, dim3(unsigned(tiles)), dim3(threads), 0, st, M, N, K, A, lda,
-                       static_cast<const u4*>(Bs), C, ldc, e);
+                       static_cast<const u4*>(Bs), C, ldc, e, static_cast<const float*>(nullptr), int64_t(0));
   };
   // measured on MI355X: 128 x 128 tiles of 8 waves where there are many
   // (131072 x 1536 x 512: 1200-1213 us against 1394-1418 for 128 x 64 and
@@ -385,6 +403,35 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
     go(gemm_nt_split_kernel<128, 64>, 128, 64, 256);
   else
     go(gemm_nt_split_kernel<64, 64>, 64, 64, 256);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// The same product from fp32 B [N, K] (ld ldb), split as it is staged: for
+// callers with no room to keep a split copy of the weights (the op-level
+// attention()'s output linear). K a multiple of 32; A and B 16-byte aligned
+// rows.
+int pet_gemm_nt_split_f32b(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                           int64_t ldc, const float* bias, const float* cin, int64_t ldcin, float beta, hipStream_t st) {
+  if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
+  if (M == 0 || N == 0) return PET_ATTN_OK;
+  if (K == 0) return PET_ATTN_EINVAL;
+  if (int64_t((M + 63) / 64) * ((N + 63) / 64) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
+  if (K % 32 || lda % 4 || ldb % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(B) & 15))
+    return PET_ATTN_EALIGN;
+  Epi e;
+  e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta;
+  auto go = [&](auto kern, int bm, int bn, int threads) {
+    const int64_t tiles = int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    hipLaunchKernelGGL(kern, dim3(unsigned(tiles)), dim3(threads), 0, st, M, N, K, A, lda, nullptr, C, ldc, e, B,
+                       ldb);
+  };
+  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
+  if (N >= 128 && t128 >= 2048)
+    go(gemm_nt_split_kernel<128, 128, 2, 4, true>, 128, 128, 512);
+  else if (t128 >= 2048)
+    go(gemm_nt_split_kernel<128, 64, 2, 2, true>, 128, 64, 256);
+  else
+    go(gemm_nt_split_kernel<64, 64, 2, 2, true>, 64, 64, 256);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 

@@ -18,6 +18,8 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
                       const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
                       float* pre, int64_t ldpre, int act, hipStream_t st);
 int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st);
+int pet_gemm_nt_split_f32b(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                           int64_t ldc, const float* bias, const float* cin, int64_t ldcin, float beta, hipStream_t st);
 
 namespace pet_attn {
 
@@ -247,6 +249,12 @@ int pet_attention(const pet_attn_shape* sh, float* out, int64_t ldo, const float
   if (int e = pet_attn_fwd(sh, qkv, ldq, off, cf_seq, ldc, merged, D, ml, stream)) return e;
   if (T == 0) return PET_ATTN_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the output linear on the split-product kernel with W_out split as it is
+  // staged (no workspace here) and b_out in its epilogue, where it is large
+  // enough to pay (M N K >= 2^32) and the operands allow; else rocBLAS
+  if (double(T) * D * D >= 4294967296.0 && D % 32 == 0 && ldo % 4 == 0 &&
+      (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (reinterpret_cast<uintptr_t>(w_out) & 15) == 0)
+    return pet_gemm_nt_split_f32b(T, D, D, merged, D, w_out, D, out, ldo, b_out, nullptr, 0, 0.0f, st);
   float beta = 0.0f;
   if (b_out) {
     const int64_t total = int64_t(T) * D;
@@ -259,11 +267,23 @@ int pet_attention(const pet_attn_shape* sh, float* out, int64_t ldo, const float
   return gemm_nt(out, ldo, merged, D, w_out, T, D, D, beta, st);
 }
 
-size_t pet_attention_bwd_workspace(const pet_attn_shape* sh) {
-  if (!sh) return 0;
+// The backward's workspace: dmerged [T, D], qkv_adj [T, 3D], cfh [N, H, S],
+// then room for split rows of W_out^T (D x D) and W_in^T (d_in x 3D), sized
+// for d_in up to D (the attention's own width; a wider d_in runs its product
+// on rocBLAS).
+size_t bwd_core_bytes(const pet_attn_shape* sh) {
   const size_t D = size_t(sh->heads) * sh->head_dim, T = size_t(sh->n_rows);
   return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) +
          align256(sizeof(float) * size_t(sh->n_atoms) * sh->slots * sh->heads);
+}
+size_t bwd_split_bytes(const pet_attn_shape* sh) {
+  const size_t D = size_t(sh->heads) * sh->head_dim;
+  return align256(6 * D * D) + align256(6 * 3 * D * D);
+}
+
+size_t pet_attention_bwd_workspace(const pet_attn_shape* sh) {
+  if (!sh) return 0;
+  return bwd_core_bytes(sh) + bwd_split_bytes(sh);
 }
 
 int pet_attention_bwd(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int d_in, float* cf_seq_adj,
@@ -277,9 +297,15 @@ int pet_attention_bwd(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int 
   if (!workspace || workspace_bytes < pet_attention_bwd_workspace(sh)) return PET_ATTN_EWORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
   if (T == 0) return PET_ATTN_OK;
+  // the input linear's product on the split-product kernel (W_in^T split into
+  // the workspace each call, a few microseconds) where it pays; dmerged's
+  // D x D product stays on rocBLAS (measured within noise of the split one)
+  char* ws = static_cast<char*>(workspace);
+  char* split = ws + bwd_core_bytes(sh);
+  void* split_in_t = d_in <= D ? split + align256(6 * size_t(D) * D) : nullptr;
   return attention_bwd_xf(sh, in_adj, ldi, d_in, cf_seq_adj, ldca, out_adj, ldo, qkv, ldq, nullptr, nullptr, cf_seq,
-                          ldc, w_in, w_out, off, merged, ml, beta, static_cast<char*>(workspace),
-                          reinterpret_cast<hipStream_t>(stream));
+                          ldc, w_in, w_out, off, merged, ml, beta, ws, reinterpret_cast<hipStream_t>(stream), nullptr,
+                          split_in_t);
 }
 
 size_t pet_attention_chunked_workspace(const pet_attn_shape* sh, const int* off_host, int chunk) {
