@@ -174,16 +174,20 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
 // B comes split once (pet_linear_split_weights: per row, per 8-element k
 // group, its three bf16 parts, 48 bytes), A is split as each k step of 32 is
 // staged, and a 16 x 16 x 32 step is the six part products of split_bf16.h
-// (6 x ~22 cycles against 8 x 32 on the fp32 instruction, at fp32's error).
+// (6 x 16 nominal cycles against 8 x 32 on the fp32 instruction, at fp32's
+// error; measured with all waves issuing, ~33 against ~42 cycles an instruction).
 // Tiles of WGM x WGN waves (64 WGM WGN threads): 64 x 64 or 128 x 64 of 2 x 2,
 // 128 x 128 of 2 x 4. K steps of 32 go through one LDS buffer, the next
 // step's slices loaded into registers under the current step's products. A
-// row's step is 4 groups x 3 parts x 16 bytes plus a 16-byte pad (13 u4, so a
-// 16-lane column of 128-bit reads is conflict-free): 26 / 39 / 52 KB a
-// workgroup. K a multiple of 32. Measured against torch's GEMM at the model's
-// shapes: even at K = 128 (27318 x 128 x 128: 16.1 against 20.0 us), ahead at
-// 26670 x 1024 x 128 (75 against 86 us) and 131072 x 1536 x 512 (1200 against
-// 1555 us); rocBLAS's fp32 kernel takes 12.8 us on the first.
+// row's step is 4 groups x 3 parts x 16 bytes plus a 32-byte pad (14 u4: the
+// 8-byte stores of an A slice's neighbouring rows then fall on distinct banks,
+// while the 128-bit operand reads stay conflict-free; measured 3-4% faster
+// than a 16-byte pad at the model's large shapes, 131072 x 1536 x 512 1160
+// against 1208 us): 28 / 42 / 56 KB a workgroup. K a multiple of 32.
+// Measured against torch's GEMM at the model's shapes: even at K = 128
+// (27318 x 128 x 128: 15 against 20 us), ahead at 26670 x 1024 x 128 (59-62
+// against 86 us) and 131072 x 1536 x 512 (1160 against 1555 us); rocBLAS's
+// fp32 kernel takes 12.8 us on the first.
 //
 // BF: B comes as fp32 rows [N, K] (ld ldb) and is split as it is staged, like
 // A (for a caller with no room to keep a split copy: twice the staging VALU).
@@ -193,7 +197,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
                                                                        const u4* __restrict__ Bs, float* C,
                                                                        int64_t ldc, Epi epi,
                                                                        const float* __restrict__ Bf, int64_t ldb) {
-  constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 13;
+  constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 14;
   constexpr int AQ = BM * 8, AL = (AQ + T - 1) / T;   // float4 of a step's A slice, a thread's share
   constexpr int BQ = BF ? BN * 8 : BN * 12, BL = (BQ + T - 1) / T;  // B slice: float4 (BF) or u4 slots
   __shared__ u4 As[BM * RP], Bt[BN * RP];
