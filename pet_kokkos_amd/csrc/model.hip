@@ -102,7 +102,9 @@ __global__ void add_bias_kernel(float* __restrict__ x, const float* __restrict__
 // output z is kept as is (the saved pre-activation is z + b) and the
 // activation passes, forward and backward, add the bias as they read it --
 // one write and one read of the pre-activation fewer than a bias fill the
-// GEMM accumulates onto.
+// GEMM accumulates onto. A layer on the split-product kernel instead takes the
+// bias and the activation in the kernel's epilogue and saves z + b itself; its
+// backward pass then gets a null bias (zero).
 
 // out = silu(z + b), fast sigmoid (linear_silu, src/ops.cpp:54-76)
 __global__ void silu_kernel(float* __restrict__ out, const float* __restrict__ z, const float* __restrict__ b,
@@ -117,7 +119,7 @@ __global__ void silu_kernel(float* __restrict__ out, const float* __restrict__ z
 __global__ void silu_bwd_kernel(float* __restrict__ g, const float* __restrict__ pre, const float* __restrict__ b,
                                 int64_t R, int W) {
   GRID_LOOP(i, R * W) {
-    const float x = pre[i] + b[i % W], sg = sig_fast(x);
+    const float x = pre[i] + (b ? b[i % W] : 0.f), sg = sig_fast(x);
     g[i] *= sg * (1.0f + x * (1.0f - sg));
   }
 }
@@ -137,7 +139,7 @@ __global__ void swiglu_kernel(float* __restrict__ h, const float2* __restrict__ 
 __global__ void swiglu_bwd_kernel(float2* __restrict__ pre_adj, const float* __restrict__ h_adj,
                                   const float2* __restrict__ pre, const float2* __restrict__ b, int64_t R, int F) {
   GRID_LOOP(i, R * F) {
-    const float2 p = pre[i], bb = b[i % F];
+    const float2 p = pre[i], bb = b ? b[i % F] : make_float2(0.f, 0.f);
     const float v = p.x + bb.x, sg = sig_fast(p.y + bb.y), g = h_adj[i];
     pre_adj[i] = make_float2(g * sg, g * v * sg * (1.0f - sg));
   }
@@ -333,11 +335,12 @@ __device__ __forceinline__ float silu_bwd1(float g, float pre, float b) {
   const float x = pre + b, sg = sig_fast(x);
   return g * (sg * (1.0f + x * (1.0f - sg)));
 }
+template <bool HB>
 __global__ void silu_bwd4_kernel(float4* __restrict__ g, const float4* __restrict__ pre, const float4* __restrict__ b,
                                  int64_t R, int W4) {
   ROWS4_LOOP(r, c, R, W4) {
     const int64_t i = r * W4 + c;
-    const float4 gg = g[i], x = pre[i], bb = b[c];
+    const float4 gg = g[i], x = pre[i], bb = HB ? b[c] : make_float4(0.f, 0.f, 0.f, 0.f);
     g[i] = make_float4(silu_bwd1(gg.x, x.x, bb.x), silu_bwd1(gg.y, x.y, bb.y), silu_bwd1(gg.z, x.z, bb.z),
                        silu_bwd1(gg.w, x.w, bb.w));
   }
@@ -355,11 +358,14 @@ __device__ __forceinline__ float2 swiglu_bwd1(float g, float pv, float pg, float
   const float v = pv + bv, sg = sig_fast(pg + bg);
   return make_float2(g * sg, g * v * sg * (1.0f - sg));
 }
+// HB false: pre holds its bias already (b unused)
+template <bool HB>
 __global__ void swiglu_bwd4_kernel(float4* __restrict__ pre_adj, const float4* __restrict__ h_adj,
                                    const float4* __restrict__ pre, const float4* __restrict__ b, int64_t R, int F4) {
   ROWS4_LOOP(r, c, R, F4) {
-    const float4 g = h_adj[r * F4 + c];
-    const float4 p0 = pre[r * 2 * F4 + 2 * c], p1 = pre[r * 2 * F4 + 2 * c + 1], b0 = b[2 * c], b1 = b[2 * c + 1];
+    const float4 g = h_adj[r * F4 + c], z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 p0 = pre[r * 2 * F4 + 2 * c], p1 = pre[r * 2 * F4 + 2 * c + 1];
+    const float4 b0 = HB ? b[2 * c] : z4, b1 = HB ? b[2 * c + 1] : z4;
     const float2 a = swiglu_bwd1(g.x, p0.x, p0.y, b0.x, b0.y), bq = swiglu_bwd1(g.y, p0.z, p0.w, b0.z, b0.w);
     const float2 cq = swiglu_bwd1(g.z, p1.x, p1.y, b1.x, b1.y), d = swiglu_bwd1(g.w, p1.z, p1.w, b1.z, b1.w);
     pre_adj[r * 2 * F4 + 2 * c] = make_float4(a.x, a.y, bq.x, bq.y);
@@ -474,6 +480,9 @@ struct pet_model {
   int gemm_mode = 4;           // PET_OPT_MODEL_GEMM for the evaluation in progress
   std::unordered_map<std::string, Mat> m;
   std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
+  // layers whose saved pre-activation holds its bias (made by the split-product
+  // kernel's epilogue in the forward in progress), read by their backward
+  std::unordered_map<std::string, bool> pre_biased;
   void* weights = nullptr;
   void* wsplit = nullptr;
   double* comp = nullptr;
@@ -519,16 +528,21 @@ bool own_gemm(const pet_model& md, int M, int K) {
 // C2 2.98 / 2.15 (residual) with rocBLAS, the same by default (no C2 product is
 // that large), 3.59 / 2.40 with all split; C5 276-279 with rocBLAS, 244 by
 // default and with all split.
-int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int N,
-           int K, float beta, hipStream_t st) {
+// W's split copy when in W^T takes the split-product kernel, else null.
+const void* split_for(const pet_model& md, const float* in, int64_t ldi, const float* W, int M, int N, int K) {
   const int mode = md.gemm_mode;
   const bool big = double(M) * N * K >= 4294967296.0;
   if ((mode == 3 || (mode == 4 && big)) && ldi % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
     auto it = md.split.find(W);
-    if (it != md.split.end())
-      return pet_gemm_nt_split(M, N, K, in, ldi, it->second, out, ldo, nullptr, nullptr, beta != 0.f ? out : nullptr,
-                               ldo, beta, nullptr, 0, 0, st);
+    if (it != md.split.end()) return it->second;
   }
+  return nullptr;
+}
+int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int N,
+           int K, float beta, hipStream_t st) {
+  if (const void* sp = split_for(md, in, ldi, W, M, N, K))
+    return pet_gemm_nt_split(M, N, K, in, ldi, sp, out, ldo, nullptr, nullptr, beta != 0.f ? out : nullptr, ldo, beta,
+                             nullptr, 0, 0, st);
   return gemm_nt(out, ldo, in, ldi, W, M, N, K, beta, st);
 }
 
@@ -541,6 +555,10 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
   const float* b = bias ? md.p(key + ".bias") : nullptr;
   if (own_gemm(md, M, K)) {
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
+    return;
+  }
+  if (const void* sp = split_for(md, in, K, W.p, M, W.rows, K)) {  // the bias in the epilogue
+    ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
   if (rows4_ok(W.rows, {out, b}))
@@ -563,6 +581,22 @@ void linear_acc(pet_model& md, float* out, const float* in, int M, int K, const 
   }
   ok(gemm_w(md, out, W.rows, in, K, W.p, M, W.rows, K, 1.0f, st));
 }
+void add_bias_pass(float* x, const float* b, int64_t R, int W, hipStream_t st);
+// out += in W^T + b: the bias in the split-product kernel's epilogue where the
+// layer takes that kernel, else a bias pass before linear_acc
+void linear_acc_bias(pet_model& md, float* out, const float* in, int M, int K, const std::string& key,
+                     hipStream_t st) {
+  const Mat& W = md.w(key + ".weight");
+  if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
+  if (M == 0) return;
+  if (const void* sp = own_gemm(md, M, K) ? nullptr : split_for(md, in, K, W.p, M, W.rows, K)) {
+    ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, md.p(key + ".bias"), out, W.rows, 1.f,
+                         nullptr, 0, 0, st));
+    return;
+  }
+  add_bias_pass(out, md.p(key + ".bias"), int64_t(M), W.rows, st);
+  linear_acc(md, out, in, M, K, key, st);
+}
 // in_adj[M, K] = out_adj W + beta in_adj
 void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const std::string& key, float beta,
                 hipStream_t st) {
@@ -581,6 +615,33 @@ void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const st
   }
   ok(gemm_w(md, z, W.rows, in, K, W.p, M, W.rows, K, 0.0f, st));
 }
+// z = in W^T + b and out = act(z) (act 1 SiLU, 2 SwiGLU) as one split-product
+// GEMM with the bias and the activation in its epilogue, where the layer takes
+// that kernel (then z holds its bias, recorded for the backward); else
+// linear_pre and the activation pass. True when fused.
+// Whether linear_act fuses the layer (then out must be a buffer other than in).
+bool act_fuses(const pet_model& md, const float* in, int M, int K, const std::string& key) {
+  const Mat& W = md.w(key + ".weight");
+  return !own_gemm(md, M, K) && split_for(md, in, K, W.p, M, W.rows, K) != nullptr;
+}
+bool linear_act(pet_model& md, float* out, float* z, const float* in, int M, int K, const std::string& key, int act,
+                hipStream_t st) {
+  const Mat& W = md.w(key + ".weight");
+  if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
+  // (out must not be the GEMM's input: other workgroups still read its rows)
+  const void* sp = own_gemm(md, M, K) || out == in ? nullptr : split_for(md, in, K, W.p, M, W.rows, K);
+  md.pre_biased[key] = sp != nullptr;
+  if (!sp || M == 0) return false;
+  ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, act == 2 ? W.rows / 2 : W.rows, nullptr, md.p(key + ".bias"),
+                       nullptr, 0, 0.f, z, W.rows, act, st));
+  return true;
+}
+// the bias the activation passes add to a saved pre-activation: none where the
+// forward's epilogue put it in already
+const float* pass_bias(const pet_model& md, const std::string& key) {
+  auto it = md.pre_biased.find(key);
+  return it != md.pre_biased.end() && it->second ? nullptr : md.p(key + ".bias");
+}
 // out = silu(z + b) of linear_pre's z under `key`
 void silu(pet_model& md, float* out, const float* z, int64_t R, const std::string& key, hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
@@ -594,12 +655,13 @@ void silu(pet_model& md, float* out, const float* z, int64_t R, const std::strin
 }
 void silu_bwd(pet_model& md, float* g, const float* z, int64_t R, const std::string& key, hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
+  const float* bp = pass_bias(md, key);
   if (R == 0) return;
   if (rows4_ok(b.rows, {g, z, b.p}))
-    hipLaunchKernelGGL(silu_bwd4_kernel, grid_rows4(R, b.rows / 4), dim3(256), 0, st, v4(g), v4(z), v4(b.p), R,
-                       b.rows / 4);
+    hipLaunchKernelGGL(bp ? silu_bwd4_kernel<true> : silu_bwd4_kernel<false>, grid_rows4(R, b.rows / 4), dim3(256),
+                       0, st, v4(g), v4(z), v4(bp), R, b.rows / 4);
   else
-    hipLaunchKernelGGL(silu_bwd_kernel, grid_for(R * b.rows), dim3(256), 0, st, g, z, b.p, R, b.rows);
+    hipLaunchKernelGGL(silu_bwd_kernel, grid_for(R * b.rows), dim3(256), 0, st, g, z, bp, R, b.rows);
   launched();
 }
 // h = swiglu(z + b) of linear_pre's z under `key` (a .w_in)
@@ -617,14 +679,15 @@ void swiglu(pet_model& md, float* h, const float* z, int64_t R, const std::strin
 void swiglu_bwd(pet_model& md, float* z_adj, const float* h_adj, const float* z, int64_t R, const std::string& key,
                 hipStream_t st) {
   const Mat& b = md.w(key + ".bias");
+  const float* bp = pass_bias(md, key);
   if (R == 0) return;
   if (b.rows % 2 == 0 && rows4_ok(b.rows / 2, {z_adj, h_adj, z, b.p}))
-    hipLaunchKernelGGL(swiglu_bwd4_kernel, grid_rows4(R, b.rows / 8), dim3(256), 0, st, v4(z_adj), v4(h_adj), v4(z),
-                       v4(b.p), R, b.rows / 8);
+    hipLaunchKernelGGL(bp ? swiglu_bwd4_kernel<true> : swiglu_bwd4_kernel<false>, grid_rows4(R, b.rows / 8),
+                       dim3(256), 0, st, v4(z_adj), v4(h_adj), v4(z), v4(bp), R, b.rows / 8);
   else
     hipLaunchKernelGGL(swiglu_bwd_kernel, grid_for(R * b.rows / 2), dim3(256), 0, st,
                        reinterpret_cast<float2*>(z_adj), h_adj, reinterpret_cast<const float2*>(z),
-                       reinterpret_cast<const float2*>(b.p), R, b.rows / 2);
+                       reinterpret_cast<const float2*>(bp), R, b.rows / 2);
   launched();
 }
 // The elementwise passes: the float4 kernels where the width and alignment allow.
@@ -749,15 +812,19 @@ struct Pass {
       // node_next += center_mlp(norm(node_res)); edge_next += mlp(norm(eps))
       float* nn = node_exp;  // consumed
       norm(md, nn, b.node_res, N, Dn, tl + ".norm_center_features", false, st);
-      linear_pre(md, b.pre_c, nn, N, Dn, tl + ".center_mlp.w_in", st);
       float* hc = md.f(int64_t(N) * md.cw / 2);
-      swiglu(md, hc, b.pre_c, N, tl + ".center_mlp.w_in", st);
+      if (!linear_act(md, hc, b.pre_c, nn, N, Dn, tl + ".center_mlp.w_in", 2, st)) {
+        linear_pre(md, b.pre_c, nn, N, Dn, tl + ".center_mlp.w_in", st);
+        swiglu(md, hc, b.pre_c, N, tl + ".center_mlp.w_in", st);
+      }
       linear_acc(md, node_next, hc, N, md.cw / 2, tl + ".center_mlp.w_out", st);
       float* en = attn_out;  // consumed: its edge rows were read by the residual pass
       norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
-      linear_pre(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
       float* he = md.f(int64_t(E) * md.ew / 2);
-      swiglu(md, he, b.pre_e, E, tl + ".mlp.w_in", st);
+      if (!linear_act(md, he, b.pre_e, en, E, D, tl + ".mlp.w_in", 2, st)) {
+        linear_pre(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
+        swiglu(md, he, b.pre_e, E, tl + ".mlp.w_in", st);
+      }
       linear_acc(md, edge_next, he, E, md.ew / 2, tl + ".mlp.w_out", st);
       md.ws.release(scope);
       node_cur = node_next;
@@ -775,12 +842,14 @@ struct Pass {
     }
     float* cn = md.f(int64_t(E) * 2 * D);
     norm(md, cn, sv.concat, E, 2 * D, "combination_norms." + ls, true, st);
-    linear_pre(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
-    silu(md, cn, sv.cph, E, "combination_mlps." + ls + ".0", st);
-    if (E) {
-      add_bias_pass(input_edge, md.p("combination_mlps." + ls + ".2.bias"), int64_t(E), D, st);
+    // the SiLU's output: in place, or a buffer of its own for the fused GEMM
+    // (which cannot write its input)
+    float* ca = act_fuses(md, cn, E, 2 * D, "combination_mlps." + ls + ".0") ? md.f(int64_t(E) * 2 * D) : cn;
+    if (!linear_act(md, ca, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", 1, st)) {
+      linear_pre(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
+      silu(md, ca, sv.cph, E, "combination_mlps." + ls + ".0", st);
     }
-    linear_acc(md, input_edge, cn, E, 2 * D, "combination_mlps." + ls + ".2", st);
+    linear_acc_bias(md, input_edge, ca, E, 2 * D, "combination_mlps." + ls + ".2", st);
     md.ws.release(scope);
   }
 
@@ -865,17 +934,22 @@ struct Pass {
     Readout r{md.f(int64_t(N) * Dh), md.f(int64_t(N) * Dh), md.f(int64_t(E) * Dh), md.f(int64_t(E) * Dh), md.f(N),
               md.f(E)};
     auto scope = md.ws.mark();
-    float* x = md.f(std::max<int64_t>(int64_t(N), int64_t(E)) * Dh);
-    linear_pre(md, r.nh0, node_rows, N, Dn, nh + ".0", st);
-    silu(md, x, r.nh0, N, nh + ".0", st);
-    linear_pre(md, r.nh1, x, N, Dh, nh + ".2", st);
-    silu(md, x, r.nh1, N, nh + ".2", st);
-    linear(md, r.npred, x, N, Dh, "node_last_layers.energy." + si + ".energy___0", st);
-    linear_pre(md, r.eh0, edge_rows, E, D, eh + ".0", st);
-    silu(md, x, r.eh0, E, eh + ".0", st);
-    linear_pre(md, r.eh1, x, E, Dh, eh + ".2", st);
-    silu(md, x, r.eh1, E, eh + ".2", st);
-    linear(md, r.epred, x, E, Dh, "edge_last_layers.energy." + si + ".energy___0", st);
+    const int64_t rows = std::max<int64_t>(int64_t(N), int64_t(E)) * Dh;
+    // a second buffer only where a fused layer would otherwise write its input
+    float* x = md.f(rows);
+    float* y = act_fuses(md, x, N, Dh, nh + ".2") || act_fuses(md, x, E, Dh, eh + ".2") ? md.f(rows) : x;
+    auto layer = [&](float* out, float* z, const float* in, int M, int K, const std::string& key) {
+      if (!linear_act(md, out, z, in, M, K, key, 1, st)) {
+        linear_pre(md, z, in, M, K, key, st);
+        silu(md, out, z, M, key, st);
+      }
+    };
+    layer(x, r.nh0, node_rows, N, Dn, nh + ".0");
+    layer(y, r.nh1, x, N, Dh, nh + ".2");
+    linear(md, r.npred, y, N, Dh, "node_last_layers.energy." + si + ".energy___0", st);
+    layer(x, r.eh0, edge_rows, E, D, eh + ".0");
+    layer(y, r.eh1, x, E, Dh, eh + ".2");
+    linear(md, r.epred, y, E, Dh, "edge_last_layers.energy." + si + ".energy___0", st);
     md.ws.release(scope);
     if (N) {
       hipLaunchKernelGGL(readout_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st, net, r.npred, r.epred,
@@ -982,9 +1056,11 @@ struct Pass {
       float* tok_a = md.f(int64_t(T) * D);
       norm(md, tok_a, b.s1, T, D, tl + ".norm_attention", true, st);
       // s2 = tok_a + b_out, then += silu(tok_a W_in^T + b_in) W_out^T
-      linear_pre(md, b.pre, tok_a, T, D, tl + ".mlp.w_in", st);
       float* hm = md.f(int64_t(T) * F);
-      silu(md, hm, b.pre, T, tl + ".mlp.w_in", st);
+      if (!linear_act(md, hm, b.pre, tok_a, T, D, tl + ".mlp.w_in", 1, st)) {
+        linear_pre(md, b.pre, tok_a, T, D, tl + ".mlp.w_in", st);
+        silu(md, hm, b.pre, T, tl + ".mlp.w_in", st);
+      }
       bias_add_pass(b.s2, tok_a, md.p(tl + ".mlp.w_out.bias"), int64_t(T), D, st);
       linear_acc(md, b.s2, hm, T, F, tl + ".mlp.w_out", st);
       norm(md, sv.tokens, b.s2, T, D, tl + ".norm_mlp", true, st);
