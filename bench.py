@@ -360,7 +360,7 @@ def main():
     )
 
     if not args.no_op_level:
-        # attention() + attention_bwd(): the core plus the W_out / W_in linears (rocBLAS).
+        # attention() + attention_bwd(): the core plus the W_out / W_in linears.
         ws = A.Workspace(device)
         tkd = A.Tokens(off, N)
         out = torch.empty((T, D), device=device)
@@ -382,17 +382,16 @@ def main():
         s1.record()
         torch.cuda.synchronize()
         extra["op_level_us"] = s0.elapsed_time(s1) * 1e3 / reps
-        # its contraction bound: the core's, plus the output linear (2 T D^2)
-        # and the input adjoint (6 T D^2) on the split-product kernel and
-        # dmerged (2 T D^2) on rocBLAS fp32
+        # its contraction bound: the core's, plus the output linear (2 T D^2),
+        # dmerged (2 T D^2) and the input adjoint (6 T D^2), each on the
+        # split-product kernel where it is large enough, else rocBLAS fp32
         big = T * D * D >= 2 ** 32
-        gemm_s = (mixed_seconds(2.0 * T * D * D, 1.0 if big else 0.0) + mixed_seconds(2.0 * T * D * D, 0.0)
-                  + mixed_seconds(6.0 * T * D * D, 1.0 if big else 0.0))
+        gemm_s = mixed_seconds(10.0 * T * D * D, 1.0 if big else 0.0)
         extra["op_level_bound_us"] = (core_mfma_s + gemm_s) * 1e6
         extra["op_level_frac_of_roofline"] = extra["op_level_bound_us"] / extra["op_level_us"]
         extra["op_level_note"] = ("attention()+attention_bwd(): core + the output linear (split-product kernel, W_out "
-                                  "split as it is staged, bias in its epilogue), dmerged = out_adj W_out (rocBLAS) and "
-                                  "the input adjoint (split-product kernel, W_in^T split into the workspace)")
+                                  "split as it is staged, bias in its epilogue), dmerged = out_adj W_out and the input "
+                                  "adjoint (split-product kernel, W_out^T and W_in^T split into the workspace)")
 
     if not args.no_rows:
         extra["rows"] = time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device)

@@ -297,14 +297,14 @@ int pet_attention_bwd(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int 
   if (!workspace || workspace_bytes < pet_attention_bwd_workspace(sh)) return PET_ATTN_EWORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return PET_ATTN_EALIGN;
   if (T == 0) return PET_ATTN_OK;
-  // the input linear's product on the split-product kernel (W_in^T split into
-  // the workspace each call, a few microseconds) where it pays; dmerged's
-  // D x D product stays on rocBLAS (measured within noise of the split one)
+  // both dense products on the split-product kernel where they are large
+  // enough (M N K >= 2^32), from W_out^T and W_in^T split into the workspace
+  // each call (a few microseconds): dmerged = out_adj W_out, in_adj = qkv_adj W_in
   char* ws = static_cast<char*>(workspace);
   char* split = ws + bwd_core_bytes(sh);
   void* split_in_t = d_in <= D ? split + align256(6 * size_t(D) * D) : nullptr;
   return attention_bwd_xf(sh, in_adj, ldi, d_in, cf_seq_adj, ldca, out_adj, ldo, qkv, ldq, nullptr, nullptr, cf_seq,
-                          ldc, w_in, w_out, off, merged, ml, beta, ws, reinterpret_cast<hipStream_t>(stream), nullptr,
+                          ldc, w_in, w_out, off, merged, ml, beta, ws, reinterpret_cast<hipStream_t>(stream), split,
                           split_in_t);
 }
 
