@@ -51,7 +51,8 @@ struct Epi {
   float beta = 0.f;
   float* pre = nullptr;              // [M, N] (ld ldpre): v before the activation
   int64_t ldpre = 0;
-  int act = 0;                       // 0 none, 1 SiLU, 2 SwiGLU (C has N/2 columns)
+  int act = 0;                       // 0 none, 1 SiLU, 2 SwiGLU (C has N/2 columns),
+                                     // 3 / 4 the backward of SiLU / SwiGLU (below)
 };
 
 // The epilogue of one result element v at (i, j), shared by the kernels. Every
@@ -59,6 +60,23 @@ struct Epi {
 // (i, j) may lie outside the result, which is then left alone.
 __device__ __forceinline__ void epi_elem(float v, int i, int j, int c, int M, int N, float* C, int64_t ldc,
                                          const Epi& epi) {
+  if (epi.act >= 3) {
+    // v is an activation's output adjoint; cin the saved pre-activation
+    // (bias the pre-activation's bias, null when cin holds it already).
+    // 3: C[i, j] = v silu'(z); 4 (SwiGLU, (value, gate) pairs of cin):
+    // C[i, 2j] = v sigmoid(g), C[i, 2j + 1] = v u sigmoid(g) (1 - sigmoid(g))
+    if (i >= M || j >= N) return;
+    const float* z = epi.cin + int64_t(i) * epi.ldcin;
+    if (epi.act == 3) {
+      const float x = z[j] + (epi.bias ? epi.bias[j] : 0.f), sg = sig_fast(x);
+      C[int64_t(i) * ldc + j] = v * (sg * (1.0f + x * (1.0f - sg)));
+    } else {
+      const float u = z[2 * j] + (epi.bias ? epi.bias[2 * j] : 0.f);
+      const float sg = sig_fast(z[2 * j + 1] + (epi.bias ? epi.bias[2 * j + 1] : 0.f));
+      *reinterpret_cast<float2*>(C + int64_t(i) * ldc + 2 * j) = make_float2(v * sg, v * u * sg * (1.0f - sg));
+    }
+    return;
+  }
   if (epi.row_scale && i < M) v *= epi.row_scale[i];
   if (epi.bias && j < N) v += epi.bias[j];
   if (epi.cin && i < M && j < N) v += epi.beta * epi.cin[int64_t(i) * epi.ldcin + j];

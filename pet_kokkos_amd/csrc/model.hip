@@ -603,6 +603,24 @@ void linear_bwd(pet_model& md, float* in_adj, const float* out_adj, int M, const
   const Mat& WT = md.w(key + ".weight^T");  // [K, Nout]: out_adj W = out_adj (W^T)^T
   if (M) ok(gemm_w(md, in_adj, WT.rows, out_adj, WT.cols, WT.p, M, WT.rows, WT.cols, beta, st));
 }
+// The backward of linear_act's activation fused into the product before it:
+// out = act'(z) * (adj W) (act 1 SiLU: out [M, Nout]; 2 SwiGLU: out [M, 2 Nout]
+// from the (value, gate) pairs of z), adj W the input adjoint of layer
+// key_out, z the saved pre-activation of layer key_act -- one split-product
+// GEMM with the activation's backward in its epilogue (the same product and
+// the same per-element arithmetic as linear_bwd then silu_bwd / swiglu_bwd),
+// where that layer takes the split kernel. True when fused.
+const float* pass_bias(const pet_model& md, const std::string& key);
+bool linear_bwd_act(pet_model& md, float* out, const float* adj, int M, const std::string& key_out, const float* z,
+                    const std::string& key_act, int act, hipStream_t st) {
+  const Mat& WT = md.w(key_out + ".weight^T");
+  const void* sp = M ? split_for(md, adj, WT.cols, WT.p, M, WT.rows, WT.cols) : nullptr;
+  if (!sp) return false;
+  const int64_t w = act == 2 ? 2 * int64_t(WT.rows) : WT.rows;
+  ok(pet_gemm_nt_split(M, WT.rows, WT.cols, adj, WT.cols, sp, out, w, nullptr, pass_bias(md, key_act), z, w, 0.f,
+                       nullptr, 0, act == 2 ? 4 : 3, st));
+  return true;
+}
 // z[M, Nout] = in W^T, no bias: the pre-activation an activation pass reads with its bias
 void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const std::string& key, hipStream_t st) {
   const Mat& W = md.w(key + ".weight");
@@ -865,8 +883,11 @@ struct Pass {
       auto s2 = md.ws.mark();
       float* cph_adj = md.f(int64_t(E) * 2 * D);
       float* cn_adj = md.f(int64_t(E) * 2 * D);
-      linear_bwd(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", 0.0f, st);
-      silu_bwd(md, cph_adj, sv.cph, E, "combination_mlps." + ls + ".0", st);
+      if (!linear_bwd_act(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", sv.cph,
+                          "combination_mlps." + ls + ".0", 1, st)) {
+        linear_bwd(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", 0.0f, st);
+        silu_bwd(md, cph_adj, sv.cph, E, "combination_mlps." + ls + ".0", st);
+      }
       linear_bwd(md, cn_adj, cph_adj, E, "combination_mlps." + ls + ".0", 0.0f, st);
       float* ca = cph_adj;  // consumed
       ok(pet_norm_rows_bwd(E, 2 * D, ca, 2 * D, 0.0f, cn_adj, 2 * D, sv.concat, 2 * D,
@@ -886,15 +907,20 @@ struct Pass {
         float* h_adj = md.f(int64_t(E) * md.ew / 2);
         float* pre_adj = md.f(int64_t(E) * md.ew);
         float* en_adj = md.f(int64_t(E) * D);
-        linear_bwd(md, h_adj, edge_adj, E, tl + ".mlp.w_out", 0.0f, st);
-        swiglu_bwd(md, pre_adj, h_adj, b.pre_e, E, tl + ".mlp.w_in", st);
+        if (!linear_bwd_act(md, pre_adj, edge_adj, E, tl + ".mlp.w_out", b.pre_e, tl + ".mlp.w_in", 2, st)) {
+          linear_bwd(md, h_adj, edge_adj, E, tl + ".mlp.w_out", 0.0f, st);
+          swiglu_bwd(md, pre_adj, h_adj, b.pre_e, E, tl + ".mlp.w_in", st);
+        }
         linear_bwd(md, en_adj, pre_adj, E, tl + ".mlp.w_in", 0.0f, st);
         ok(pet_norm_rows_bwd(E, D, edge_adj, D, 1.0f, en_adj, D, b.eps, D, md.p(tl + ".norm_mlp.weight"), 0, st));
         float* hc_adj = md.f(int64_t(N) * md.cw / 2);
         float* prec_adj = md.f(int64_t(N) * md.cw);
         float* cn_adj = md.f(int64_t(N) * Dn);
-        linear_bwd(md, hc_adj, node_adj, N, tl + ".center_mlp.w_out", 0.0f, st);
-        swiglu_bwd(md, prec_adj, hc_adj, b.pre_c, N, tl + ".center_mlp.w_in", st);
+        if (!linear_bwd_act(md, prec_adj, node_adj, N, tl + ".center_mlp.w_out", b.pre_c, tl + ".center_mlp.w_in", 2,
+                            st)) {
+          linear_bwd(md, hc_adj, node_adj, N, tl + ".center_mlp.w_out", 0.0f, st);
+          swiglu_bwd(md, prec_adj, hc_adj, b.pre_c, N, tl + ".center_mlp.w_in", st);
+        }
         linear_bwd(md, cn_adj, prec_adj, N, tl + ".center_mlp.w_in", 0.0f, st);
         ok(pet_norm_rows_bwd(N, Dn, node_adj, Dn, 1.0f, cn_adj, Dn, b.node_res, Dn,
                              md.p(tl + ".norm_center_features.weight"), 0, st));
@@ -970,15 +996,19 @@ struct Pass {
                          e.cut, r.epred, acc ? 1 : 0, N, E);
       launched();
     }
-    linear_bwd(md, a1, npa, N, "node_last_layers.energy." + si + ".energy___0", 0.0f, st);
-    silu_bwd(md, a1, r.nh1, N, nh + ".2", st);
-    linear_bwd(md, a0, a1, N, nh + ".2", 0.0f, st);
-    silu_bwd(md, a0, r.nh0, N, nh + ".0", st);
+    // each SiLU's backward in the epilogue of the product before it where it can be
+    auto bwd_act = [&](float* out, const float* adj, int M, const std::string& ko, const float* z,
+                       const std::string& ka) {
+      if (!linear_bwd_act(md, out, adj, M, ko, z, ka, 1, st)) {
+        linear_bwd(md, out, adj, M, ko, 0.0f, st);
+        silu_bwd(md, out, z, M, ka, st);
+      }
+    };
+    bwd_act(a1, npa, N, "node_last_layers.energy." + si + ".energy___0", r.nh1, nh + ".2");
+    bwd_act(a0, a1, N, nh + ".2", r.nh0, nh + ".0");
     linear_bwd(md, node_adj, a0, N, nh + ".0", 0.0f, st);
-    linear_bwd(md, a1, epa, E, "edge_last_layers.energy." + si + ".energy___0", 0.0f, st);
-    silu_bwd(md, a1, r.eh1, E, eh + ".2", st);
-    linear_bwd(md, a0, a1, E, eh + ".2", 0.0f, st);
-    silu_bwd(md, a0, r.eh0, E, eh + ".0", st);
+    bwd_act(a1, epa, E, "edge_last_layers.energy." + si + ".energy___0", r.eh1, eh + ".2");
+    bwd_act(a0, a1, E, eh + ".2", r.eh0, eh + ".0");
     linear_bwd(md, edge_adj, a0, E, eh + ".0", 0.0f, st);
     md.ws.release(scope);
   }
@@ -1083,8 +1113,10 @@ struct Pass {
       ok(pet_norm_rows_bwd(T, D, s2_adj, D, 0.0f, tokens_adj, D, b.s2, D, md.p(tl + ".norm_mlp.weight"), 1, st));
       copy_pass(tok_a_adj, s2_adj, int64_t(T) * D, st);
       float* h_adj = md.f(int64_t(T) * F);
-      linear_bwd(md, h_adj, s2_adj, T, tl + ".mlp.w_out", 0.0f, st);
-      silu_bwd(md, h_adj, b.pre, T, tl + ".mlp.w_in", st);
+      if (!linear_bwd_act(md, h_adj, s2_adj, T, tl + ".mlp.w_out", b.pre, tl + ".mlp.w_in", 1, st)) {
+        linear_bwd(md, h_adj, s2_adj, T, tl + ".mlp.w_out", 0.0f, st);
+        silu_bwd(md, h_adj, b.pre, T, tl + ".mlp.w_in", st);
+      }
       linear_bwd(md, tok_a_adj, h_adj, T, tl + ".mlp.w_in", 1.0f, st);
       // tok_a = LN(s1): s1_adj into tokens_adj (consumed); the attention's input
       // adjoint then accumulates onto it (s1 = tokens + attention(tokens))
