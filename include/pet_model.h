@@ -107,6 +107,14 @@ PET_ATTN_API int pet_model_compute(pet_model* model, const pet_model_edges* edge
  *   for act 2 (SwiGLU, W's rows interleaved value/gate) C[i][j/2] = v_j sigmoid(v_{j+1})
  *   for even j. cin may be C itself (a residual accumulated in place). A fixed
  *   summation order: results repeat bit for bit.
+ * act 3 and 4 fuse an activation's backward instead: v = (A W^T)[i][j] is the
+ *   adjoint of the activation's output, cin its saved pre-activation z (required;
+ *   bias, when non-null, z's bias not yet added to it; row_scale, beta and pre
+ *   unused, row_scale and pre must be null):
+ *   act 3 (SiLU): C[i][j] = v silu'(z[i][j]);
+ *   act 4 (SwiGLU, z [M, 2N] of interleaved (value u, gate g) pairs, C [M, 2N]):
+ *   C[i][2j] = v sigmoid(g), C[i][2j+1] = v u sigmoid(g) (1 - sigmoid(g)),
+ *   the adjoint of the pair (u, g) for h = u sigmoid(g).
  * Replaces the reference's fused GEMMs (src/fused_gemm_hip.cpp: linear_fused,
  * silu_in_fused, swiglu_in_fused; src/ops.hpp:84-96). */
 PET_ATTN_API int pet_linear_fused(int M, int N, int K, const float* A, int64_t lda, const float* W, int64_t ldw,

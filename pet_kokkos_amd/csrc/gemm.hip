@@ -385,11 +385,26 @@ int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const fl
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
+// The epilogue arguments of the public entry points: C's and cin's widths
+// per act (act 4 writes and reads 2N columns), cin required by the backward
+// codes 3 and 4, which take no row scale and no pre.
+static bool epi_args_ok(int N, const float* C, int64_t ldc, const float* row_scale, const float* cin, int64_t ldcin,
+                        const float* pre, int64_t ldpre, int act) {
+  if (act < 0 || act > 4 || !C) return false;
+  if (act >= 3) {
+    const int64_t w = act == 4 ? 2 * int64_t(N) : N;
+    // act 4 stores (value, gate) adjoint pairs as 8-byte words
+    const bool pairs_ok = act == 3 || ((reinterpret_cast<uintptr_t>(C) & 7) == 0 && ldc % 2 == 0);
+    return cin && ldcin >= w && ldc >= w && !row_scale && !pre && pairs_ok;
+  }
+  return ldc >= (act == 2 ? N / 2 : N) && (!cin || ldcin >= N) && (!pre || ldpre >= N);
+}
+
 extern "C" int pet_linear_fused(int M, int N, int K, const float* A, int64_t lda, const float* W, int64_t ldw,
                                 float* C, int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                 int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream) {
-  if ((M > 0 && N > 0) && (!A || !W || !C || ldc < (act == 2 ? N / 2 : N) || lda < K || ldw < K ||
-                           (cin && ldcin < N) || (pre && ldpre < N) || act < 0 || act > 2))
+  if ((M > 0 && N > 0) && (!A || !W || !C || lda < K || ldw < K || !epi_args_ok(N, C, ldc, row_scale, cin, ldcin,
+                                                                                    pre, ldpre, act)))
     return PET_ATTN_EINVAL;
   return pet_gemm_nt_fused(M, N, K, A, lda, W, ldw, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
                            reinterpret_cast<hipStream_t>(stream));
@@ -492,8 +507,8 @@ extern "C" int pet_linear_split_weights_transposed(const float* W, int N, int K,
 extern "C" int pet_linear_fused_split(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit, float* C,
                                       int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                       int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream) {
-  if ((M > 0 && N > 0) && (!A || !Wsplit || !C || ldc < (act == 2 ? N / 2 : N) || lda < K ||
-                           (cin && ldcin < N) || (pre && ldpre < N) || act < 0 || act > 2))
+  if ((M > 0 && N > 0) && (!A || !Wsplit || !C || lda < K || !epi_args_ok(N, C, ldc, row_scale, cin, ldcin, pre,
+                                                                              ldpre, act)))
     return PET_ATTN_EINVAL;
   return pet_gemm_nt_split(M, N, K, A, lda, Wsplit, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
                            reinterpret_cast<hipStream_t>(stream));

@@ -58,8 +58,8 @@ def _check(t, name, rows=None, cols=None, vector=False, device=None):
 
 
 def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
-    if act not in (0, 1, 2):
-        raise ValueError(f"act {act}: 0 (none), 1 (SiLU) or 2 (SwiGLU)")
+    if act not in (0, 1, 2, 3, 4):
+        raise ValueError(f"act {act}: 0 (none), 1 (SiLU), 2 (SwiGLU), 3 / 4 (their backward)")
     _check(A, "A")
     M, K = A.shape
     dev = A.device
@@ -74,13 +74,17 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
         raise ValueError(f"A has K = {K}, W has K = {Kw}")
     if act == 2 and N % 2:
         raise ValueError("SwiGLU needs an even number of weight rows (value, gate pairs)")
-    _check(C, "C", M, N // 2 if act == 2 else N, device=dev)
+    # the backward codes: cin is the saved pre-activation, 2N wide (pairs) for SwiGLU's
+    width = 2 * N if act == 4 else N
+    if act >= 3 and (cin is None or row_scale is not None or pre is not None):
+        raise ValueError(f"act {act}: cin (the pre-activation) is required, row_scale and pre are not taken")
+    _check(C, "C", M, N // 2 if act == 2 else width, device=dev)
     if row_scale is not None:
         _check(row_scale, "row_scale", M, vector=True, device=dev)
     if bias is not None:
-        _check(bias, "bias", N, vector=True, device=dev)
+        _check(bias, "bias", width, vector=True, device=dev)
     if cin is not None:
-        _check(cin, "cin", M, N, device=dev)
+        _check(cin, "cin", M, width, device=dev)
     if pre is not None:
         _check(pre, "pre", M, N, device=dev)
     p = lambda t: None if t is None else t.data_ptr()
@@ -99,7 +103,10 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
 
 def fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
     """C = act(row_scale * (A W^T) + bias + beta cin), pre = the value before
-    act; act 0 none, 1 SiLU, 2 SwiGLU (C [M, N/2]). W a tensor or SplitWeights."""
+    act; act 0 none, 1 SiLU, 2 SwiGLU (C [M, N/2]). W a tensor or SplitWeights.
+    act 3 / 4: A W^T is the adjoint of a SiLU / SwiGLU output and cin its saved
+    pre-activation z (bias z's bias if not yet in it): C = adjoint silu'(z), or
+    for SwiGLU (z and C [M, 2N], (value, gate) pairs) each pair's adjoint."""
     _call(A, W, C, row_scale, bias, cin, beta, pre, act)
 
 

@@ -1,7 +1,7 @@
 """The fused dense layer (pet_linear_fused, csrc/gemm.hip) against float64
 matrix products of the same fp32 inputs, for every epilogue: a row scale (the
 RMSNorm fold), a bias, a residual accumulated in place, the kept
-pre-activation, SiLU and SwiGLU. Tolerance 1e-5 of the largest output
+pre-activation, SiLU and SwiGLU, and their backward (act 3, 4). Tolerance 1e-5 of the largest output
 magnitude (fp32 sums over K <= 1024); runs repeat bit for bit. The same for
 its split-product form (pet_linear_fused_split over weights split by
 pet_linear_split_weights), whose split is checked exactly: three bf16 parts
@@ -79,6 +79,51 @@ def test_epilogues(split, device):
     ref = z[:, 0::2] * torch.sigmoid(z[:, 1::2])
     assert (C.double() - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
     assert (pre.double() - z).abs().max().item() <= 1e-5 * z.abs().max().item()
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
+@pytest.mark.parametrize("M,N,K", [(300, 128, 128), (16385, 512, 256)])
+def test_backward_epilogues(M, N, K, split, device):
+    """act 3 / 4: the SiLU / SwiGLU backward fused into the input-adjoint
+    product (A W^T is the activation output's adjoint, cin the saved
+    pre-activation, bias its bias when not yet added), against float64."""
+    g = torch.Generator(device=device).manual_seed(M + N)
+    A = torch.randn(M, K, device=device, generator=g)
+    W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
+    v = A.double() @ W.double().T
+    for with_bias in (False, True):
+        # SiLU: C = v silu'(z), z = cin (+ bias)
+        z = 3.0 * torch.randn(M, N, device=device, generator=g)
+        b = torch.randn(N, device=device, generator=g) if with_bias else None
+        zz = z.double() + (b.double() if with_bias else 0.0)
+        sg = torch.sigmoid(zz)
+        ref = v * (sg * (1.0 + zz * (1.0 - sg)))
+        C = torch.empty(M, N, device=device)
+        linear_fused(A, W, C, bias=b, cin=z, act=3, split=split)
+        assert (C.double() - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
+        C2 = torch.empty_like(C)
+        linear_fused(A, W, C2, bias=b, cin=z, act=3, split=split)
+        assert torch.equal(C, C2)
+        # SwiGLU: z [M, 2N] of (value u, gate g) pairs; C [M, 2N] their adjoints
+        z2 = 3.0 * torch.randn(M, 2 * N, device=device, generator=g)
+        b2 = torch.randn(2 * N, device=device, generator=g) if with_bias else None
+        zz = z2.double() + (b2.double() if with_bias else 0.0)
+        u, sg = zz[:, 0::2], torch.sigmoid(zz[:, 1::2])
+        ref = torch.empty(M, 2 * N, dtype=torch.float64, device=device)
+        ref[:, 0::2] = v * sg
+        ref[:, 1::2] = v * u * sg * (1.0 - sg)
+        C = torch.empty(M, 2 * N, device=device)
+        linear_fused(A, W, C, bias=b2, cin=z2, act=4, split=split)
+        assert (C.double() - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
+    A, W, C = torch.zeros(8, 32, device=device), torch.zeros(8, 32, device=device), torch.zeros(8, 8, device=device)
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, act=3, split=split)  # no pre-activation
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, cin=C, act=4, split=split)  # SwiGLU's C and cin are 2N wide
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, cin=C, pre=C, act=3, split=split)  # no pre taken
+    with pytest.raises(ValueError):
+        linear_fused(A, W, C, cin=C, act=5, split=split)
 
 
 def test_rejects(device):

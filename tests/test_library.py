@@ -62,6 +62,25 @@ def test_error_codes_without_device():
         assert _lib.strerror(code)
 
 
+def test_linear_epilogue_arguments_without_device():
+    """The dense layer's argument checks return before any device work: the
+    backward epilogues (act 3, 4) need cin, take no row scale or pre, and
+    read and write 2N columns for SwiGLU."""
+    lib = _lib.load()
+    A, Ws, C, z = 4096, 8192, 16384, 32768  # stand-in addresses: nothing is launched on a rejection
+    for fn, w in ((lib.pet_linear_fused, (Ws, 32)), (lib.pet_linear_fused_split, (Ws,))):
+        def call(ldc, cin, ldcin, act, rs=None, pre=None):
+            args = [8, 8, 32, A, 32, *w, C, ldc, rs, None, cin, ldcin, 0.0, pre, 8, act, None]
+            return fn(*args)
+        assert call(8, None, 0, 3) == _lib.EINVAL  # no pre-activation
+        assert call(8, z, 8, 4) == _lib.EINVAL  # SwiGLU's cin and C are 2N = 16 wide
+        assert call(16, z, 8, 4) == _lib.EINVAL
+        assert call(8, z, 8, 3, rs=z) == _lib.EINVAL  # no row scale
+        assert call(8, z, 8, 3, pre=z) == _lib.EINVAL  # no pre
+        assert call(8, z, 8, 5) == _lib.EINVAL
+        assert call(8, z, 8, -1) == _lib.EINVAL
+
+
 def test_error_raises():
     with pytest.raises(_lib.PetAttnError):
         _lib.check(_lib.EHEADDIM, "x")
