@@ -32,17 +32,21 @@ sys.path.insert(0, ROOT)
 
 METRIC = "µs per attention fwd+bwd and ms per E+F eval (1 GPU), % of HBM/MFMA roofline"
 PEAK_FP32_MFMA = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
-PEAK_BF16_MFMA = 2.5e15  # FLOP/s, MI355X dense bf16 matrix
+PEAK_BF16_MFMA = 2.5e15  # FLOP/s, MI355X dense bf16 (and fp16) matrix
 # an fp32 product as six bf16 products (the split-fp32 scheme): fp32 FLOP/s
 PEAK_SPLIT_FP32 = PEAK_BF16_MFMA / 6
+# an fp32 product as three fp16 products (the fp16-pair scheme)
+PEAK_PAIR_FP32 = PEAK_BF16_MFMA / 3
 PEAK_HBM = 8.0e12  # B/s
 
 
-def mixed_seconds(flops, split_share):
+def mixed_seconds(flops, split_share, pair_share=0.0):
     """Time at the matrix-core ceilings of the instructions that run: the
     split_share of the FLOPs as split-fp32 products on the bf16 matrix cores
-    (2.5 PFLOP/s / 6), the rest on the fp32 matrix cores (157.3 TFLOP/s)."""
-    return flops * ((1.0 - split_share) / PEAK_FP32_MFMA + split_share / PEAK_SPLIT_FP32)
+    (2.5 PFLOP/s / 6), the pair_share as fp16-pair products (2.5 PFLOP/s / 3),
+    the rest on the fp32 matrix cores (157.3 TFLOP/s)."""
+    rest = 1.0 - split_share - pair_share
+    return flops * (rest / PEAK_FP32_MFMA + split_share / PEAK_SPLIT_FP32 + pair_share / PEAK_PAIR_FP32)
 
 
 def split_shares(plan):
@@ -122,7 +126,8 @@ def time_rows(args, conf, tk, x, w_in, b_in, w_out, b_out, dm, off, cf, device):
         L.attention_layer_bwd(ws, "b", tadj, ca, dm, x, nw, None, w_in, b_in, cf, w_out, tkd, S, H, hd, 1.0)), reps)
     out["layer_note"] = ("attention block of a PET layer: RMSNorm, QKV linear, attention, output linear, and the "
                          "backward (rebuilt norm and QKV, attention_bwd, norm backward into the token adjoint); "
-                         "its dense products on the split-product kernel (fp32 accuracy on the bf16 matrix cores)")
+                         "its dense products on the split-product kernel (fp32 accuracy on the 16-bit matrix cores: fp16 pairs "
+                         "from K = 256, bf16 parts below)")
     cfgs = systems.CONFIGS[args.config]
     s = systems.build_structure(cfgs.structure, 0)
     pk = systems.packed_edges(len(s.positions), systems.neighbor_list(s, cfgs.cutoff), cfgs.cutoff, cfgs.width)
@@ -203,16 +208,17 @@ def time_ef(device, reps, cpu: bool):
         fl = ef_flops(h, x.n_atoms, x.n_edges, float((cnt * cnt).sum()))
         n = max(3, reps // (5 if name != "c5" else 20))
         # contraction bound at the ceilings of the instructions that run: the
-        # large dense products as split-fp32 on the bf16 matrix cores, the rest
-        # (small products, the attention at head_dim 64) on the fp32 ones
-        bound_ms = mixed_seconds(fl["forces"], fl["split"] / fl["forces"]) * 1e3
+        # large dense products as fp16 pairs or bf16 parts on the 16-bit matrix
+        # cores, the rest (small products, the attention at head_dim 64) on the
+        # fp32 ones
+        bound_ms = mixed_seconds(fl["forces"], fl["split"] / fl["forces"], fl["pair"] / fl["forces"]) * 1e3
         o = m.compute(x, True)
         e_ms = _timed(lambda: m.compute(x, False, out=o), n) / 1e3
         ef_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
         res[name] = dict(featurizer=h.featurizer, structures=len(sts), atoms=x.n_atoms, edges=x.n_edges,
                          d_pet=h.d_pet, heads=h.num_heads, ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
                          ef_bound_ms=bound_ms, ef_frac_of_roofline=bound_ms / ef_ms,
-                         ef_split_share=fl["split"] / fl["forces"],
+                         ef_split_share=fl["split"] / fl["forces"], ef_pair_share=fl["pair"] / fl["forces"],
                          workspace_gb=m.workspace_bytes / 1e9)
         if name in ("c2", "c2-residual") and cpu:
             cpu_cases.append((name, h, w, comp, x.species.cpu().numpy(), x.host))
@@ -382,11 +388,13 @@ def main():
         s1.record()
         torch.cuda.synchronize()
         extra["op_level_us"] = s0.elapsed_time(s1) * 1e3 / reps
-        # its contraction bound: the core's, plus the output linear (2 T D^2),
-        # dmerged (2 T D^2) and the input adjoint (6 T D^2), each on the
-        # split-product kernel where it is large enough, else rocBLAS fp32
+        # its contraction bound: the core's, plus the output linear (2 T D^2,
+        # W_out split as it is staged: bf16 parts), dmerged (2 T D^2, K = D) and
+        # the input adjoint (6 T D^2, K = 3D), each on the split-product kernel
+        # where it is large enough (fp16 pairs from K = 256), else rocBLAS fp32
         big = T * D * D >= 2 ** 32
-        gemm_s = mixed_seconds(10.0 * T * D * D, 1.0 if big else 0.0)
+        pair = (2.0 * (D >= 256) + 6.0 * (3 * D >= 256)) / 10.0 if big else 0.0
+        gemm_s = mixed_seconds(10.0 * T * D * D, (1.0 - pair) if big else 0.0, pair)
         extra["op_level_bound_us"] = (core_mfma_s + gemm_s) * 1e6
         extra["op_level_frac_of_roofline"] = extra["op_level_bound_us"] / extra["op_level_us"]
         extra["op_level_note"] = ("attention()+attention_bwd(): core + the output linear (split-product kernel, W_out "

@@ -121,12 +121,16 @@ PET_ATTN_API int pet_linear_fused(int M, int N, int K, const float* A, int64_t l
                                   float* C, int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                   int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
 
-/* The same dense layer with its products on the bf16 matrix cores at fp32
- * accuracy (each fp32 operand split into three bf16 parts, the six part
- * products whose order sum is at most 2 accumulated in fp32; error at or below
- * the fp32 instruction's). W is given split once by pet_linear_split_weights:
- * W [N, K] (ld ldw, K a multiple of 32) into out, N * K * 6 bytes, 16-byte
- * aligned. pet_linear_fused_split then takes the split W in place of W and
+/* The same dense layer with its products on the 16-bit matrix cores at fp32
+ * accuracy; error at or below the fp32 instruction's. From K = 256 each row of
+ * A and of W is scaled by a power of two and each element split into two fp16
+ * parts (22 of its 24 significand bits), three part products accumulated in
+ * fp32 and the scales undone in the epilogue; below K = 256 each fp32 operand
+ * is split into three bf16 parts, the six part products whose order sum is at
+ * most 2 accumulated in fp32. W is given split once by
+ * pet_linear_split_weights: W [N, K] (ld ldw, K a multiple of 32) into out, at
+ * most N * K * 6 bytes (N * K * 4 + N * 4 from K = 256), 16-byte aligned; the
+ * form follows K, so a split copy always matches the product that reads it. pet_linear_fused_split then takes the split W in place of W and
  * ldw, K a multiple of 32, otherwise as pet_linear_fused; results repeat bit
  * for bit. No counterpart in the reference, which runs its dense layers in
  * fp32 (src/fused_gemm_hip.cpp); a faster form of pet_linear_fused. */

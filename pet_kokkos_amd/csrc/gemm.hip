@@ -23,7 +23,9 @@
 // order is fixed: results repeat bit for bit).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <type_traits>
 #include <cstdlib>
 
 #include "../../include/pet_model.h"
@@ -214,7 +216,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
                                                                        const float* __restrict__ A, int64_t lda,
                                                                        const u4* __restrict__ Bs, float* C,
                                                                        int64_t ldc, Epi epi,
-                                                                       const float* __restrict__ Bf, int64_t ldb) {
+                                                                       const float* __restrict__ Bf, int64_t ldb,
+                                                                       int /* one tile an item */) {
   constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 14;
   constexpr int AQ = BM * 8, AL = (AQ + T - 1) / T;   // float4 of a step's A slice, a thread's share
   constexpr int BQ = BF ? BN * 8 : BN * 12, BL = (BQ + T - 1) / T;  // B slice: float4 (BF) or u4 slots
@@ -352,9 +355,274 @@ __global__ void split_rows_kernel(const float* __restrict__ W, int N, int K, int
   for (int p = 0; p < 3; ++p) out[t * 3 + p] = parts[p];
 }
 
+// ---- fp32 products from fp16 pairs on the 16-bit matrix cores --------------
+// A row of a matrix, scaled by a power of two s that puts its largest |x| in
+// [2^14, 2^15), splits into two fp16 values per element: hi = x s with its
+// low 13 significand bits cleared (its leading 11 bits, exact in fp16) and
+// lo = x s - hi (exact in fp32) rounded to the nearest fp16. hi + lo holds 22
+// of x's 24 significand bits, the rounding of lo within 2^-22 |x| (and within
+// 2^-37 of the row's largest element where x s leaves fp16's normal range). A product a.b over k is then (a_hi b_hi + a_hi b_lo + a_lo b_hi) /
+// (s_a s_b) with the three part products accumulated in fp32 by
+// v_mfma_f32_16x16x32_f16 and the scales undone in the epilogue; the dropped
+// a_lo b_lo is below 2^-22 |a||b|. Measured error on fp32 operands spread over
+// many octaves per row: 2.9e-8 of sum |a_k b_k| before the fp32 accumulation
+// (three bf16 parts with six products: 2.1e-8; the fp32 instruction's
+// accumulation alone: 1.6e-7). Three matrix instructions where the bf16 form
+// takes six.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f4 mfma_h(const u4& a, const u4& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+// c += a.b from (hi, lo) parts, the small products first
+__device__ __forceinline__ f4 mfma3(const u4* a, const u4* b, f4 c) {
+  c = mfma_h(a[1], b[0], c);
+  c = mfma_h(a[0], b[1], c);
+  return mfma_h(a[0], b[0], c);
+}
+// two scaled values as a register of hi parts and a register of lo parts
+__device__ __forceinline__ void pair2(float x, float y, unsigned& hi, unsigned& lo) {
+  const float hx = __uint_as_float(__float_as_uint(x) & 0xffffe000u);
+  const float hy = __uint_as_float(__float_as_uint(y) & 0xffffe000u);
+  hi = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(hx, hy));  // exact
+  const h2v l = {(_Float16)(x - hx), (_Float16)(y - hy)};                 // to nearest
+  lo = __builtin_bit_cast(unsigned, l);
+}
+// The row scale 2^(15 - e) for a largest |x| m = f 2^e (f in [0.5, 1)); 1 for
+// a zero row (and for one holding a NaN, which then propagates).
+__device__ __forceinline__ float pair_scale(float m) {
+  if (!(m > 0.f) || m > 3.0e38f) return 1.f;
+  const int e = __builtin_amdgcn_frexp_expf(m);
+  return __builtin_amdgcn_ldexpf(1.f, min(15 - e, 126));
+}
+
+// C = epi(A B^T) with B as fp16 pairs made once (pair_rows_kernel:
+// per row, per 8-element k group, its hi and lo parts, 32 bytes, then the
+// rows' inverse scales) and A split as each k step of 32 is staged, after a
+// first pass over the tile's rows for their scales. Tiles of WGM x WGN waves
+// (64 WGM WGN threads): 64 x 64 or 128 x 64 of 2 x 2, 128 x 128 of 2 x 4. K
+// steps of 32 go through one LDS buffer, the next step's slices loaded into
+// registers under the current step's products. A row's step is 4 groups x 2
+// parts x 16 bytes plus a 16-byte pad (9 u4: 16 consecutive rows' 128-bit
+// operand reads fall on distinct banks). K a multiple of 32.
+//
+// BF: B comes as fp32 rows [N, K] (ld ldb) and is split as it is staged, like
+// A (for a caller with no room to keep a split copy), its row scales from the
+// same first pass.
+template <int BM, int BN, int WGM = 2, int WGN = 2, bool BF = false>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_pair_kernel(int M, int N, int K,
+                                                                       const float* __restrict__ A, int64_t lda,
+                                                                       const u4* __restrict__ Bs, float* C,
+                                                                       int64_t ldc, Epi epi,
+                                                                       const float* __restrict__ Bf, int64_t ldb,
+                                                                       int cpw) {
+  constexpr int T = 64 * WGM * WGN, NW = T / 64, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 9;
+  constexpr int AL = BM * 8 / T;  // float4 of a step's A slice, a thread's share
+  constexpr int BL = BN * 8 / T;  // B slice: float4 (BF) or u4 slots, a thread's share
+  static_assert(AL * T == BM * 8 && BL * T == BN * 8, "a step's slices divide evenly over the threads");
+  __shared__ u4 As[BM * RP], Bt[BN * RP];
+  __shared__ float sa[BM], sb[BF ? BN : 1];  // row scales of the tile's A rows (and B rows with BF)
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  const int wm = w / WGN, wn = w % WGN;
+  // Workgroups go to the 8 XCDs in turn (an L2 each): XCD k takes a
+  // contiguous run of tiles in row-block order, so a row block's column tiles
+  // share an L2 (509730 x 512 x 512: 1547 against 1624 us in launch order).
+  // A bijection of the tiles whatever the hardware's order.
+  // A 1-D grid of work items, item t = (row block t / NG, its column tiles
+  // cpw (t % NG) .. in turn): the A rows' scales are found once for cpw tiles.
+  const int NT = (N + BN - 1) / BN, NG = (NT + cpw - 1) / cpw, total = gridDim.x, L = blockIdx.x;
+  const int q = total / 8, r = total % 8, x = L % 8;
+  const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + L / 8;
+  const int tm = t / NG, tn0 = (t % NG) * cpw, tn1 = min(tn0 + cpw, NT);
+  const int m0 = tm * BM, KG = K / 8;
+  int n0 = tn0 * BN;
+
+  // The first pass: wave w takes rows w, w + NW, ..., a float4 a lane along
+  // k, all its rows' loads in flight together, then each row's largest |x|
+  // reduced over the wave. Rows past M (N) read the last row: their results
+  // are never stored.
+  auto row_scales = [&](const float* X, int64_t ldx, int rows, auto nr, float* s) {
+    constexpr int RW = decltype(nr)::value / NW, RB = RW < 8 ? RW : 8;  // rows a wave, a batch
+#pragma unroll
+    for (int j0 = 0; j0 < RW; j0 += RB) {
+      unsigned o[RB];  // row offsets from X (a tile's rows: within 2^32 floats)
+      float m[RB];
+#pragma unroll
+      for (int j = 0; j < RB; ++j) o[j] = unsigned(min(w + NW * (j0 + j), rows - 1)) * unsigned(ldx), m[j] = 0.f;
+      for (int k = 4 * l; k < K; k += 256) {
+        float4 v[RB];
+#pragma unroll
+        for (int j = 0; j < RB; ++j) v[j] = *reinterpret_cast<const float4*>(X + o[j] + k);
+#pragma unroll
+        for (int j = 0; j < RB; ++j)
+          m[j] = fmaxf(m[j], fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+      }
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m[j] = fmaxf(m[j], __shfl_xor(m[j], o));
+        if (l == 0) s[w + NW * (j0 + j)] = pair_scale(m[j]);
+      }
+    }
+  };
+  row_scales(A + int64_t(m0) * lda, lda, M - m0, std::integral_constant<int, BM>(), sa);
+  __syncthreads();
+
+  // A: thread t's float4 slots q = t + T u, row q / 8, k 4 (q % 8) .. ;
+  // B: u4 slots q, row q / 8, part (q % 8) of the row's step
+  float4 ra[AL];
+  float rsa[AL];
+  u4 rb[BF ? 1 : BL];
+  float4 rbf[BF ? BL : 1];
+  float rsb[BF ? BL : 1];
+  const float* pa[AL];
+#pragma unroll
+  for (int u = 0; u < AL; ++u) {
+    const int qq = tid + T * u;
+    pa[u] = A + int64_t(min(m0 + qq / 8, M - 1)) * lda + 4 * (qq % 8);
+    rsa[u] = sa[qq / 8];
+  }
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < AL; ++u) ra[u] = *reinterpret_cast<const float4*>(pa[u] + k0);
+#pragma unroll
+    for (int u = 0; u < BL; ++u) {
+      const int qq = tid + T * u, j = min(n0 + qq / 8, N - 1);
+      if constexpr (BF)
+        rbf[u] = *reinterpret_cast<const float4*>(Bf + int64_t(j) * ldb + k0 + 4 * (qq % 8));
+      else
+        rb[u] = Bs[(int64_t(j) * KG + k0 / 8) * 2 + qq % 8];
+    }
+  };
+  // a float4 of row `row`'s k slots 4 (q % 8) .. , scaled by s, into its
+  // row's hi and lo parts of k group (q % 8) / 2, half q & 1, of tile X
+  auto store_pair = [&](u4* X, int row, int qq, const float4& v, float s) {
+    unsigned h0, l0, h1, l1;
+    pair2(v.x * s, v.y * s, h0, l0);
+    pair2(v.z * s, v.w * s, h1, l1);
+    unsigned* dst = reinterpret_cast<unsigned*>(&X[row * RP + ((qq % 8) / 2) * 2]) + 2 * (qq & 1);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(h0, h1);
+    *reinterpret_cast<uint2*>(dst + 4) = make_uint2(l0, l1);
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int u = 0; u < AL; ++u) {
+      const int qq = tid + T * u;
+      store_pair(As, qq / 8, qq, ra[u], rsa[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < BL; ++u) {
+      const int qq = tid + T * u;
+      if constexpr (BF)
+        store_pair(Bt, qq / 8, qq, rbf[u], rsb[u]);
+      else
+        Bt[(qq / 8) * RP + qq % 8] = rb[u];
+    }
+  };
+
+  const int steps = K / 32;
+  for (int tn = tn0; tn < tn1; ++tn) {
+  n0 = tn * BN;
+  if constexpr (BF) {
+    row_scales(Bf + int64_t(n0) * ldb, ldb, N - n0, std::integral_constant<int, BN>(), sb);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < BL; ++u) rsb[u] = sb[(tid + T * u) / 8];
+  }
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  store();
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    if (s + 1 < steps) load((s + 1) * 32);
+    u4 av[TM][2], bv[TN][2];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) av[a][p] = As[(wm * WM + 16 * a + c) * RP + 2 * g + p];
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) bv[b][p] = Bt[(wn * WN + 16 * b + c) * RP + 2 * g + p];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b) acc[a][b] = mfma3(av[a], bv[b], acc[a][b]);
+    if (s + 1 < steps) {
+      __syncthreads();  // every wave is done with the step's slices
+      store();
+      __syncthreads();
+    }
+  }
+  // the scales undone: rows 4g + r of each 16-row block (from LDS), this
+  // lane's columns (from the split weights' inverse scales, or LDS with BF)
+  const float* inv_b = reinterpret_cast<const float*>(Bs + int64_t(N) * KG * 2);
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const int jj = wn * WN + 16 * b + c;
+    const float ib = BF ? 1.f / sb[jj] : inv_b[min(n0 + jj, N - 1)];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) acc[a][b][rr] = acc[a][b][rr] * (1.f / sa[wm * WM + 16 * a + 4 * g + rr]) * ib;
+  }
+  // (m0 laundered per tile: the epilogue's row addresses are then made
+  // here, not hoisted out of the tile loop into registers held across it)
+  int m0t = m0;
+  asm volatile("" : "+s"(m0t));
+  epilogue<WM, WN>(acc, m0t, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  __syncthreads();  // the next tile's first slices overwrite this one's last
+  }
+}
+
+// Rows of B = W (transposed false: W [N, K], ld ldw) or B = W^T (transposed
+// true: W [K, N]) as fp16 pairs: out[(n K/8 + j) 2 + p] = part p (hi, lo) of
+// row n's k group j, scaled by the row's s_n; then at byte N K 4 the N
+// inverse scales 1 / s_n. One workgroup a row: its largest |x|, then its
+// groups.
+__global__ void __launch_bounds__(256) pair_rows_kernel(const float* __restrict__ W, int N, int K, int64_t ldw,
+                                                         bool transposed, u4* __restrict__ out) {
+  __shared__ float red[4];
+  const int n = blockIdx.x, tid = threadIdx.x, KG = K / 8;
+  auto at = [&](int k) { return transposed ? W[int64_t(k) * ldw + n] : W[int64_t(n) * ldw + k]; };
+  float m = 0.f;
+  for (int k = tid; k < K; k += 256) m = fmaxf(m, fabsf(at(k)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  const float s = pair_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  for (int j = tid; j < KG; j += 256) {
+    u4 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      unsigned h, lw;
+      pair2(at(8 * j + 2 * e) * s, at(8 * j + 2 * e + 1) * s, h, lw);
+      hi[e] = h, lo[e] = lw;
+    }
+    out[(int64_t(n) * KG + j) * 2] = hi;
+    out[(int64_t(n) * KG + j) * 2 + 1] = lo;
+  }
+  if (tid == 0) reinterpret_cast<float*>(out + int64_t(N) * KG * 2)[n] = 1.f / s;
+}
+
 }  // namespace pet_gemm
 
 using namespace pet_gemm;
+
+// Which split a K takes: fp16 pairs from K = 256 (three matrix instructions a
+// product where the bf16 form takes six, and a first pass over A's rows for
+// their scales, which pays once the K loop is long enough: measured 131072 x
+// 1536 x 512 908-923 against 1220 us, 122688 x 768 x 256 289 against 345 us,
+// but 26670 x 1024 x 128 78 against 70 us), three bf16 parts below. The
+// weights' split and the product both follow it, so a split copy matches the
+// kernel that reads it.
+static bool pair_form(int K) { return K >= 256; }
 
 // The tile shape for a problem: wide outputs take 128 x 128; narrow ones
 // (N <= 64) or too few tiles to fill 256 CUs take smaller tiles.
@@ -423,10 +691,17 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
   Epi e;
   e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
   e.act = act;
-  auto go = [&](auto kern, int bm, int bn, int threads) {  // a 1-D grid of every tile
-    const int64_t tiles = int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    hipLaunchKernelGGL(kern, dim3(unsigned(tiles)), dim3(threads), 0, st, M, N, K, A, lda,
-                       static_cast<const u4*>(Bs), C, ldc, e, static_cast<const float*>(nullptr), int64_t(0));
+  auto go = [&](auto kern, int bm, int bn, int threads, bool pair) {  // a 1-D grid of every work item
+    const int64_t rb = (M + bm - 1) / bm, nt = (N + bn - 1) / bn;
+    // column tiles per item (pair kernel): about 2048 items, four rounds of
+    // two workgroups a CU (the rows' scales are found once an item; measured
+    // against 1024, 1536 and 3072 items: 131072 x 1536 x 512 842 against
+    // 883-850 us, 131072 x 512 x 2048 1062 against 1203-1055 us)
+    const int64_t c0 = pair ? std::max<int64_t>(1, std::min<int64_t>(nt, rb * nt / 2048)) : 1;
+    const int64_t ng = (nt + c0 - 1) / c0, cpw = (nt + ng - 1) / ng;
+    hipLaunchKernelGGL(kern, dim3(unsigned(rb * ((nt + cpw - 1) / cpw))), dim3(threads), 0, st, M, N, K, A, lda,
+                       static_cast<const u4*>(Bs), C, ldc, e, static_cast<const float*>(nullptr), int64_t(0),
+                       int(cpw));
   };
   // measured on MI355X: 128 x 128 tiles of 8 waves where there are many
   // (131072 x 1536 x 512: 1200-1213 us against 1394-1418 for 128 x 64 and
@@ -434,12 +709,21 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
   // faster), 64 x 64 otherwise (27318 x 128 x 128: 16.1 against 18.4 us); one
   // LDS buffer beat two in every shape
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
-  if (N >= 128 && t128 >= 2048)
-    go(gemm_nt_split_kernel<128, 128, 2, 4>, 128, 128, 512);
-  else if (t128 >= 2048)
-    go(gemm_nt_split_kernel<128, 64>, 128, 64, 256);
-  else
-    go(gemm_nt_split_kernel<64, 64>, 64, 64, 256);
+  if (pair_form(K)) {
+    if (N >= 128 && t128 >= 2048)
+      go(gemm_nt_pair_kernel<128, 128, 2, 4>, 128, 128, 512, true);
+    else if (t128 >= 2048)
+      go(gemm_nt_pair_kernel<128, 64>, 128, 64, 256, true);
+    else
+      go(gemm_nt_pair_kernel<64, 64>, 64, 64, 256, true);
+  } else {
+    if (N >= 128 && t128 >= 2048)
+      go(gemm_nt_split_kernel<128, 128, 2, 4>, 128, 128, 512, false);
+    else if (t128 >= 2048)
+      go(gemm_nt_split_kernel<128, 64>, 128, 64, 256, false);
+    else
+      go(gemm_nt_split_kernel<64, 64>, 64, 64, 256, false);
+  }
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -460,7 +744,7 @@ int pet_gemm_nt_split_f32b(int M, int N, int K, const float* A, int64_t lda, con
   auto go = [&](auto kern, int bm, int bn, int threads) {
     const int64_t tiles = int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     hipLaunchKernelGGL(kern, dim3(unsigned(tiles)), dim3(threads), 0, st, M, N, K, A, lda, nullptr, C, ldc, e, B,
-                       ldb);
+                       ldb, 1);
   };
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
   if (N >= 128 && t128 >= 2048)
@@ -478,7 +762,10 @@ int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool trans
   if (N < 0 || K < 0 || K % 32 || (reinterpret_cast<uintptr_t>(out) & 15)) return PET_ATTN_EINVAL;
   const int64_t n = int64_t(N) * (K / 8);
   if (n == 0) return PET_ATTN_OK;
-  if (transposed)
+  if (pair_form(K))
+    hipLaunchKernelGGL(pair_rows_kernel, dim3(unsigned(N)), dim3(256), 0, st, W, N, K, ldw, transposed,
+                       static_cast<u4*>(out));
+  else if (transposed)
     hipLaunchKernelGGL(split_rows_t_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, W, N, K, ldw,
                        static_cast<u4*>(out));
   else
@@ -492,9 +779,7 @@ extern "C" int pet_linear_split_weights(const float* W, int N, int K, int64_t ld
   if (reinterpret_cast<uintptr_t>(out) & 15) return PET_ATTN_EALIGN;
   const int64_t n = int64_t(N) * (K / 8);
   if (n == 0) return PET_ATTN_OK;
-  hipLaunchKernelGGL(split_rows_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), W, N, K, ldw, static_cast<u4*>(out));
-  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+  return pet_gemm_split_weights(W, N, K, ldw, false, out, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pet_linear_split_weights_transposed(const float* W, int N, int K, int64_t ldw, void* out,

@@ -1417,7 +1417,7 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
                                 ld.shapes[i].second};
     }
     if (hipMemcpy(md->weights, host.data(), total, hipMemcpyHostToDevice) != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
-    // split-row copies (6 bytes an element) of the matrices whose K is a
+    // split-row copies (at most 6 bytes an element) of the matrices whose K is a
     // multiple of 32, for the split-product dense layers
     size_t stotal = 0;
     std::vector<std::pair<const Mat*, size_t>> sat;

@@ -17,8 +17,10 @@ from . import _lib
 
 
 class SplitWeights:
-    """W [N, K] (K a multiple of 32) as its three bf16 parts, N K 6 bytes of
-    device memory: made once, then used in place of W by every call."""
+    """W [N, K] (K a multiple of 32) split for the 16-bit matrix cores (fp16
+    pairs of power-of-two-scaled rows from K = 256, three bf16 parts below),
+    at most N K 6 bytes of device memory: made once, then used in place of W
+    by every call."""
 
     def __init__(self, W: torch.Tensor, transposed: bool = False):
         """transposed: the split of W^T, from W [K, N] as it is stored."""

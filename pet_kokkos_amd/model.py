@@ -265,24 +265,35 @@ def ef_gemms(h: Hypers, n_atoms: int, n_edges: int) -> list:
 
 
 # The model's dense products with M N K >= 2^32 run on the split-product kernel
-# by default (fp32 accuracy, six bf16 products on the bf16 matrix cores); the
-# rest on rocBLAS fp32.
+# by default (fp32 accuracy on the 16-bit matrix cores: from K = 256 as fp16
+# pairs, three products; below as three bf16 parts, six products); the rest on
+# rocBLAS fp32.
 SPLIT_THRESHOLD = 2.0 ** 32
+PAIR_MIN_K = 256
 
 
 def ef_flops(h: Hypers, n_atoms: int, n_edges: int, sum_cnt2: float) -> dict:
     """Algorithmic FLOPs of one evaluation: 2 M N K per dense layer forward and
-    once more for its input adjoint (forces need no weight gradients), the
-    attention's 4 (forward) and 10 (backward) sum(cnt^2) D per block; and the
-    part of the forces FLOPs in dense products large enough for the
-    split-product kernel ("split")."""
+    once more for its input adjoint (M K N: forces need no weight gradients),
+    the attention's 4 (forward) and 10 (backward) sum(cnt^2) D per block; and
+    the parts of the forces FLOPs in dense products large enough for the
+    split-product kernel, as fp16 pairs ("pair", contraction length >= 256)
+    or bf16 parts ("split")."""
     gm = ef_gemms(h, n_atoms, n_edges)
     g = float(sum(m * n * k for m, n, k in gm))
-    big = float(sum(m * n * k for m, n, k in gm if float(m) * n * k >= SPLIT_THRESHOLD))
+    pair = split = 0.0
+    for m, n, k in gm:
+        if float(m) * n * k < SPLIT_THRESHOLD:
+            continue
+        for kk in (k, n):  # the forward's contraction, then the adjoint's
+            if kk >= PAIR_MIN_K:
+                pair += 2.0 * m * n * k
+            else:
+                split += 2.0 * m * n * k
     blocks = h.num_gnn_layers * h.num_attention_layers
     D = h.d_pet
     return dict(energy=2.0 * g + blocks * 4.0 * sum_cnt2 * D,
-                forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D, split=4.0 * big)
+                forces=4.0 * g + blocks * 14.0 * sum_cnt2 * D, split=split, pair=pair)
 
 
 def ef_workload(name: str, seed: int = 0):

@@ -205,6 +205,45 @@ def test_split_weights_exact(device):
     assert np.all(np.abs(parts[:, :, 1, :]) <= np.abs(w) * 2.0 ** -7)
 
 
+@pytest.mark.parametrize("transposed", [False, True], ids=["W", "W^T"])
+def test_pair_weights_exact(transposed, device):
+    """From K = 256 the split is fp16 pairs: per row a power-of-two scale s
+    with max |w| s in [2^14, 2^15), then per 8-element k group a hi part (w s
+    with its low 13 significand bits cleared, exact in fp16) and a lo part
+    (the rest, rounded to the nearest fp16: hi + lo within 2^-22 |w s|, or
+    1.5 fp16 subnormal steps below fp16's normal range), and after the N K 4 bytes of parts the rows' 1 / s.
+    The split of W^T from W equals that of W^T made contiguous."""
+    N, K = 40, 256
+    g = torch.Generator(device=device).manual_seed(6)
+    W = torch.randn(N, K, device=device, generator=g) * torch.logspace(-12, 12, K, device=device)
+    W[3] *= 1e-30  # a row far below fp16's range before scaling
+    W[5] = 0.0  # a zero row
+    if transposed:
+        Wt = W.t().contiguous()
+        data = L.SplitWeights(Wt, transposed=True).data
+        used = (N * K * 4 + 4 * N) // 2  # int16 elements written (the buffer is sized for the bf16 form)
+        assert torch.equal(data[:used], split_weights(W).data[:used])
+    else:
+        data = split_weights(W).data
+    raw = data.cpu().numpy().view(np.uint8)
+    parts = raw[: N * K * 4].view(np.float16).reshape(N, K // 8, 2, 8).astype(np.float64)
+    inv = raw[N * K * 4: N * K * 4 + 4 * N].view(np.float32).astype(np.float64)
+    w = W.cpu().numpy().astype(np.float64).reshape(N, K // 8, 8)
+    s = 1.0 / inv
+    assert np.array_equal(np.exp2(np.round(np.log2(s))), s)  # powers of two
+    m = np.abs(w).reshape(N, K).max(1)
+    live = m > 0
+    assert np.all((m[live] * s[live] >= 2.0 ** 14) & (m[live] * s[live] < 2.0 ** 15))
+    assert s[5] == 1.0 and np.all(parts[5] == 0)
+    ws = w * s[:, None, None]
+    hi, lo = parts[:, :, 0, :], parts[:, :, 1, :]
+    normal = np.abs(ws) >= 2.0 ** -14
+    hi_ref = (ws.astype(np.float32).view(np.uint32) & 0xFFFFE000).view(np.float32).astype(np.float64)
+    assert np.array_equal(hi[normal], hi_ref[normal])
+    # below fp16's normal range hi is truncated to the subnormal step (2^-24) and lo rounded to it
+    assert np.all(np.abs(hi + lo - ws) <= 2.0 ** -22 * np.abs(ws) + 1.5 * 2.0 ** -24)
+
+
 def test_split_rejects(device):
     W = torch.zeros(8, 48, device=device)
     with pytest.raises(_lib.PetAttnError):
