@@ -101,7 +101,9 @@ enum {
                               0 rocBLAS only; 1 / 2 the fp32 fused kernel for every / <= 4096-row forward layer;
                               3 the split-product kernel wherever K is a multiple of 32 */
   PET_OPT_ATTN_STREAM = 6, /* 0 (default): the LDS-staged kernels where they hold the shape; 1: the streaming kernels always */
-  PET_OPT_COUNT = 7
+  PET_OPT_BWD_KERNEL = 7,  /* 0 (default): at head_dim 32 the fp16-pair backward (every product on the 16-bit matrix
+                              cores) where it fits, with PET_OPT_SPLIT 1; 1: the tile-exchange backward */
+  PET_OPT_COUNT = 8
 };
 
 /* Sets an option; PET_ATTN_EINVAL for an unknown option or a value out of range. */
@@ -122,6 +124,7 @@ typedef struct pet_attn_plan {
   int bwd_split_dp;           /* backward dP as split-fp32 products on the bf16 matrix cores */
   int bwd_v_staged, bwd_tile_buffers;
   int bwd_lds_bytes, bwd_workgroups_per_cu;
+  int bwd_pair;               /* the fp16-pair backward: every product as fp16 pairs on the 16-bit matrix cores */
 } pet_attn_plan;
 PET_ATTN_API int pet_attn_describe(const pet_attn_shape* shape, pet_attn_plan* out);
 

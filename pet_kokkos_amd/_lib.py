@@ -73,7 +73,7 @@ class Plan(ctypes.Structure):
     """pet_attn_plan (include/pet_attn.h)."""
     _fields_ = [(n, ctypes.c_int) for n in ("streaming", "waves", "fwd_split_scores", "fwd_valu", "fwd_lds_bytes",
                                              "fwd_workgroups_per_cu", "bwd_split_dp", "bwd_v_staged",
-                                             "bwd_tile_buffers", "bwd_lds_bytes", "bwd_workgroups_per_cu")]
+                                             "bwd_tile_buffers", "bwd_lds_bytes", "bwd_workgroups_per_cu", "bwd_pair")]
 
 
 def describe(n_atoms, n_rows, slots, heads, head_dim) -> dict:
@@ -219,11 +219,11 @@ def load() -> ctypes.CDLL:
     return lib
 
 
-OPTIONS = {"split": 1, "fwd_kernel": 2, "bwd_vlds": 3, "bwd_nbuf": 4, "model_gemm": 5, "attn_stream": 6}
+OPTIONS = {"split": 1, "fwd_kernel": 2, "bwd_vlds": 3, "bwd_nbuf": 4, "model_gemm": 5, "attn_stream": 6, "bwd_kernel": 7}
 
 
 def set_option(name: str, value: int) -> None:
-    """pet_attn_set_option by name (split, fwd_kernel, bwd_vlds, bwd_nbuf, model_gemm, attn_stream)."""
+    """pet_attn_set_option by name (split, fwd_kernel, bwd_vlds, bwd_nbuf, model_gemm, attn_stream, bwd_kernel)."""
     check(load().pet_attn_set_option(OPTIONS[name], int(value)), f"pet_attn_set_option({name}={value})")
 
 

@@ -696,7 +696,7 @@ int waves_for(int S) { return (S + 15) / 16; }
 
 // Process-wide tuning options (pet_attn_set_option): each an atomic read
 // once per launch, never the environment.
-std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {4}, {0}};
+std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {4}, {0}, {0}};
 int option(int o) { return g_options[o].load(std::memory_order_relaxed); }
 bool split_enabled() { return option(PET_OPT_SPLIT) != 0; }
 
@@ -754,8 +754,16 @@ struct Plan {
   bool split = false;     // forward: the scores; backward: dP, on the bf16 matrix cores
   bool valu = false;      // forward: the vector-ALU kernel
   int vlds = 0, nbuf = 0; // backward: V staged, tile buffers
+  bool pair = false;      // backward: the fp16-pair kernel (attention_pair.hip)
   int resident = 0;       // workgroups a CU
 };
+
+// The fp16-pair backward (attention_pair.hip), head_dim 32.
+size_t pair_bwd_bytes(int NW);
+const void* pair_bwd_kernel_ptr();
+int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+             const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
+             const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st);
 
 template <int HD>
 Plan plan_fwd(const pet_attn_shape& sh, bool xf) {
@@ -865,6 +873,13 @@ Plan plan_bwd(const pet_attn_shape& sh) {
     if ((b == 1 || b == 2) && fb <= cap) p.vlds = v, p.nbuf = b, p.bytes = fb, p.resident = resident_wgs(k, NW, fb);
   }
   if constexpr (HD == 32) {
+    // every product as fp16 pairs (attention_pair.hip) unless an option asks
+    // for the tile-exchange kernel or for fp32 products only
+    const size_t pb = pair_bwd_bytes(NW);
+    if (split_enabled() && option(PET_OPT_BWD_KERNEL) == 0 && !force_v && !force_b && pb <= cap) {
+      p.pair = true, p.vlds = 0, p.nbuf = 2, p.bytes = pb, p.resident = resident_wgs(pair_bwd_kernel_ptr(), NW, pb);
+      return p;
+    }
     const size_t sb = sizeof(float) * Lds<HD>::bwd_floats(NW, p.nbuf, true, true);
     if (p.vlds && split_enabled() && sb <= cap) {
       const void* ks = reinterpret_cast<const void*>(attn_bwd_kernel<HD, 512, false, true>);
@@ -885,6 +900,9 @@ int launch_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
   const int NW = waves_for(sh.slots);
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
+  if (p.pair)
+    return pair_bwd(sh, n0, n1, eb, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, xf,
+                    st);
   const bool x = xf.rs || xf.b;
   auto k = NW <= 8 ? (x ? attn_bwd_kernel<HD, 512, true> : attn_bwd_kernel<HD, 512, false>)
                    : (x ? attn_bwd_kernel<HD, 1024, true> : attn_bwd_kernel<HD, 1024, false>);
@@ -965,7 +983,7 @@ const char* pet_attn_strerror(int code) {
 
 int pet_attn_set_option(int opt, int value) {
   if (opt <= 0 || opt >= PET_OPT_COUNT) return PET_ATTN_EINVAL;
-  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 4, 1};
+  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 4, 1, 1};
   if (value < lo[opt] || value > hi[opt]) return PET_ATTN_EINVAL;
   g_options[opt].store(value, std::memory_order_relaxed);
   return PET_ATTN_OK;
@@ -1015,7 +1033,7 @@ extern "C" int pet_attn_describe(const pet_attn_shape* sh, pet_attn_plan* out) {
     out->fwd_split_scores = f.split, out->fwd_valu = f.valu, out->fwd_lds_bytes = int(f.bytes);
     out->fwd_workgroups_per_cu = f.resident;
     out->bwd_split_dp = b.split, out->bwd_v_staged = b.vlds, out->bwd_tile_buffers = b.nbuf;
-    out->bwd_lds_bytes = int(b.bytes), out->bwd_workgroups_per_cu = b.resident;
+    out->bwd_lds_bytes = int(b.bytes), out->bwd_workgroups_per_cu = b.resident, out->bwd_pair = b.pair;
     out->waves = waves_for(sh->slots);
     return PET_ATTN_OK;
   });

@@ -1,0 +1,390 @@
+// The attention backward at head_dim 32 from fp16 pairs on gfx950's 16-bit
+// matrix cores: every product of the backward (S, dP, dK, dV, dQ) at fp32
+// accuracy in three f16 matrix instructions where the fp32 instruction takes
+// eight (split_bf16.h: an fp32 x scaled by a power of two splits into an fp16
+// hi holding its leading 11 bits and an fp16 lo holding the next 11).
+//
+// Semantics: the reference's attention_bwd core (peterspackman/pet-kokkos
+// src/attention.cpp:1570-1697, Queries<HD> and Keys<HD,DK,DV>, and its MFMA
+// backward :451-593): for query i and key j of an (atom, head),
+//   P_ij = exp(sc q_i.k_j + log cf_j - m_i) / l_i   (m, 1/l the forward's ml)
+//   dS_ij = P_ij (dO_i.v_j - dO_i.O_i)
+//   dQ_i = sc sum_j dS_ij k_j, dK_j = sc sum_i dS_ij q_i, dV_j = sum_i P_ij dO_i,
+//   cfh_j = sum_i dS_ij (the cf adjoint's share of this head).
+//
+// Work decomposition: one workgroup per (atom, head), wave w owning key block
+// w (16 keys). At step s wave w takes query block I = (w + s) mod nb:
+//   S = Q_I K_w^T and dP = dO_I V_w^T on the 16x16x32 instruction, a lane
+//   holding key 16w + c against queries 16I + 4g + r (lane l = (c, g) =
+//   (l % 16, l / 16), register r of the result);
+//   P and dS, scaled and split in registers, are then already the b operand
+//   of the 16x16x16 instruction for dV_w^T += dO_I^T P and dK_w^T += Q_I^T dS
+//   (k = the block's 16 queries), so the key block's dK and dV never leave the
+//   wave's registers; only dS goes through LDS, transposed, to the owner of
+//   query block I, which adds dQ_I^T += K_w^T dS^T after the step's barrier.
+// Every product is formed once, every output has one owner summing in a fixed
+// order, nothing is atomic: results repeat bit for bit.
+//
+// Scales: per item, powers of two put the largest |Q|, |K|, |V|, |dO| at
+// [2^14, 2^15) (so everything down to 2^-29 of the item's largest value keeps
+// 22 significand bits), P is scaled by 2^15 (P <= 1), and dS by the power of
+// two that puts the bound max|v| max|dO| + max|dO.O| >= max|dS| there (row
+// norms).
+// The scales are undone in fp32 where the results are stored.
+//
+// LDS (bytes, R = 16 NW rows): Q and dO as split rows [R][hi 32 | lo 32 | pad]
+// (the a operand of S and dP, 144-byte pitch: 16-lane groups of 16-byte reads
+// on distinct banks); Q^T, dO^T, K^T as hi and lo planes [32 dims][R + 8]
+// (the a operand of dK, dV, dQ: 8-byte reads of four consecutive tokens, the
+// pitch R / 2 + 4 words putting a 16-lane column on distinct banks); the
+// per-query (max, 2^15 / sum, scaled dO.O); two buffers of one 16 x 20-word dS
+// tile a wave, a word holding (hi | lo) of one element. 70.8 KB at 5 waves:
+// two workgroups a CU.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "../../include/pet_attn.h"
+#include "attn_common.h"
+#include "split_bf16.h"
+
+namespace pet_attn {
+
+using pet_split::mfma3;
+using pet_split::mfma3_16;
+using pet_split::u2;
+using pet_split::u4;
+
+namespace {
+
+constexpr int kPairHD = 32;
+constexpr int kPairMaxWaves = 8;  // 128 slots; beyond, the tile-exchange kernel
+
+struct PairLds {
+  static constexpr int RP = 4 * kPairHD + 16;  // bytes of a split row
+  static constexpr int TP = 20;                // words a dS tile row
+  int R, PT;                                   // rows; plane pitch in halves
+  size_t qr, gr, pl, st, red, tb, bytes;
+  __host__ __device__ constexpr explicit PairLds(int NW)
+      : R(16 * NW), PT(16 * NW + 8), qr(0), gr(size_t(R) * RP), pl(2 * size_t(R) * RP),
+        st(pl + size_t(6) * kPairHD * PT * 2),  // 6 planes: Q^T, dO^T, K^T, each hi then lo
+        red(st + size_t(3) * R * 4),            // 8 words a wave: its maxima
+        tb(red + size_t(8) * NW * 4), bytes(tb + size_t(2) * NW * 16 * TP * 4) {}
+};
+
+// Two scaled values as fp16 (hi, lo) registers, hi the truncation of x to
+// fp16 (also where x is an fp16 subnormal) and lo the remainder x - hi (exact
+// in fp32) rounded to the nearest fp16: |x - hi - lo| <= 2^-22 |x|, or <= 2^-25
+// where x is below fp16's normal range.
+__device__ __forceinline__ void pair2x(float x, float y, unsigned& hi, unsigned& lo) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(x, y);
+  const pet_split::h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
+  hi = __builtin_bit_cast(unsigned, h);
+  lo = __builtin_bit_cast(unsigned, l);
+}
+
+// The largest x over a row of 16 lanes, in every lane of the row (DPP row
+// rotations by 1, 2, 4, 8: vector instructions, no LDS).
+__device__ __forceinline__ float row_max16(float x) {
+#define PET_ROR(n) \
+  x = fmaxf(x, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x120 + (n), 0xf, 0xf, false)))
+  PET_ROR(1);
+  PET_ROR(2);
+  PET_ROR(4);
+  PET_ROR(8);
+#undef PET_ROR
+  return x;
+}
+// The exponent k of the pair scale 2^k that puts m = f 2^e (f in [0.5, 1))
+// at [2^14, 2^15): 15 - e; 0 for a zero (or non-finite) m.
+__device__ __forceinline__ int pair_exp(float m) {
+  if (!(m > 0.f) || m > 3.0e38f) return 0;
+  return min(15 - __builtin_amdgcn_frexp_expf(m), 126);
+}
+// (low half of a | low half of b << 16) and the same of the high halves
+__device__ __forceinline__ unsigned lo_lo(unsigned a, unsigned b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ unsigned hi_hi(unsigned a, unsigned b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+}  // namespace
+
+template <int NW, bool XF>
+__global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq,
+                                                             const int* __restrict__ off, int N, int n0, int64_t eb,
+                                                             int S, int H, float sc,
+                                                             const float* __restrict__ dmerged, int64_t ldg,
+                                                             const float* __restrict__ merged, int64_t ldm,
+                                                             const float* __restrict__ ml,
+                                                             const float* __restrict__ cf_seq, int64_t ldc,
+                                                             float* __restrict__ qkv_adj, int64_t lda,
+                                                             float* __restrict__ cfh, QkvXf xf) {
+  constexpr int HD = kPairHD, W = HD / 4, DT = HD / 16;
+  extern __shared__ float lds_f[];
+  unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
+  const int D = H * HD;
+  constexpr PairLds L(NW);
+  constexpr int PT = L.PT;
+  const u4* QR = reinterpret_cast<const u4*>(lds + L.qr);
+  const u4* GR = reinterpret_cast<const u4*>(lds + L.gr);
+  _Float16* planes = reinterpret_cast<_Float16*>(lds + L.pl);
+  constexpr int PS = HD * PT;  // halves a plane part
+  _Float16* QTh = planes;
+  _Float16* GTh = planes + 2 * PS;
+  _Float16* KTh = planes + 4 * PS;
+  float* STm = reinterpret_cast<float*>(lds + L.st);
+  float* STl = STm + L.R;
+  float* STd = STl + L.R;
+  float* red = reinterpret_cast<float*>(lds + L.red);
+  unsigned* TB = reinterpret_cast<unsigned*>(lds + L.tb);
+
+  // the wave index in a scalar register: the step's block offsets are then
+  // scalar too
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int i = 16 * w + c;  // this lane's row: its query slot, and its key slot
+  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  const bool active = w < at.nb, real = active && i < at.cnt;
+
+  // ---- the wave's own block: rows 16w .. 16w + 15, lane (c, g) dims 8g .. 8g + 7
+  float q[W], k[W], v[W], go[W], oo[W];
+  float mi = kOff, li = 0.f, pcf = 0.f;
+  if (real) {
+    const size_t r = at.row(i);
+    qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
+    qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
+    qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
+    gmem_get<W>(dmerged + r * ldg + at.h * HD + g * W, go);
+    gmem_get<W>(merged + at.grow(i) * ldm + at.h * HD + g * W, oo);
+    const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
+    mi = m2[0], li = m2[1];
+    pcf = cf_seq[size_t(at.n) * ldc + i];
+  } else {
+#pragma unroll
+    for (int t = 0; t < W; ++t) q[t] = k[t] = v[t] = go[t] = oo[t] = 0.f;
+  }
+  // Row norms (over the head's dims; every lane of a row gets its row's), then
+  // their largest over the item: the scales come from them (a row's largest
+  // |x| is at most its norm).
+  float nq = 0.f, nk = 0.f, nv = 0.f, ng = 0.f, dot = 0.f;
+#pragma unroll
+  for (int t = 0; t < W; ++t) {
+    nq += q[t] * q[t], nk += k[t] * k[t], nv += v[t] * v[t], ng += go[t] * go[t];
+    dot += go[t] * oo[t];
+  }
+  const float Di = sum_g(dot);  // dO_i . O_i
+  float m5[5] = {sum_g(nq), sum_g(nk), sum_g(nv), sum_g(ng), Di * Di};
+#pragma unroll
+  for (int u = 0; u < 5; ++u) m5[u] = row_max16(m5[u]);
+  if (l == 0) {
+    *reinterpret_cast<float4*>(red + 8 * w) = make_float4(m5[0], m5[1], m5[2], m5[3]);
+    red[8 * w + 4] = m5[4];
+  }
+  lds_barrier();
+  float M[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int x = 0; x < NW; ++x) {
+    const float4 a = *reinterpret_cast<const float4*>(red + 8 * x);
+    M[0] = fmaxf(M[0], a.x), M[1] = fmaxf(M[1], a.y), M[2] = fmaxf(M[2], a.z), M[3] = fmaxf(M[3], a.w);
+    M[4] = fmaxf(M[4], red[8 * x + 4]);
+  }
+#pragma unroll
+  for (int u = 0; u < 5; ++u) M[u] = sqrtf(M[u]);  // largest norms, largest |D|
+  // scales 2^k: Q, K, V, dO by their largest row norm; dS by its bound
+  // |dS_ij| = P_ij |dO_i.v_j - D_i| <= max|v| max|dO| + max|D| (Cauchy-Schwarz, P <= 1)
+  const int kQ = pair_exp(M[0]), kK = pair_exp(M[1]), kV = pair_exp(M[2]), kG = pair_exp(M[3]);
+  const int kS = pair_exp(M[2] * M[3] + M[4]);
+  constexpr int kP = 15;  // P's scale 2^15
+  const float sQ = __builtin_amdgcn_ldexpf(1.f, kQ), sK = __builtin_amdgcn_ldexpf(1.f, kK);
+  const float sV = __builtin_amdgcn_ldexpf(1.f, kV), sG = __builtin_amdgcn_ldexpf(1.f, kG);
+  const float scS = __builtin_amdgcn_ldexpf(sc, -kQ - kK);        // scores from the scaled product
+  const float alpha = __builtin_amdgcn_ldexpf(1.f, kS - kP - kV - kG);  // dP's scale into dS's, over P's
+
+  // own rows split: K and V stay in registers (the b operand of S and dP);
+  // Q and dO go to their split rows and, with K, to the transposed planes
+  u4 kb[2], vb[2];
+  {
+    u4 qs[2], gs[2];
+#pragma unroll
+    for (int j = 0; j < W / 2; ++j) {
+      unsigned h[4], lo[4];
+      pair2x(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);
+      pair2x(go[2 * j] * sG, go[2 * j + 1] * sG, h[1], lo[1]);
+      pair2x(k[2 * j] * sK, k[2 * j + 1] * sK, h[2], lo[2]);
+      pair2x(v[2 * j] * sV, v[2 * j + 1] * sV, h[3], lo[3]);
+      qs[0][j] = h[0], qs[1][j] = lo[0], gs[0][j] = h[1], gs[1][j] = lo[1];
+      kb[0][j] = h[2], kb[1][j] = lo[2], vb[0][j] = h[3], vb[1][j] = lo[3];
+    }
+    if (active) {
+      u4* qr = const_cast<u4*>(QR) + i * (PairLds::RP / 16);
+      u4* gr = const_cast<u4*>(GR) + i * (PairLds::RP / 16);
+      qr[g] = qs[0], qr[4 + g] = qs[1];
+      gr[g] = gs[0], gr[4 + g] = gs[1];
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        const int o = (8 * g + e) * PT + i;
+        auto half = [&](unsigned x) { return __builtin_bit_cast(pet_split::h2v, x)[e & 1]; };
+        QTh[o] = half(qs[0][e >> 1]), QTh[PS + o] = half(qs[1][e >> 1]);
+        GTh[o] = half(gs[0][e >> 1]), GTh[PS + o] = half(gs[1][e >> 1]);
+        KTh[o] = half(kb[0][e >> 1]), KTh[PS + o] = half(kb[1][e >> 1]);
+      }
+      if (g == 0) {
+        // a query with no live key (li = 0): an exponent near -1e30, exp gives 0
+        STm[i] = li > 0.f ? mi : 1e30f;
+        STl[i] = __builtin_amdgcn_ldexpf(li, kP);
+        STd[i] = __builtin_amdgcn_ldexpf(Di, kS - kP);
+      }
+    }
+  }
+  const float lcj = pcf > 0.f ? log_cf(pcf) : kOff;  // this lane's key's log cf (kOff past the count)
+
+  f4 dq[DT], dk[DT], dv[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) dq[t] = dk[t] = dv[t] = f4{0.f, 0.f, 0.f, 0.f};
+  float cfa = 0.f;
+  const int nb = at.nb;
+
+  // Phase 1 of step s: query block I = (w + s) mod nb against the own keys.
+  auto phase1 = [&](int s) {
+    int I = w + s;
+    if (I >= nb) I -= nb;
+    const u4* qr = QR + (16 * I + c) * (PairLds::RP / 16);
+    const u4* gr = GR + (16 * I + c) * (PairLds::RP / 16);
+    const u4 qa[2] = {qr[g], qr[4 + g]}, ga[2] = {gr[g], gr[4 + g]};
+    const f4 z = {0.f, 0.f, 0.f, 0.f};
+    const f4 st = mfma3(qa, kb, z);  // S: key 16w + c (column), queries 16I + 4g + r
+    const f4 dp = mfma3(ga, vb, z);
+    const float4 m4 = *reinterpret_cast<const float4*>(STm + 16 * I + 4 * g);
+    const float4 l4 = *reinterpret_cast<const float4*>(STl + 16 * I + 4 * g);
+    const float4 d4 = *reinterpret_cast<const float4*>(STd + 16 * I + 4 * g);
+    const float mm[4] = {m4.x, m4.y, m4.z, m4.w}, ll[4] = {l4.x, l4.y, l4.z, l4.w}, dd[4] = {d4.x, d4.y, d4.z, d4.w};
+    float pp[4], ds[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pp[r] = __expf(st[r] * scS + (lcj - mm[r])) * ll[r];  // 2^15 P
+      ds[r] = pp[r] * fmaf(dp[r], alpha, -dd[r]);           // sS dS
+      cfa += ds[r];
+    }
+    unsigned h[4], lo[4];
+    pair2x(pp[0], pp[1], h[0], lo[0]);
+    pair2x(pp[2], pp[3], h[1], lo[1]);
+    pair2x(ds[0], ds[1], h[2], lo[2]);
+    pair2x(ds[2], ds[3], h[3], lo[3]);
+    const u2 ph = {h[0], h[1]}, pl = {lo[0], lo[1]}, sh = {h[2], h[3]}, sl = {lo[2], lo[3]};
+    // dV^T += dO_I^T P and dK^T += Q_I^T dS: a operand rows 16t + c of the
+    // planes, the block's queries 16I + 4g .. + 3
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int o = (16 * t + c) * PT + 16 * I + 4 * g;
+      const u2 gth = *reinterpret_cast<const u2*>(GTh + o), gtl = *reinterpret_cast<const u2*>(GTh + PS + o);
+      const u2 qth = *reinterpret_cast<const u2*>(QTh + o), qtl = *reinterpret_cast<const u2*>(QTh + PS + o);
+      dv[t] = mfma3_16(gth, gtl, ph, pl, dv[t]);
+      dk[t] = mfma3_16(qth, qtl, sh, sl, dk[t]);
+    }
+    // dS to query block I's owner, transposed: T[query 4g + r][key c]
+    unsigned* tb = TB + ((s & 1) * NW + w) * (16 * PairLds::TP);
+    tb[(4 * g) * PairLds::TP + c] = lo_lo(sh[0], sl[0]);
+    tb[(4 * g + 1) * PairLds::TP + c] = hi_hi(sh[0], sl[0]);
+    tb[(4 * g + 2) * PairLds::TP + c] = lo_lo(sh[1], sl[1]);
+    tb[(4 * g + 3) * PairLds::TP + c] = hi_hi(sh[1], sl[1]);
+  };
+  // Phase 2 of step s: the own query block's tile from key block J = (w - s)
+  // mod nb: dQ_w^T += K_J^T dS^T.
+  auto phase2 = [&](int s) {
+    int J = w - s;
+    if (J < 0) J += nb;
+    const unsigned* tb = TB + ((s & 1) * NW + J) * (16 * PairLds::TP);
+    const uint4 p = *reinterpret_cast<const uint4*>(tb + c * PairLds::TP + 4 * g);  // query c, keys 4g .. + 3
+    const u2 bh = {lo_lo(p.x, p.y), lo_lo(p.z, p.w)}, bl = {hi_hi(p.x, p.y), hi_hi(p.z, p.w)};
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int o = (16 * t + c) * PT + 16 * J + 4 * g;
+      const u2 kth = *reinterpret_cast<const u2*>(KTh + o), ktl = *reinterpret_cast<const u2*>(KTh + PS + o);
+      dq[t] = mfma3_16(kth, ktl, bh, bl, dq[t]);
+    }
+  };
+  // Software-pipelined: between two barriers a wave has phase 2 of the last
+  // step and phase 1 of this one. Step 0 is the diagonal tile, which reads
+  // only what the wave itself staged, so it runs before the first barrier.
+  if (active) phase1(0);
+  lds_barrier();
+  for (int s = 1; s < nb; ++s) {
+    if (active) {
+      phase2(s - 1);
+      phase1(s);
+    }
+    lds_barrier();
+  }
+  if (active) phase2(nb - 1);
+
+  // ---- stores: dQ | dK | dV of the own row, lane dims 16t + 4g .. + 3
+  const float cft = __builtin_amdgcn_ldexpf(sum_g(cfa), -kS);
+  if (real) {
+    float* o = qkv_adj + at.row(i) * lda + at.h * HD + 4 * g;
+    const float fq = __builtin_amdgcn_ldexpf(sc, -kK - kS), fk = __builtin_amdgcn_ldexpf(sc, -kQ - kS);
+    const float fv = __builtin_amdgcn_ldexpf(1.f, -kP - kG);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      *reinterpret_cast<float4*>(o + 16 * t) = make_float4(dq[t][0] * fq, dq[t][1] * fq, dq[t][2] * fq, dq[t][3] * fq);
+      *reinterpret_cast<float4*>(o + D + 16 * t) =
+          make_float4(dk[t][0] * fk, dk[t][1] * fk, dk[t][2] * fk, dk[t][3] * fk);
+      *reinterpret_cast<float4*>(o + 2 * D + 16 * t) =
+          make_float4(dv[t][0] * fv, dv[t][1] * fv, dv[t][2] * fv, dv[t][3] * fv);
+    }
+  }
+  if (g == 0 && i < S) cfh[(size_t(at.n) * H + at.h) * S + i] = real ? cft : 0.f;
+}
+
+// ---- host side ---------------------------------------------------------------
+
+size_t pair_bwd_bytes(int NW) { return NW <= kPairMaxWaves ? PairLds(NW).bytes : ~size_t(0); }
+
+const void* pair_bwd_kernel_ptr() { return reinterpret_cast<const void*>(attn_bwd_pair_kernel<5, false>); }
+
+namespace {
+template <int NW>
+auto pair_kernel(bool x) {
+  return x ? attn_bwd_pair_kernel<NW, true> : attn_bwd_pair_kernel<NW, false>;
+}
+}  // namespace
+
+int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+             const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
+             const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st) {
+  const int NW = (sh.slots + 15) / 16;
+  if (NW > kPairMaxWaves) return PET_ATTN_ESLOTS;
+  const int64_t items = int64_t(n1 - n0) * sh.heads;
+  if (items == 0) return PET_ATTN_OK;
+  const size_t bytes = pair_bwd_bytes(NW);
+  const bool x = xf.rs || xf.b;
+  decltype(&attn_bwd_pair_kernel<1, false>) k = nullptr;
+  switch (NW) {
+    case 1: k = pair_kernel<1>(x); break;
+    case 2: k = pair_kernel<2>(x); break;
+    case 3: k = pair_kernel<3>(x); break;
+    case 4: k = pair_kernel<4>(x); break;
+    case 5: k = pair_kernel<5>(x); break;
+    case 6: k = pair_kernel<6>(x); break;
+    case 7: k = pair_kernel<7>(x); break;
+    default: k = pair_kernel<8>(x); break;
+  }
+  if (bytes > 65536) {  // the dynamic LDS limit raised once per (device, kernel) to the largest size asked
+    static std::map<std::pair<int, const void*>, size_t> raised;
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return PET_ATTN_ELAUNCH;
+    const void* kp = reinterpret_cast<const void*>(k);
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = raised[{dev, kp}];
+    if (have < bytes) {
+      if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess)
+        return PET_ATTN_ELAUNCH;
+      have = bytes;
+    }
+  }
+  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots,
+                     sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, xf);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+}  // namespace pet_attn

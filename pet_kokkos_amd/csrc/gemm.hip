@@ -39,6 +39,10 @@ using pet_split::pack_hi;
 using pet_split::split3;
 using pet_split::split8;
 using pet_split::u4;
+using pet_split::mfma3;
+using pet_split::mfma_h;
+using pet_split::pair2;
+using pet_split::pair_scale;
 
 __device__ __forceinline__ f4 mfma(float a, float b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -353,48 +357,6 @@ __global__ void split_rows_kernel(const float* __restrict__ W, int N, int K, int
   split8(x, parts);
 #pragma unroll
   for (int p = 0; p < 3; ++p) out[t * 3 + p] = parts[p];
-}
-
-// ---- fp32 products from fp16 pairs on the 16-bit matrix cores --------------
-// A row of a matrix, scaled by a power of two s that puts its largest |x| in
-// [2^14, 2^15), splits into two fp16 values per element: hi = x s with its
-// low 13 significand bits cleared (its leading 11 bits, exact in fp16) and
-// lo = x s - hi (exact in fp32) rounded to the nearest fp16. hi + lo holds 22
-// of x's 24 significand bits, the rounding of lo within 2^-22 |x| (and within
-// 2^-37 of the row's largest element where x s leaves fp16's normal range). A product a.b over k is then (a_hi b_hi + a_hi b_lo + a_lo b_hi) /
-// (s_a s_b) with the three part products accumulated in fp32 by
-// v_mfma_f32_16x16x32_f16 and the scales undone in the epilogue; the dropped
-// a_lo b_lo is below 2^-22 |a||b|. Measured error on fp32 operands spread over
-// many octaves per row: 2.9e-8 of sum |a_k b_k| before the fp32 accumulation
-// (three bf16 parts with six products: 2.1e-8; the fp32 instruction's
-// accumulation alone: 1.6e-7). Three matrix instructions where the bf16 form
-// takes six.
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f4 mfma_h(const u4& a, const u4& b, const f4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
-}
-// c += a.b from (hi, lo) parts, the small products first
-__device__ __forceinline__ f4 mfma3(const u4* a, const u4* b, f4 c) {
-  c = mfma_h(a[1], b[0], c);
-  c = mfma_h(a[0], b[1], c);
-  return mfma_h(a[0], b[0], c);
-}
-// two scaled values as a register of hi parts and a register of lo parts
-__device__ __forceinline__ void pair2(float x, float y, unsigned& hi, unsigned& lo) {
-  const float hx = __uint_as_float(__float_as_uint(x) & 0xffffe000u);
-  const float hy = __uint_as_float(__float_as_uint(y) & 0xffffe000u);
-  hi = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(hx, hy));  // exact
-  const h2v l = {(_Float16)(x - hx), (_Float16)(y - hy)};                 // to nearest
-  lo = __builtin_bit_cast(unsigned, l);
-}
-// The row scale 2^(15 - e) for a largest |x| m = f 2^e (f in [0.5, 1)); 1 for
-// a zero row (and for one holding a NaN, which then propagates).
-__device__ __forceinline__ float pair_scale(float m) {
-  if (!(m > 0.f) || m > 3.0e38f) return 1.f;
-  const int e = __builtin_amdgcn_frexp_expf(m);
-  return __builtin_amdgcn_ldexpf(1.f, min(15 - e, 126));
 }
 
 // C = epi(A B^T) with B as fp16 pairs made once (pair_rows_kernel:

@@ -1,4 +1,4 @@
-// Split-fp32 products on gfx950's bf16 matrix cores, shared by the attention
+// Split-fp32 products on gfx950's 16-bit matrix cores (bf16 parts, fp16 pairs), shared by the attention
 // kernels (attention.hip) and the dense layers (gemm.hip).
 #pragma once
 
@@ -54,6 +54,62 @@ __device__ __forceinline__ f4 mfma6(const u4* a, const u4* b, f4 c) {
   c = mfma_bf(a[0], b[1], c);
   c = mfma_bf(a[1], b[0], c);
   return mfma_bf(a[0], b[0], c);
+}
+
+// ---- fp32 products from fp16 pairs on the 16-bit matrix cores --------------
+// A row of a matrix, scaled by a power of two s that puts its largest |x| in
+// [2^14, 2^15), splits into two fp16 values per element: hi = x s with its
+// low 13 significand bits cleared (its leading 11 bits, exact in fp16) and
+// lo = x s - hi (exact in fp32) rounded to the nearest fp16. hi + lo holds 22
+// of x's 24 significand bits, the rounding of lo within 2^-22 |x| (and within
+// 2^-37 of the row's largest element where x s leaves fp16's normal range). A product a.b over k is then (a_hi b_hi + a_hi b_lo + a_lo b_hi) /
+// (s_a s_b) with the three part products accumulated in fp32 by
+// v_mfma_f32_16x16x32_f16 and the scales undone in the epilogue; the dropped
+// a_lo b_lo is below 2^-22 |a||b|. Measured error on fp32 operands spread over
+// many octaves per row: 2.9e-8 of sum |a_k b_k| before the fp32 accumulation
+// (three bf16 parts with six products: 2.1e-8; the fp32 instruction's
+// accumulation alone: 1.6e-7). Three matrix instructions where the bf16 form
+// takes six.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f4 mfma_h(const u4& a, const u4& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+// c += a.b from (hi, lo) parts, the small products first
+__device__ __forceinline__ f4 mfma3(const u4* a, const u4* b, f4 c) {
+  c = mfma_h(a[1], b[0], c);
+  c = mfma_h(a[0], b[1], c);
+  return mfma_h(a[0], b[0], c);
+}
+// two scaled values as a register of hi parts and a register of lo parts
+__device__ __forceinline__ void pair2(float x, float y, unsigned& hi, unsigned& lo) {
+  const float hx = __uint_as_float(__float_as_uint(x) & 0xffffe000u);
+  const float hy = __uint_as_float(__float_as_uint(y) & 0xffffe000u);
+  hi = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(hx, hy));  // exact
+  const h2v l = {(_Float16)(x - hx), (_Float16)(y - hy)};                 // to nearest
+  lo = __builtin_bit_cast(unsigned, l);
+}
+// The row scale 2^(15 - e) for a largest |x| m = f 2^e (f in [0.5, 1)); 1 for
+// a zero row (and for one holding a NaN, which then propagates).
+__device__ __forceinline__ float pair_scale(float m) {
+  if (!(m > 0.f) || m > 3.0e38f) return 1.f;
+  const int e = __builtin_amdgcn_frexp_expf(m);
+  return __builtin_amdgcn_ldexpf(1.f, min(15 - e, 126));
+}
+
+// The same pairs on the 16 x 16 x 16 instruction (k = 16: four fp16 values a
+// lane, two registers), for products whose contraction is one 16-row block.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef unsigned u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f4 mfma_h16(const u2& a, const u2& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
+}
+// c += a.b from (hi, lo) parts a = (ah, al), b = (bh, bl), the small products first
+__device__ __forceinline__ f4 mfma3_16(const u2& ah, const u2& al, const u2& bh, const u2& bl, f4 c) {
+  c = mfma_h16(al, bh, c);
+  c = mfma_h16(ah, bl, c);
+  return mfma_h16(ah, bh, c);
 }
 
 }  // namespace pet_split

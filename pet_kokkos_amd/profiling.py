@@ -33,7 +33,13 @@ def main(argv=None):
     ap.add_argument("--rows", action="store_true",
                     help="also run the token norm (forward, backward) and the forces' edge term and fold each step")
     ap.add_argument("--model", choices=["c2", "c2-residual", "c5"], help="profile whole energy+forces evaluations instead")
+    ap.add_argument("--option", action="append", default=[], metavar="NAME=VALUE",
+                    help="a library option (pet_attn_set_option by name, e.g. bwd_kernel=1), repeatable")
     args = ap.parse_args(argv)
+    from . import _lib
+    for o in args.option:
+        name, _, value = o.partition("=")
+        _lib.set_option(name, int(value))
     device = torch.device("cuda", 0)
     if args.model:
         return profile_model(args, device)

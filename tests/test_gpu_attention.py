@@ -203,6 +203,43 @@ def test_backward_layouts(device, hd, vlds, nbuf, split):
                              tk.cf_seq, qkv, dm, 2, hd)
 
 
+@pytest.mark.parametrize("qk,v,g,spread", [(1.0, 1.0, 1.0, 0.0), (0.05, 1e3, 1e-7, 0.0), (0.5, 1e-4, 3e4, 0.0),
+                                            (0.5, 1.0, 1.0, 3.0)])
+def test_pair_backward_scales(device, qk, v, g, spread):
+    # The fp16-pair backward (the default at head_dim 32) puts each item's
+    # largest |Q|, |K|, |V|, |dO| at 2^15 by powers of two and bounds dS
+    # from them: V and dO far from unit scale, and V and dO rows spread over
+    # 10^+-spread within an item, must meet the same bar against the oracle.
+    # (Q and K stay moderate: scores of hundreds make exp amplify any fp32
+    # rounding of them, a conditioning no product order escapes.)
+    counts = [0, 15, 16, 31, 47, 5, 60, 33, 70, 79]
+    tk, qkv, dm = random_case(counts, 2, 32, seed=300 + int(spread), cf_kind="random")
+    rng = np.random.default_rng(11)
+    D = 2 * 32
+    qkv[:, :2 * D] *= qk
+    qkv[:, 2 * D:] *= v * 10.0 ** rng.uniform(-spread, spread, (qkv.shape[0], 1))
+    dm = (dm * g * 10.0 ** rng.uniform(-spread, spread, (dm.shape[0], 1))).astype(np.float32)
+    qkv = qkv.astype(np.float32)
+    assert A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 2, 32)["bwd_pair"] == 1
+    check_against_oracle(device, f"pair backward qk x{qk} v x{v} dO x{g} spread 1e+-{spread}", tk.off,
+                         tk.cf_seq, qkv, dm, 2, 32)
+
+
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_backward_kernels(device, kernel):
+    # Both head_dim-32 backwards (option bwd_kernel: 0 the fp16-pair kernel,
+    # 1 the tile-exchange kernel) on ragged atoms with dead rows, each
+    # bit-identical when repeated.
+    counts = [0, 15, 16, 31, 47, 5, 60, 33, 70]
+    tk, qkv, dm = random_case(counts, 3, 32, seed=400, cf_kind="random")
+    with A._lib.options(bwd_kernel=kernel):
+        assert A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 3, 32)["bwd_pair"] == (kernel == 0)
+        first = check_against_oracle(device, f"backward kernel {kernel}", tk.off, tk.cf_seq, qkv, dm, 3, 32)
+        again = gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 3, 32)
+    for a, b in zip(first, again):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_cf_adjoint_accumulates(device):
     tk, qkv, dm = random_case([12, 40, 7], 2, 32, seed=6)
     start = np.random.default_rng(0).standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
