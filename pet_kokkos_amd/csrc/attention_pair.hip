@@ -20,8 +20,8 @@
 //   P and dS, scaled and split in registers, are then already the b operand
 //   of the 16x16x16 instruction for dV_w^T += dO_I^T P and dK_w^T += Q_I^T dS
 //   (k = the block's 16 queries), so the key block's dK and dV never leave the
-//   wave's registers; only dS goes through LDS, transposed, to the owner of
-//   query block I, which adds dQ_I^T += K_w^T dS^T after the step's barrier.
+//   wave's registers; only dS goes through LDS to the owner of query block
+//   I, which adds dQ_I^T += K_w^T dS^T after the step's barrier.
 // Every product is formed once, every output has one owner summing in a fixed
 // order, nothing is atomic: results repeat bit for bit.
 //
@@ -32,14 +32,12 @@
 // norms).
 // The scales are undone in fp32 where the results are stored.
 //
-// LDS (bytes, R = 16 NW rows): Q and dO as split rows [R][hi 32 | lo 32 | pad]
-// (the a operand of S and dP, 144-byte pitch: 16-lane groups of 16-byte reads
-// on distinct banks); Q^T, dO^T, K^T as hi and lo planes [32 dims][R + 8]
-// (the a operand of dK, dV, dQ: 8-byte reads of four consecutive tokens, the
-// pitch R / 2 + 4 words putting a 16-lane column on distinct banks); the
-// per-query (max, 2^15 / sum, scaled dO.O); two buffers of one 16 x 20-word dS
-// tile a wave, a word holding (hi | lo) of one element. 70.8 KB at 5 waves:
-// two workgroups a CU.
+// LDS (R = 16 NW rows): Q^T, dO^T, K^T as hi and lo planes [32 dims][R + 8
+// halves] (token-contiguous: the a operand of dK, dV and dQ as 8-byte reads of
+// four consecutive tokens; Q's and dO's rows for S and dP through the
+// transposing read), the per-query (max, 2^15 / sum, scaled dO.O), and two
+// buffers of one dS tile a wave (hi and lo, [16 keys][16 queries + 4 pad]).
+// 47.7 KB at 5 waves: three workgroups a CU.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -64,16 +62,26 @@ constexpr int kPairHD = 32;
 constexpr int kPairMaxWaves = 8;  // 128 slots; beyond, the tile-exchange kernel
 
 struct PairLds {
-  static constexpr int RP = 4 * kPairHD + 16;  // bytes of a split row
-  static constexpr int TP = 20;                // words a dS tile row
-  int R, PT;                                   // rows; plane pitch in halves
-  size_t qr, gr, pl, st, red, tb, bytes;
+  static constexpr int TP = 20;  // halves a dS tile row (16 queries, 4 of pad)
+  static constexpr int TS = 16 * TP;  // halves a tile part
+  int R, PT;                     // rows; plane pitch in halves
+  size_t pl, st, red, tb, bytes;
   __host__ __device__ constexpr explicit PairLds(int NW)
-      : R(16 * NW), PT(16 * NW + 8), qr(0), gr(size_t(R) * RP), pl(2 * size_t(R) * RP),
+      : R(16 * NW), PT(16 * NW + 8), pl(0),
         st(pl + size_t(6) * kPairHD * PT * 2),  // 6 planes: Q^T, dO^T, K^T, each hi then lo
         red(st + size_t(3) * R * 4),            // 8 words a wave: its maxima
-        tb(red + size_t(8) * NW * 4), bytes(tb + size_t(2) * NW * 16 * TP * 4) {}
+        tb(red + size_t(8) * NW * 4), bytes(tb + size_t(2) * NW * 2 * TS * 2) {}
 };
+
+// gfx950's transposing LDS read (ds_read_b64_tr_b16), on the 16 lanes of a
+// row: lane j's element m is element j % 4 of what lane 4m + j / 4 addressed.
+// A lane addressing the four consecutive tokens 4(L % 4) .. + 3 of plane row
+// d0 + L / 4 thus receives its own token's dims d0 .. d0 + 3.
+typedef short s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u2 lds_tr16(const _Float16* p) {
+  typedef __attribute__((address_space(3))) s4 lds_s4;
+  return __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
+}
 
 // Two scaled values as fp16 (hi, lo) registers, hi the truncation of x to
 // fp16 (also where x is an fp16 subnormal) and lo the remainder x - hi (exact
@@ -104,10 +112,6 @@ __device__ __forceinline__ int pair_exp(float m) {
   if (!(m > 0.f) || m > 3.0e38f) return 0;
   return min(15 - __builtin_amdgcn_frexp_expf(m), 126);
 }
-// (low half of a | low half of b << 16) and the same of the high halves
-__device__ __forceinline__ unsigned lo_lo(unsigned a, unsigned b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-__device__ __forceinline__ unsigned hi_hi(unsigned a, unsigned b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
-
 }  // namespace
 
 template <int NW, bool XF>
@@ -126,8 +130,6 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   const int D = H * HD;
   constexpr PairLds L(NW);
   constexpr int PT = L.PT;
-  const u4* QR = reinterpret_cast<const u4*>(lds + L.qr);
-  const u4* GR = reinterpret_cast<const u4*>(lds + L.gr);
   _Float16* planes = reinterpret_cast<_Float16*>(lds + L.pl);
   constexpr int PS = HD * PT;  // halves a plane part
   _Float16* QTh = planes;
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   float* STl = STm + L.R;
   float* STd = STl + L.R;
   float* red = reinterpret_cast<float*>(lds + L.red);
-  unsigned* TB = reinterpret_cast<unsigned*>(lds + L.tb);
+  _Float16* TB = reinterpret_cast<_Float16*>(lds + L.tb);
 
   // the wave index in a scalar register: the step's block offsets are then
   // scalar too
@@ -201,7 +203,7 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   const float alpha = __builtin_amdgcn_ldexpf(1.f, kS - kP - kV - kG);  // dP's scale into dS's, over P's
 
   // own rows split: K and V stay in registers (the b operand of S and dP);
-  // Q and dO go to their split rows and, with K, to the transposed planes
+  // Q, dO and K go to the transposed planes
   u4 kb[2], vb[2];
   {
     u4 qs[2], gs[2];
@@ -216,10 +218,6 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
       kb[0][j] = h[2], kb[1][j] = lo[2], vb[0][j] = h[3], vb[1][j] = lo[3];
     }
     if (active) {
-      u4* qr = const_cast<u4*>(QR) + i * (PairLds::RP / 16);
-      u4* gr = const_cast<u4*>(GR) + i * (PairLds::RP / 16);
-      qr[g] = qs[0], qr[4 + g] = qs[1];
-      gr[g] = gs[0], gr[4 + g] = gs[1];
 #pragma unroll
       for (int e = 0; e < W; ++e) {
         const int o = (8 * g + e) * PT + i;
@@ -248,9 +246,17 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   auto phase1 = [&](int s) {
     int I = w + s;
     if (I >= nb) I -= nb;
-    const u4* qr = QR + (16 * I + c) * (PairLds::RP / 16);
-    const u4* gr = GR + (16 * I + c) * (PairLds::RP / 16);
-    const u4 qa[2] = {qr[g], qr[4 + g]}, ga[2] = {gr[g], gr[4 + g]};
+    // a operand: query 16I + c, dims 8g .. 8g + 7, read transposed from the
+    // planes (rows 8g + 4u + c / 4, tokens 16I + 4 (c % 4) .. + 3)
+    u4 qa[2], ga[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int o = (8 * g + 4 * u + (c >> 2)) * PT + 16 * I + 4 * (c & 3);
+      const u2 x0 = lds_tr16(QTh + o), x1 = lds_tr16(QTh + PS + o);
+      const u2 y0 = lds_tr16(GTh + o), y1 = lds_tr16(GTh + PS + o);
+      qa[0][2 * u] = x0[0], qa[0][2 * u + 1] = x0[1], qa[1][2 * u] = x1[0], qa[1][2 * u + 1] = x1[1];
+      ga[0][2 * u] = y0[0], ga[0][2 * u + 1] = y0[1], ga[1][2 * u] = y1[0], ga[1][2 * u + 1] = y1[1];
+    }
     const f4 z = {0.f, 0.f, 0.f, 0.f};
     const f4 st = mfma3(qa, kb, z);  // S: key 16w + c (column), queries 16I + 4g + r
     const f4 dp = mfma3(ga, vb, z);
@@ -281,21 +287,21 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
       dv[t] = mfma3_16(gth, gtl, ph, pl, dv[t]);
       dk[t] = mfma3_16(qth, qtl, sh, sl, dk[t]);
     }
-    // dS to query block I's owner, transposed: T[query 4g + r][key c]
-    unsigned* tb = TB + ((s & 1) * NW + w) * (16 * PairLds::TP);
-    tb[(4 * g) * PairLds::TP + c] = lo_lo(sh[0], sl[0]);
-    tb[(4 * g + 1) * PairLds::TP + c] = hi_hi(sh[0], sl[0]);
-    tb[(4 * g + 2) * PairLds::TP + c] = lo_lo(sh[1], sl[1]);
-    tb[(4 * g + 3) * PairLds::TP + c] = hi_hi(sh[1], sl[1]);
+    // dS to query block I's owner: hi and lo tiles T[key c][query 4g + r],
+    // read back transposed
+    _Float16* tb = TB + ((s & 1) * NW + w) * (2 * PairLds::TS) + c * PairLds::TP + 4 * g;
+    *reinterpret_cast<u2*>(tb) = sh;
+    *reinterpret_cast<u2*>(tb + PairLds::TS) = sl;
   };
   // Phase 2 of step s: the own query block's tile from key block J = (w - s)
   // mod nb: dQ_w^T += K_J^T dS^T.
   auto phase2 = [&](int s) {
     int J = w - s;
     if (J < 0) J += nb;
-    const unsigned* tb = TB + ((s & 1) * NW + J) * (16 * PairLds::TP);
-    const uint4 p = *reinterpret_cast<const uint4*>(tb + c * PairLds::TP + 4 * g);  // query c, keys 4g .. + 3
-    const u2 bh = {lo_lo(p.x, p.y), lo_lo(p.z, p.w)}, bl = {hi_hi(p.x, p.y), hi_hi(p.z, p.w)};
+    // b operand: query c, keys 4g .. 4g + 3 (tile rows 4g + c / 4, queries
+    // 4 (c % 4) .. + 3)
+    const _Float16* tb = TB + ((s & 1) * NW + J) * (2 * PairLds::TS) + (4 * g + (c >> 2)) * PairLds::TP + 4 * (c & 3);
+    const u2 bh = lds_tr16(tb), bl = lds_tr16(tb + PairLds::TS);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
       const int o = (16 * t + c) * PT + 16 * J + 4 * g;
