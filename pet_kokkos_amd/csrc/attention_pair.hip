@@ -97,8 +97,7 @@ __device__ __forceinline__ void pair2x(float x, float y, unsigned& hi, unsigned&
 // The largest x over a row of 16 lanes, in every lane of the row (DPP row
 // rotations by 1, 2, 4, 8: vector instructions, no LDS).
 __device__ __forceinline__ float row_max16(float x) {
-#define PET_ROR(n) \
-  x = fmaxf(x, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x120 + (n), 0xf, 0xf, false)))
+#define PET_ROR(n) x = fmaxf(x, __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(x), 0x120 + (n), 0xf, 0xf, false)))
   PET_ROR(1);
   PET_ROR(2);
   PET_ROR(4);
@@ -149,21 +148,22 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   const bool active = w < at.nb, real = active && i < at.cnt;
 
   // ---- the wave's own block: rows 16w .. 16w + 15, lane (c, g) dims 8g .. 8g + 7
+  // A slot past the count loads slot 0's rows instead of zeros: as a query it
+  // has 1/sum 0 and as a key log cf kOff, so its P and dS are exactly 0 and
+  // it adds nothing (and, a copy of a row of the item, it moves no scale).
   float q[W], k[W], v[W], go[W], oo[W];
   float mi = kOff, li = 0.f, pcf = 0.f;
-  if (real) {
-    const size_t r = at.row(i);
+  if (active) {  // wave-uniform
+    const int si = real ? i : 0;
+    const size_t r = at.row(si);
     qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
     qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
     qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
     gmem_get<W>(dmerged + r * ldg + at.h * HD + g * W, go);
-    gmem_get<W>(merged + at.grow(i) * ldm + at.h * HD + g * W, oo);
-    const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
-    mi = m2[0], li = m2[1];
-    pcf = cf_seq[size_t(at.n) * ldc + i];
-  } else {
-#pragma unroll
-    for (int t = 0; t < W; ++t) q[t] = k[t] = v[t] = go[t] = oo[t] = 0.f;
+    gmem_get<W>(merged + at.grow(si) * ldm + at.h * HD + g * W, oo);
+    const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + si);
+    const float m0 = m2[0], l0 = m2[1], c0 = cf_seq[size_t(at.n) * ldc + si];
+    mi = real ? m0 : kOff, li = real ? l0 : 0.f, pcf = real ? c0 : 0.f;
   }
   // Row norms (over the head's dims; every lane of a row gets its row's), then
   // their largest over the item: the scales come from them (a row's largest
@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   const float Di = sum_g(dot);  // dO_i . O_i
   float m5[5] = {sum_g(nq), sum_g(nk), sum_g(nv), sum_g(ng), Di * Di};
 #pragma unroll
-  for (int u = 0; u < 5; ++u) m5[u] = row_max16(m5[u]);
+  for (int u = 0; u < 5; ++u) m5[u] = active ? row_max16(m5[u]) : 0.f;  // an idle wave's registers hold nothing
   if (l == 0) {
     *reinterpret_cast<float4*>(red + 8 * w) = make_float4(m5[0], m5[1], m5[2], m5[3]);
     red[8 * w + 4] = m5[4];
@@ -191,7 +191,7 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
     M[4] = fmaxf(M[4], red[8 * x + 4]);
   }
 #pragma unroll
-  for (int u = 0; u < 5; ++u) M[u] = sqrtf(M[u]);  // largest norms, largest |D|
+  for (int u = 0; u < 5; ++u) M[u] = __builtin_amdgcn_sqrtf(M[u]);  // largest norms, largest |D| (only their exponents matter)
   // scales 2^k: Q, K, V, dO by their largest row norm; dS by its bound
   // |dS_ij| = P_ij |dO_i.v_j - D_i| <= max|v| max|dO| + max|D| (Cauchy-Schwarz, P <= 1)
   const int kQ = pair_exp(M[0]), kK = pair_exp(M[1]), kV = pair_exp(M[2]), kG = pair_exp(M[3]);
