@@ -37,25 +37,43 @@ PEAK_BF16_MFMA = 2.5e15  # FLOP/s, MI355X dense bf16 (and fp16) matrix
 PEAK_SPLIT_FP32 = PEAK_BF16_MFMA / 6
 # an fp32 product as three fp16 products (the fp16-pair scheme)
 PEAK_PAIR_FP32 = PEAK_BF16_MFMA / 3
+# the same on the 16x16x16 fp16 instruction, which issues at half the 16x16x32
+# one's FLOP rate (measured on MI355X: 703 against 1236 TFLOP/s at best)
+PEAK_PAIR16_FP32 = PEAK_BF16_MFMA / 2 / 3
 PEAK_HBM = 8.0e12  # B/s
 
 
-def mixed_seconds(flops, split_share, pair_share=0.0):
+def mixed_seconds(flops, split_share, pair_share=0.0, pair16_share=0.0):
     """Time at the matrix-core ceilings of the instructions that run: the
     split_share of the FLOPs as split-fp32 products on the bf16 matrix cores
     (2.5 PFLOP/s / 6), the pair_share as fp16-pair products (2.5 PFLOP/s / 3),
-    the rest on the fp32 matrix cores (157.3 TFLOP/s)."""
-    rest = 1.0 - split_share - pair_share
-    return flops * (rest / PEAK_FP32_MFMA + split_share / PEAK_SPLIT_FP32 + pair_share / PEAK_PAIR_FP32)
+    the pair16_share as fp16-pair products on the 16x16x16 instruction
+    (1.25 PFLOP/s / 3), the rest on the fp32 matrix cores (157.3 TFLOP/s)."""
+    rest = 1.0 - split_share - pair_share - pair16_share
+    return flops * (rest / PEAK_FP32_MFMA + split_share / PEAK_SPLIT_FP32 + pair_share / PEAK_PAIR_FP32
+                    + pair16_share / PEAK_PAIR16_FP32)
 
 
 def split_shares(plan):
-    """Shares of the forward's and the backward's FLOPs that run as split
-    products: the forward's scores are half its FLOPs (scores, PV), the
-    backward's dP a fifth (scores, dP, dQ, dK, dV)."""
+    """Shares (split, pair, pair16) of the forward's and the backward's FLOPs
+    by the instructions that run them: the forward's scores are half its FLOPs
+    (scores, PV) and run split where fwd_split_scores; the backward's five
+    products (scores, dP, dQ, dK, dV) a fifth each: with bwd_pair the scores
+    and dP as fp16 pairs on the 16x16x32 instruction and the other three on
+    the 16x16x16 one, else dP split where bwd_split_dp."""
     if plan.get("streaming"):
-        return 0.0, 0.0
-    return 0.5 * plan["fwd_split_scores"], 0.2 * plan["bwd_split_dp"]
+        return (0.0, 0.0, 0.0), (0.0, 0.0, 0.0)
+    fwd = (0.5 * plan["fwd_split_scores"], 0.0, 0.0)
+    bwd = (0.0, 0.4, 0.6) if plan.get("bwd_pair") else (0.2 * plan["bwd_split_dp"], 0.0, 0.0)
+    return fwd, bwd
+
+
+def bwd_kernel_name(plan, hd):
+    if plan.get("streaming"):
+        return "attn_bwd_stream_kernel"
+    if plan.get("bwd_pair"):
+        return f"attn_bwd_pair_kernel<{plan['waves']}, false>"
+    return f"attn_bwd_kernel<{hd}, 512>"
 
 
 def algorithmic(tk, D, H):
@@ -175,7 +193,7 @@ def other_configs(device, reps):
         alg = algorithmic(tk, D, H)
         plan = _lib.describe(N, T, S, H, hd)
         fsh, bsh = split_shares(plan)
-        bound = max(mixed_seconds(alg["fwd_flops"], fsh) + mixed_seconds(alg["bwd_flops"], bsh),
+        bound = max(mixed_seconds(alg["fwd_flops"], *fsh) + mixed_seconds(alg["bwd_flops"], *bsh),
                     (alg["fwd_bytes"] + alg["bwd_bytes"]) / PEAK_HBM) * 1e6
         res[name] = dict(workload=conf.name, atoms=N, tokens=T, head_dim=hd, fwd_us=f_us, bwd_us=b_us,
                          bound_us=bound, frac_of_roofline=bound / (f_us + b_us), kernel_plan=plan)
@@ -329,20 +347,23 @@ def main():
     fsh, bsh = split_shares(plan)
     core_bytes = alg["fwd_bytes"] + alg["bwd_bytes"]
     # the core's bound at the ceilings of the instructions that run
-    core_mfma_s = mixed_seconds(alg["fwd_flops"], fsh) + mixed_seconds(alg["bwd_flops"], bsh)
+    core_mfma_s = mixed_seconds(alg["fwd_flops"], *fsh) + mixed_seconds(alg["bwd_flops"], *bsh)
     bound_us = max(core_mfma_s, core_bytes / PEAK_HBM) * 1e6
-    bwd_mfma_s = mixed_seconds(alg["bwd_flops"], bsh)
+    bwd_mfma_s = mixed_seconds(alg["bwd_flops"], *bsh)
+    kname = bwd_kernel_name(plan, hd) + " (+ attn_cf_adjoint_kernel)"
     if bwd_mfma_s >= alg["bwd_bytes"] / PEAK_HBM:
         peak = alg["bwd_flops"] / bwd_mfma_s  # fp32-equivalent FLOP/s of the instruction mix
         achieved = alg["bwd_flops"] / (bwd_avg * 1e-6) / 1e12
-        roof = dict(kernel=f"attn_bwd_kernel<{hd}, 512> (+ attn_cf_adjoint_kernel)", bound="mfma", achieved=achieved,
+        roof = dict(kernel=kname, bound="mfma", achieved=achieved,
                     peak=peak / 1e12, unit="TFLOP/s", frac=achieved / (peak / 1e12),
-                    ceiling=f"fp32 matrix peak 157.3 TFLOP/s for {100 * (1 - bsh):.0f}% of the FLOPs, split-fp32 on "
-                            f"the bf16 matrix cores (2.5 PFLOP/s / 6) for {100 * bsh:.0f}%")
+                    ceiling=f"fp32 matrix peak 157.3 TFLOP/s for {100 * (1 - sum(bsh)):.0f}% of the FLOPs, split-fp32 "
+                            f"on the bf16 matrix cores (2.5 PFLOP/s / 6) for {100 * bsh[0]:.0f}%")
     else:
         achieved = alg["bwd_bytes"] / (bwd_avg * 1e-6) / 1e9
-        roof = dict(kernel="attn_bwd_kernel", bound="hbm", achieved=achieved, peak=PEAK_HBM / 1e9, unit="GB/s",
-                    frac=achieved / (PEAK_HBM / 1e9))
+        roof = dict(kernel=kname, bound="hbm", achieved=achieved, peak=PEAK_HBM / 1e9, unit="GB/s",
+                    frac=achieved / (PEAK_HBM / 1e9),
+                    ceiling=f"HBM 8 TB/s; the matrix-core time at the ceilings of the instructions that run is "
+                            f"{bwd_mfma_s * 1e6:.1f} us")
     roof["traffic"] = None
     tpath = os.path.join(ROOT, "profiles", f"attn_bwd_{args.config}_traffic.json")
     if os.path.exists(tpath):
