@@ -57,13 +57,15 @@ def mixed_seconds(flops, split_share, pair_share=0.0, pair16_share=0.0):
 def split_shares(plan):
     """Shares (split, pair, pair16) of the forward's and the backward's FLOPs
     by the instructions that run them: the forward's scores are half its FLOPs
-    (scores, PV) and run split where fwd_split_scores; the backward's five
+    (scores, PV): with fwd_pair the scores as fp16 pairs on the 16x16x32
+    instruction and PV on the 16x16x16 one, else the scores split where
+    fwd_split_scores; the backward's five
     products (scores, dP, dQ, dK, dV) a fifth each: with bwd_pair the scores
     and dP as fp16 pairs on the 16x16x32 instruction and the other three on
     the 16x16x16 one, else dP split where bwd_split_dp."""
     if plan.get("streaming"):
         return (0.0, 0.0, 0.0), (0.0, 0.0, 0.0)
-    fwd = (0.5 * plan["fwd_split_scores"], 0.0, 0.0)
+    fwd = (0.0, 0.5, 0.5) if plan.get("fwd_pair") else (0.5 * plan["fwd_split_scores"], 0.0, 0.0)
     bwd = (0.0, 0.4, 0.6) if plan.get("bwd_pair") else (0.2 * plan["bwd_split_dp"], 0.0, 0.0)
     return fwd, bwd
 

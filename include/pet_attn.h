@@ -94,7 +94,9 @@ PET_ATTN_API int pet_attn_max_slots(int head_dim);
  * counterpart is its process-global GEMM mode (include/pet/gemm.hpp:119-122). */
 enum {
   PET_OPT_SPLIT = 1,       /* 1 (default): fp32 products split over the bf16 matrix cores where they pay; 0: fp32 MFMA only */
-  PET_OPT_FWD_KERNEL = 2,  /* 0 (default): matrix-core forward; 3: the vector-ALU forward (head_dim <= 64), for comparison */
+  PET_OPT_FWD_KERNEL = 2,  /* 0 (default): matrix-core forward, at head_dim 32 the fp16-pair one where it fits (with
+                              PET_OPT_SPLIT 1); 1: the staged forward with split-bf16 scores; 3: the vector-ALU
+                              forward (head_dim <= 64), for comparison */
   PET_OPT_BWD_VLDS = 3,    /* 0 (default): automatic; 1: V staged in LDS; 2: V read from global memory (where it fits) */
   PET_OPT_BWD_NBUF = 4,    /* 0 (default): automatic; 1 or 2 backward tile buffers (where it fits) */
   PET_OPT_MODEL_GEMM = 5,  /* the model's dense layers: 4 (default) split-product kernel for M*N*K >= 2^32, else rocBLAS;
@@ -125,6 +127,7 @@ typedef struct pet_attn_plan {
   int bwd_v_staged, bwd_tile_buffers;
   int bwd_lds_bytes, bwd_workgroups_per_cu;
   int bwd_pair;               /* the fp16-pair backward: every product as fp16 pairs on the 16-bit matrix cores */
+  int fwd_pair;               /* the fp16-pair forward */
 } pet_attn_plan;
 PET_ATTN_API int pet_attn_describe(const pet_attn_shape* shape, pet_attn_plan* out);
 

@@ -73,7 +73,7 @@ class Plan(ctypes.Structure):
     """pet_attn_plan (include/pet_attn.h)."""
     _fields_ = [(n, ctypes.c_int) for n in ("streaming", "waves", "fwd_split_scores", "fwd_valu", "fwd_lds_bytes",
                                              "fwd_workgroups_per_cu", "bwd_split_dp", "bwd_v_staged",
-                                             "bwd_tile_buffers", "bwd_lds_bytes", "bwd_workgroups_per_cu", "bwd_pair")]
+                                             "bwd_tile_buffers", "bwd_lds_bytes", "bwd_workgroups_per_cu", "bwd_pair", "fwd_pair")]
 
 
 def describe(n_atoms, n_rows, slots, heads, head_dim) -> dict:

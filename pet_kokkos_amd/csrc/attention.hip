@@ -758,7 +758,11 @@ struct Plan {
   int resident = 0;       // workgroups a CU
 };
 
-// The fp16-pair backward (attention_pair.hip), head_dim 32.
+// The fp16-pair forward and backward (attention_pair.hip), head_dim 32.
+size_t pair_fwd_bytes(int NW);
+const void* pair_fwd_kernel_ptr();
+int pair_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+             const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st);
 size_t pair_bwd_bytes(int NW);
 const void* pair_bwd_kernel_ptr();
 int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
@@ -786,11 +790,16 @@ Plan plan_fwd(const pet_attn_shape& sh, bool xf) {
       if (r >= p.resident) p.split = true, p.bytes = sbytes, p.resident = r;
     }
   }
+  if constexpr (HD == 32) {  // the fp16-pair forward (attention_pair.hip) unless an option asks otherwise
+    const size_t pb = pair_fwd_bytes(NW);
+    if (split_enabled() && option(PET_OPT_FWD_KERNEL) == 0 && pb <= cap)
+      p.pair = true, p.split = false, p.bytes = pb, p.resident = resident_wgs(pair_fwd_kernel_ptr(), NW, pb);
+  }
   if constexpr (HD <= 64) {  // option PET_OPT_FWD_KERNEL 3: the vector-ALU kernel, for comparison
     const int threads = 64 * ((sh.slots + 63) / 64);
     const size_t vb = sizeof(float) * (size_t(2) * threads * HD + threads);
     if (option(PET_OPT_FWD_KERNEL) == 3 && !xf && threads <= 256 && vb <= cap)
-      p.valu = true, p.split = false, p.bytes = vb, p.resident = 0;
+      p.valu = true, p.split = false, p.pair = false, p.bytes = vb, p.resident = 0;
   }
   return p;
 }
@@ -814,6 +823,7 @@ int launch_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float
       return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
     }
   }
+  if (p.pair) return pair_fwd(sh, n0, n1, eb, qkv, ldq, off, cf_seq, ldc, merged, ldm, ml, xf, st);
   using KT = decltype(&attn_fwd_kernel<HD, 512, false, false>);
   KT k;
   if constexpr (HD % 32 == 0) {
@@ -1033,7 +1043,7 @@ extern "C" int pet_attn_describe(const pet_attn_shape* sh, pet_attn_plan* out) {
     out->fwd_split_scores = f.split, out->fwd_valu = f.valu, out->fwd_lds_bytes = int(f.bytes);
     out->fwd_workgroups_per_cu = f.resident;
     out->bwd_split_dp = b.split, out->bwd_v_staged = b.vlds, out->bwd_tile_buffers = b.nbuf;
-    out->bwd_lds_bytes = int(b.bytes), out->bwd_workgroups_per_cu = b.resident, out->bwd_pair = b.pair;
+    out->bwd_lds_bytes = int(b.bytes), out->bwd_workgroups_per_cu = b.resident, out->bwd_pair = b.pair, out->fwd_pair = f.pair;
     out->waves = waves_for(sh->slots);
     return PET_ATTN_OK;
   });

@@ -43,6 +43,7 @@
 #include <cstdint>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "../../include/pet_attn.h"
@@ -341,6 +342,208 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   if (g == 0 && i < S) cfh[(size_t(at.n) * H + at.h) * S + i] = real ? cft : 0.f;
 }
 
+// ---- forward ---------------------------------------------------------------
+// The forward at head_dim 32 from the same pairs: a workgroup per (atom,
+// head), wave w owning query block w. Per key block J:
+//   S^T = K_J Q_w^T on the 16x16x32 instruction (K's rows read transposed from
+//   the K^T plane, Q_w split once in registers), a lane holding query 16w + c
+//   against keys 16J + 4g + r, so the online softmax reduces across the four
+//   g lanes only;
+//   O^T += V_J^T P^T on the 16x16x16 instruction, P (scaled by 2^15, split in
+//   registers) already its b operand, V^T's a operand 8-byte reads of the V^T
+//   plane.
+// The reference's forward (src/attention.cpp:205-266, :375-449): O_i =
+// sum_j softmax_j(sc q_i.k_j + log cf_j) v_j, (max, 1/sum) saved per query.
+// LDS: K^T and V^T as hi and lo planes [32 dims][R + 8 halves], log cf of
+// the R slots, the waves' maxima: 23.0 KB at five waves.
+struct PairFwdLds {
+  int R, PT;
+  size_t pl, lc, red, bytes;
+  __host__ __device__ constexpr explicit PairFwdLds(int NW)
+      : R(16 * NW), PT(16 * NW + 8), pl(0), lc(size_t(4) * kPairHD * PT * 2), red(lc + size_t(R) * 4),
+        bytes(red + size_t(8) * NW * 4) {}
+};
+
+template <int NW, bool XF>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(8)))
+attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __restrict__ off, int N, int n0,
+                     int64_t eb, int S, int H, float sc, const float* __restrict__ cf_seq, int64_t ldc,
+                     float* __restrict__ merged, int64_t ldm, float* __restrict__ ml, QkvXf xf) {
+  constexpr int HD = kPairHD, W = HD / 4, DT = HD / 16;
+  extern __shared__ float lds_f[];
+  unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
+  const int D = H * HD;
+  constexpr PairFwdLds L(NW);
+  constexpr int PT = L.PT, PS = HD * PT;
+  _Float16* KTh = reinterpret_cast<_Float16*>(lds + L.pl);
+  _Float16* VTh = KTh + 2 * PS;
+  float* lcf = reinterpret_cast<float*>(lds + L.lc);
+  float* red = reinterpret_cast<float*>(lds + L.red);
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int i = 16 * w + c;
+  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  const bool active = w < at.nb, real = active && i < at.cnt;
+
+  // own rows (lane (c, g): row 16w + c, dims 8g .. 8g + 7); a slot past the
+  // count loads slot 0's rows: its key's log cf is kOff (weight exactly 0)
+  // and its query's results are not stored
+  float q[W], k[W], v[W];
+  float pcf = 0.f;
+  if (active) {
+    const size_t r = at.row(real ? i : 0);
+    qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
+    qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
+    qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
+    const float c0 = cf_seq[size_t(at.n) * ldc + (real ? i : 0)];
+    pcf = real ? c0 : 0.f;
+  }
+  float nq = 0.f, nk = 0.f, nv = 0.f;
+#pragma unroll
+  for (int t = 0; t < W; ++t) nq += q[t] * q[t], nk += k[t] * k[t], nv += v[t] * v[t];
+  float m3[3] = {sum_g(nq), sum_g(nk), sum_g(nv)};
+#pragma unroll
+  for (int u = 0; u < 3; ++u) m3[u] = active ? row_max16(m3[u]) : 0.f;
+  if (l == 0) red[8 * w] = m3[0], red[8 * w + 1] = m3[1], red[8 * w + 2] = m3[2];
+  if (g == 0) lcf[i] = pcf > 0.f ? log_cf(pcf) : kOff;
+  lds_barrier();
+  float M[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int x = 0; x < NW; ++x) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) M[u] = fmaxf(M[u], red[8 * x + u]);
+  }
+  const int kQ = pair_exp(__builtin_amdgcn_sqrtf(M[0])), kK = pair_exp(__builtin_amdgcn_sqrtf(M[1]));
+  const int kV = pair_exp(__builtin_amdgcn_sqrtf(M[2]));
+  const float sQ = __builtin_amdgcn_ldexpf(1.f, kQ), sK = __builtin_amdgcn_ldexpf(1.f, kK);
+  const float sV = __builtin_amdgcn_ldexpf(1.f, kV);
+  const float scS = __builtin_amdgcn_ldexpf(sc, -kQ - kK);
+  u4 qb[2];
+  {
+#pragma unroll
+    for (int j = 0; j < W / 2; ++j) {
+      unsigned h[3], lo[3];
+      pair2x(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);
+      pair2x(k[2 * j] * sK, k[2 * j + 1] * sK, h[1], lo[1]);
+      pair2x(v[2 * j] * sV, v[2 * j + 1] * sV, h[2], lo[2]);
+      qb[0][j] = h[0], qb[1][j] = lo[0];
+      if (active) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int o = (8 * g + 2 * j + e) * PT + i;
+          KTh[o] = __builtin_bit_cast(pet_split::h2v, h[1])[e], KTh[PS + o] = __builtin_bit_cast(pet_split::h2v, lo[1])[e];
+          VTh[o] = __builtin_bit_cast(pet_split::h2v, h[2])[e], VTh[PS + o] = __builtin_bit_cast(pet_split::h2v, lo[2])[e];
+        }
+      }
+    }
+  }
+  if (!active) {  // slots past the atom's tokens: their sentinel statistics, and the workgroup barrier
+    if (ml && g == 0 && i < S) {
+      float* mlq = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
+      mlq[0] = kOff, mlq[1] = 0.f;
+    }
+    lds_barrier();
+    return;
+  }
+  float mx = kFloor, sum = 0.f;
+  f4 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  // S^T of key block J: s[r] = query i against key 16J + 4g + r
+  auto scores = [&](int J) {
+    u4 a[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int o = (8 * g + 4 * u + (c >> 2)) * PT + 16 * J + 4 * (c & 3);
+      const u2 x0 = lds_tr16(KTh + o), x1 = lds_tr16(KTh + PS + o);
+      a[0][2 * u] = x0[0], a[0][2 * u + 1] = x0[1], a[1][2 * u] = x1[0], a[1][2 * u + 1] = x1[1];
+    }
+    return mfma3(a, qb, f4{0.f, 0.f, 0.f, 0.f});
+  };
+  // O^T += V_J^T P^T from the block's weights p (2^15 P)
+  auto pv = [&](int J, const float* p) {
+    unsigned h[2], lo[2];
+    pair2x(p[0], p[1], h[0], lo[0]);
+    pair2x(p[2], p[3], h[1], lo[1]);
+    const u2 ph = {h[0], h[1]}, pl = {lo[0], lo[1]};
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int o = (16 * t + c) * PT + 16 * J + 4 * g;
+      acc[t] = mfma3_16(*reinterpret_cast<const u2*>(VTh + o), *reinterpret_cast<const u2*>(VTh + PS + o), ph, pl,
+                        acc[t]);
+    }
+  };
+  constexpr float kP = 32768.f;
+  auto block = [&](int J, const f4& s) {
+    const float4 l4 = *reinterpret_cast<const float4*>(lcf + 16 * J + 4 * g);
+    const float lc[4] = {l4.x, l4.y, l4.z, l4.w};
+    float x[4], bm = kOff;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = s[r] * scS + lc[r], bm = fmaxf(bm, x[r]);
+    const float nm = fmaxf(mx, max_g(bm));
+    const float alpha = __expf(mx - nm);
+    float p[4], ps[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = __expf(x[r] - nm), ps[r] = p[r] * kP;
+    sum = sum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    mx = nm;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    pv(J, ps);
+  };
+  auto block2 = [&](int J0, const f4& s0, int J1, const f4& s1) {
+    const float4 a4 = *reinterpret_cast<const float4*>(lcf + 16 * J0 + 4 * g);
+    const float4 b4 = *reinterpret_cast<const float4*>(lcf + 16 * J1 + 4 * g);
+    const float lc[8] = {a4.x, a4.y, a4.z, a4.w, b4.x, b4.y, b4.z, b4.w};
+    float x[8], bm = kOff;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = s0[r] * scS + lc[r], x[4 + r] = s1[r] * scS + lc[4 + r];
+      bm = fmaxf(bm, fmaxf(x[r], x[4 + r]));
+    }
+    const float nm = fmaxf(mx, max_g(bm));
+    const float alpha = __expf(mx - nm);
+    float p[8], ps[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) p[r] = __expf(x[r] - nm), ps[r] = p[r] * kP;
+    sum = sum * alpha + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+    mx = nm;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    pv(J0, ps);
+    pv(J1, ps + 4);
+  };
+  // the own key block first (the wave staged it itself), before the barrier;
+  // then the others w + 1, w + 2, ... (mod nb), two at a time, an odd one last
+  block(w, scores(w));
+  lds_barrier();
+  auto next = [&](int j) { return j + 1 < at.nb ? j + 1 : 0; };
+  int rem = at.nb - 1, J0 = next(w);
+  for (; rem >= 2; rem -= 2) {
+    const int J1 = next(J0);
+    const f4 s0 = scores(J0), s1 = scores(J1);
+    block2(J0, s0, J1, s1);
+    J0 = next(J1);
+  }
+  if (rem == 1) block(J0, scores(J0));
+  const float tot = sum_g(sum);
+  // a query on an edge at its cutoff gets zeros
+  const bool live = real && (i == 0 || !is_off(lcf[i]));
+  const float invl = live && tot > 0.f ? 1.0f / tot : 0.f;
+  const float mxs = live && tot > 0.f ? mx : kOff;  // no live key: the max never left kFloor
+  if (real) {
+    const float f = __builtin_amdgcn_ldexpf(invl, -15 - kV);
+    float* o = merged + at.grow(i) * ldm + at.h * HD + 4 * g;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+      *reinterpret_cast<float4*>(o + 16 * t) = make_float4(acc[t][0] * f, acc[t][1] * f, acc[t][2] * f, acc[t][3] * f);
+  }
+  if (ml && g == 0 && i < S) {
+    float* mlq = ml + 2 * ((size_t(at.n) * H + at.h) * S + i);
+    mlq[0] = real ? mxs : kOff, mlq[1] = real ? invl : 0.f;
+  }
+}
+
 // ---- host side ---------------------------------------------------------------
 
 size_t pair_bwd_bytes(int NW) { return NW <= kPairMaxWaves ? PairLds(NW).bytes : ~size_t(0); }
@@ -390,6 +593,37 @@ int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* 
   }
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots,
                      sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, xf);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+size_t pair_fwd_bytes(int NW) { return NW <= kPairMaxWaves ? PairFwdLds(NW).bytes : ~size_t(0); }
+
+const void* pair_fwd_kernel_ptr() { return reinterpret_cast<const void*>(attn_fwd_pair_kernel<5, false>); }
+
+int pair_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
+             const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st) {
+  const int NW = (sh.slots + 15) / 16;
+  if (NW > kPairMaxWaves) return PET_ATTN_ESLOTS;
+  const int64_t items = int64_t(n1 - n0) * sh.heads;
+  if (items == 0) return PET_ATTN_OK;
+  const bool x = xf.rs || xf.b;
+  decltype(&attn_fwd_pair_kernel<1, false>) k = nullptr;
+  auto pick = [&](auto nw) {
+    constexpr int V = decltype(nw)::value;
+    k = x ? attn_fwd_pair_kernel<V, true> : attn_fwd_pair_kernel<V, false>;
+  };
+  switch (NW) {
+    case 1: pick(std::integral_constant<int, 1>{}); break;
+    case 2: pick(std::integral_constant<int, 2>{}); break;
+    case 3: pick(std::integral_constant<int, 3>{}); break;
+    case 4: pick(std::integral_constant<int, 4>{}); break;
+    case 5: pick(std::integral_constant<int, 5>{}); break;
+    case 6: pick(std::integral_constant<int, 6>{}); break;
+    case 7: pick(std::integral_constant<int, 7>{}); break;
+    default: pick(std::integral_constant<int, 8>{}); break;
+  }
+  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), pair_fwd_bytes(NW), st, qkv, ldq, off, sh.n_atoms, n0,
+                     eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 

@@ -220,21 +220,24 @@ def test_pair_backward_scales(device, qk, v, g, spread):
     qkv[:, 2 * D:] *= v * 10.0 ** rng.uniform(-spread, spread, (qkv.shape[0], 1))
     dm = (dm * g * 10.0 ** rng.uniform(-spread, spread, (dm.shape[0], 1))).astype(np.float32)
     qkv = qkv.astype(np.float32)
-    assert A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 2, 32)["bwd_pair"] == 1
+    plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 2, 32)
+    assert plan["bwd_pair"] == 1 and plan["fwd_pair"] == 1
     check_against_oracle(device, f"pair backward qk x{qk} v x{v} dO x{g} spread 1e+-{spread}", tk.off,
                          tk.cf_seq, qkv, dm, 2, 32)
 
 
-@pytest.mark.parametrize("kernel", [0, 1])
-def test_backward_kernels(device, kernel):
-    # Both head_dim-32 backwards (option bwd_kernel: 0 the fp16-pair kernel,
-    # 1 the tile-exchange kernel) on ragged atoms with dead rows, each
-    # bit-identical when repeated.
+@pytest.mark.parametrize("fwd,bwd", [(0, 0), (1, 1), (0, 1), (1, 0)])
+def test_pair_and_staged_kernels(device, fwd, bwd):
+    # The head_dim-32 kernels in each combination (option fwd_kernel / bwd_kernel:
+    # 0 the fp16-pair kernels, 1 the staged split-bf16 forward and the
+    # tile-exchange backward) on ragged atoms, each bit-identical when repeated.
     counts = [0, 15, 16, 31, 47, 5, 60, 33, 70]
     tk, qkv, dm = random_case(counts, 3, 32, seed=400, cf_kind="random")
-    with A._lib.options(bwd_kernel=kernel):
-        assert A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 3, 32)["bwd_pair"] == (kernel == 0)
-        first = check_against_oracle(device, f"backward kernel {kernel}", tk.off, tk.cf_seq, qkv, dm, 3, 32)
+    with A._lib.options(fwd_kernel=fwd, bwd_kernel=bwd):
+        plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 3, 32)
+        assert plan["fwd_pair"] == (fwd == 0) and plan["bwd_pair"] == (bwd == 0)
+        first = check_against_oracle(device, f"forward kernel {fwd}, backward kernel {bwd}", tk.off, tk.cf_seq, qkv,
+                                     dm, 3, 32)
         again = gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 3, 32)
     for a, b in zip(first, again):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
