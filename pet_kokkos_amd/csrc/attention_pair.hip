@@ -50,10 +50,18 @@
 #include "attn_common.h"
 #include "split_bf16.h"
 
+// No implicit contraction in this file: a split's hi and lo must come from one
+// rounded fp32 value, and a multiply contracted into lo's subtraction (an
+// fma_mix on the unrounded product) can disagree with the hi taken from the
+// rounded product by an fp16 ulp. Where a fused multiply-add is meant, fmaf.
+#pragma clang fp contract(off)
+
 namespace pet_attn {
 
 using pet_split::mfma3;
 using pet_split::mfma3_16;
+using pet_split::mfma4;
+using pet_split::mfma4_16;
 using pet_split::u2;
 using pet_split::u4;
 
@@ -84,12 +92,18 @@ __device__ __forceinline__ u2 lds_tr16(const _Float16* p) {
   return __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
 }
 
-// Two scaled values as fp16 (hi, lo) registers, hi the truncation of x to
-// fp16 (also where x is an fp16 subnormal) and lo the remainder x - hi (exact
-// in fp32) rounded to the nearest fp16: |x - hi - lo| <= 2^-22 |x|, or <= 2^-25
-// where x is below fp16's normal range.
+// Two scaled values as fp16 (hi, lo) registers: hi x rounded to 11
+// significant bits (to nearest, ties away from zero, on the fp32 bits: exact in
+// fp16's normal range; below it the conversion truncates further), lo the
+// remainder x - hi (exact in fp32, from the fp16 hi itself) rounded to the
+// nearest fp16: |x - hi - lo| <= 2^-23 |x|, or <= 2^-25 below fp16's normal
+// range (|x| < 2^15 here). The integer rounding also pins x to one rounded
+// fp32 value: a multiply fused into an fp16 conversion (fma_mix on the
+// unrounded product) could otherwise give hi and lo different x's.
 __device__ __forceinline__ void pair2x(float x, float y, unsigned& hi, unsigned& lo) {
-  const auto h = __builtin_amdgcn_cvt_pkrtz(x, y);
+  const float hx = __uint_as_float((__float_as_uint(x) + 0x1000u) & 0xffffe000u);
+  const float hy = __uint_as_float((__float_as_uint(y) + 0x1000u) & 0xffffe000u);
+  const auto h = __builtin_amdgcn_cvt_pkrtz(hx, hy);
   const pet_split::h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
   hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
@@ -172,8 +186,8 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   float nq = 0.f, nk = 0.f, nv = 0.f, ng = 0.f, dot = 0.f;
 #pragma unroll
   for (int t = 0; t < W; ++t) {
-    nq += q[t] * q[t], nk += k[t] * k[t], nv += v[t] * v[t], ng += go[t] * go[t];
-    dot += go[t] * oo[t];
+    nq = fmaf(q[t], q[t], nq), nk = fmaf(k[t], k[t], nk), nv = fmaf(v[t], v[t], nv), ng = fmaf(go[t], go[t], ng);
+    dot = fmaf(go[t], oo[t], dot);
   }
   const float Di = sum_g(dot);  // dO_i . O_i
   float m5[5] = {sum_g(nq), sum_g(nk), sum_g(nv), sum_g(ng), Di * Di};
@@ -196,7 +210,7 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
   // scales 2^k: Q, K, V, dO by their largest row norm; dS by its bound
   // |dS_ij| = P_ij |dO_i.v_j - D_i| <= max|v| max|dO| + max|D| (Cauchy-Schwarz, P <= 1)
   const int kQ = pair_exp(M[0]), kK = pair_exp(M[1]), kV = pair_exp(M[2]), kG = pair_exp(M[3]);
-  const int kS = pair_exp(M[2] * M[3] + M[4]);
+  const int kS = pair_exp(fmaf(M[2], M[3], M[4]));
   constexpr int kP = 15;  // P's scale 2^15
   const float sQ = __builtin_amdgcn_ldexpf(1.f, kQ), sK = __builtin_amdgcn_ldexpf(1.f, kK);
   const float sV = __builtin_amdgcn_ldexpf(1.f, kV), sG = __builtin_amdgcn_ldexpf(1.f, kG);
@@ -268,7 +282,7 @@ __global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __r
     float pp[4], ds[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      pp[r] = __expf(st[r] * scS + (lcj - mm[r])) * ll[r];  // 2^15 P
+      pp[r] = __expf(fmaf(st[r], scS, lcj - mm[r])) * ll[r];  // 2^15 P
       ds[r] = pp[r] * fmaf(dp[r], alpha, -dd[r]);           // sS dS
       cfa += ds[r];
     }
@@ -400,7 +414,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   }
   float nq = 0.f, nk = 0.f, nv = 0.f;
 #pragma unroll
-  for (int t = 0; t < W; ++t) nq += q[t] * q[t], nk += k[t] * k[t], nv += v[t] * v[t];
+  for (int t = 0; t < W; ++t) nq = fmaf(q[t], q[t], nq), nk = fmaf(k[t], k[t], nk), nv = fmaf(v[t], v[t], nv);
   float m3[3] = {sum_g(nq), sum_g(nk), sum_g(nv)};
 #pragma unroll
   for (int u = 0; u < 3; ++u) m3[u] = active ? row_max16(m3[u]) : 0.f;
@@ -479,13 +493,13 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     const float lc[4] = {l4.x, l4.y, l4.z, l4.w};
     float x[4], bm = kOff;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = s[r] * scS + lc[r], bm = fmaxf(bm, x[r]);
+    for (int r = 0; r < 4; ++r) x[r] = fmaf(s[r], scS, lc[r]), bm = fmaxf(bm, x[r]);
     const float nm = fmaxf(mx, max_g(bm));
     const float alpha = __expf(mx - nm);
     float p[4], ps[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) p[r] = __expf(x[r] - nm), ps[r] = p[r] * kP;
-    sum = sum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    sum = fmaf(sum, alpha, (p[0] + p[1]) + (p[2] + p[3]));
     mx = nm;
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc[t] *= alpha;
@@ -498,7 +512,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     float x[8], bm = kOff;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      x[r] = s0[r] * scS + lc[r], x[4 + r] = s1[r] * scS + lc[4 + r];
+      x[r] = fmaf(s0[r], scS, lc[r]), x[4 + r] = fmaf(s1[r], scS, lc[4 + r]);
       bm = fmaxf(bm, fmaxf(x[r], x[4 + r]));
     }
     const float nm = fmaxf(mx, max_g(bm));
@@ -506,7 +520,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     float p[8], ps[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) p[r] = __expf(x[r] - nm), ps[r] = p[r] * kP;
-    sum = sum * alpha + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+    sum = fmaf(sum, alpha, ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
     mx = nm;
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc[t] *= alpha;

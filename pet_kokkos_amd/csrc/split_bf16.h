@@ -76,6 +76,15 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ f4 mfma_h(const u4& a, const u4& b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
 }
+// c += a.b with the fourth part product a_lo b_lo too: the error left is the
+// rounding of the lo parts (2^-22 |a||b| at most, fp32's own order), where
+// mfma3 also drops a_lo b_lo (up to 2^-20 |a||b|)
+__device__ __forceinline__ f4 mfma4(const u4* a, const u4* b, f4 c) {
+  c = mfma_h(a[1], b[1], c);
+  c = mfma_h(a[1], b[0], c);
+  c = mfma_h(a[0], b[1], c);
+  return mfma_h(a[0], b[0], c);
+}
 // c += a.b from (hi, lo) parts, the small products first
 __device__ __forceinline__ f4 mfma3(const u4* a, const u4* b, f4 c) {
   c = mfma_h(a[1], b[0], c);
@@ -104,6 +113,13 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef unsigned u2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ f4 mfma_h16(const u2& a, const u2& b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
+}
+// the same with a_lo b_lo too (as mfma4)
+__device__ __forceinline__ f4 mfma4_16(const u2& ah, const u2& al, const u2& bh, const u2& bl, f4 c) {
+  c = mfma_h16(al, bl, c);
+  c = mfma_h16(al, bh, c);
+  c = mfma_h16(ah, bl, c);
+  return mfma_h16(ah, bh, c);
 }
 // c += a.b from (hi, lo) parts a = (ah, al), b = (bh, bl), the small products first
 __device__ __forceinline__ f4 mfma3_16(const u2& ah, const u2& al, const u2& bh, const u2& bl, f4 c) {
