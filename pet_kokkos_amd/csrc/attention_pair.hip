@@ -129,7 +129,7 @@ __device__ __forceinline__ int pair_exp(float m) {
 }  // namespace
 
 template <int NW, bool XF>
-__global__ void __launch_bounds__(64 * NW) attn_bwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq,
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW >= 4 ? 6 : 5))) attn_bwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                              const int* __restrict__ off, int N, int n0, int64_t eb,
                                                              int S, int H, float sc,
                                                              const float* __restrict__ dmerged, int64_t ldg,
