@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 // The reference's forward (src/attention.cpp:205-266, :375-449): O_i =
 // sum_j softmax_j(sc q_i.k_j + log cf_j) v_j, (max, 1/sum) saved per query.
 // LDS: K^T and V^T as hi and lo planes [32 dims][R + 8 halves], log cf of
-// the R slots, the waves' maxima: 23.0 KB at five waves.
+// the R slots, each key block's two scale exponents: 23.0 KB at five waves.
 struct PairFwdLds {
   int R, PT;
   size_t pl, lc, red, bytes;
@@ -412,26 +412,26 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     const float c0 = cf_seq[size_t(at.n) * ldc + (real ? i : 0)];
     pcf = real ? c0 : 0.f;
   }
+  // Scales per 16-slot block, from the wave's own rows: Q's (this wave's
+  // queries), K's and V's (this key block's), each the power of two putting
+  // the block's largest row norm at [2^14, 2^15). A block's scores are undone
+  // by 2^-(kQ + kK_J); P V accumulates in units of a running V scale 2^kcur,
+  // the smallest kV_J seen so far (the largest V), with block J's weights
+  // scaled by 2^(15 + kcur - kV_J) <= 2^15 and the accumulator rescaled by a
+  // power of two (with the softmax's own rescale) when kcur drops. No
+  // workgroup-wide maximum, so a wave computes its own block before the
+  // workgroup's only barrier.
+  int* kex = reinterpret_cast<int*>(red);  // kK_J at 2J, kV_J at 2J + 1
   float nq = 0.f, nk = 0.f, nv = 0.f;
 #pragma unroll
   for (int t = 0; t < W; ++t) nq = fmaf(q[t], q[t], nq), nk = fmaf(k[t], k[t], nk), nv = fmaf(v[t], v[t], nv);
-  float m3[3] = {sum_g(nq), sum_g(nk), sum_g(nv)};
-#pragma unroll
-  for (int u = 0; u < 3; ++u) m3[u] = active ? row_max16(m3[u]) : 0.f;
-  if (l == 0) red[8 * w] = m3[0], red[8 * w + 1] = m3[1], red[8 * w + 2] = m3[2];
+  const int kQ = __builtin_amdgcn_readfirstlane(pair_exp(__builtin_amdgcn_sqrtf(row_max16(sum_g(nq)))));
+  const int kKw = __builtin_amdgcn_readfirstlane(pair_exp(__builtin_amdgcn_sqrtf(row_max16(sum_g(nk)))));
+  const int kVw = __builtin_amdgcn_readfirstlane(pair_exp(__builtin_amdgcn_sqrtf(row_max16(sum_g(nv)))));
+  if (l == 0) kex[2 * w] = kKw, kex[2 * w + 1] = kVw;
   if (g == 0) lcf[i] = pcf > 0.f ? log_cf(pcf) : kOff;
-  lds_barrier();
-  float M[3] = {0.f, 0.f, 0.f};
-#pragma unroll
-  for (int x = 0; x < NW; ++x) {
-#pragma unroll
-    for (int u = 0; u < 3; ++u) M[u] = fmaxf(M[u], red[8 * x + u]);
-  }
-  const int kQ = pair_exp(__builtin_amdgcn_sqrtf(M[0])), kK = pair_exp(__builtin_amdgcn_sqrtf(M[1]));
-  const int kV = pair_exp(__builtin_amdgcn_sqrtf(M[2]));
-  const float sQ = __builtin_amdgcn_ldexpf(1.f, kQ), sK = __builtin_amdgcn_ldexpf(1.f, kK);
-  const float sV = __builtin_amdgcn_ldexpf(1.f, kV);
-  const float scS = __builtin_amdgcn_ldexpf(sc, -kQ - kK);
+  const float sQ = __builtin_amdgcn_ldexpf(1.f, kQ), sK = __builtin_amdgcn_ldexpf(1.f, kKw);
+  const float sV = __builtin_amdgcn_ldexpf(1.f, kVw);
   u4 qb[2];
   {
 #pragma unroll
@@ -460,10 +460,14 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     return;
   }
   float mx = kFloor, sum = 0.f;
+  int kcur = kVw;
   f4 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  // S^T of key block J: s[r] = query i against key 16J + 4g + r
+  // block J's scale exponents (the own block's in registers)
+  auto kK_of = [&](int J) { return J == w ? kKw : __builtin_amdgcn_readfirstlane(kex[2 * J]); };
+  auto kV_of = [&](int J) { return J == w ? kVw : __builtin_amdgcn_readfirstlane(kex[2 * J + 1]); };
+  // S^T of key block J: s[r] = query i against key 16J + 4g + r, in 2^(kQ + kK_J) units
   auto scores = [&](int J) {
     u4 a[2];
 #pragma unroll
@@ -474,7 +478,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     }
     return mfma3(a, qb, f4{0.f, 0.f, 0.f, 0.f});
   };
-  // O^T += V_J^T P^T from the block's weights p (2^15 P)
+  // O^T += V_J^T P^T from the block's scaled weights p
   auto pv = [&](int J, const float* p) {
     unsigned h[2], lo[2];
     pair2x(p[0], p[1], h[0], lo[0]);
@@ -487,8 +491,9 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
                         acc[t]);
     }
   };
-  constexpr float kP = 32768.f;
   auto block = [&](int J, const f4& s) {
+    const float scS = __builtin_amdgcn_ldexpf(sc, -kQ - kK_of(J));
+    const int kv = kV_of(J);
     const float4 l4 = *reinterpret_cast<const float4*>(lcf + 16 * J + 4 * g);
     const float lc[4] = {l4.x, l4.y, l4.z, l4.w};
     float x[4], bm = kOff;
@@ -496,34 +501,45 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     for (int r = 0; r < 4; ++r) x[r] = fmaf(s[r], scS, lc[r]), bm = fmaxf(bm, x[r]);
     const float nm = fmaxf(mx, max_g(bm));
     const float alpha = __expf(mx - nm);
+    const int kn = min(kcur, kv);
     float p[4], ps[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = __expf(x[r] - nm), ps[r] = p[r] * kP;
+    for (int r = 0; r < 4; ++r) p[r] = __expf(x[r] - nm), ps[r] = __builtin_amdgcn_ldexpf(p[r], 15 + kn - kv);
     sum = fmaf(sum, alpha, (p[0] + p[1]) + (p[2] + p[3]));
     mx = nm;
+    const float f = __builtin_amdgcn_ldexpf(alpha, kn - kcur);
+    kcur = kn;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    for (int t = 0; t < DT; ++t) acc[t] *= f;
     pv(J, ps);
   };
   auto block2 = [&](int J0, const f4& s0, int J1, const f4& s1) {
+    const float sc0 = __builtin_amdgcn_ldexpf(sc, -kQ - kK_of(J0)), sc1 = __builtin_amdgcn_ldexpf(sc, -kQ - kK_of(J1));
+    const int kv0 = kV_of(J0), kv1 = kV_of(J1);
     const float4 a4 = *reinterpret_cast<const float4*>(lcf + 16 * J0 + 4 * g);
     const float4 b4 = *reinterpret_cast<const float4*>(lcf + 16 * J1 + 4 * g);
     const float lc[8] = {a4.x, a4.y, a4.z, a4.w, b4.x, b4.y, b4.z, b4.w};
     float x[8], bm = kOff;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      x[r] = fmaf(s0[r], scS, lc[r]), x[4 + r] = fmaf(s1[r], scS, lc[4 + r]);
+      x[r] = fmaf(s0[r], sc0, lc[r]), x[4 + r] = fmaf(s1[r], sc1, lc[4 + r]);
       bm = fmaxf(bm, fmaxf(x[r], x[4 + r]));
     }
     const float nm = fmaxf(mx, max_g(bm));
     const float alpha = __expf(mx - nm);
+    const int kn = min(kcur, min(kv0, kv1));
     float p[8], ps[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) p[r] = __expf(x[r] - nm), ps[r] = p[r] * kP;
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __expf(x[r] - nm), ps[r] = __builtin_amdgcn_ldexpf(p[r], 15 + kn - kv0);
+      p[4 + r] = __expf(x[4 + r] - nm), ps[4 + r] = __builtin_amdgcn_ldexpf(p[4 + r], 15 + kn - kv1);
+    }
     sum = fmaf(sum, alpha, ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
     mx = nm;
+    const float f = __builtin_amdgcn_ldexpf(alpha, kn - kcur);
+    kcur = kn;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    for (int t = 0; t < DT; ++t) acc[t] *= f;
     pv(J0, ps);
     pv(J1, ps + 4);
   };
@@ -546,7 +562,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   const float invl = live && tot > 0.f ? 1.0f / tot : 0.f;
   const float mxs = live && tot > 0.f ? mx : kOff;  // no live key: the max never left kFloor
   if (real) {
-    const float f = __builtin_amdgcn_ldexpf(invl, -15 - kV);
+    const float f = __builtin_amdgcn_ldexpf(invl, -15 - kcur);
     float* o = merged + at.grow(i) * ldm + at.h * HD + 4 * g;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
