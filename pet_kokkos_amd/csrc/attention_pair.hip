@@ -109,6 +109,16 @@ __device__ __forceinline__ void pair2x(float x, float y, unsigned& hi, unsigned&
   lo = __builtin_bit_cast(unsigned, l);
 }
 
+// pair2x for values that are not a product (an exp's result scaled by ldexp):
+// hi the fp16 nearest x, lo the remainder; no multiply can be fused into the
+// conversion, so one rounded x serves both parts. Same bounds.
+__device__ __forceinline__ void pair2n(float x, float y, unsigned& hi, unsigned& lo) {
+  const pet_split::h2v h = {(_Float16)x, (_Float16)y};
+  const pet_split::h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
+  hi = __builtin_bit_cast(unsigned, h);
+  lo = __builtin_bit_cast(unsigned, l);
+}
+
 // The largest x over a row of 16 lanes, in every lane of the row (DPP row
 // rotations by 1, 2, 4, 8: vector instructions, no LDS).
 __device__ __forceinline__ float row_max16(float x) {
@@ -481,8 +491,8 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   // O^T += V_J^T P^T from the block's scaled weights p
   auto pv = [&](int J, const float* p) {
     unsigned h[2], lo[2];
-    pair2x(p[0], p[1], h[0], lo[0]);
-    pair2x(p[2], p[3], h[1], lo[1]);
+    pair2n(p[0], p[1], h[0], lo[0]);
+    pair2n(p[2], p[3], h[1], lo[1]);
     const u2 ph = {h[0], h[1]}, pl = {lo[0], lo[1]};
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
