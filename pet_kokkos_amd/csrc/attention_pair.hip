@@ -109,9 +109,9 @@ __device__ __forceinline__ void pair2x(float x, float y, unsigned& hi, unsigned&
   lo = __builtin_bit_cast(unsigned, l);
 }
 
-// pair2x for values that are not a product (an exp's result scaled by ldexp):
-// hi the fp16 nearest x, lo the remainder; no multiply can be fused into the
-// conversion, so one rounded x serves both parts. Same bounds.
+// pair2x for values whose rounding to fp16 cannot be fused with an inexact
+// multiply (an exp's result scaled by ldexp, a product by a power of two):
+// hi the fp16 nearest x, lo the remainder from that hi. Same bounds.
 __device__ __forceinline__ void pair2n(float x, float y, unsigned& hi, unsigned& lo) {
   const pet_split::h2v h = {(_Float16)x, (_Float16)y};
   const pet_split::h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
@@ -235,10 +235,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 #pragma unroll
     for (int j = 0; j < W / 2; ++j) {
       unsigned h[4], lo[4];
-      pair2x(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);
-      pair2x(go[2 * j] * sG, go[2 * j + 1] * sG, h[1], lo[1]);
-      pair2x(k[2 * j] * sK, k[2 * j + 1] * sK, h[2], lo[2]);
-      pair2x(v[2 * j] * sV, v[2 * j + 1] * sV, h[3], lo[3]);
+      // products by powers of two are exact: a conversion fused with them
+      // rounds the same value (pair2n)
+      pair2n(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);
+      pair2n(go[2 * j] * sG, go[2 * j + 1] * sG, h[1], lo[1]);
+      pair2n(k[2 * j] * sK, k[2 * j + 1] * sK, h[2], lo[2]);
+      pair2n(v[2 * j] * sV, v[2 * j + 1] * sV, h[3], lo[3]);
       qs[0][j] = h[0], qs[1][j] = lo[0], gs[0][j] = h[1], gs[1][j] = lo[1];
       kb[0][j] = h[2], kb[1][j] = lo[2], vb[0][j] = h[3], vb[1][j] = lo[3];
     }
@@ -447,9 +449,9 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
 #pragma unroll
     for (int j = 0; j < W / 2; ++j) {
       unsigned h[3], lo[3];
-      pair2x(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);
-      pair2x(k[2 * j] * sK, k[2 * j + 1] * sK, h[1], lo[1]);
-      pair2x(v[2 * j] * sV, v[2 * j + 1] * sV, h[2], lo[2]);
+      pair2n(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);  // exact products (pair2n)
+      pair2n(k[2 * j] * sK, k[2 * j + 1] * sK, h[1], lo[1]);
+      pair2n(v[2 * j] * sV, v[2 * j + 1] * sV, h[2], lo[2]);
       qb[0][j] = h[0], qb[1][j] = lo[0];
       if (active) {
 #pragma unroll
