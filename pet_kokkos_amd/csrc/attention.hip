@@ -759,8 +759,8 @@ struct Plan {
 };
 
 // The fp16-pair forward and backward (attention_pair.hip), head_dim 32.
-size_t pair_fwd_bytes(int NW);
-const void* pair_fwd_kernel_ptr();
+size_t pair_fwd_bytes(int HD, int NW);
+const void* pair_fwd_kernel_ptr(int HD);
 int pair_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st);
 size_t pair_bwd_bytes(int NW);
@@ -790,10 +790,10 @@ Plan plan_fwd(const pet_attn_shape& sh, bool xf) {
       if (r >= p.resident) p.split = true, p.bytes = sbytes, p.resident = r;
     }
   }
-  if constexpr (HD == 32) {  // the fp16-pair forward (attention_pair.hip) unless an option asks otherwise
-    const size_t pb = pair_fwd_bytes(NW);
+  if constexpr (HD == 32 || HD == 64) {  // the fp16-pair forward (attention_pair.hip) unless an option asks otherwise
+    const size_t pb = pair_fwd_bytes(HD, NW);
     if (split_enabled() && option(PET_OPT_FWD_KERNEL) == 0 && pb <= cap)
-      p.pair = true, p.split = false, p.bytes = pb, p.resident = resident_wgs(pair_fwd_kernel_ptr(), NW, pb);
+      p.pair = true, p.split = false, p.bytes = pb, p.resident = resident_wgs(pair_fwd_kernel_ptr(HD), NW, pb);
   }
   if constexpr (HD <= 64) {  // option PET_OPT_FWD_KERNEL 3: the vector-ALU kernel, for comparison
     const int threads = 64 * ((sh.slots + 63) / 64);

@@ -385,21 +385,23 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 struct PairFwdLds {
   int R, PT;
   size_t pl, lc, red, bytes;
-  __host__ __device__ constexpr explicit PairFwdLds(int NW)
-      : R(16 * NW), PT(16 * NW + 8), pl(0), lc(size_t(4) * kPairHD * PT * 2), red(lc + size_t(R) * 4),
+  __host__ __device__ constexpr PairFwdLds(int HD, int NW)
+      : R(16 * NW), PT(16 * NW + 8), pl(0), lc(size_t(4) * HD * PT * 2), red(lc + size_t(R) * 4),
         bytes(red + size_t(8) * NW * 4) {}
 };
 
-template <int NW, bool XF>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(8)))
+template <int HD, int NW, bool XF>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD <= 32 ? 8 : 5)))
 attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __restrict__ off, int N, int n0,
                      int64_t eb, int S, int H, float sc, const float* __restrict__ cf_seq, int64_t ldc,
                      float* __restrict__ merged, int64_t ldm, float* __restrict__ ml, QkvXf xf) {
-  constexpr int HD = kPairHD, W = HD / 4, DT = HD / 16;
+  // KC 32-dim chunks of the head: lane (c, g) holds dims 32kc + 8g .. + 7 of its row
+  constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
+  static_assert(HD % 32 == 0, "head_dim a multiple of 32");
   extern __shared__ float lds_f[];
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
   const int D = H * HD;
-  constexpr PairFwdLds L(NW);
+  constexpr PairFwdLds L(HD, NW);
   constexpr int PT = L.PT, PS = HD * PT;
   _Float16* KTh = reinterpret_cast<_Float16*>(lds + L.pl);
   _Float16* VTh = KTh + 2 * PS;
@@ -411,16 +413,20 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   const Atom at(off, blockIdx.x, H, N, S, n0, eb);
   const bool active = w < at.nb, real = active && i < at.cnt;
 
-  // own rows (lane (c, g): row 16w + c, dims 8g .. 8g + 7); a slot past the
-  // count loads slot 0's rows: its key's log cf is kOff (weight exactly 0)
+  // own rows (lane (c, g): row 16w + c, dims 32kc + 8g .. + 7); a slot past
+  // the count loads slot 0's rows: its key's log cf is kOff (weight exactly 0)
   // and its query's results are not stored
   float q[W], k[W], v[W];
   float pcf = 0.f;
   if (active) {
     const size_t r = at.row(real ? i : 0);
-    qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
-    qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
-    qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int col = at.h * HD + 32 * kc + 8 * g;
+      qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
+      qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
+      qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+    }
     const float c0 = cf_seq[size_t(at.n) * ldc + (real ? i : 0)];
     pcf = real ? c0 : 0.f;
   }
@@ -444,19 +450,21 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   if (g == 0) lcf[i] = pcf > 0.f ? log_cf(pcf) : kOff;
   const float sQ = __builtin_amdgcn_ldexpf(1.f, kQ), sK = __builtin_amdgcn_ldexpf(1.f, kKw);
   const float sV = __builtin_amdgcn_ldexpf(1.f, kVw);
-  u4 qb[2];
-  {
+  u4 qb[KC][2];
 #pragma unroll
-    for (int j = 0; j < W / 2; ++j) {
+  for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int x = 8 * kc + 2 * j;
       unsigned h[3], lo[3];
-      pair2n(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);  // exact products (pair2n)
-      pair2n(k[2 * j] * sK, k[2 * j + 1] * sK, h[1], lo[1]);
-      pair2n(v[2 * j] * sV, v[2 * j + 1] * sV, h[2], lo[2]);
-      qb[0][j] = h[0], qb[1][j] = lo[0];
+      pair2n(q[x] * sQ, q[x + 1] * sQ, h[0], lo[0]);  // exact products (pair2n)
+      pair2n(k[x] * sK, k[x + 1] * sK, h[1], lo[1]);
+      pair2n(v[x] * sV, v[x + 1] * sV, h[2], lo[2]);
+      qb[kc][0][j] = h[0], qb[kc][1][j] = lo[0];
       if (active) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const int o = (8 * g + 2 * j + e) * PT + i;
+          const int o = (32 * kc + 8 * g + 2 * j + e) * PT + i;
           KTh[o] = __builtin_bit_cast(pet_split::h2v, h[1])[e], KTh[PS + o] = __builtin_bit_cast(pet_split::h2v, lo[1])[e];
           VTh[o] = __builtin_bit_cast(pet_split::h2v, h[2])[e], VTh[PS + o] = __builtin_bit_cast(pet_split::h2v, lo[2])[e];
         }
@@ -481,14 +489,19 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   auto kV_of = [&](int J) { return J == w ? kVw : __builtin_amdgcn_readfirstlane(kex[2 * J + 1]); };
   // S^T of key block J: s[r] = query i against key 16J + 4g + r, in 2^(kQ + kK_J) units
   auto scores = [&](int J) {
-    u4 a[2];
+    f4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int o = (8 * g + 4 * u + (c >> 2)) * PT + 16 * J + 4 * (c & 3);
-      const u2 x0 = lds_tr16(KTh + o), x1 = lds_tr16(KTh + PS + o);
-      a[0][2 * u] = x0[0], a[0][2 * u + 1] = x0[1], a[1][2 * u] = x1[0], a[1][2 * u + 1] = x1[1];
+    for (int kc = 0; kc < KC; ++kc) {
+      u4 a[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int o = (32 * kc + 8 * g + 4 * u + (c >> 2)) * PT + 16 * J + 4 * (c & 3);
+        const u2 x0 = lds_tr16(KTh + o), x1 = lds_tr16(KTh + PS + o);
+        a[0][2 * u] = x0[0], a[0][2 * u + 1] = x0[1], a[1][2 * u] = x1[0], a[1][2 * u + 1] = x1[1];
+      }
+      st = mfma3(a, qb[kc], st);
     }
-    return mfma3(a, qb, f4{0.f, 0.f, 0.f, 0.f});
+    return st;
   };
   // O^T += V_J^T P^T from the block's scaled weights p
   auto pv = [&](int J, const float* p) {
@@ -638,34 +651,58 @@ int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* 
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
-size_t pair_fwd_bytes(int NW) { return NW <= kPairMaxWaves ? PairFwdLds(NW).bytes : ~size_t(0); }
+size_t pair_fwd_bytes(int HD, int NW) { return NW <= kPairMaxWaves ? PairFwdLds(HD, NW).bytes : ~size_t(0); }
 
-const void* pair_fwd_kernel_ptr() { return reinterpret_cast<const void*>(attn_fwd_pair_kernel<5, false>); }
+const void* pair_fwd_kernel_ptr(int HD) {
+  return HD == 64 ? reinterpret_cast<const void*>(attn_fwd_pair_kernel<64, 5, false>)
+                  : reinterpret_cast<const void*>(attn_fwd_pair_kernel<32, 5, false>);
+}
 
 int pair_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st) {
-  const int NW = (sh.slots + 15) / 16;
-  if (NW > kPairMaxWaves) return PET_ATTN_ESLOTS;
+  const int NW = (sh.slots + 15) / 16, HD = sh.head_dim;
+  if (NW > kPairMaxWaves || (HD != 32 && HD != 64)) return PET_ATTN_ESLOTS;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
   const bool x = xf.rs || xf.b;
-  decltype(&attn_fwd_pair_kernel<1, false>) k = nullptr;
-  auto pick = [&](auto nw) {
-    constexpr int V = decltype(nw)::value;
-    k = x ? attn_fwd_pair_kernel<V, true> : attn_fwd_pair_kernel<V, false>;
+  const size_t bytes = pair_fwd_bytes(HD, NW);
+  decltype(&attn_fwd_pair_kernel<32, 1, false>) k = nullptr;
+  auto pick = [&](auto hd, auto nw) {
+    constexpr int D_ = decltype(hd)::value, V = decltype(nw)::value;
+    k = x ? attn_fwd_pair_kernel<D_, V, true> : attn_fwd_pair_kernel<D_, V, false>;
   };
-  switch (NW) {
-    case 1: pick(std::integral_constant<int, 1>{}); break;
-    case 2: pick(std::integral_constant<int, 2>{}); break;
-    case 3: pick(std::integral_constant<int, 3>{}); break;
-    case 4: pick(std::integral_constant<int, 4>{}); break;
-    case 5: pick(std::integral_constant<int, 5>{}); break;
-    case 6: pick(std::integral_constant<int, 6>{}); break;
-    case 7: pick(std::integral_constant<int, 7>{}); break;
-    default: pick(std::integral_constant<int, 8>{}); break;
+  auto by_waves = [&](auto hd) {
+    switch (NW) {
+      case 1: pick(hd, std::integral_constant<int, 1>{}); break;
+      case 2: pick(hd, std::integral_constant<int, 2>{}); break;
+      case 3: pick(hd, std::integral_constant<int, 3>{}); break;
+      case 4: pick(hd, std::integral_constant<int, 4>{}); break;
+      case 5: pick(hd, std::integral_constant<int, 5>{}); break;
+      case 6: pick(hd, std::integral_constant<int, 6>{}); break;
+      case 7: pick(hd, std::integral_constant<int, 7>{}); break;
+      default: pick(hd, std::integral_constant<int, 8>{}); break;
+    }
+  };
+  if (HD == 64)
+    by_waves(std::integral_constant<int, 64>{});
+  else
+    by_waves(std::integral_constant<int, 32>{});
+  if (bytes > 65536) {  // the dynamic LDS limit raised once per (device, kernel) to the largest size asked
+    static std::map<std::pair<int, const void*>, size_t> raised;
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return PET_ATTN_ELAUNCH;
+    const void* kp = reinterpret_cast<const void*>(k);
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = raised[{dev, kp}];
+    if (have < bytes) {
+      if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess)
+        return PET_ATTN_ELAUNCH;
+      have = bytes;
+    }
   }
-  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), pair_fwd_bytes(NW), st, qkv, ldq, off, sh.n_atoms, n0,
-                     eb, sh.slots, sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
+  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots,
+                     sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
