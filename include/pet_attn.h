@@ -94,17 +94,17 @@ PET_ATTN_API int pet_attn_max_slots(int head_dim);
  * counterpart is its process-global GEMM mode (include/pet/gemm.hpp:119-122). */
 enum {
   PET_OPT_SPLIT = 1,       /* 1 (default): fp32 products split over the bf16 matrix cores where they pay; 0: fp32 MFMA only */
-  PET_OPT_FWD_KERNEL = 2,  /* 0 (default): matrix-core forward, at head_dim 32 the fp16-pair one where it fits (with
-                              PET_OPT_SPLIT 1); 1: the staged forward with split-bf16 scores; 3: the vector-ALU
-                              forward (head_dim <= 64), for comparison */
+  PET_OPT_FWD_KERNEL = 2,  /* 0 (default): matrix-core forward, at head_dim 32 and 64 the fp16-pair one where it fits
+                              (with PET_OPT_SPLIT 1); 1: the staged forward (split-bf16 scores where they pay);
+                              3: the vector-ALU forward (head_dim <= 64), for comparison */
   PET_OPT_BWD_VLDS = 3,    /* 0 (default): automatic; 1: V staged in LDS; 2: V read from global memory (where it fits) */
   PET_OPT_BWD_NBUF = 4,    /* 0 (default): automatic; 1 or 2 backward tile buffers (where it fits) */
   PET_OPT_MODEL_GEMM = 5,  /* the model's dense layers: 4 (default) split-product kernel for M*N*K >= 2^32, else rocBLAS;
                               0 rocBLAS only; 1 / 2 the fp32 fused kernel for every / <= 4096-row forward layer;
                               3 the split-product kernel wherever K is a multiple of 32 */
   PET_OPT_ATTN_STREAM = 6, /* 0 (default): the LDS-staged kernels where they hold the shape; 1: the streaming kernels always */
-  PET_OPT_BWD_KERNEL = 7,  /* 0 (default): at head_dim 32 the fp16-pair backward (every product on the 16-bit matrix
-                              cores) where it fits, with PET_OPT_SPLIT 1; 1: the tile-exchange backward */
+  PET_OPT_BWD_KERNEL = 7,  /* 0 (default): at head_dim 32 and 64 the fp16-pair backward (every product on the 16-bit
+                              matrix cores) where it fits, with PET_OPT_SPLIT 1; 1: the tile-exchange backward */
   PET_OPT_COUNT = 8
 };
 

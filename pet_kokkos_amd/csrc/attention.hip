@@ -763,8 +763,8 @@ size_t pair_fwd_bytes(int HD, int NW);
 const void* pair_fwd_kernel_ptr(int HD);
 int pair_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* cf_seq, int64_t ldc, float* merged, int64_t ldm, float* ml, QkvXf xf, hipStream_t st);
-size_t pair_bwd_bytes(int NW);
-const void* pair_bwd_kernel_ptr();
+size_t pair_bwd_bytes(int HD, int NW);
+const void* pair_bwd_kernel_ptr(int HD);
 int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
              const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st);
@@ -882,14 +882,16 @@ Plan plan_bwd(const pet_attn_shape& sh) {
     const size_t fb = sizeof(float) * Lds<HD>::bwd_floats(NW, b, v);
     if ((b == 1 || b == 2) && fb <= cap) p.vlds = v, p.nbuf = b, p.bytes = fb, p.resident = resident_wgs(k, NW, fb);
   }
-  if constexpr (HD == 32) {
+  if constexpr (HD == 32 || HD == 64) {
     // every product as fp16 pairs (attention_pair.hip) unless an option asks
     // for the tile-exchange kernel or for fp32 products only
-    const size_t pb = pair_bwd_bytes(NW);
+    const size_t pb = pair_bwd_bytes(HD, NW);
     if (split_enabled() && option(PET_OPT_BWD_KERNEL) == 0 && !force_v && !force_b && pb <= cap) {
-      p.pair = true, p.vlds = 0, p.nbuf = 2, p.bytes = pb, p.resident = resident_wgs(pair_bwd_kernel_ptr(), NW, pb);
+      p.pair = true, p.vlds = 0, p.nbuf = 2, p.bytes = pb, p.resident = resident_wgs(pair_bwd_kernel_ptr(HD), NW, pb);
       return p;
     }
+  }
+  if constexpr (HD == 32) {
     const size_t sb = sizeof(float) * Lds<HD>::bwd_floats(NW, p.nbuf, true, true);
     if (p.vlds && split_enabled() && sb <= cap) {
       const void* ks = reinterpret_cast<const void*>(attn_bwd_kernel<HD, 512, false, true>);

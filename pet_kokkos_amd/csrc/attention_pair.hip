@@ -73,11 +73,11 @@ constexpr int kPairMaxWaves = 8;  // 128 slots; beyond, the tile-exchange kernel
 struct PairLds {
   static constexpr int TP = 20;  // halves a dS tile row (16 queries, 4 of pad)
   static constexpr int TS = 16 * TP;  // halves a tile part
-  int R, PT;                     // rows; plane pitch in halves
+  int R, PT;                     // rows; plane pitch in halves (a 4-half pad at head_dim 64: two workgroups a CU)
   size_t pl, st, red, tb, bytes;
-  __host__ __device__ constexpr explicit PairLds(int NW)
-      : R(16 * NW), PT(16 * NW + 8), pl(0),
-        st(pl + size_t(6) * kPairHD * PT * 2),  // 6 planes: Q^T, dO^T, K^T, each hi then lo
+  __host__ __device__ constexpr PairLds(int HD, int NW)
+      : R(16 * NW), PT(16 * NW + (HD <= 32 ? 8 : 4)), pl(0),
+        st(pl + size_t(6) * HD * PT * 2),  // 6 planes: Q^T, dO^T, K^T, each hi then lo
         red(st + size_t(3) * R * 4),            // 8 words a wave: its maxima
         tb(red + size_t(8) * NW * 4), bytes(tb + size_t(2) * NW * 2 * TS * 2) {}
 };
@@ -138,8 +138,8 @@ __device__ __forceinline__ int pair_exp(float m) {
 }
 }  // namespace
 
-template <int NW, bool XF>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW >= 4 ? 6 : 5))) attn_bwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq,
+template <int HD, int NW, bool XF>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD > 32 ? 4 : NW >= 4 ? 6 : 5))) attn_bwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq,
                                                              const int* __restrict__ off, int N, int n0, int64_t eb,
                                                              int S, int H, float sc,
                                                              const float* __restrict__ dmerged, int64_t ldg,
@@ -148,11 +148,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                                                              const float* __restrict__ cf_seq, int64_t ldc,
                                                              float* __restrict__ qkv_adj, int64_t lda,
                                                              float* __restrict__ cfh, QkvXf xf) {
-  constexpr int HD = kPairHD, W = HD / 4, DT = HD / 16;
+  // KC 32-dim chunks of the head: lane (c, g) holds dims 32kc + 8g .. + 7 of its row
+  constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
+  static_assert(HD % 32 == 0, "head_dim a multiple of 32");
   extern __shared__ float lds_f[];
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
   const int D = H * HD;
-  constexpr PairLds L(NW);
+  constexpr PairLds L(HD, NW);
   constexpr int PT = L.PT;
   _Float16* planes = reinterpret_cast<_Float16*>(lds + L.pl);
   constexpr int PS = HD * PT;  // halves a plane part
@@ -172,7 +174,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
   const Atom at(off, blockIdx.x, H, N, S, n0, eb);
   const bool active = w < at.nb, real = active && i < at.cnt;
 
-  // ---- the wave's own block: rows 16w .. 16w + 15, lane (c, g) dims 8g .. 8g + 7
+  // ---- the wave's own block: rows 16w .. 16w + 15, lane (c, g) dims 32kc + 8g .. + 7
   // A slot past the count loads slot 0's rows instead of zeros: as a query it
   // has 1/sum 0 and as a key log cf kOff, so its P and dS are exactly 0 and
   // it adds nothing (and, a copy of a row of the item, it moves no scale).
@@ -181,11 +183,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
   if (active) {  // wave-uniform
     const int si = real ? i : 0;
     const size_t r = at.row(si);
-    qkv_get<W, XF>(qkv, ldq, r, at.h * HD + g * W, xf, q);
-    qkv_get<W, XF>(qkv, ldq, r, D + at.h * HD + g * W, xf, k);
-    qkv_get<W, XF>(qkv, ldq, r, 2 * D + at.h * HD + g * W, xf, v);
-    gmem_get<W>(dmerged + r * ldg + at.h * HD + g * W, go);
-    gmem_get<W>(merged + at.grow(si) * ldm + at.h * HD + g * W, oo);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int col = at.h * HD + 32 * kc + 8 * g;
+      qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
+      qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
+      qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+      gmem_get<8>(dmerged + r * ldg + col, go + 8 * kc);
+      gmem_get<8>(merged + at.grow(si) * ldm + col, oo + 8 * kc);
+    }
     const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + si);
     const float m0 = m2[0], l0 = m2[1], c0 = cf_seq[size_t(at.n) * ldc + si];
     mi = real ? m0 : kOff, li = real ? l0 : 0.f, pcf = real ? c0 : 0.f;
@@ -229,30 +235,35 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 
   // own rows split: K and V stay in registers (the b operand of S and dP);
   // Q, dO and K go to the transposed planes
-  u4 kb[2], vb[2];
+  u4 kb[KC][2], vb[KC][2];
   {
-    u4 qs[2], gs[2];
+    u4 qs[KC][2], gs[KC][2];
 #pragma unroll
-    for (int j = 0; j < W / 2; ++j) {
-      unsigned h[4], lo[4];
-      // products by powers of two are exact: a conversion fused with them
-      // rounds the same value (pair2n)
-      pair2n(q[2 * j] * sQ, q[2 * j + 1] * sQ, h[0], lo[0]);
-      pair2n(go[2 * j] * sG, go[2 * j + 1] * sG, h[1], lo[1]);
-      pair2n(k[2 * j] * sK, k[2 * j + 1] * sK, h[2], lo[2]);
-      pair2n(v[2 * j] * sV, v[2 * j + 1] * sV, h[3], lo[3]);
-      qs[0][j] = h[0], qs[1][j] = lo[0], gs[0][j] = h[1], gs[1][j] = lo[1];
-      kb[0][j] = h[2], kb[1][j] = lo[2], vb[0][j] = h[3], vb[1][j] = lo[3];
-    }
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int x = 8 * kc + 2 * j;
+        unsigned h[4], lo[4];
+        // products by powers of two are exact: a conversion fused with them
+        // rounds the same value (pair2n)
+        pair2n(q[x] * sQ, q[x + 1] * sQ, h[0], lo[0]);
+        pair2n(go[x] * sG, go[x + 1] * sG, h[1], lo[1]);
+        pair2n(k[x] * sK, k[x + 1] * sK, h[2], lo[2]);
+        pair2n(v[x] * sV, v[x + 1] * sV, h[3], lo[3]);
+        qs[kc][0][j] = h[0], qs[kc][1][j] = lo[0], gs[kc][0][j] = h[1], gs[kc][1][j] = lo[1];
+        kb[kc][0][j] = h[2], kb[kc][1][j] = lo[2], vb[kc][0][j] = h[3], vb[kc][1][j] = lo[3];
+      }
     if (active) {
 #pragma unroll
-      for (int e = 0; e < W; ++e) {
-        const int o = (8 * g + e) * PT + i;
-        auto half = [&](unsigned x) { return __builtin_bit_cast(pet_split::h2v, x)[e & 1]; };
-        QTh[o] = half(qs[0][e >> 1]), QTh[PS + o] = half(qs[1][e >> 1]);
-        GTh[o] = half(gs[0][e >> 1]), GTh[PS + o] = half(gs[1][e >> 1]);
-        KTh[o] = half(kb[0][e >> 1]), KTh[PS + o] = half(kb[1][e >> 1]);
-      }
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int o = (32 * kc + 8 * g + e) * PT + i;
+          auto half = [&](unsigned x) { return __builtin_bit_cast(pet_split::h2v, x)[e & 1]; };
+          QTh[o] = half(qs[kc][0][e >> 1]), QTh[PS + o] = half(qs[kc][1][e >> 1]);
+          GTh[o] = half(gs[kc][0][e >> 1]), GTh[PS + o] = half(gs[kc][1][e >> 1]);
+          KTh[o] = half(kb[kc][0][e >> 1]), KTh[PS + o] = half(kb[kc][1][e >> 1]);
+        }
       if (g == 0) {
         // a query with no live key (li = 0): an exponent near -1e30, exp gives 0
         STm[i] = li > 0.f ? mi : 1e30f;
@@ -273,20 +284,23 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
   auto phase1 = [&](int s) {
     int I = w + s;
     if (I >= nb) I -= nb;
-    // a operand: query 16I + c, dims 8g .. 8g + 7, read transposed from the
-    // planes (rows 8g + 4u + c / 4, tokens 16I + 4 (c % 4) .. + 3)
-    u4 qa[2], ga[2];
+    // a operand: query 16I + c, dims 32kc + 8g .. + 7, read transposed from
+    // the planes (rows 32kc + 8g + 4u + c / 4, tokens 16I + 4 (c % 4) .. + 3)
+    f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};  // S: key 16w + c (column), queries 16I + 4g + r
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int o = (8 * g + 4 * u + (c >> 2)) * PT + 16 * I + 4 * (c & 3);
-      const u2 x0 = lds_tr16(QTh + o), x1 = lds_tr16(QTh + PS + o);
-      const u2 y0 = lds_tr16(GTh + o), y1 = lds_tr16(GTh + PS + o);
-      qa[0][2 * u] = x0[0], qa[0][2 * u + 1] = x0[1], qa[1][2 * u] = x1[0], qa[1][2 * u + 1] = x1[1];
-      ga[0][2 * u] = y0[0], ga[0][2 * u + 1] = y0[1], ga[1][2 * u] = y1[0], ga[1][2 * u + 1] = y1[1];
+    for (int kc = 0; kc < KC; ++kc) {
+      u4 qa[2], ga[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int o = (32 * kc + 8 * g + 4 * u + (c >> 2)) * PT + 16 * I + 4 * (c & 3);
+        const u2 x0 = lds_tr16(QTh + o), x1 = lds_tr16(QTh + PS + o);
+        const u2 y0 = lds_tr16(GTh + o), y1 = lds_tr16(GTh + PS + o);
+        qa[0][2 * u] = x0[0], qa[0][2 * u + 1] = x0[1], qa[1][2 * u] = x1[0], qa[1][2 * u + 1] = x1[1];
+        ga[0][2 * u] = y0[0], ga[0][2 * u + 1] = y0[1], ga[1][2 * u] = y1[0], ga[1][2 * u + 1] = y1[1];
+      }
+      st = mfma3(qa, kb[kc], st);
+      dp = mfma3(ga, vb[kc], dp);
     }
-    const f4 z = {0.f, 0.f, 0.f, 0.f};
-    const f4 st = mfma3(qa, kb, z);  // S: key 16w + c (column), queries 16I + 4g + r
-    const f4 dp = mfma3(ga, vb, z);
     const float4 m4 = *reinterpret_cast<const float4*>(STm + 16 * I + 4 * g);
     const float4 l4 = *reinterpret_cast<const float4*>(STl + 16 * I + 4 * g);
     const float4 d4 = *reinterpret_cast<const float4*>(STd + 16 * I + 4 * g);
@@ -601,37 +615,43 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
 
 // ---- host side ---------------------------------------------------------------
 
-size_t pair_bwd_bytes(int NW) { return NW <= kPairMaxWaves ? PairLds(NW).bytes : ~size_t(0); }
+size_t pair_bwd_bytes(int HD, int NW) { return NW <= kPairMaxWaves ? PairLds(HD, NW).bytes : ~size_t(0); }
 
-const void* pair_bwd_kernel_ptr() { return reinterpret_cast<const void*>(attn_bwd_pair_kernel<5, false>); }
+const void* pair_bwd_kernel_ptr(int HD) {
+  return HD == 64 ? reinterpret_cast<const void*>(attn_bwd_pair_kernel<64, 5, false>)
+                  : reinterpret_cast<const void*>(attn_bwd_pair_kernel<32, 5, false>);
+}
 
 namespace {
-template <int NW>
+template <int HD, int NW>
 auto pair_kernel(bool x) {
-  return x ? attn_bwd_pair_kernel<NW, true> : attn_bwd_pair_kernel<NW, false>;
+  return x ? attn_bwd_pair_kernel<HD, NW, true> : attn_bwd_pair_kernel<HD, NW, false>;
+}
+template <int HD>
+auto pair_kernel_nw(int NW, bool x) {
+  switch (NW) {
+    case 1: return pair_kernel<HD, 1>(x);
+    case 2: return pair_kernel<HD, 2>(x);
+    case 3: return pair_kernel<HD, 3>(x);
+    case 4: return pair_kernel<HD, 4>(x);
+    case 5: return pair_kernel<HD, 5>(x);
+    case 6: return pair_kernel<HD, 6>(x);
+    case 7: return pair_kernel<HD, 7>(x);
+    default: return pair_kernel<HD, 8>(x);
+  }
 }
 }  // namespace
 
 int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
              const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st) {
-  const int NW = (sh.slots + 15) / 16;
-  if (NW > kPairMaxWaves) return PET_ATTN_ESLOTS;
+  const int NW = (sh.slots + 15) / 16, HD = sh.head_dim;
+  if (NW > kPairMaxWaves || (HD != 32 && HD != 64)) return PET_ATTN_ESLOTS;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
-  const size_t bytes = pair_bwd_bytes(NW);
+  const size_t bytes = pair_bwd_bytes(HD, NW);
   const bool x = xf.rs || xf.b;
-  decltype(&attn_bwd_pair_kernel<1, false>) k = nullptr;
-  switch (NW) {
-    case 1: k = pair_kernel<1>(x); break;
-    case 2: k = pair_kernel<2>(x); break;
-    case 3: k = pair_kernel<3>(x); break;
-    case 4: k = pair_kernel<4>(x); break;
-    case 5: k = pair_kernel<5>(x); break;
-    case 6: k = pair_kernel<6>(x); break;
-    case 7: k = pair_kernel<7>(x); break;
-    default: k = pair_kernel<8>(x); break;
-  }
+  const auto k = HD == 64 ? pair_kernel_nw<64>(NW, x) : pair_kernel_nw<32>(NW, x);
   if (bytes > 65536) {  // the dynamic LDS limit raised once per (device, kernel) to the largest size asked
     static std::map<std::pair<int, const void*>, size_t> raised;
     static std::mutex mu;

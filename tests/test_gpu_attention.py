@@ -203,42 +203,44 @@ def test_backward_layouts(device, hd, vlds, nbuf, split):
                              tk.cf_seq, qkv, dm, 2, hd)
 
 
+@pytest.mark.parametrize("hd", [32, 64])
 @pytest.mark.parametrize("qk,v,g,spread", [(1.0, 1.0, 1.0, 0.0), (0.05, 1e3, 1e-7, 0.0), (0.5, 1e-4, 3e4, 0.0),
                                             (0.5, 1.0, 1.0, 3.0)])
-def test_pair_backward_scales(device, qk, v, g, spread):
-    # The fp16-pair backward (the default at head_dim 32) puts each item's
+def test_pair_backward_scales(device, qk, v, g, spread, hd):
+    # The fp16-pair kernels (the default at head_dim 32 and 64): the backward puts each item's
     # largest |Q|, |K|, |V|, |dO| at 2^15 by powers of two and bounds dS
     # from them: V and dO far from unit scale, and V and dO rows spread over
     # 10^+-spread within an item, must meet the same bar against the oracle.
     # (Q and K stay moderate: scores of hundreds make exp amplify any fp32
     # rounding of them, a conditioning no product order escapes.)
     counts = [0, 15, 16, 31, 47, 5, 60, 33, 70, 79]
-    tk, qkv, dm = random_case(counts, 2, 32, seed=300 + int(spread), cf_kind="random")
+    tk, qkv, dm = random_case(counts, 2, hd, seed=300 + int(spread), cf_kind="random")
     rng = np.random.default_rng(11)
-    D = 2 * 32
+    D = 2 * hd
     qkv[:, :2 * D] *= qk
     qkv[:, 2 * D:] *= v * 10.0 ** rng.uniform(-spread, spread, (qkv.shape[0], 1))
     dm = (dm * g * 10.0 ** rng.uniform(-spread, spread, (dm.shape[0], 1))).astype(np.float32)
     qkv = qkv.astype(np.float32)
-    plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 2, 32)
+    plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 2, hd)
     assert plan["bwd_pair"] == 1 and plan["fwd_pair"] == 1
-    check_against_oracle(device, f"pair backward qk x{qk} v x{v} dO x{g} spread 1e+-{spread}", tk.off,
-                         tk.cf_seq, qkv, dm, 2, 32)
+    check_against_oracle(device, f"pair kernels hd {hd} qk x{qk} v x{v} dO x{g} spread 1e+-{spread}", tk.off,
+                         tk.cf_seq, qkv, dm, 2, hd)
 
 
+@pytest.mark.parametrize("hd", [32, 64])
 @pytest.mark.parametrize("fwd,bwd", [(0, 0), (1, 1), (0, 1), (1, 0)])
-def test_pair_and_staged_kernels(device, fwd, bwd):
-    # The head_dim-32 kernels in each combination (option fwd_kernel / bwd_kernel:
+def test_pair_and_staged_kernels(device, fwd, bwd, hd):
+    # The head_dim-32 and -64 kernels in each combination (option fwd_kernel / bwd_kernel:
     # 0 the fp16-pair kernels, 1 the staged split-bf16 forward and the
     # tile-exchange backward) on ragged atoms, each bit-identical when repeated.
     counts = [0, 15, 16, 31, 47, 5, 60, 33, 70]
-    tk, qkv, dm = random_case(counts, 3, 32, seed=400, cf_kind="random")
+    tk, qkv, dm = random_case(counts, 3, hd, seed=400, cf_kind="random")
     with A._lib.options(fwd_kernel=fwd, bwd_kernel=bwd):
-        plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 3, 32)
+        plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 3, hd)
         assert plan["fwd_pair"] == (fwd == 0) and plan["bwd_pair"] == (bwd == 0)
-        first = check_against_oracle(device, f"forward kernel {fwd}, backward kernel {bwd}", tk.off, tk.cf_seq, qkv,
-                                     dm, 3, 32)
-        again = gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 3, 32)
+        first = check_against_oracle(device, f"hd {hd}: forward kernel {fwd}, backward kernel {bwd}", tk.off,
+                                     tk.cf_seq, qkv, dm, 3, hd)
+        again = gpu_fwd_bwd(device, tk.off, tk.cf_seq, qkv, dm, 3, hd)
     for a, b in zip(first, again):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
