@@ -136,6 +136,24 @@ __device__ __forceinline__ int pair_exp(float m) {
   if (!(m > 0.f) || m > 3.0e38f) return 0;
   return min(15 - __builtin_amdgcn_frexp_expf(m), 126);
 }
+
+// The fused QKV transform (QkvXf: qkv[r][j] rs[r] + b[j]) applied to a lane's
+// q, k, v values (dims col0 + 32kc .. + 7 of each) once every row load of
+// the item is issued: the row scale loaded once, the bias per chunk.
+template <int KC>
+__device__ __forceinline__ void xf_rows(const QkvXf& xf, size_t r, int col0, int D, float* q, float* k, float* v) {
+  const float sr = xf.rs ? xf.rs[r] : 1.f;
+  float* x[3] = {q, k, v};
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      float bb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (xf.b) gmem_get<8>(xf.b + m * D + col0 + 32 * kc, bb);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) x[m][8 * kc + t] = fmaf(x[m][8 * kc + t], sr, bb[t]);
+    }
+}
 }  // namespace
 
 template <int HD, int NW, bool XF>
@@ -151,6 +169,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
   // KC 32-dim chunks of the head: lane (c, g) holds dims 32kc + 8g .. + 7 of its row
   constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
   static_assert(HD % 32 == 0, "head_dim a multiple of 32");
+  // the fused transform after every row load is issued (one chunk a lane at
+  // head_dim 32; at 64 the raw rows held together would spill, so each
+  // chunk's load is transformed as it arrives)
+  constexpr bool XF_LATE = XF && KC == 1;
   extern __shared__ float lds_f[];
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
   const int D = H * HD;
@@ -186,12 +208,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       const int col = at.h * HD + 32 * kc + 8 * g;
-      qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
-      qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
-      qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+      if constexpr (XF_LATE) {
+        gmem_get<8>(qkv + r * ldq + col, q + 8 * kc);
+        gmem_get<8>(qkv + r * ldq + D + col, k + 8 * kc);
+        gmem_get<8>(qkv + r * ldq + 2 * D + col, v + 8 * kc);
+      } else {
+        qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
+        qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
+        qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+      }
       gmem_get<8>(dmerged + r * ldg + col, go + 8 * kc);
       gmem_get<8>(merged + at.grow(si) * ldm + col, oo + 8 * kc);
     }
+    if constexpr (XF_LATE) xf_rows<KC>(xf, r, at.h * HD + 8 * g, D, q, k, v);
     const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + si);
     const float m0 = m2[0], l0 = m2[1], c0 = cf_seq[size_t(at.n) * ldc + si];
     mi = real ? m0 : kOff, li = real ? l0 : 0.f, pcf = real ? c0 : 0.f;
@@ -412,6 +441,10 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   // KC 32-dim chunks of the head: lane (c, g) holds dims 32kc + 8g .. + 7 of its row
   constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
   static_assert(HD % 32 == 0, "head_dim a multiple of 32");
+  // the fused transform after every row load is issued (one chunk a lane at
+  // head_dim 32; at 64 the raw rows held together would spill, so each
+  // chunk's load is transformed as it arrives)
+  constexpr bool XF_LATE = XF && KC == 1;
   extern __shared__ float lds_f[];
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
   const int D = H * HD;
@@ -437,10 +470,17 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       const int col = at.h * HD + 32 * kc + 8 * g;
-      qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
-      qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
-      qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+      if constexpr (XF_LATE) {
+        gmem_get<8>(qkv + r * ldq + col, q + 8 * kc);
+        gmem_get<8>(qkv + r * ldq + D + col, k + 8 * kc);
+        gmem_get<8>(qkv + r * ldq + 2 * D + col, v + 8 * kc);
+      } else {
+        qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
+        qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
+        qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+      }
     }
+    if constexpr (XF_LATE) xf_rows<KC>(xf, r, at.h * HD + 8 * g, D, q, k, v);
     const float c0 = cf_seq[size_t(at.n) * ldc + (real ? i : 0)];
     pcf = real ? c0 : 0.f;
   }
