@@ -154,6 +154,23 @@ __device__ __forceinline__ void xf_rows(const QkvXf& xf, size_t r, int col0, int
       for (int t = 0; t < 8; ++t) x[m][8 * kc + t] = fmaf(x[m][8 * kc + t], sr, bb[t]);
     }
 }
+// qkv_get with the transform but no branch: a missing row scale or bias reads
+// a valid address (the row itself) and selects 1 or 0, so one chunk's loads
+// and the next chunk's stay in one block and are all in flight together.
+template <bool XF>
+__device__ __forceinline__ void qkv_get8(const float* qkv, int64_t ldq, size_t r, int col, const QkvXf& xf,
+                                         float* out) {
+  const float* row = qkv + r * ldq + col;
+  gmem_get<8>(row, out);
+  if constexpr (!XF) return;
+  const bool hs = xf.rs != nullptr, hb = xf.b != nullptr;
+  const float s0 = *(hs ? xf.rs + r : row);
+  float bb[8];
+  gmem_get<8>(hb ? xf.b + col : row, bb);
+  const float sr = hs ? s0 : 1.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) out[t] = fmaf(out[t], sr, hb ? bb[t] : 0.f);
+}
 }  // namespace
 
 template <int HD, int NW, bool XF>
@@ -170,8 +187,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
   constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
   static_assert(HD % 32 == 0, "head_dim a multiple of 32");
   // the fused transform after every row load is issued (one chunk a lane at
-  // head_dim 32; at 64 the raw rows held together would spill, so each
-  // chunk's load is transformed as it arrives)
+  // head_dim 32); at 64 the raw rows held together would spill, so each
+  // chunk is transformed as it arrives, branch-free (qkv_get8) so that every
+  // chunk's loads are still issued together
   constexpr bool XF_LATE = XF && KC == 1;
   extern __shared__ float lds_f[];
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
@@ -213,9 +231,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
         gmem_get<8>(qkv + r * ldq + D + col, k + 8 * kc);
         gmem_get<8>(qkv + r * ldq + 2 * D + col, v + 8 * kc);
       } else {
-        qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
-        qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
-        qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+        qkv_get8<XF>(qkv, ldq, r, col, xf, q + 8 * kc);
+        qkv_get8<XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
+        qkv_get8<XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
       }
       gmem_get<8>(dmerged + r * ldg + col, go + 8 * kc);
       gmem_get<8>(merged + at.grow(si) * ldm + col, oo + 8 * kc);
@@ -442,8 +460,9 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
   static_assert(HD % 32 == 0, "head_dim a multiple of 32");
   // the fused transform after every row load is issued (one chunk a lane at
-  // head_dim 32; at 64 the raw rows held together would spill, so each
-  // chunk's load is transformed as it arrives)
+  // head_dim 32); at 64 the raw rows held together would spill, so each
+  // chunk is transformed as it arrives, branch-free (qkv_get8) so that every
+  // chunk's loads are still issued together
   constexpr bool XF_LATE = XF && KC == 1;
   extern __shared__ float lds_f[];
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
@@ -475,9 +494,9 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
         gmem_get<8>(qkv + r * ldq + D + col, k + 8 * kc);
         gmem_get<8>(qkv + r * ldq + 2 * D + col, v + 8 * kc);
       } else {
-        qkv_get<8, XF>(qkv, ldq, r, col, xf, q + 8 * kc);
-        qkv_get<8, XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
-        qkv_get<8, XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
+        qkv_get8<XF>(qkv, ldq, r, col, xf, q + 8 * kc);
+        qkv_get8<XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
+        qkv_get8<XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
       }
     }
     if constexpr (XF_LATE) xf_rows<KC>(xf, r, at.h * HD + 8 * g, D, q, k, v);
