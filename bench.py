@@ -74,7 +74,7 @@ def bwd_kernel_name(plan, hd):
     if plan.get("streaming"):
         return "attn_bwd_stream_kernel"
     if plan.get("bwd_pair"):
-        return f"attn_bwd_pair_kernel<{plan['waves']}, false>"
+        return f"attn_bwd_pair_kernel<{hd}, {plan['waves']}, false>"
     return f"attn_bwd_kernel<{hd}, 512>"
 
 
