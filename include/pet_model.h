@@ -144,6 +144,19 @@ PET_ATTN_API int pet_linear_fused_split(int M, int N, int K, const float* A, int
                                         int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                         int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
 
+/* Activation rows as fp16 pairs, the A operand of pet_linear_fused_pairs: X [M, K]
+ * (ld ldx, K a multiple of 32 and at least 256, rows 16-byte aligned) into out,
+ * M * K * 4 + M * 4 bytes, 16-byte aligned (each row scaled by a power of two,
+ * split into a high part exact in fp16 and the rest rounded to fp16, then the
+ * rows' inverse scales). Split once, an activation feeds any number of products. */
+PET_ATTN_API int pet_linear_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, void* stream);
+/* pet_linear_fused_split with A as pet_linear_pair_rows made it: the same bits,
+ * with no arithmetic but the products in the K loop. No counterpart in the
+ * reference (src/fused_gemm_hip.cpp runs its layers in fp32). */
+PET_ATTN_API int pet_linear_fused_pairs(int M, int N, int K, const void* Apairs, const void* Wsplit, float* C,
+                                        int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                        int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
+
 /* Bytes of device workspace the model holds now (its high-water mark). */
 PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
 

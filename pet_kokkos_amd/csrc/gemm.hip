@@ -25,6 +25,8 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 #include <cstdlib>
 
@@ -573,6 +575,298 @@ __global__ void __launch_bounds__(256) pair_rows_kernel(const float* __restrict_
   if (tid == 0) reinterpret_cast<float*>(out + int64_t(N) * KG * 2)[n] = 1.f / s;
 }
 
+// Rows of an activation X [M, K] (ld ldx) as fp16 pairs in pair_rows_kernel's
+// layout (the M inverse scales after the pairs), one wave a row: lane j takes
+// k groups j, j + 64, ..., held in registers from the row's largest |x| to
+// its split (NGL groups a lane; NGL 0: any K, the row read twice, the second
+// time from cache). Each lane writes 32 contiguous bytes a group.
+template <int NGL>
+__global__ void __launch_bounds__(256) pair_act_kernel(const float* __restrict__ X, int M, int K, int64_t ldx,
+                                                        u4* __restrict__ out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63, KG = K / 8;
+  if (row >= M) return;
+  const float* x = X + int64_t(row) * ldx;
+  constexpr int NV = NGL > 0 ? 2 * NGL : 2;
+  float4 v[NV];
+  float m = 0.f;
+  auto amax = [](const float4& a) { return fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))); };
+  if constexpr (NGL > 0) {
+#pragma unroll
+    for (int i = 0; i < NGL; ++i) {
+      const int j = l + 64 * i;
+      if (j < KG) {
+        v[2 * i] = *reinterpret_cast<const float4*>(x + 8 * j);
+        v[2 * i + 1] = *reinterpret_cast<const float4*>(x + 8 * j + 4);
+        m = fmaxf(m, fmaxf(amax(v[2 * i]), amax(v[2 * i + 1])));
+      }
+    }
+  } else {
+    for (int j = l; j < KG; j += 64)
+      m = fmaxf(m, fmaxf(amax(*reinterpret_cast<const float4*>(x + 8 * j)),
+                         amax(*reinterpret_cast<const float4*>(x + 8 * j + 4))));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const float s = pair_scale(m);
+  auto put = [&](int j, const float4& a, const float4& b) {
+    u4 hi, lo;
+    unsigned h, lw;
+    pair2(a.x * s, a.y * s, h, lw), hi[0] = h, lo[0] = lw;
+    pair2(a.z * s, a.w * s, h, lw), hi[1] = h, lo[1] = lw;
+    pair2(b.x * s, b.y * s, h, lw), hi[2] = h, lo[2] = lw;
+    pair2(b.z * s, b.w * s, h, lw), hi[3] = h, lo[3] = lw;
+    u4* o = out + (int64_t(row) * KG + j) * 2;
+    o[0] = hi, o[1] = lo;
+  };
+  if constexpr (NGL > 0) {
+#pragma unroll
+    for (int i = 0; i < NGL; ++i)
+      if (l + 64 * i < KG) put(l + 64 * i, v[2 * i], v[2 * i + 1]);
+  } else {
+    for (int j = l; j < KG; j += 64)
+      put(j, *reinterpret_cast<const float4*>(x + 8 * j), *reinterpret_cast<const float4*>(x + 8 * j + 4));
+  }
+  if (l == 0) reinterpret_cast<float*>(out + int64_t(M) * KG * 2)[row] = 1.f / s;
+}
+
+// The K loop's barrier: no memory fence, since any fence, even one on LDS
+// alone, makes the compiler wait for every global-to-LDS load in flight (the
+// prefetches too). The loop's own vmcnt wait before it covers the step's
+// loads; a wave's LDS reads of the step before have returned before it passes
+// (their products consumed them); the empty asm keeps the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// The epilogue through LDS, for a tile whose columns all lie in the result:
+// the waves' results (already unscaled) go to a BM x BN fp32 tile in LDS
+// (float4 slot q of row R at q ^ s(R), s(R) = 4 (R / 4) mod BN / 4, so the
+// four row groups of a store fall on distinct banks), then each thread takes
+// float4 runs of a row and applies epi_elem's arithmetic, in its order, with
+// 16-byte loads and stores (C, pre, cin, bias) in place of a wave's 4-byte
+// stores to four rows. False (nothing written) where a pointer or leading
+// dimension does not allow the 16-byte accesses; the caller then uses
+// epilogue(). tile: BM BN floats of LDS no wave still reads.
+template <int BM, int BN, int WGM, int WGN>
+__device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][BN / WGN / 16], float* tile, int m0,
+                                                int n0, int M, int N, float* C, int64_t ldc, const Epi& epi) {
+  constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, F = BN / 4;
+  static_assert(T % F == 0, "whole rows a pass");
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool act4 = epi.act == 4, act2 = epi.act == 2;
+  // C's columns: 2 N (act 4), N / 2 (act 2), else N; j stays a multiple of 4
+  const bool ok = n0 + BN <= N && a16(C) && ldc % 4 == 0 && (!epi.bias || a16(epi.bias)) &&
+                  (!epi.cin || (a16(epi.cin) && epi.ldcin % 4 == 0)) && (!epi.pre || (a16(epi.pre) && epi.ldpre % 4 == 0));
+  if (!ok) return false;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  const int wm = w / WGN, wn = w % WGN;
+  auto slot = [](int R, int q) { return R * BN + 4 * (q ^ ((4 * (R >> 2)) & (F - 1))); };
+  __syncthreads();  // every wave done with the LDS the tile reuses
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int R = wm * WM + 16 * a + 4 * g + rr, Cc = wn * WN + 16 * b + c;
+        tile[slot(R, Cc >> 2) + (Cc & 3)] = acc[a][b][rr];
+      }
+  __syncthreads();
+  const int q = tid % F;
+  const int j = n0 + 4 * q;
+  float4 bj = make_float4(0.f, 0.f, 0.f, 0.f), bj2 = bj;
+  if (epi.bias) {
+    if (act4) {
+      bj = *reinterpret_cast<const float4*>(epi.bias + 2 * j);
+      bj2 = *reinterpret_cast<const float4*>(epi.bias + 2 * j + 4);
+    } else {
+      bj = *reinterpret_cast<const float4*>(epi.bias + j);
+    }
+  }
+  for (int R = tid / F; R < BM; R += T / F) {
+    const int i = m0 + R;
+    if (i >= M) break;
+    const float4 t4 = *reinterpret_cast<const float4*>(tile + slot(R, q));
+    float v[4] = {t4.x, t4.y, t4.z, t4.w};
+    if (epi.act >= 3) {
+      const float* z = epi.cin + int64_t(i) * epi.ldcin;
+      if (!act4) {
+        const float4 z4 = *reinterpret_cast<const float4*>(z + j);
+        const float zz[4] = {z4.x, z4.y, z4.z, z4.w}, bb[4] = {bj.x, bj.y, bj.z, bj.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = zz[e] + (epi.bias ? bb[e] : 0.f), sg = sig_fast(x);
+          o[e] = v[e] * (sg * (1.0f + x * (1.0f - sg)));
+        }
+        *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(o[0], o[1], o[2], o[3]);
+      } else {
+        const float4 z0 = *reinterpret_cast<const float4*>(z + 2 * j), z1 = *reinterpret_cast<const float4*>(z + 2 * j + 4);
+        const float zz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        const float bb[8] = {bj.x, bj.y, bj.z, bj.w, bj2.x, bj2.y, bj2.z, bj2.w};
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float u = zz[2 * e] + (epi.bias ? bb[2 * e] : 0.f);
+          const float sg = sig_fast(zz[2 * e + 1] + (epi.bias ? bb[2 * e + 1] : 0.f));
+          o[2 * e] = v[e] * sg, o[2 * e + 1] = v[e] * u * sg * (1.0f - sg);
+        }
+        float* dst = C + int64_t(i) * ldc + 2 * j;
+        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      }
+      continue;
+    }
+    if (epi.row_scale) {
+      const float rs = epi.row_scale[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] *= rs;
+    }
+    if (epi.bias) v[0] += bj.x, v[1] += bj.y, v[2] += bj.z, v[3] += bj.w;
+    if (epi.cin) {
+      const float4 c4 = *reinterpret_cast<const float4*>(epi.cin + int64_t(i) * epi.ldcin + j);
+      v[0] += epi.beta * c4.x, v[1] += epi.beta * c4.y, v[2] += epi.beta * c4.z, v[3] += epi.beta * c4.w;
+    }
+    if (epi.pre) *reinterpret_cast<float4*>(epi.pre + int64_t(i) * epi.ldpre + j) = make_float4(v[0], v[1], v[2], v[3]);
+    if (act2) {
+      *reinterpret_cast<float2*>(C + int64_t(i) * ldc + j / 2) = make_float2(v[0] * sig_fast(v[1]), v[2] * sig_fast(v[3]));
+    } else {
+      if (epi.act == 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] * sig_fast(v[e]);
+      *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+  return true;
+}
+
+// 16 bytes a lane from global memory into LDS, a wave's 64 lanes filling
+// dst .. dst + 1 KB in lane order (dst wave-uniform). A device function: the
+// builtin, called in a lambda of a kernel, stops the host side from emitting
+// the kernel.
+__device__ __forceinline__ void ring_load(const u4* src, u4* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+// s_waitcnt on the vector-memory counter alone (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14; expcnt 7 and lgkmcnt 15 wait for nothing).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// C = epi(A B^T) with both operands as fp16 pairs (pair_act_kernel's and
+// pair_rows_kernel's layout): a row's K step of 32 is 8 u4, part p = 2 group +
+// (0 hi, 1 lo). No vector arithmetic in the K loop: the steps go from global
+// memory straight into an LDS ring of ST stages (global_load_lds_dwordx4, a
+// wave's instruction filling 8 rows' steps, 1 KB), ST - 1 steps in flight, one
+// barrier a step. Part p of row r sits in 16-byte slot p ^ f(r) of the row's
+// 128 bytes, f(r) = bit 2 of r as bit 0 and bit 3 as bit 2: a 128-bit LDS
+// read serves 32 lanes (16 rows, two k groups) a cycle over 128 banks, rows
+// r, r + 4, r + 8, r + 12 share banks, and f gives their two groups' slots
+// {x, x ^ 2} four disjoint pairs (measured: f = r & 7 2-way conflicts, 17% of
+// cycles; f = (r >> 1) & 7 25%). The swizzle is applied on the global side
+// (lane L of an instruction loads the part its slot L % 8 holds). The k order and the
+// epilogue's unscaling are gemm_nt_pair_kernel's, so the two give the same bits.
+// Tiles of WGM x WGN waves; K a multiple of 32.
+template <int BM, int BN, int WGM, int WGN, int ST>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_pp_kernel(int M, int N, int K, const u4* __restrict__ Ap,
+                                                                  const u4* __restrict__ Bs, float* C, int64_t ldc,
+                                                                  Epi epi) {
+  constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+  constexpr int SR = BM + BN, LPW = SR / 8 / NW;  // rows a stage; load instructions a wave a step
+  static_assert(LPW * 8 * NW == SR && ST >= 2 && ST <= 6, "a stage's rows divide over the waves");
+  extern __shared__ u4 ring[];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  const int wm = w / WGN, wn = w % WGN;
+  // the XCD-contiguous tile order of gemm_nt_pair_kernel, one tile an item
+  const int NT = (N + BN - 1) / BN, total = gridDim.x, L = blockIdx.x;
+  const int q = total / 8, r = total % 8, x = L % 8;
+  const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + L / 8;
+  const int m0 = (t / NT) * BM, n0 = (t % NT) * BN, KG = K / 8;
+
+  // this lane's source for each of the wave's load instructions: stage row
+  // R = 8 (w LPW + i) + l / 8 (A rows first, then B), part (l % 8) ^ (l / 8)
+  const u4* src[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int R = 8 * (w * LPW + i) + (l >> 3), p = (l & 7) ^ (((R >> 2) & 1) | ((R >> 1) & 4));
+    src[i] = R < BM ? Ap + int64_t(min(m0 + R, M - 1)) * KG * 2 + p
+                    : Bs + int64_t(min(n0 + R - BM, N - 1)) * KG * 2 + p;
+  }
+  const int steps = K / 32;
+  auto issue = [&](int s) {
+    u4* dst = ring + (s % ST) * SR * 8 + w * LPW * 64;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i)
+      ring_load(src[i] + 8 * s, dst + 64 * i);
+  };
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s)
+    if (s < steps) issue(s);
+  const int fc = ((c >> 2) & 1) | ((c >> 1) & 4);  // f(row), row & 15 = c
+  const int sw0 = (2 * g) ^ fc, sw1 = (2 * g + 1) ^ fc;
+  for (int s = 0; s < steps; ++s) {
+    // step s's loads done (those after it may still fly), then every wave's
+    const int after = min(ST - 2, steps - 1 - s);
+    if (after >= ST - 2) wait_vm<(ST - 2) * LPW>();
+    else if constexpr (ST >= 4) {
+      if (after == 1) wait_vm<LPW>();
+      else if (ST >= 5 && after == 2) wait_vm<2 * LPW>();
+      else if (ST >= 6 && after == 3) wait_vm<3 * LPW>();
+      else wait_vm<0>();
+    } else {
+      wait_vm<0>();
+    }
+    ring_barrier();
+    if (s + ST - 1 < steps) issue(s + ST - 1);  // into the stage step s - 1 used
+    const u4* st = ring + (s % ST) * SR * 8;
+    u4 av[TM][2], bv[TN][2];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const u4* row = st + (wm * WM + 16 * a + c) * 8;
+      av[a][0] = row[sw0], av[a][1] = row[sw1];
+    }
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const u4* row = st + (BM + wn * WN + 16 * b + c) * 8;
+      bv[b][0] = row[sw0], bv[b][1] = row[sw1];
+    }
+    // mfma3's three products (hi lo, lo hi, hi hi), each over every tile
+    // before the next: TM TN independent accumulators between two dependent
+    // instructions, the same sums in the same order
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          acc[a][b] = pet_split::mfma_h(av[a][p == 0 ? 1 : 0], bv[b][p == 1 ? 1 : 0], acc[a][b]);
+  }
+  const float* inv_a = reinterpret_cast<const float*>(Ap + int64_t(M) * KG * 2);
+  const float* inv_b = reinterpret_cast<const float*>(Bs + int64_t(N) * KG * 2);
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const float ib = inv_b[min(n0 + wn * WN + 16 * b + c, N - 1)];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        acc[a][b][rr] = acc[a][b][rr] * inv_a[min(m0 + wm * WM + 16 * a + 4 * g + rr, M - 1)] * ib;
+  }
+  static_assert(ST * (BM + BN) * 128 >= BM * BN * 4, "the ring holds the result tile");
+  if (staged_epilogue<BM, BN, WGM, WGN>(acc, reinterpret_cast<float*>(ring), m0, n0, M, N, C, ldc, epi)) return;
+  epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+}
+
 }  // namespace pet_gemm
 
 using namespace pet_gemm;
@@ -640,9 +934,20 @@ extern "C" int pet_linear_fused(int M, int N, int K, const float* A, int64_t lda
                            reinterpret_cast<hipStream_t>(stream));
 }
 
+int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C, int64_t ldc, const Epi& e,
+                   hipStream_t st);
+int pet_gemm_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, hipStream_t st);
+
+// The pairs-by-pairs path's threshold: from N = 512 the products' gain
+// outweighs splitting A (C5 energy+forces on MI355X, same bits: N >= 1024
+// 176.4 ms, N >= 512 171.4, N >= 256 171.4, never 191; plain products, same
+// process: 131072 x 1536 x 512 1060 against 95 + 800 us, 498338 x 2048 x 512
+// 4634 against 342 + 3443; with a kept pre-activation 5760 against 4244).
+constexpr int kPairsMinN = 512;
+
 int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
                       const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
-                      float* pre, int64_t ldpre, int act, hipStream_t st) {
+                      float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch, size_t scratch_bytes) {
   if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
   if (K == 0) return PET_ATTN_EINVAL;
@@ -653,6 +958,22 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
   Epi e;
   e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
   e.act = act;
+  // A's rows split into the scratch a chunk at a time (as many rows as it
+  // holds, a multiple of 128), each chunk's product from the pairs
+  const int64_t chunk = scratch ? int64_t(scratch_bytes / (size_t(K) * 4 + 4)) / 128 * 128 : 0;
+  if (pair_form(K) && N >= kPairsMinN && chunk >= 128 && (reinterpret_cast<uintptr_t>(scratch) & 15) == 0) {
+    for (int64_t r0 = 0; r0 < M; r0 += chunk) {
+      const int m = int(std::min<int64_t>(chunk, M - r0));
+      Epi ec = e;
+      if (ec.row_scale) ec.row_scale += r0;
+      if (ec.cin) ec.cin += r0 * ldcin;
+      if (ec.pre) ec.pre += r0 * ldpre;
+      int rc = pet_gemm_pair_rows(A + r0 * lda, m, K, lda, scratch, st);
+      if (rc == PET_ATTN_OK) rc = pet_gemm_nt_pp(m, N, K, scratch, Bs, C + r0 * ldc, ldc, ec, st);
+      if (rc != PET_ATTN_OK) return rc;
+    }
+    return PET_ATTN_OK;
+  }
   auto go = [&](auto kern, int bm, int bn, int threads, bool pair) {  // a 1-D grid of every work item
     const int64_t rb = (M + bm - 1) / bm, nt = (N + bn - 1) / bn;
     // column tiles per item (pair kernel): about 2048 items, four rounds of
@@ -758,5 +1079,88 @@ extern "C" int pet_linear_fused_split(int M, int N, int K, const float* A, int64
                                                                               ldpre, act)))
     return PET_ATTN_EINVAL;
   return pet_gemm_nt_split(M, N, K, A, lda, Wsplit, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
-                           reinterpret_cast<hipStream_t>(stream));
+                           reinterpret_cast<hipStream_t>(stream), nullptr, 0);
+}
+
+// fp16-pair rows of an activation X [M, K] into out (M K 4 + M 4 bytes,
+// 16-byte aligned): the A operand of pet_gemm_nt_pp. Pair-form K only.
+int pet_gemm_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, hipStream_t st) {
+  if (M < 0 || K < 0 || !pair_form(K) || K % 32 || ldx % 4 || (reinterpret_cast<uintptr_t>(X) & 15) ||
+      (reinterpret_cast<uintptr_t>(out) & 15))
+    return PET_ATTN_EINVAL;
+  if (M == 0) return PET_ATTN_OK;
+  const dim3 grid(unsigned((M + 3) / 4));
+  u4* o = static_cast<u4*>(out);
+  if (K <= 512)
+    hipLaunchKernelGGL(pair_act_kernel<1>, grid, dim3(256), 0, st, X, M, K, ldx, o);
+  else if (K <= 1024)
+    hipLaunchKernelGGL(pair_act_kernel<2>, grid, dim3(256), 0, st, X, M, K, ldx, o);
+  else if (K <= 2048)
+    hipLaunchKernelGGL(pair_act_kernel<4>, grid, dim3(256), 0, st, X, M, K, ldx, o);
+  else
+    hipLaunchKernelGGL(pair_act_kernel<0>, grid, dim3(256), 0, st, X, M, K, ldx, o);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// The pairs-by-pairs kernel's shapes: tile, waves, LDS stages.
+struct PPShape {
+  void (*kern)(int, int, int, const u4*, const u4*, float*, int64_t, Epi);
+  int bm, bn, threads, stages;
+  size_t lds() const { return size_t(stages) * (bm + bn) * 128; }
+};
+// measured on MI355X (131072 x 1536 x 512, plain epilogue): 128 x 128 tiles
+// of 8 waves with two stages (two workgroups a CU) 752-813 us; four stages (one
+// workgroup) 1128; three 991; 256 x 128 tiles, three stages 827-874; 128 x
+// 128 of 4 waves 1300; the operand reads of the next step issued before this
+// step's products (a second register set, three or four stages) 695-1018
+const PPShape kPP[] = {
+    {gemm_pp_kernel<128, 128, 2, 4, 2>, 128, 128, 512, 2},  // many tiles, N >= 128
+    {gemm_pp_kernel<128, 64, 2, 2, 4>, 128, 64, 256, 4},    // fewer tiles, N >= 64
+    {gemm_pp_kernel<64, 64, 2, 2, 4>, 64, 64, 256, 4},      // the rest
+};
+
+// C = epi(A B^T) from the pairs of A (pet_gemm_pair_rows) and of B
+// (pet_gemm_split_weights), K of the pair form.
+int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C, int64_t ldc, const Epi& e,
+                   hipStream_t st) {
+  if (M < 0 || N < 0 || !pair_form(K) || K % 32) return PET_ATTN_EINVAL;
+  if (M == 0 || N == 0) return PET_ATTN_OK;
+  if ((reinterpret_cast<uintptr_t>(Ap) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15)) return PET_ATTN_EALIGN;
+  if (int64_t((M + 63) / 64) * ((N + 63) / 64) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
+  // each shape's dynamic LDS above the 64 KB default, set once a process for
+  // every shape (on the device current then)
+  static std::once_flag once;
+  static hipError_t set_err = hipSuccess;
+  std::call_once(once, [] {
+    for (const PPShape& k : kPP) {
+      const hipError_t r = hipFuncSetAttribute(reinterpret_cast<const void*>(k.kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(k.lds()));
+      if (r != hipSuccess) set_err = r;
+    }
+  });
+  if (set_err != hipSuccess) return PET_ATTN_ELAUNCH;
+  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
+  const PPShape& k = kPP[N >= 128 && t128 >= 1024 ? 0 : N >= 64 ? 1 : 2];
+  const int64_t tiles = int64_t((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
+  hipLaunchKernelGGL(k.kern, dim3(unsigned(tiles)), dim3(k.threads), k.lds(), st, M, N, K,
+                     static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+extern "C" int pet_linear_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, void* stream) {
+  if (M < 0 || K < 0 || ldx < K || (M > 0 && K > 0 && (!X || !out))) return PET_ATTN_EINVAL;
+  return pet_gemm_pair_rows(X, M, K, ldx, out, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pet_linear_fused_pairs(int M, int N, int K, const void* Apairs, const void* Wsplit, float* C,
+                                      int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                      int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream) {
+  if ((M > 0 && N > 0) && (!Apairs || !Wsplit || !C || !epi_args_ok(N, C, ldc, row_scale, cin, ldcin, pre,
+                                                                      ldpre, act)))
+    return PET_ATTN_EINVAL;
+  if (act == 2 && N % 2) return PET_ATTN_EINVAL;
+  Epi e;
+  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
+  e.act = act;
+  return pet_gemm_nt_pp(M, N, K, Apairs, Wsplit, C, ldc, e, reinterpret_cast<hipStream_t>(stream));
 }

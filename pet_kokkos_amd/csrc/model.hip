@@ -44,7 +44,8 @@ int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const fl
                       float beta, float* pre, int64_t ldpre, int act, hipStream_t st);
 int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
                       const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
-                      float* pre, int64_t ldpre, int act, hipStream_t st);
+                      float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch = nullptr,
+                      size_t scratch_bytes = 0);
 
 namespace pet_model_impl {
 
@@ -486,6 +487,10 @@ struct pet_model {
   void* weights = nullptr;
   void* wsplit = nullptr;
   double* comp = nullptr;
+  // A's fp16 pairs for the split-product kernel's pairs-by-pairs path, a row
+  // chunk at a time (null: that path is not taken)
+  void* pairs = nullptr;
+  static constexpr size_t kPairsBytes = size_t(512) << 20;
   Arena ws;
 
   ~pet_model() {
@@ -493,6 +498,7 @@ struct pet_model {
     if (weights) (void) hipFree(weights);
     if (wsplit) (void) hipFree(wsplit);
     if (comp) (void) hipFree(comp);
+    if (pairs) (void) hipFree(pairs);
   }
   const Mat& w(const std::string& name) const {
     auto it = m.find(name);
@@ -542,7 +548,7 @@ int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_
            int K, float beta, hipStream_t st) {
   if (const void* sp = split_for(md, in, ldi, W, M, N, K))
     return pet_gemm_nt_split(M, N, K, in, ldi, sp, out, ldo, nullptr, nullptr, beta != 0.f ? out : nullptr, ldo, beta,
-                             nullptr, 0, 0, st);
+                             nullptr, 0, 0, st, md.pairs, md.pairs ? md.kPairsBytes : 0);
   return gemm_nt(out, ldo, in, ldi, W, M, N, K, beta, st);
 }
 
@@ -558,7 +564,8 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
     return;
   }
   if (const void* sp = split_for(md, in, K, W.p, M, W.rows, K)) {  // the bias in the epilogue
-    ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
+    ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st,
+                         md.pairs, md.pairs ? md.kPairsBytes : 0));
     return;
   }
   if (rows4_ok(W.rows, {out, b}))
@@ -591,7 +598,7 @@ void linear_acc_bias(pet_model& md, float* out, const float* in, int M, int K, c
   if (M == 0) return;
   if (const void* sp = own_gemm(md, M, K) ? nullptr : split_for(md, in, K, W.p, M, W.rows, K)) {
     ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, md.p(key + ".bias"), out, W.rows, 1.f,
-                         nullptr, 0, 0, st));
+                         nullptr, 0, 0, st, md.pairs, md.pairs ? md.kPairsBytes : 0));
     return;
   }
   add_bias_pass(out, md.p(key + ".bias"), int64_t(M), W.rows, st);
@@ -618,7 +625,7 @@ bool linear_bwd_act(pet_model& md, float* out, const float* adj, int M, const st
   if (!sp) return false;
   const int64_t w = act == 2 ? 2 * int64_t(WT.rows) : WT.rows;
   ok(pet_gemm_nt_split(M, WT.rows, WT.cols, adj, WT.cols, sp, out, w, nullptr, pass_bias(md, key_act), z, w, 0.f,
-                       nullptr, 0, act == 2 ? 4 : 3, st));
+                       nullptr, 0, act == 2 ? 4 : 3, st, md.pairs, md.pairs ? md.kPairsBytes : 0));
   return true;
 }
 // z[M, Nout] = in W^T, no bias: the pre-activation an activation pass reads with its bias
@@ -651,7 +658,7 @@ bool linear_act(pet_model& md, float* out, float* z, const float* in, int M, int
   md.pre_biased[key] = sp != nullptr;
   if (!sp || M == 0) return false;
   ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, act == 2 ? W.rows / 2 : W.rows, nullptr, md.p(key + ".bias"),
-                       nullptr, 0, 0.f, z, W.rows, act, st));
+                       nullptr, 0, 0.f, z, W.rows, act, st, md.pairs, md.pairs ? md.kPairsBytes : 0));
   return true;
 }
 // the bias the activation passes add to a saved pre-activation: none where the
@@ -1436,6 +1443,12 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
     std::vector<double> comp(ns, 0.0);
     if (composition) comp.assign(composition, composition + ns);
     if (hipMalloc(&md->comp, sizeof(double) * ns) != hipSuccess) throw Error{PET_MODEL_EMEMORY};
+    // the pairs scratch, where the device has room (else the products split
+    // A as they stage it)
+    if (md->wsplit && hipMalloc(&md->pairs, pet_model::kPairsBytes) != hipSuccess) {
+      md->pairs = nullptr;
+      (void) hipGetLastError();
+    }
     if (hipMemcpy(md->comp, comp.data(), sizeof(double) * ns, hipMemcpyHostToDevice) != hipSuccess)
       throw Error{PET_ATTN_ELAUNCH};
   } catch (const Error& err) {

@@ -16,7 +16,8 @@
 // gemm.hip: the split-product dense layer and its weight split
 int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
                       const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
-                      float* pre, int64_t ldpre, int act, hipStream_t st);
+                      float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch = nullptr,
+                      size_t scratch_bytes = 0);
 int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st);
 int pet_gemm_nt_split_f32b(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                            int64_t ldc, const float* bias, const float* cin, int64_t ldcin, float beta, hipStream_t st);

@@ -33,6 +33,24 @@ class SplitWeights:
                    "pet_linear_split_weights" + ("_transposed" if transposed else ""))
 
 
+class PairRows:
+    """A [M, K] (K a multiple of 32 and at least 256) as fp16 pairs of
+    power-of-two-scaled rows, M K 4 + M 4 bytes of device memory: made once
+    (pet_linear_pair_rows), then used in place of A by any number of products
+    with split weights; their results are those of A itself, bit for bit."""
+
+    def __init__(self, A: torch.Tensor):
+        _check(A, "A")
+        M, K = A.shape
+        if K % 32 or K < 256:
+            raise ValueError(f"A has K = {K}: the pair rows need K a multiple of 32 and at least 256")
+        self.shape = (M, K)
+        self.data = torch.empty(M * K * 2 + 2 * M + 8, dtype=torch.int16, device=A.device)
+        _lib.check(_lib.load().pet_linear_pair_rows(A.data_ptr(), M, K, A.stride(0), self.data.data_ptr(),
+                                                    torch.cuda.current_stream().cuda_stream),
+                   "pet_linear_pair_rows")
+
+
 def _check(t, name, rows=None, cols=None, vector=False, device=None):
     """A float32 CUDA tensor, unit stride along its last axis, of the stated
     extents (a row may be longer than `cols` in a 2-D view: the leading
@@ -62,9 +80,15 @@ def _check(t, name, rows=None, cols=None, vector=False, device=None):
 def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
     if act not in (0, 1, 2, 3, 4):
         raise ValueError(f"act {act}: 0 (none), 1 (SiLU), 2 (SwiGLU), 3 / 4 (their backward)")
-    _check(A, "A")
-    M, K = A.shape
-    dev = A.device
+    if isinstance(A, PairRows):
+        if not isinstance(W, SplitWeights):
+            raise ValueError("A as pair rows needs W as SplitWeights")
+        M, K = A.shape
+        dev = A.data.device
+    else:
+        _check(A, "A")
+        M, K = A.shape
+        dev = A.device
     if isinstance(W, SplitWeights):
         N, Kw = W.shape
         if W.data.device != dev:
@@ -93,7 +117,11 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
     ld = lambda t: 0 if t is None else t.stride(0)
     st = torch.cuda.current_stream().cuda_stream
     lib = _lib.load()
-    if isinstance(W, SplitWeights):
+    if isinstance(A, PairRows):
+        _lib.check(lib.pet_linear_fused_pairs(M, N, K, A.data.data_ptr(), W.data.data_ptr(), p(C), C.stride(0),
+                                              p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
+                   "pet_linear_fused_pairs")
+    elif isinstance(W, SplitWeights):
         _lib.check(lib.pet_linear_fused_split(M, N, K, p(A), A.stride(0), W.data.data_ptr(), p(C), C.stride(0),
                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
                    "pet_linear_fused_split")
@@ -105,7 +133,8 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
 
 def fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
     """C = act(row_scale * (A W^T) + bias + beta cin), pre = the value before
-    act; act 0 none, 1 SiLU, 2 SwiGLU (C [M, N/2]). W a tensor or SplitWeights.
+    act; act 0 none, 1 SiLU, 2 SwiGLU (C [M, N/2]). W a tensor or SplitWeights;
+    A a tensor or, with W as SplitWeights, PairRows.
     act 3 / 4: A W^T is the adjoint of a SiLU / SwiGLU output and cin its saved
     pre-activation z (bias z's bias if not yet in it): C = adjoint silu'(z), or
     for SwiGLU (z and C [M, 2N], (value, gate) pairs) each pair's adjoint."""

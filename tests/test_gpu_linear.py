@@ -273,3 +273,40 @@ def test_reference_named_wrappers(device):
         L.swiglu_in_fused(pre, h, A, w, b)
         ref = z[:, 0::2] * torch.sigmoid(z[:, 1::2])
         assert (h.double() - ref).abs().max().item() <= tol(ref)
+
+
+# pairs-by-pairs (A split once into PairRows): whole 128 x 128 tiles take the
+# LDS-staged epilogue, N = 300 and ragged M the per-element one; every epilogue
+# must give the bits of the split-weights product from A itself
+@pytest.mark.parametrize("M,N,K", [(1000, 1024, 512), (777, 300, 256), (20000, 2048, 512), (4096, 512, 1024),
+                                   (300, 64, 288)])
+def test_pair_rows_same_bits(M, N, K, device):
+    print(f"[gpu] pair rows M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(M + N + K)
+    A = torch.randn(M, K, device=device, generator=g) * 3.0
+    W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
+    Ws, Ap = L.SplitWeights(W), L.PairRows(A)
+    b = torch.randn(N, device=device, generator=g)
+    b2 = torch.randn(2 * N, device=device, generator=g)
+    rs = torch.rand(M, device=device, generator=g) + 0.5
+    res = torch.randn(M, N, device=device, generator=g)
+    z = torch.randn(M, N, device=device, generator=g)
+    z2 = torch.randn(M, 2 * N, device=device, generator=g)
+    cases = [dict(bias=b), dict(row_scale=rs, bias=b, cin=res, beta=0.5, pre="N"), dict(bias=b, pre="N", act=1),
+             dict(bias=b, pre="N", act=2), dict(bias=b, cin=z, act=3), dict(bias=b2, cin=z2, act=4), dict()]
+    for kw in cases:
+        act = kw.get("act", 0)
+        width = N // 2 if act == 2 else 2 * N if act == 4 else N
+        outs = []
+        for a in (A, Ap):
+            C = torch.full((M, width), float("nan"), device=device)
+            pre = torch.full((M, N), float("nan"), device=device) if kw.get("pre") else None
+            L.fused(a, Ws, C, **{**kw, "pre": pre})
+            outs.append((C, pre))
+        assert torch.equal(outs[0][0], outs[1][0]), kw.keys()
+        if outs[0][1] is not None:
+            assert torch.equal(outs[0][1], outs[1][1])
+    with pytest.raises(ValueError):
+        L.fused(Ap, W, torch.empty(M, N, device=device))  # pair rows need split weights
+    with pytest.raises(ValueError):
+        L.PairRows(torch.zeros(8, 128, device=device))  # K below 256
