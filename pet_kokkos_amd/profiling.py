@@ -6,7 +6,11 @@ the benchmark configurations, preceded by a plain device copy of known size
     python -m pet_kokkos_amd.profiling --model c2 --steps 10
 
 With ``--model`` the steps are whole energy+forces evaluations of the PET
-model on that workload (C2: 648-atom water; C5: 32 structures) instead.
+model on that workload (C2: 648-atom water; C5: 32 structures) instead; with
+``--gemm M,N,K`` one dense product C = A W^T (+ bias) on random operands, each
+step once from fp32 A (pet_linear_fused_split) and once from its pair rows
+(pet_linear_pair_rows, then pet_linear_fused_pairs), optionally keeping the
+pre-activation (``--gemm-pre``).
 
 Under ``rocprofv3 --kernel-trace --stats`` it gives each kernel's average
 duration; under ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``) each
@@ -33,6 +37,8 @@ def main(argv=None):
     ap.add_argument("--rows", action="store_true",
                     help="also run the token norm (forward, backward) and the forces' edge term and fold each step")
     ap.add_argument("--model", choices=["c2", "c2-residual", "c5"], help="profile whole energy+forces evaluations instead")
+    ap.add_argument("--gemm", metavar="M,N,K", help="profile one dense product instead")
+    ap.add_argument("--gemm-pre", action="store_true", help="with --gemm: bias and kept pre-activation epilogue")
     ap.add_argument("--option", action="append", default=[], metavar="NAME=VALUE",
                     help="a library option (pet_attn_set_option by name, e.g. bwd_kernel=1), repeatable")
     args = ap.parse_args(argv)
@@ -43,6 +49,8 @@ def main(argv=None):
     device = torch.device("cuda", 0)
     if args.model:
         return profile_model(args, device)
+    if args.gemm:
+        return profile_gemm(args, device)
     conf, tk = systems.config_tokens(args.config, seed=0)
     H, hd, D = conf.heads, conf.head_dim, conf.d_model
     N, S, T = tk.n_atoms, tk.slots, tk.n_rows
@@ -108,6 +116,31 @@ def profile_model(args, device):
         m.compute(x, True, out=out)
     torch.cuda.synchronize()
     print(json.dumps({"model": args.model, "steps": args.steps, "atoms": x.n_atoms, "edges": x.n_edges}), flush=True)
+    return 0
+
+
+def profile_gemm(args, device):
+    from . import linear as L
+    M, N, K = (int(v) for v in args.gemm.split(","))
+    g = torch.Generator(device=device)
+    g.manual_seed(3)
+    A = torch.randn((M, K), device=device, generator=g)
+    W = torch.randn((N, K), device=device, generator=g) / K ** 0.5
+    b = torch.randn(N, device=device, generator=g)
+    C = torch.empty((M, N), device=device)
+    pre = torch.empty((M, N), device=device) if args.gemm_pre else None
+    Ws = L.SplitWeights(W)
+    src = torch.randn(args.copy_mib * (1 << 20) // 4, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    del src, dst
+    kw = dict(bias=b, pre=pre) if args.gemm_pre else {}
+    for _ in range(args.steps):
+        L.fused(A, Ws, C, **kw)
+        L.fused(L.PairRows(A), Ws, C, **kw)
+    torch.cuda.synchronize()
+    print(json.dumps({"gemm": [M, N, K], "steps": args.steps, "pre": args.gemm_pre}), flush=True)
     return 0
 
 
