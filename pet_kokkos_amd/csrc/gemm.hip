@@ -112,6 +112,113 @@ __device__ __forceinline__ void epilogue(const f4 (&acc)[WM / 16][WN / 16], int 
         epi_elem(acc[a][b][r], m0 + wm * WM + 16 * a + 4 * g + r, n0 + wn * WN + 16 * b + c, c, M, N, C, ldc, epi);
 }
 
+// The epilogue through LDS, for a tile whose columns all lie in the result:
+// the waves' results (already unscaled) go to a BM x BN fp32 tile in LDS
+// (float4 slot q of row R at q ^ s(R), s(R) = 4 (R / 4) mod BN / 4, so the
+// four row groups of a store fall on distinct banks), then each thread takes
+// float4 runs of a row and applies epi_elem's arithmetic, in its order, with
+// 16-byte loads and stores (C, pre, cin, bias) in place of a wave's 4-byte
+// stores to four rows. False (nothing written) where a pointer or leading
+// dimension does not allow the 16-byte accesses; the caller then uses
+// epilogue(). tile: BM BN floats of LDS no wave still reads.
+template <int BM, int BN, int WGM, int WGN, int PASSES = 1>
+__device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][BN / WGN / 16], float* tile, int m0,
+                                                int n0, int M, int N, float* C, int64_t ldc, const Epi& epi) {
+  constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, F = BN / 4;
+  constexpr int RB = BM / PASSES;  // the tile's rows a pass (the rows of WGM / PASSES wave rows)
+  static_assert(T % F == 0 && WGM % PASSES == 0, "whole rows a pass, whole wave rows a pass");
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool act4 = epi.act == 4, act2 = epi.act == 2;
+  // C's columns: 2 N (act 4), N / 2 (act 2), else N; j stays a multiple of 4
+  const bool ok = n0 + BN <= N && a16(C) && ldc % 4 == 0 && (!epi.bias || a16(epi.bias)) &&
+                  (!epi.cin || (a16(epi.cin) && epi.ldcin % 4 == 0)) && (!epi.pre || (a16(epi.pre) && epi.ldpre % 4 == 0));
+  if (!ok) return false;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  const int wm = w / WGN, wn = w % WGN;
+  auto slot = [](int R, int q) { return R * BN + 4 * (q ^ ((4 * (R >> 2)) & (F - 1))); };
+  const int q = tid % F;
+  const int j = n0 + 4 * q;
+  float4 bj = make_float4(0.f, 0.f, 0.f, 0.f), bj2 = bj;
+  if (epi.bias) {
+    if (act4) {
+      bj = *reinterpret_cast<const float4*>(epi.bias + 2 * j);
+      bj2 = *reinterpret_cast<const float4*>(epi.bias + 2 * j + 4);
+    } else {
+      bj = *reinterpret_cast<const float4*>(epi.bias + j);
+    }
+  }
+  for (int h = 0; h < PASSES; ++h) {
+  __syncthreads();  // every wave done with the LDS the tile reuses
+  if (wm / (WGM / PASSES) == h) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int R = wm * WM + 16 * a + 4 * g + rr - h * RB, Cc = wn * WN + 16 * b + c;
+          tile[slot(R, Cc >> 2) + (Cc & 3)] = acc[a][b][rr];
+        }
+  }
+  __syncthreads();
+  for (int R = tid / F; R < RB; R += T / F) {
+    const int i = m0 + h * RB + R;
+    if (i >= M) break;
+    const float4 t4 = *reinterpret_cast<const float4*>(tile + slot(R, q));
+    float v[4] = {t4.x, t4.y, t4.z, t4.w};
+    if (epi.act >= 3) {
+      const float* z = epi.cin + int64_t(i) * epi.ldcin;
+      if (!act4) {
+        const float4 z4 = *reinterpret_cast<const float4*>(z + j);
+        const float zz[4] = {z4.x, z4.y, z4.z, z4.w}, bb[4] = {bj.x, bj.y, bj.z, bj.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = zz[e] + (epi.bias ? bb[e] : 0.f), sg = sig_fast(x);
+          o[e] = v[e] * (sg * (1.0f + x * (1.0f - sg)));
+        }
+        *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(o[0], o[1], o[2], o[3]);
+      } else {
+        const float4 z0 = *reinterpret_cast<const float4*>(z + 2 * j), z1 = *reinterpret_cast<const float4*>(z + 2 * j + 4);
+        const float zz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        const float bb[8] = {bj.x, bj.y, bj.z, bj.w, bj2.x, bj2.y, bj2.z, bj2.w};
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float u = zz[2 * e] + (epi.bias ? bb[2 * e] : 0.f);
+          const float sg = sig_fast(zz[2 * e + 1] + (epi.bias ? bb[2 * e + 1] : 0.f));
+          o[2 * e] = v[e] * sg, o[2 * e + 1] = v[e] * u * sg * (1.0f - sg);
+        }
+        float* dst = C + int64_t(i) * ldc + 2 * j;
+        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      }
+      continue;
+    }
+    if (epi.row_scale) {
+      const float rs = epi.row_scale[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] *= rs;
+    }
+    if (epi.bias) v[0] += bj.x, v[1] += bj.y, v[2] += bj.z, v[3] += bj.w;
+    if (epi.cin) {
+      const float4 c4 = *reinterpret_cast<const float4*>(epi.cin + int64_t(i) * epi.ldcin + j);
+      v[0] += epi.beta * c4.x, v[1] += epi.beta * c4.y, v[2] += epi.beta * c4.z, v[3] += epi.beta * c4.w;
+    }
+    if (epi.pre) *reinterpret_cast<float4*>(epi.pre + int64_t(i) * epi.ldpre + j) = make_float4(v[0], v[1], v[2], v[3]);
+    if (act2) {
+      *reinterpret_cast<float2*>(C + int64_t(i) * ldc + j / 2) = make_float2(v[0] * sig_fast(v[1]), v[2] * sig_fast(v[3]));
+    } else {
+      if (epi.act == 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] * sig_fast(v[e]);
+      *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+  }
+  return true;
+}
+
 template <int BM, int BN, int BK = 32>
 __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const float* __restrict__ A, int64_t lda,
                                                       const float* __restrict__ B, int64_t ldb, float* C, int64_t ldc,
@@ -227,7 +334,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
   constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, RP = 14;
   constexpr int AQ = BM * 8, AL = (AQ + T - 1) / T;   // float4 of a step's A slice, a thread's share
   constexpr int BQ = BF ? BN * 8 : BN * 12, BL = (BQ + T - 1) / T;  // B slice: float4 (BF) or u4 slots
-  __shared__ u4 As[BM * RP], Bt[BN * RP];
+  __shared__ u4 lds_ab[(BM + BN) * RP];  // A's and B's step slices, one array (the epilogue's tile spans both)
+  u4* const As = lds_ab;
+  u4* const Bt = lds_ab + BM * RP;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
   const int wm = w / WGN, wn = w % WGN;
   // Workgroups go to the 8 XCDs in turn (an L2 each): XCD k takes a
@@ -327,7 +436,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_split_kernel(int M, in
       __syncthreads();
     }
   }
-  epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  // through LDS (the slices', done with), a pass per wave row
+  static_assert((BM / WGM) * BN * 4 <= (BM + BN) * RP * 16, "a wave row's results fit the slices' LDS");
+  if (!staged_epilogue<BM, BN, WGM, WGN, WGM>(acc, reinterpret_cast<float*>(lds_ab), m0, n0, M, N, C, ldc, epi))
+    epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
 }
 
 // W^T as split rows, W [K, N] (ld ldw): out[(n K/8 + j) 3 + p] = part p of
@@ -375,7 +487,7 @@ __global__ void split_rows_kernel(const float* __restrict__ W, int N, int K, int
 // A (for a caller with no room to keep a split copy), its row scales from the
 // same first pass.
 template <int BM, int BN, int WGM = 2, int WGN = 2, bool BF = false>
-__global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_pair_kernel(int M, int N, int K,
+__global__ void __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(BN == 128 ? 4 : BM == 128 ? 2 : 3))) gemm_nt_pair_kernel(int M, int N, int K,
                                                                        const float* __restrict__ A, int64_t lda,
                                                                        const u4* __restrict__ Bs, float* C,
                                                                        int64_t ldc, Epi epi,
@@ -385,7 +497,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_pair_kernel(int M, int
   constexpr int AL = BM * 8 / T;  // float4 of a step's A slice, a thread's share
   constexpr int BL = BN * 8 / T;  // B slice: float4 (BF) or u4 slots, a thread's share
   static_assert(AL * T == BM * 8 && BL * T == BN * 8, "a step's slices divide evenly over the threads");
-  __shared__ u4 As[BM * RP], Bt[BN * RP];
+  __shared__ u4 lds_ab[(BM + BN) * RP];  // A's and B's step slices, one array (the epilogue's tile spans both)
+  u4* const As = lds_ab;
+  u4* const Bt = lds_ab + BM * RP;
   __shared__ float sa[BM], sb[BF ? BN : 1];  // row scales of the tile's A rows (and B rows with BF)
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
   const int wm = w / WGN, wn = w % WGN;
@@ -539,7 +653,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_nt_pair_kernel(int M, int
   // here, not hoisted out of the tile loop into registers held across it)
   int m0t = m0;
   asm volatile("" : "+s"(m0t));
-  epilogue<WM, WN>(acc, m0t, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  // through LDS (As and Bt, done with), a pass per wave row
+  static_assert((BM / WGM) * BN * 4 <= (BM + BN) * RP * 16, "a wave row's results fit the slices' LDS");
+  if (!staged_epilogue<BM, BN, WGM, WGN, WGM>(acc, reinterpret_cast<float*>(As), m0t, n0, M, N, C, ldc, epi))
+    epilogue<WM, WN>(acc, m0t, n0, wm, wn, c, g, M, N, C, ldc, epi);
   __syncthreads();  // the next tile's first slices overwrite this one's last
   }
 }
@@ -641,107 +758,6 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// The epilogue through LDS, for a tile whose columns all lie in the result:
-// the waves' results (already unscaled) go to a BM x BN fp32 tile in LDS
-// (float4 slot q of row R at q ^ s(R), s(R) = 4 (R / 4) mod BN / 4, so the
-// four row groups of a store fall on distinct banks), then each thread takes
-// float4 runs of a row and applies epi_elem's arithmetic, in its order, with
-// 16-byte loads and stores (C, pre, cin, bias) in place of a wave's 4-byte
-// stores to four rows. False (nothing written) where a pointer or leading
-// dimension does not allow the 16-byte accesses; the caller then uses
-// epilogue(). tile: BM BN floats of LDS no wave still reads.
-template <int BM, int BN, int WGM, int WGN>
-__device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][BN / WGN / 16], float* tile, int m0,
-                                                int n0, int M, int N, float* C, int64_t ldc, const Epi& epi) {
-  constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, F = BN / 4;
-  static_assert(T % F == 0, "whole rows a pass");
-  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  const bool act4 = epi.act == 4, act2 = epi.act == 2;
-  // C's columns: 2 N (act 4), N / 2 (act 2), else N; j stays a multiple of 4
-  const bool ok = n0 + BN <= N && a16(C) && ldc % 4 == 0 && (!epi.bias || a16(epi.bias)) &&
-                  (!epi.cin || (a16(epi.cin) && epi.ldcin % 4 == 0)) && (!epi.pre || (a16(epi.pre) && epi.ldpre % 4 == 0));
-  if (!ok) return false;
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
-  const int wm = w / WGN, wn = w % WGN;
-  auto slot = [](int R, int q) { return R * BN + 4 * (q ^ ((4 * (R >> 2)) & (F - 1))); };
-  __syncthreads();  // every wave done with the LDS the tile reuses
-#pragma unroll
-  for (int a = 0; a < TM; ++a)
-#pragma unroll
-    for (int b = 0; b < TN; ++b)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int R = wm * WM + 16 * a + 4 * g + rr, Cc = wn * WN + 16 * b + c;
-        tile[slot(R, Cc >> 2) + (Cc & 3)] = acc[a][b][rr];
-      }
-  __syncthreads();
-  const int q = tid % F;
-  const int j = n0 + 4 * q;
-  float4 bj = make_float4(0.f, 0.f, 0.f, 0.f), bj2 = bj;
-  if (epi.bias) {
-    if (act4) {
-      bj = *reinterpret_cast<const float4*>(epi.bias + 2 * j);
-      bj2 = *reinterpret_cast<const float4*>(epi.bias + 2 * j + 4);
-    } else {
-      bj = *reinterpret_cast<const float4*>(epi.bias + j);
-    }
-  }
-  for (int R = tid / F; R < BM; R += T / F) {
-    const int i = m0 + R;
-    if (i >= M) break;
-    const float4 t4 = *reinterpret_cast<const float4*>(tile + slot(R, q));
-    float v[4] = {t4.x, t4.y, t4.z, t4.w};
-    if (epi.act >= 3) {
-      const float* z = epi.cin + int64_t(i) * epi.ldcin;
-      if (!act4) {
-        const float4 z4 = *reinterpret_cast<const float4*>(z + j);
-        const float zz[4] = {z4.x, z4.y, z4.z, z4.w}, bb[4] = {bj.x, bj.y, bj.z, bj.w};
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x = zz[e] + (epi.bias ? bb[e] : 0.f), sg = sig_fast(x);
-          o[e] = v[e] * (sg * (1.0f + x * (1.0f - sg)));
-        }
-        *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(o[0], o[1], o[2], o[3]);
-      } else {
-        const float4 z0 = *reinterpret_cast<const float4*>(z + 2 * j), z1 = *reinterpret_cast<const float4*>(z + 2 * j + 4);
-        const float zz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
-        const float bb[8] = {bj.x, bj.y, bj.z, bj.w, bj2.x, bj2.y, bj2.z, bj2.w};
-        float o[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float u = zz[2 * e] + (epi.bias ? bb[2 * e] : 0.f);
-          const float sg = sig_fast(zz[2 * e + 1] + (epi.bias ? bb[2 * e + 1] : 0.f));
-          o[2 * e] = v[e] * sg, o[2 * e + 1] = v[e] * u * sg * (1.0f - sg);
-        }
-        float* dst = C + int64_t(i) * ldc + 2 * j;
-        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
-      }
-      continue;
-    }
-    if (epi.row_scale) {
-      const float rs = epi.row_scale[i];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] *= rs;
-    }
-    if (epi.bias) v[0] += bj.x, v[1] += bj.y, v[2] += bj.z, v[3] += bj.w;
-    if (epi.cin) {
-      const float4 c4 = *reinterpret_cast<const float4*>(epi.cin + int64_t(i) * epi.ldcin + j);
-      v[0] += epi.beta * c4.x, v[1] += epi.beta * c4.y, v[2] += epi.beta * c4.z, v[3] += epi.beta * c4.w;
-    }
-    if (epi.pre) *reinterpret_cast<float4*>(epi.pre + int64_t(i) * epi.ldpre + j) = make_float4(v[0], v[1], v[2], v[3]);
-    if (act2) {
-      *reinterpret_cast<float2*>(C + int64_t(i) * ldc + j / 2) = make_float2(v[0] * sig_fast(v[1]), v[2] * sig_fast(v[3]));
-    } else {
-      if (epi.act == 1)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v[e] * sig_fast(v[e]);
-      *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(v[0], v[1], v[2], v[3]);
-    }
-  }
-  return true;
-}
 
 // 16 bytes a lane from global memory into LDS, a wave's 64 lanes filling
 // dst .. dst + 1 KB in lane order (dst wave-uniform). A device function: the
