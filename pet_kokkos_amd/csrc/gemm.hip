@@ -226,7 +226,9 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16, PK = BK + 4, Q4 = BK / 4;
   // float4 slots of a step's A / B slice (4 a row), and a thread's share
   constexpr int AQ = BM * BK / 4, BQ = BN * BK / 4, AL = (AQ + 255) / 256, BL = (BQ + 255) / 256;
-  __shared__ float As[2][BM * PK], Bs[2][BN * PK];
+  __shared__ float lds_ab[2 * (BM + BN) * PK];  // both buffers of A's and B's slices, one array
+  float (*const As)[BM * PK] = reinterpret_cast<float (*)[BM * PK]>(lds_ab);
+  float (*const Bs)[BN * PK] = reinterpret_cast<float (*)[BN * PK]>(lds_ab + 2 * BM * PK);
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
   const int wm = w >> 1, wn = w & 1;
   // a 1-D grid of tiles, a row block's column tiles consecutive
@@ -299,8 +301,10 @@ __global__ void __launch_bounds__(256) gemm_nt_kernel(int M, int N, int K, const
       __syncthreads();
     }
   }
-
-  epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  // through LDS (both slice buffers, done with), a pass per wave row
+  static_assert((BM / 2) * BN <= 2 * (BM + BN) * PK, "a wave row's results fit the slices' LDS");
+  if (!staged_epilogue<BM, BN, 2, 2, 2>(acc, &As[0][0], m0, n0, M, N, C, ldc, epi))
+    epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
 }
 
 // The same product with the fp32 matrix cores' work moved to the bf16 ones:
