@@ -57,6 +57,42 @@ class SplitWeights {
 
 inline DenseWeight plain_weight(const float* W, int N, int K, int64_t ldw) { return {W, ldw, nullptr, N, K}; }
 
+// An activation A [M, K] (ld lda, K a multiple of 32, at least 256) split once
+// into fp16 pair rows in device memory it owns: the A operand of dense_pairs,
+// which gives the bits of dense on A itself with W in the split form.
+class PairRows {
+ public:
+  PairRows(const float* A, int M, int K, int64_t lda, hipStream_t stream = nullptr) : m_(M), k_(K) {
+    if (hipMalloc(&p_, size_t(4) * M * K + size_t(4) * M + 16) != hipSuccess)
+      throw std::runtime_error("pet: PairRows: hipMalloc");
+    const int e = pet_linear_pair_rows(A, M, K, lda, p_, stream);
+    if (e) {
+      (void) hipFree(p_);
+      linear_check(e, "pet_linear_pair_rows");
+    }
+  }
+  PairRows(const PairRows&) = delete;
+  PairRows& operator=(const PairRows&) = delete;
+  ~PairRows() { (void) hipFree(p_); }
+  const void* data() const { return p_; }
+  int rows() const { return m_; }
+  int cols() const { return k_; }
+
+ private:
+  void* p_ = nullptr;
+  int m_, k_;
+};
+
+// dense() with A as pair rows; W must be split (SplitWeights::weight()).
+inline void dense_pairs(const PairRows& A, const DenseWeight& W, float* C, int64_t ldc, const float* row_scale,
+                        const float* bias, const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre,
+                        int act, hipStream_t stream) {
+  if (!W.split || W.cols != A.cols()) throw std::runtime_error("pet: dense_pairs: W split with A's K is needed");
+  linear_check(pet_linear_fused_pairs(A.rows(), W.rows, W.cols, A.data(), W.split, C, ldc, row_scale, bias, cin,
+                                      ldcin, beta, pre, ldpre, act, stream),
+               "pet_linear_fused_pairs");
+}
+
 // C = act(row_scale (A W^T) + bias + beta cin), pre = the value before act.
 inline void dense(int M, const float* A, int64_t lda, const DenseWeight& W, float* C, int64_t ldc,
                   const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta, float* pre,

@@ -171,6 +171,32 @@ int main(int argc, char** argv) {
       (void) hipFree(dA), (void) hipFree(dW), (void) hipFree(db), (void) hipFree(dC);
       if (worst <= 1e-5 * big) std::fclose(std::fopen((dir + "/linear.ok").c_str(), "wb"));
     }
+    {  // pair rows: dense_pairs gives dense's bits on the split weights (K >= 256)
+      const int M = 1000, Nw = 640, K = 256;
+      std::vector<float> A(size_t(M) * K), W(size_t(Nw) * K), b(Nw);
+      unsigned x = 777u;
+      auto rnd = [&x] { return (x = x * 1664525u + 1013904223u, float(int(x >> 9) - (1 << 22)) / float(1 << 22)); };
+      for (float& v : A) v = rnd();
+      for (float& v : W) v = rnd();
+      for (float& v : b) v = rnd();
+      float *dA, *dW, *db, *dC;
+      if (hipMalloc(&dA, A.size() * 4) || hipMalloc(&dW, W.size() * 4) || hipMalloc(&db, b.size() * 4) ||
+          hipMalloc(&dC, size_t(2) * M * Nw * 4))
+        fail("hipMalloc");
+      (void) hipMemcpy(dA, A.data(), A.size() * 4, hipMemcpyHostToDevice);
+      (void) hipMemcpy(dW, W.data(), W.size() * 4, hipMemcpyHostToDevice);
+      (void) hipMemcpy(db, b.data(), b.size() * 4, hipMemcpyHostToDevice);
+      const pet::SplitWeights ws(dW, Nw, K, K);
+      const pet::PairRows ap(dA, M, K, K);
+      float* dC2 = dC + size_t(M) * Nw;
+      pet::dense(M, dA, K, ws.weight(), dC, Nw, nullptr, db, nullptr, 0, 0.f, nullptr, 0, 1, nullptr);
+      pet::dense_pairs(ap, ws.weight(), dC2, Nw, nullptr, db, nullptr, 0, 0.f, nullptr, 0, 1, nullptr);
+      std::vector<float> C(size_t(2) * M * Nw);
+      (void) hipMemcpy(C.data(), dC, C.size() * 4, hipMemcpyDeviceToHost);
+      (void) hipFree(dA), (void) hipFree(dW), (void) hipFree(db), (void) hipFree(dC);
+      if (std::memcmp(C.data(), C.data() + size_t(M) * Nw, size_t(M) * Nw * 4) == 0)
+        std::fclose(std::fopen((dir + "/pairs.ok").c_str(), "wb"));
+    }
   } catch (const std::exception& e) {
     fail(e.what());
   }

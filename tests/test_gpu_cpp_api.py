@@ -154,3 +154,4 @@ def test_cpp_model_calculator(tmp_path, name):
     assert abs(fd - f0) <= 1e-2 + 1e-3 * abs(f0), (fd, f0)
     assert (tmp_path / "graph.ok").exists(), "Calculator(graph = true): a replayed step differed from an eager one"
     assert (tmp_path / "linear.ok").exists(), "pet::linear_fused (plain or split weights) missed the host product"
+    assert (tmp_path / "pairs.ok").exists(), "pet::dense_pairs missed the bits of pet::dense on split weights"
