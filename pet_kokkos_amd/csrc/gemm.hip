@@ -1147,18 +1147,23 @@ int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C
   if (M == 0 || N == 0) return PET_ATTN_OK;
   if ((reinterpret_cast<uintptr_t>(Ap) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15)) return PET_ATTN_EALIGN;
   if (int64_t((M + 63) / 64) * ((N + 63) / 64) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
-  // each shape's dynamic LDS above the 64 KB default, set once a process for
-  // every shape (on the device current then)
-  static std::once_flag once;
-  static hipError_t set_err = hipSuccess;
-  std::call_once(once, [] {
-    for (const PPShape& k : kPP) {
-      const hipError_t r = hipFuncSetAttribute(reinterpret_cast<const void*>(k.kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(k.lds()));
-      if (r != hipSuccess) set_err = r;
+  // each shape's dynamic LDS above the 64 KB default, set once a device (the
+  // attribute is the current device's) for every shape
+  static std::mutex mu;
+  static signed char set_on[64] = {};  // 0 not yet, 1 set, -1 failed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return PET_ATTN_ELAUNCH;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (set_on[dev] == 0) {
+      set_on[dev] = 1;
+      for (const PPShape& k : kPP)
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(k.kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(k.lds())) != hipSuccess)
+          set_on[dev] = -1;
     }
-  });
-  if (set_err != hipSuccess) return PET_ATTN_ELAUNCH;
+    if (set_on[dev] < 0) return PET_ATTN_ELAUNCH;
+  }
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
   const PPShape& k = kPP[N >= 128 && t128 >= 1024 ? 0 : N >= 64 ? 1 : 2];
   const int64_t tiles = int64_t((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
