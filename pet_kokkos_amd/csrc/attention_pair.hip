@@ -92,29 +92,34 @@ __device__ __forceinline__ u2 lds_tr16(const _Float16* p) {
   return __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
 }
 
-// Two scaled values as fp16 (hi, lo) registers: hi x rounded to 11
-// significant bits (to nearest, ties away from zero, on the fp32 bits: exact in
-// fp16's normal range; below it the conversion truncates further), lo the
-// remainder x - hi (exact in fp32, from the fp16 hi itself) rounded to the
-// nearest fp16: |x - hi - lo| <= 2^-23 |x|, or <= 2^-25 below fp16's normal
-// range (|x| < 2^15 here). The integer rounding also pins x to one rounded
-// fp32 value: a multiply fused into an fp16 conversion (fma_mix on the
-// unrounded product) could otherwise give hi and lo different x's.
-__device__ __forceinline__ void pair2x(float x, float y, unsigned& hi, unsigned& lo) {
-  const float hx = __uint_as_float((__float_as_uint(x) + 0x1000u) & 0xffffe000u);
-  const float hy = __uint_as_float((__float_as_uint(y) + 0x1000u) & 0xffffe000u);
-  const auto h = __builtin_amdgcn_cvt_pkrtz(hx, hy);
-  const pet_split::h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
+// An opaque 1.0 in a register (an empty asm, no instruction): fmaf(x, one, -h)
+// then cannot fold into a subtraction, so the remainder of a split is one
+// v_fma_mix reading the fp16 h directly, not a conversion back to fp32 and a
+// subtraction.
+__device__ __forceinline__ float opaque_one() {
+  float o = 1.f;
+  asm("" : "+v"(o));
+  return o;
+}
+// Two values as fp16 (hi, lo) registers, both to nearest: hi the fp16 nearest
+// x, lo the fp16 nearest x - hi (exact in fp32): |x - hi - lo| <= 2^-23 |x|,
+// or <= 2^-25 below fp16's normal range (|x| < 2^15 here). x and y are pinned
+// to registers first (an empty asm), so both parts come from one rounded fp32
+// value: a multiply fused into the fp16 conversion (fma_mix on the unrounded
+// product) could otherwise give hi and lo different x's. Three instructions
+// for two values: one packed conversion, two fma_mix.
+__device__ __forceinline__ void pair2x(float x, float y, float one, unsigned& hi, unsigned& lo) {
+  asm("" : "+v"(x), "+v"(y));
+  const pet_split::h2v h = {(_Float16)x, (_Float16)y};
+  const pet_split::h2v l = {(_Float16)fmaf(x, one, -float(h[0])), (_Float16)fmaf(y, one, -float(h[1]))};
   hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
 }
-
-// pair2x for values whose rounding to fp16 cannot be fused with an inexact
-// multiply (an exp's result scaled by ldexp, a product by a power of two):
-// hi the fp16 nearest x, lo the remainder from that hi. Same bounds.
-__device__ __forceinline__ void pair2n(float x, float y, unsigned& hi, unsigned& lo) {
-  const pet_split::h2v h = {(_Float16)x, (_Float16)y};
-  const pet_split::h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
+// pair2x of x s and y s for a power of two s (exact products): the remainder
+// x s - hi is formed from x and s by the fma_mix itself.
+__device__ __forceinline__ void pair2s(float x, float y, float s, unsigned& hi, unsigned& lo) {
+  const pet_split::h2v h = {(_Float16)(x * s), (_Float16)(y * s)};
+  const pet_split::h2v l = {(_Float16)fmaf(x, s, -float(h[0])), (_Float16)fmaf(y, s, -float(h[1]))};
   hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
 }
@@ -291,12 +296,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
       for (int j = 0; j < 4; ++j) {
         const int x = 8 * kc + 2 * j;
         unsigned h[4], lo[4];
-        // products by powers of two are exact: a conversion fused with them
-        // rounds the same value (pair2n)
-        pair2n(q[x] * sQ, q[x + 1] * sQ, h[0], lo[0]);
-        pair2n(go[x] * sG, go[x + 1] * sG, h[1], lo[1]);
-        pair2n(k[x] * sK, k[x + 1] * sK, h[2], lo[2]);
-        pair2n(v[x] * sV, v[x + 1] * sV, h[3], lo[3]);
+        pair2s(q[x], q[x + 1], sQ, h[0], lo[0]);
+        pair2s(go[x], go[x + 1], sG, h[1], lo[1]);
+        pair2s(k[x], k[x + 1], sK, h[2], lo[2]);
+        pair2s(v[x], v[x + 1], sV, h[3], lo[3]);
         qs[kc][0][j] = h[0], qs[kc][1][j] = lo[0], gs[kc][0][j] = h[1], gs[kc][1][j] = lo[1];
         kb[kc][0][j] = h[2], kb[kc][1][j] = lo[2], vb[kc][0][j] = h[3], vb[kc][1][j] = lo[3];
       }
@@ -326,6 +329,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
   for (int t = 0; t < DT; ++t) dq[t] = dk[t] = dv[t] = f4{0.f, 0.f, 0.f, 0.f};
   float cfa = 0.f;
   const int nb = at.nb;
+  const float one = opaque_one();
 
   // Phase 1 of step s: query block I = (w + s) mod nb against the own keys.
   auto phase1 = [&](int s) {
@@ -360,10 +364,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
       cfa += ds[r];
     }
     unsigned h[4], lo[4];
-    pair2x(pp[0], pp[1], h[0], lo[0]);
-    pair2x(pp[2], pp[3], h[1], lo[1]);
-    pair2x(ds[0], ds[1], h[2], lo[2]);
-    pair2x(ds[2], ds[3], h[3], lo[3]);
+    pair2x(pp[0], pp[1], one, h[0], lo[0]);
+    pair2x(pp[2], pp[3], one, h[1], lo[1]);
+    pair2x(ds[0], ds[1], one, h[2], lo[2]);
+    pair2x(ds[2], ds[3], one, h[3], lo[3]);
     const u2 ph = {h[0], h[1]}, pl = {lo[0], lo[1]}, sh = {h[2], h[3]}, sl = {lo[2], lo[3]};
     // dV^T += dO_I^T P and dK^T += Q_I^T dS: a operand rows 16t + c of the
     // planes, the block's queries 16I + 4g .. + 3
@@ -530,9 +534,9 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     for (int j = 0; j < 4; ++j) {
       const int x = 8 * kc + 2 * j;
       unsigned h[3], lo[3];
-      pair2n(q[x] * sQ, q[x + 1] * sQ, h[0], lo[0]);  // exact products (pair2n)
-      pair2n(k[x] * sK, k[x + 1] * sK, h[1], lo[1]);
-      pair2n(v[x] * sV, v[x + 1] * sV, h[2], lo[2]);
+      pair2s(q[x], q[x + 1], sQ, h[0], lo[0]);
+      pair2s(k[x], k[x + 1], sK, h[1], lo[1]);
+      pair2s(v[x], v[x + 1], sV, h[2], lo[2]);
       qb[kc][0][j] = h[0], qb[kc][1][j] = lo[0];
       if (active) {
 #pragma unroll
@@ -553,6 +557,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     return;
   }
   float mx = kFloor, sum = 0.f;
+  const float one = opaque_one();
   int kcur = kVw;
   f4 acc[DT];
 #pragma unroll
@@ -579,8 +584,8 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   // O^T += V_J^T P^T from the block's scaled weights p
   auto pv = [&](int J, const float* p) {
     unsigned h[2], lo[2];
-    pair2n(p[0], p[1], h[0], lo[0]);
-    pair2n(p[2], p[3], h[1], lo[1]);
+    pair2x(p[0], p[1], one, h[0], lo[0]);
+    pair2x(p[2], p[3], one, h[1], lo[1]);
     const u2 ph = {h[0], h[1]}, pl = {lo[0], lo[1]};
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
