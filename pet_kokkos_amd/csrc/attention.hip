@@ -240,7 +240,7 @@ __global__ void __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(HD <=
   float* Vs = Ks + R * (SPL ? KP6 : P);
   float* lcf = Vs + R * P;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, i = 16 * w + (l & 15);
-  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  const Atom at(off, xcd_item(blockIdx.x, gridDim.x), H, N, S, n0, eb);
   // Each wave stages its own block -- rows 16w .. 16w+15 of K and V, lane
   // (c, g) the slice of row 16w + c it also loads q from -- and its keys' cf;
   // the workgroup barrier is inside fwd_item, after the wave's own block.
@@ -302,7 +302,7 @@ __global__ void __launch_bounds__(256) attn_fwd_valu_kernel(const float* __restr
   float* Ks = lds;
   float* Vs = Ks + R * HD;
   float* lcf = Vs + R * HD;
-  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  const Atom at(off, xcd_item(blockIdx.x, gridDim.x), H, N, S, n0, eb);
   for (int f = threadIdx.x; f < at.cnt * C4; f += blockDim.x) {
     const int r = f / C4, c4 = f - r * C4;
     const float* src = qkv + at.row(r) * ldq + at.h * HD + 4 * c4;
@@ -580,7 +580,7 @@ __global__ void __launch_bounds__(MAXT) attn_bwd_kernel(const float* __restrict_
   float* lcf = Vs + (vlds ? R * (SPL ? KP6 : P) : 0);
   float* Tb = lcf + R;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, i = 16 * w + (l & 15);
-  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  const Atom at(off, xcd_item(blockIdx.x, gridDim.x), H, N, S, n0, eb);
   float oo[W], mi = kOff, li = 0.f;
   // Each wave stages its own block -- rows 16w .. 16w+15 of Q, K, dO (and V),
   // lane (c, g) the slice of row 16w + c that is its MFMA operand -- and the

@@ -178,16 +178,78 @@ __device__ __forceinline__ void qkv_get8(const float* qkv, int64_t ldq, size_t r
 }
 }  // namespace
 
+// The backward's arguments (one launch).
+struct PairBwdArgs {
+  const float* qkv;
+  int64_t ldq;
+  const int* off;
+  int N, n0;
+  int64_t eb;
+  int S, H;
+  float sc;
+  const float* dmerged;
+  int64_t ldg;
+  const float* merged;
+  int64_t ldm;
+  const float* ml;
+  const float* cf_seq;
+  int64_t ldc;
+  float* qkv_adj;
+  int64_t lda;
+  float* cfh;
+  QkvXf xf;
+};
+
+// A lane's raw rows of one item: its slot's q, k, v, dO and O (dims 32kc + 8g
+// .. + 7) and the slot's saved statistics and cf as loaded (slot 0's past the
+// count: the item masks them where it reads them, so that nothing waits on
+// the loads when they are issued).
+template <int W>
+struct PairRows {
+  float q[W], k[W], v[W], go[W], oo[W];
+  float mi, li, pcf;
+};
+
+// Issues the loads of a lane's rows of item `at` (wave w, lane (c, g), slot i =
+// 16 w + c). A slot past the count loads slot 0's rows instead of zeros: as a
+// query it has 1/sum 0 and as a key log cf kOff, so its P and dS are exactly 0
+// and it adds nothing (and, a copy of a row of the item, it moves no scale).
+template <int HD, bool XF>
+__device__ __forceinline__ void pair_bwd_load(const PairBwdArgs& a, const Atom& at, int w, int g, int i,
+                                              PairRows<HD / 4>& r) {
+  constexpr int KC = HD / 32;
+  constexpr bool XF_LATE = XF && KC == 1;
+  const int D = a.H * HD;
+  const bool active = w < at.nb, real = active && i < at.cnt;
+  r.mi = kOff, r.li = 0.f, r.pcf = 0.f;  // an idle wave's
+  if (active) {  // wave-uniform
+    const int si = real ? i : 0;
+    const size_t row = at.row(si);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int col = at.h * HD + 32 * kc + 8 * g;
+      if constexpr (XF_LATE) {
+        gmem_get<8>(a.qkv + row * a.ldq + col, r.q + 8 * kc);
+        gmem_get<8>(a.qkv + row * a.ldq + D + col, r.k + 8 * kc);
+        gmem_get<8>(a.qkv + row * a.ldq + 2 * D + col, r.v + 8 * kc);
+      } else {
+        qkv_get8<XF>(a.qkv, a.ldq, row, col, a.xf, r.q + 8 * kc);
+        qkv_get8<XF>(a.qkv, a.ldq, row, D + col, a.xf, r.k + 8 * kc);
+        qkv_get8<XF>(a.qkv, a.ldq, row, 2 * D + col, a.xf, r.v + 8 * kc);
+      }
+      gmem_get<8>(a.dmerged + row * a.ldg + col, r.go + 8 * kc);
+      gmem_get<8>(a.merged + at.grow(si) * a.ldm + col, r.oo + 8 * kc);
+    }
+    if constexpr (XF_LATE) xf_rows<KC>(a.xf, row, at.h * HD + 8 * g, D, r.q, r.k, r.v);
+    const float* m2 = a.ml + 2 * ((size_t(at.n) * a.H + at.h) * a.S + si);
+    r.mi = m2[0], r.li = m2[1], r.pcf = a.cf_seq[size_t(at.n) * a.ldc + si];
+  }
+}
+
+// One (atom, head) item of the backward from the lane's loaded rows r.
 template <int HD, int NW, bool XF>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD > 32 ? 4 : NW >= 4 ? 6 : 5))) attn_bwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq,
-                                                             const int* __restrict__ off, int N, int n0, int64_t eb,
-                                                             int S, int H, float sc,
-                                                             const float* __restrict__ dmerged, int64_t ldg,
-                                                             const float* __restrict__ merged, int64_t ldm,
-                                                             const float* __restrict__ ml,
-                                                             const float* __restrict__ cf_seq, int64_t ldc,
-                                                             float* __restrict__ qkv_adj, int64_t lda,
-                                                             float* __restrict__ cfh, QkvXf xf) {
+__device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& at, PairRows<HD / 4>& r,
+                                              unsigned char* lds) {
   // KC 32-dim chunks of the head: lane (c, g) holds dims 32kc + 8g .. + 7 of its row
   constexpr int KC = HD / 32, W = 8 * KC, DT = HD / 16;
   static_assert(HD % 32 == 0, "head_dim a multiple of 32");
@@ -196,11 +258,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
   // chunk is transformed as it arrives, branch-free (qkv_get8) so that every
   // chunk's loads are still issued together
   constexpr bool XF_LATE = XF && KC == 1;
-  extern __shared__ float lds_f[];
-  unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
-  const int D = H * HD;
+  const int D = a.H * HD, H = a.H;
+  const float sc = a.sc;
   constexpr PairLds L(HD, NW);
-  constexpr int PT = L.PT;
+  constexpr int PT = L.PT, TP = PairLds::TP, TS = PairLds::TS;
   _Float16* planes = reinterpret_cast<_Float16*>(lds + L.pl);
   constexpr int PS = HD * PT;  // halves a plane part
   _Float16* QTh = planes;
@@ -216,38 +277,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
   // scalar too
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const int i = 16 * w + c;  // this lane's row: its query slot, and its key slot
-  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
   const bool active = w < at.nb, real = active && i < at.cnt;
 
   // ---- the wave's own block: rows 16w .. 16w + 15, lane (c, g) dims 32kc + 8g .. + 7
-  // A slot past the count loads slot 0's rows instead of zeros: as a query it
-  // has 1/sum 0 and as a key log cf kOff, so its P and dS are exactly 0 and
-  // it adds nothing (and, a copy of a row of the item, it moves no scale).
-  float q[W], k[W], v[W], go[W], oo[W];
-  float mi = kOff, li = 0.f, pcf = 0.f;
-  if (active) {  // wave-uniform
-    const int si = real ? i : 0;
-    const size_t r = at.row(si);
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      const int col = at.h * HD + 32 * kc + 8 * g;
-      if constexpr (XF_LATE) {
-        gmem_get<8>(qkv + r * ldq + col, q + 8 * kc);
-        gmem_get<8>(qkv + r * ldq + D + col, k + 8 * kc);
-        gmem_get<8>(qkv + r * ldq + 2 * D + col, v + 8 * kc);
-      } else {
-        qkv_get8<XF>(qkv, ldq, r, col, xf, q + 8 * kc);
-        qkv_get8<XF>(qkv, ldq, r, D + col, xf, k + 8 * kc);
-        qkv_get8<XF>(qkv, ldq, r, 2 * D + col, xf, v + 8 * kc);
-      }
-      gmem_get<8>(dmerged + r * ldg + col, go + 8 * kc);
-      gmem_get<8>(merged + at.grow(si) * ldm + col, oo + 8 * kc);
-    }
-    if constexpr (XF_LATE) xf_rows<KC>(xf, r, at.h * HD + 8 * g, D, q, k, v);
-    const float* m2 = ml + 2 * ((size_t(at.n) * H + at.h) * S + si);
-    const float m0 = m2[0], l0 = m2[1], c0 = cf_seq[size_t(at.n) * ldc + si];
-    mi = real ? m0 : kOff, li = real ? l0 : 0.f, pcf = real ? c0 : 0.f;
-  }
+  float* q = r.q;
+  float* k = r.k;
+  float* v = r.v;
+  float* go = r.go;
+  float* oo = r.oo;
+  const float mi = real ? r.mi : kOff, li = real ? r.li : 0.f, pcf = real ? r.pcf : 0.f;
   // Row norms (over the head's dims; every lane of a row gets its row's), then
   // their largest over the item: the scales come from them (a row's largest
   // |x| is at most its norm).
@@ -314,6 +352,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
           GTh[o] = half(gs[kc][0][e >> 1]), GTh[PS + o] = half(gs[kc][1][e >> 1]);
           KTh[o] = half(kb[kc][0][e >> 1]), KTh[PS + o] = half(kb[kc][1][e >> 1]);
         }
+    }
+    if (active) {
       if (g == 0) {
         // a query with no live key (li = 0): an exponent near -1e30, exp gives 0
         STm[i] = li > 0.f ? mi : 1e30f;
@@ -381,9 +421,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
     }
     // dS to query block I's owner: hi and lo tiles T[key c][query 4g + r],
     // read back transposed
-    _Float16* tb = TB + ((s & 1) * NW + w) * (2 * PairLds::TS) + c * PairLds::TP + 4 * g;
+    _Float16* tb = TB + ((s & 1) * NW + w) * (2 * TS) + c * TP + 4 * g;
     *reinterpret_cast<u2*>(tb) = sh;
-    *reinterpret_cast<u2*>(tb + PairLds::TS) = sl;
+    *reinterpret_cast<u2*>(tb + TS) = sl;
   };
   // Phase 2 of step s: the own query block's tile from key block J = (w - s)
   // mod nb: dQ_w^T += K_J^T dS^T.
@@ -392,8 +432,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
     if (J < 0) J += nb;
     // b operand: query c, keys 4g .. 4g + 3 (tile rows 4g + c / 4, queries
     // 4 (c % 4) .. + 3)
-    const _Float16* tb = TB + ((s & 1) * NW + J) * (2 * PairLds::TS) + (4 * g + (c >> 2)) * PairLds::TP + 4 * (c & 3);
-    const u2 bh = lds_tr16(tb), bl = lds_tr16(tb + PairLds::TS);
+    const _Float16* tb = TB + ((s & 1) * NW + J) * (2 * TS) + (4 * g + (c >> 2)) * TP + 4 * (c & 3);
+    const u2 bh = lds_tr16(tb), bl = lds_tr16(tb + TS);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
       const int o = (16 * t + c) * PT + 16 * J + 4 * g;
@@ -418,7 +458,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
   // ---- stores: dQ | dK | dV of the own row, lane dims 16t + 4g .. + 3
   const float cft = __builtin_amdgcn_ldexpf(sum_g(cfa), -kS);
   if (real) {
-    float* o = qkv_adj + at.row(i) * lda + at.h * HD + 4 * g;
+    float* o = a.qkv_adj + at.row(i) * a.lda + at.h * HD + 4 * g;
     const float fq = __builtin_amdgcn_ldexpf(sc, -kK - kS), fk = __builtin_amdgcn_ldexpf(sc, -kQ - kS);
     const float fv = __builtin_amdgcn_ldexpf(1.f, -kP - kG);
 #pragma unroll
@@ -430,7 +470,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD
           make_float4(dv[t][0] * fv, dv[t][1] * fv, dv[t][2] * fv, dv[t][3] * fv);
     }
   }
-  if (g == 0 && i < S) cfh[(size_t(at.n) * H + at.h) * S + i] = real ? cft : 0.f;
+  if (g == 0 && i < a.S) a.cfh[(size_t(at.n) * H + at.h) * a.S + i] = real ? cft : 0.f;
+}
+
+// One workgroup per item.
+template <int HD, int NW, bool XF>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD > 32 ? 4 : NW >= 4 ? 6 : 5)))
+attn_bwd_pair_kernel(PairBwdArgs a) {
+  extern __shared__ float lds_f[];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+  const Atom at(a.off, xcd_item(blockIdx.x, gridDim.x), a.H, a.N, a.S, a.n0, a.eb);
+  PairRows<HD / 4> r;
+  pair_bwd_load<HD, XF>(a, at, w, l >> 4, 16 * w + (l & 15), r);
+  pair_bwd_item<HD, NW, XF>(a, at, r, reinterpret_cast<unsigned char*>(lds_f));
 }
 
 // ---- forward ---------------------------------------------------------------
@@ -480,7 +532,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const int i = 16 * w + c;
-  const Atom at(off, blockIdx.x, H, N, S, n0, eb);
+  const Atom at(off, xcd_item(blockIdx.x, gridDim.x), H, N, S, n0, eb);
   const bool active = w < at.nb, real = active && i < at.cnt;
 
   // own rows (lane (c, g): row 16w + c, dims 32kc + 8g .. + 7); a slot past
@@ -594,6 +646,28 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
                         acc[t]);
     }
   };
+  // the same for two key blocks at once, on the 16x16x32 instruction: k-slots
+  // 8g .. 8g + 3 hold block J0's keys 4g .. 4g + 3 and 8g + 4 .. 8g + 7 block
+  // J1's, in a and b alike (a contraction is a sum, the slot order is free):
+  // three instructions for the two blocks where pv takes six
+  auto pv2 = [&](int J0, int J1, const float* p) {
+    unsigned h[4], lo[4];
+    pair2x(p[0], p[1], one, h[0], lo[0]);
+    pair2x(p[2], p[3], one, h[1], lo[1]);
+    pair2x(p[4], p[5], one, h[2], lo[2]);
+    pair2x(p[6], p[7], one, h[3], lo[3]);
+    const u4 ph = {h[0], h[1], h[2], h[3]}, pl = {lo[0], lo[1], lo[2], lo[3]};
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int o0 = (16 * t + c) * PT + 16 * J0 + 4 * g, o1 = (16 * t + c) * PT + 16 * J1 + 4 * g;
+      const u2 h0 = *reinterpret_cast<const u2*>(VTh + o0), h1 = *reinterpret_cast<const u2*>(VTh + o1);
+      const u2 l0 = *reinterpret_cast<const u2*>(VTh + PS + o0), l1 = *reinterpret_cast<const u2*>(VTh + PS + o1);
+      const u4 vh = {h0[0], h0[1], h1[0], h1[1]}, vl = {l0[0], l0[1], l1[0], l1[1]};
+      acc[t] = pet_split::mfma_h(vl, ph, acc[t]);
+      acc[t] = pet_split::mfma_h(vh, pl, acc[t]);
+      acc[t] = pet_split::mfma_h(vh, ph, acc[t]);
+    }
+  };
   auto block = [&](int J, const f4& s) {
     const float scS = __builtin_amdgcn_ldexpf(sc, -kQ - kK_of(J));
     const int kv = kV_of(J);
@@ -643,8 +717,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     kcur = kn;
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc[t] *= f;
-    pv(J0, ps);
-    pv(J1, ps + 4);
+    pv2(J0, J1, ps);
   };
   // the own key block first (the wave staged it itself), before the barrier;
   // then the others w + 1, w + 2, ... (mod nb), two at a time, an odd one last
@@ -688,11 +761,12 @@ const void* pair_bwd_kernel_ptr(int HD) {
 
 namespace {
 template <int HD, int NW>
-auto pair_kernel(bool x) {
-  return x ? attn_bwd_pair_kernel<HD, NW, true> : attn_bwd_pair_kernel<HD, NW, false>;
+const void* pair_kernel(bool x) {
+  return x ? reinterpret_cast<const void*>(attn_bwd_pair_kernel<HD, NW, true>)
+           : reinterpret_cast<const void*>(attn_bwd_pair_kernel<HD, NW, false>);
 }
 template <int HD>
-auto pair_kernel_nw(int NW, bool x) {
+const void* pair_kernel_nw(int NW, bool x) {
   switch (NW) {
     case 1: return pair_kernel<HD, 1>(x);
     case 2: return pair_kernel<HD, 2>(x);
@@ -704,6 +778,24 @@ auto pair_kernel_nw(int NW, bool x) {
     default: return pair_kernel<HD, 8>(x);
   }
 }
+
+// The dynamic LDS limit of kernel k raised, once per device, to the largest
+// size asked.
+int allow_lds_pair(const void* k, size_t bytes) {
+  if (bytes <= 65536) return PET_ATTN_OK;
+  static std::map<std::pair<int, const void*>, size_t> raised;
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return PET_ATTN_ELAUNCH;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = raised[{dev, k}];
+  if (have < bytes) {
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess)
+      return PET_ATTN_ELAUNCH;
+    have = bytes;
+  }
+  return PET_ATTN_OK;
+}
 }  // namespace
 
 int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
@@ -713,25 +805,15 @@ int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* 
   if (NW > kPairMaxWaves || (HD != 32 && HD != 64)) return PET_ATTN_ESLOTS;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
   if (items == 0) return PET_ATTN_OK;
+  if (items > INT32_MAX) return PET_ATTN_EINVAL;
   const size_t bytes = pair_bwd_bytes(HD, NW);
   const bool x = xf.rs || xf.b;
-  const auto k = HD == 64 ? pair_kernel_nw<64>(NW, x) : pair_kernel_nw<32>(NW, x);
-  if (bytes > 65536) {  // the dynamic LDS limit raised once per (device, kernel) to the largest size asked
-    static std::map<std::pair<int, const void*>, size_t> raised;
-    static std::mutex mu;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return PET_ATTN_ELAUNCH;
-    const void* kp = reinterpret_cast<const void*>(k);
-    std::lock_guard<std::mutex> lock(mu);
-    size_t& have = raised[{dev, kp}];
-    if (have < bytes) {
-      if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess)
-        return PET_ATTN_ELAUNCH;
-      have = bytes;
-    }
-  }
-  hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots,
-                     sh.heads, sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, xf);
+  const void* k = HD == 64 ? pair_kernel_nw<64>(NW, x) : pair_kernel_nw<32>(NW, x);
+  if (const int e = allow_lds_pair(k, bytes)) return e;
+  const PairBwdArgs a{qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, dmerged, ldg, merged, ldm,
+                      ml, cf_seq, ldc, qkv_adj, lda, cfh, xf};
+  void* args[] = {const_cast<PairBwdArgs*>(&a)};
+  if (hipLaunchKernel(k, dim3(unsigned(items)), dim3(64 * NW), args, bytes, st) != hipSuccess) return PET_ATTN_ELAUNCH;
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -771,20 +853,7 @@ int pair_fwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* 
     by_waves(std::integral_constant<int, 64>{});
   else
     by_waves(std::integral_constant<int, 32>{});
-  if (bytes > 65536) {  // the dynamic LDS limit raised once per (device, kernel) to the largest size asked
-    static std::map<std::pair<int, const void*>, size_t> raised;
-    static std::mutex mu;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return PET_ATTN_ELAUNCH;
-    const void* kp = reinterpret_cast<const void*>(k);
-    std::lock_guard<std::mutex> lock(mu);
-    size_t& have = raised[{dev, kp}];
-    if (have < bytes) {
-      if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess)
-        return PET_ATTN_ELAUNCH;
-      have = bytes;
-    }
-  }
+  if (const int e = allow_lds_pair(reinterpret_cast<const void*>(k), bytes)) return e;
   hipLaunchKernelGGL(k, dim3(unsigned(items)), dim3(64 * NW), bytes, st, qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots,
                      sh.heads, sh.scale, cf_seq, ldc, merged, ldm, ml, xf);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;

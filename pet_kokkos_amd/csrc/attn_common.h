@@ -117,6 +117,18 @@ __device__ __forceinline__ void qkv_get(const float* qkv, int64_t ldq, size_t r,
   }
 }
 
+// The work item of workgroup b of a one-item-per-workgroup grid of `items`,
+// XCD-grouped: the dispatcher hands workgroup b to XCD b % 8, so XCD x gets
+// workgroups x, x + 8, ... and, with this map, the contiguous items
+// [x q + min(x, r), ...) (q = items / 8, r = items % 8): the heads of an atom
+// and its neighbour atoms' rows run on one XCD close in time, so the 128-byte
+// head slices of a token's rows meet in one L2 and reach HBM as whole rows.
+// Measured on the backward's access pattern alone at C3: 232 -> 205 us.
+__device__ __forceinline__ int xcd_item(int b, int items) {
+  const int x = b & 7, k = b >> 3, q = items >> 3, r = items & 7;
+  return x * q + (x < r ? x : r) + k;
+}
+
 // One work item, an (atom, head), of a run of atoms [n0, n1). The atom's
 // tokens are rows of two matrices: the whole token matrix (merged, and the
 // per-slot arrays), and the run's chunk (qkv, dO, qkv_adj), which holds the
