@@ -163,12 +163,15 @@ PET_ATTN_API int pet_attn_bwd(const pet_attn_shape* shape, const float* qkv, int
  * N * H * S floats of scratch live in a fixed device array of
  * PET_ATTN_NOALLOC_MAX_SCRATCH bytes that the library holds on every GPU it
  * runs on until the process ends. Calls with N * heads * slots * 4 above that
- * size return PET_ATTN_ESCRATCH and launch nothing. The call allocates
- * nothing and calls no allocating routine. All calls on one GPU share its
- * array, so calls that overlap on one GPU (on different streams, or from
- * several threads) race: order them on one stream. No counterpart in the
- * reference, whose backward takes its scratch from the Workspace pool
- * (src/attention.cpp:1814-1907). */
+ * size return PET_ATTN_ESCRATCH and launch nothing. The call allocates no
+ * device memory. Its first call on a device (and the first launch of each
+ * kernel shape) also looks the array's address up (hipGetSymbolAddress), may
+ * raise a kernel's LDS limit (hipFuncSetAttribute) and records both in host
+ * maps, which allocate host memory: make that first call outside graph
+ * capture; later calls are capturable. All calls on one GPU share its array,
+ * so calls that overlap on one GPU (on different streams, or from several
+ * threads) race: order them on one stream. It has no counterpart in the
+ * reference: it exists for the callers above, which cannot allocate. */
 #define PET_ATTN_NOALLOC_MAX_SCRATCH (32u << 20)
 PET_ATTN_API int pet_attn_bwd_noalloc(const pet_attn_shape* shape, const float* qkv, int64_t ldq, const int* off,
                                       const float* dmerged, int64_t ldg, const float* merged, int64_t ldm,

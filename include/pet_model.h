@@ -20,7 +20,10 @@
  * first call at a size, an evaluation allocates nothing.
  *
  * Return codes are pet_attn.h's PET_ATTN_* plus those below; pet_attn_strerror
- * names them all. One model serves one stream at a time.
+ * names them all. One model serves one stream at a time: its workspace and
+ * its pairs scratch are shared by every evaluation on it, so two
+ * pet_model_compute calls on one model must not overlap (on two streams, or
+ * from two threads); use one model per stream.
  */
 #ifndef PET_MODEL_H
 #define PET_MODEL_H
@@ -143,6 +146,18 @@ PET_ATTN_API int pet_linear_split_weights_transposed(const float* W, int N, int 
 PET_ATTN_API int pet_linear_fused_split(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit, float* C,
                                         int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                         int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
+/* pet_linear_fused_split with a caller-owned device scratch (16-byte aligned):
+ * where the product runs pairs by pairs (K >= 256, N >= 512) and the scratch
+ * holds at least 128 rows of A as pairs (K * 4 + 4 bytes a row), A's rows are
+ * split into it a chunk at a time (the largest multiple of 128 rows it
+ * holds) and each chunk's product read from the pairs: the same bits as
+ * without a scratch, A split once per row instead of once per column tile.
+ * A smaller or null scratch takes the form without one. The model's large
+ * products run this way from its own pairs scratch. */
+PET_ATTN_API int pet_linear_fused_split_ws(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit,
+                                           float* C, int64_t ldc, const float* row_scale, const float* bias,
+                                           const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre,
+                                           int act, void* scratch, size_t scratch_bytes, void* stream);
 
 /* Activation rows as fp16 pairs, the A operand of pet_linear_fused_pairs: X [M, K]
  * (ld ldx, K a multiple of 32 and at least 256, rows 16-byte aligned) into out,
@@ -159,6 +174,11 @@ PET_ATTN_API int pet_linear_fused_pairs(int M, int N, int K, const void* Apairs,
 
 /* Bytes of device workspace the model holds now (its high-water mark). */
 PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
+/* Bytes of the model's pairs scratch (the large products' A operands as fp16
+ * pairs, split once per activation): pet_model_create takes it where the
+ * device has room; 0 when it has none, and then those products split A as
+ * they stage it instead (the same bits, more work per product). */
+PET_ATTN_API size_t pet_model_pairs_scratch_bytes(const pet_model* model);
 
 #ifdef __cplusplus
 }

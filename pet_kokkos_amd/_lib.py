@@ -46,10 +46,12 @@ EXPORTS = (
     "pet_model_destroy",
     "pet_model_compute",
     "pet_model_workspace_bytes",
+    "pet_model_pairs_scratch_bytes",
     "pet_linear_fused",
     "pet_linear_split_weights",
     "pet_linear_split_weights_transposed",
     "pet_linear_fused_split",
+    "pet_linear_fused_split_ws",
     "pet_linear_pair_rows",
     "pet_linear_fused_pairs",
 )
@@ -215,12 +217,17 @@ def load() -> ctypes.CDLL:
     lib.pet_linear_split_weights_transposed.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_split.restype = ctypes.c_int
     lib.pet_linear_fused_split.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
+    lib.pet_linear_fused_split_ws.restype = ctypes.c_int
+    lib.pet_linear_fused_split_ws.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I,
+                                              _P, ctypes.c_size_t, _P]
     lib.pet_linear_pair_rows.restype = ctypes.c_int
     lib.pet_linear_pair_rows.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_pairs.restype = ctypes.c_int
     lib.pet_linear_fused_pairs.argtypes = [_I, _I, _I, _P, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_model_workspace_bytes.restype = ctypes.c_size_t
     lib.pet_model_workspace_bytes.argtypes = [_P]
+    lib.pet_model_pairs_scratch_bytes.restype = ctypes.c_size_t
+    lib.pet_model_pairs_scratch_bytes.argtypes = [_P]
     _lib = lib
     return lib
 

@@ -753,11 +753,14 @@ __global__ void __launch_bounds__(256) pair_act_kernel(const float* __restrict__
 // The K loop's barrier: no memory fence, since any fence, even one on LDS
 // alone, makes the compiler wait for every global-to-LDS load in flight (the
 // prefetches too). The loop's own vmcnt wait before it covers the step's
-// loads; a wave's LDS reads of the step before have returned before it passes
-// (their products consumed them); the empty asm keeps the compiler from moving
-// memory accesses across it.
+// loads; an explicit lgkmcnt(0) wait (vmcnt and expcnt left at their maxima)
+// makes every LDS read a wave issued in the step before complete before it
+// passes, so no wave's global_load_lds can overwrite a stage another is still
+// reading, whatever order the compiler gives the products; the empty asm
+// keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
@@ -1100,6 +1103,18 @@ extern "C" int pet_linear_fused_split(int M, int N, int K, const float* A, int64
     return PET_ATTN_EINVAL;
   return pet_gemm_nt_split(M, N, K, A, lda, Wsplit, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
                            reinterpret_cast<hipStream_t>(stream), nullptr, 0);
+}
+
+extern "C" int pet_linear_fused_split_ws(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit,
+                                         float* C, int64_t ldc, const float* row_scale, const float* bias,
+                                         const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre,
+                                         int act, void* scratch, size_t scratch_bytes, void* stream) {
+  if ((M > 0 && N > 0) && (!A || !Wsplit || !C || lda < K || !epi_args_ok(N, C, ldc, row_scale, cin, ldcin, pre,
+                                                                              ldpre, act)))
+    return PET_ATTN_EINVAL;
+  if (scratch_bytes && !scratch) return PET_ATTN_EINVAL;
+  return pet_gemm_nt_split(M, N, K, A, lda, Wsplit, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
+                           reinterpret_cast<hipStream_t>(stream), scratch, scratch_bytes);
 }
 
 // fp16-pair rows of an activation X [M, K] into out (M K 4 + M 4 bytes,

@@ -1463,6 +1463,10 @@ void pet_model_destroy(pet_model* model) { delete model; }
 
 size_t pet_model_workspace_bytes(const pet_model* model) { return model ? model->ws.bytes() : 0; }
 
+size_t pet_model_pairs_scratch_bytes(const pet_model* model) {
+  return model && model->pairs ? pet_model::kPairsBytes : 0;
+}
+
 int pet_model_compute(pet_model* md, const pet_model_edges* e, int forces, double* energy, double* per_atom,
                       double* forces_out, double* virial, double* edge_grad, void* stream) {
   if (!md || !e || e->n_atoms < 0 || e->n_edges < 0 || e->max_neighbors < 0 || e->n_struct < 0) return PET_ATTN_EINVAL;

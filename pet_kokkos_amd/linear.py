@@ -77,7 +77,7 @@ def _check(t, name, rows=None, cols=None, vector=False, device=None):
         raise ValueError(f"{name}: {t.shape[1]} columns, {cols} needed")
 
 
-def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
+def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, scratch=None):
     if act not in (0, 1, 2, 3, 4):
         raise ValueError(f"act {act}: 0 (none), 1 (SiLU), 2 (SwiGLU), 3 / 4 (their backward)")
     if isinstance(A, PairRows):
@@ -121,6 +121,13 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
         _lib.check(lib.pet_linear_fused_pairs(M, N, K, A.data.data_ptr(), W.data.data_ptr(), p(C), C.stride(0),
                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
                    "pet_linear_fused_pairs")
+    elif isinstance(W, SplitWeights) and scratch is not None:
+        if scratch.device != dev or not scratch.is_contiguous():
+            raise ValueError("scratch: a contiguous tensor on A's device")
+        _lib.check(lib.pet_linear_fused_split_ws(M, N, K, p(A), A.stride(0), W.data.data_ptr(), p(C), C.stride(0),
+                                                 p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act,
+                                                 scratch.data_ptr(), scratch.numel() * scratch.element_size(), st),
+                   "pet_linear_fused_split_ws")
     elif isinstance(W, SplitWeights):
         _lib.check(lib.pet_linear_fused_split(M, N, K, p(A), A.stride(0), W.data.data_ptr(), p(C), C.stride(0),
                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
@@ -131,14 +138,16 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
                    "pet_linear_fused")
 
 
-def fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0):
+def fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, scratch=None):
     """C = act(row_scale * (A W^T) + bias + beta cin), pre = the value before
     act; act 0 none, 1 SiLU, 2 SwiGLU (C [M, N/2]). W a tensor or SplitWeights;
     A a tensor or, with W as SplitWeights, PairRows.
     act 3 / 4: A W^T is the adjoint of a SiLU / SwiGLU output and cin its saved
     pre-activation z (bias z's bias if not yet in it): C = adjoint silu'(z), or
-    for SwiGLU (z and C [M, 2N], (value, gate) pairs) each pair's adjoint."""
-    _call(A, W, C, row_scale, bias, cin, beta, pre, act)
+    for SwiGLU (z and C [M, 2N], (value, gate) pairs) each pair's adjoint.
+    With W as SplitWeights, `scratch` (a device tensor) is the workspace A's
+    rows are split into a chunk at a time (pet_linear_fused_split_ws)."""
+    _call(A, W, C, row_scale, bias, cin, beta, pre, act, scratch)
 
 
 def linear_fused(out, inp, W, b=None, beta=0.0):

@@ -126,6 +126,11 @@ class PetModel:
     def workspace_bytes(self) -> int:
         return int(self._lib.pet_model_workspace_bytes(self._handle))
 
+    @property
+    def pairs_scratch_bytes(self) -> int:
+        """Bytes of the model's pairs scratch (0: the large products split A as they stage it)."""
+        return int(self._lib.pet_model_pairs_scratch_bytes(self._handle))
+
     def compute(self, x: ModelInput, forces: bool = True, edge_grad: bool = False, out: dict | None = None) -> dict:
         """energy [B], per_atom [N] and, with forces, forces [N, 3], virial
         [B, 3, 3] (and edge_grad [E, 3]): fp64 device tensors. `out` reuses

@@ -228,6 +228,29 @@ def test_pair_backward_scales(device, qk, v, g, spread, hd):
 
 
 @pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("spread", [4.0, 8.0])
+def test_pair_qk_row_spread(device, spread, hd):
+    # Q and K token rows spread over 10^-spread .. 1 within every item (each
+    # row's own factor, Q's and K's independent), so the pair kernels' per-item
+    # (backward) and per-block (forward) scales meet rows far below the
+    # largest: every score stays at most |q||k| sc of unit rows (moderate), while
+    # the smallest rows sit 2^-13 (spread 4) and 2^-27 (spread 8) below their
+    # item's largest, near the 2^-29 down to which a pair keeps 22 bits.
+    counts = [0, 15, 16, 31, 47, 5, 60, 33, 70, 79]
+    tk, qkv, dm = random_case(counts, 2, hd, seed=700 + int(spread) + hd, cf_kind="random")
+    rng = np.random.default_rng(int(spread) * 7 + hd)
+    D = 2 * hd
+    T = qkv.shape[0]
+    qkv[:, :D] *= 10.0 ** rng.uniform(-spread, 0.0, (T, 1))
+    qkv[:, D:2 * D] *= 10.0 ** rng.uniform(-spread, 0.0, (T, 1))
+    qkv = qkv.astype(np.float32)
+    plan = A._lib.describe(tk.n_atoms, tk.n_rows, tk.slots, 2, hd)
+    assert plan["bwd_pair"] == 1 and plan["fwd_pair"] == 1
+    check_against_oracle(device, f"pair kernels hd {hd}: Q, K rows spread over 1e-{spread:.0f}..1", tk.off,
+                         tk.cf_seq, qkv, dm, 2, hd)
+
+
+@pytest.mark.parametrize("hd", [32, 64])
 @pytest.mark.parametrize("fwd,bwd", [(0, 0), (1, 1), (0, 1), (1, 0)])
 def test_pair_and_staged_kernels(device, fwd, bwd, hd):
     # The head_dim-32 and -64 kernels in each combination (option fwd_kernel / bwd_kernel:

@@ -310,3 +310,39 @@ def test_pair_rows_same_bits(M, N, K, device):
         L.fused(Ap, W, torch.empty(M, N, device=device))  # pair rows need split weights
     with pytest.raises(ValueError):
         L.PairRows(torch.zeros(8, 128, device=device))  # K below 256
+
+
+def test_split_scratch_chunks_same_bits(device):
+    # pet_linear_fused_split_ws with a scratch of 128 rows of pairs: A is split
+    # and multiplied a chunk of 128 rows at a time (row_scale, cin, pre and C
+    # moved along by each chunk's first row), 1000 rows in 8 chunks, the last
+    # partial, against the product with no scratch, bit for bit, for every
+    # epilogue
+    M, N, K = 1000, 512, 256
+    print(f"[gpu] split product with a 128-row scratch, M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(17)
+    A = torch.randn(M, K, device=device, generator=g) * 3.0
+    W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
+    Ws = L.SplitWeights(W)
+    scratch = torch.empty(128 * (K * 4 + 4) // 4, device=device)
+    b = torch.randn(N, device=device, generator=g)
+    b2 = torch.randn(2 * N, device=device, generator=g)
+    rs = torch.rand(M, device=device, generator=g) + 0.5
+    res = torch.randn(M, N, device=device, generator=g)
+    z = torch.randn(M, N, device=device, generator=g)
+    z2 = torch.randn(M, 2 * N, device=device, generator=g)
+    cases = [dict(bias=b), dict(row_scale=rs, bias=b, cin=res, beta=0.5, pre="N"), dict(bias=b, pre="N", act=1),
+             dict(bias=b, pre="N", act=2), dict(bias=b, cin=z, act=3), dict(bias=b2, cin=z2, act=4), dict()]
+    for kw in cases:
+        act = kw.get("act", 0)
+        width = N // 2 if act == 2 else 2 * N if act == 4 else N
+        outs = []
+        for sc in (None, scratch):
+            C = torch.full((M, width), float("nan"), device=device)
+            pre = torch.full((M, N), float("nan"), device=device) if kw.get("pre") else None
+            L.fused(A, Ws, C, **{**kw, "pre": pre}, scratch=sc)
+            outs.append((C, pre))
+        assert not torch.isnan(outs[1][0]).any(), kw.keys()
+        assert torch.equal(outs[0][0], outs[1][0]), kw.keys()
+        if outs[0][1] is not None:
+            assert torch.equal(outs[0][1], outs[1][1])

@@ -78,3 +78,45 @@ def test_noalloc_size_limit(device):
     code = lib.pet_attn_bwd_noalloc(ctypes.byref(sh), p, 3 * 256, p, p, 256, p, 256, p, p, S, p, 3 * 256, p, S, None)
     assert code == _lib.ESCRATCH
     assert "scratch" in _lib.strerror(code)
+
+
+def test_noalloc_under_graph_capture(device):
+    """After one warm call (the device's first: symbol lookup, LDS limit), the
+    next call is captured into a HIP graph; three replays, each after the
+    inputs it accumulates onto are reset eagerly, give the eager bits."""
+    conf, tk = systems.config_tokens("c1")
+    H, hd = conf.heads, conf.head_dim
+    print("[gpu] pet_attn_bwd_noalloc under graph capture: c1", flush=True)
+    c = _case(device, tk, H, hd, 5)
+    lib = _lib.load()
+    N, T, S, D = tk.n_atoms, tk.n_rows, tk.slots, H * hd
+    sh = _lib.Shape(N, T, S, H, hd, 0, lib.pet_attn_scale(hd, 1.0))
+    merged = torch.empty((T, D), device=device)
+    ml = torch.empty((N * H * S, 2), device=device)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(lib.pet_attn_fwd(ctypes.byref(sh), _p(c["qkv"]), 3 * D, _p(c["off"]), _p(c["cf"]), S, _p(merged), D,
+                                _p(ml), st), "pet_attn_fwd")
+    qa = torch.empty((T, 3 * D), device=device)
+    ca = c["ca0"].clone()
+
+    def call(stream):
+        return lib.pet_attn_bwd_noalloc(ctypes.byref(sh), _p(c["qkv"]), 3 * D, _p(c["off"]), _p(c["dm"]), D,
+                                        _p(merged), D, _p(ml), _p(c["cf"]), S, _p(qa), 3 * D, _p(ca), S, stream)
+
+    _lib.check(call(st), "warm call")
+    torch.cuda.synchronize()
+    want = (qa.cpu().numpy().copy(), ca.cpu().numpy().copy())
+    g = torch.cuda.CUDAGraph()
+    ca.copy_(c["ca0"])
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        code = call(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(code, "captured call")
+    for _ in range(3):
+        qa.fill_(7.0)
+        ca.copy_(c["ca0"])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(qa.cpu().numpy().view(np.uint32), want[0].view(np.uint32))
+        assert np.array_equal(ca.cpu().numpy().view(np.uint32), want[1].view(np.uint32))
