@@ -54,18 +54,24 @@ def mixed_seconds(flops, split_share, pair_share=0.0, pair16_share=0.0):
                     + pair16_share / PEAK_PAIR16_FP32)
 
 
-def split_shares(plan):
+def split_shares(plan, slots):
     """Shares (split, pair, pair16) of the forward's and the backward's FLOPs
-    by the instructions that run them: the forward's scores are half its FLOPs
-    (scores, PV): with fwd_pair the scores as fp16 pairs on the 16x16x32
-    instruction and PV on the 16x16x16 one, else the scores split where
-    fwd_split_scores; the backward's five
-    products (scores, dP, dQ, dK, dV) a fifth each: with bwd_pair the scores
-    and dP as fp16 pairs on the 16x16x32 instruction and the other three on
-    the 16x16x16 one, else dP split where bwd_split_dp."""
+    by the instructions that run them. Forward, scores and PV half each: with
+    fwd_pair the scores as fp16 pairs on the 16x16x32 instruction, PV on it
+    for key blocks taken two at a time and on the 16x16x16 one for a block
+    alone (the own block, and an odd last one), else the scores split where
+    fwd_split_scores. Backward, five products (scores, dP, dQ, dK, dV) a fifth
+    each: with bwd_pair the scores and dP as fp16 pairs on the 16x16x32
+    instruction and the other three on the 16x16x16 one, else dP split where
+    bwd_split_dp."""
     if plan.get("streaming"):
         return (0.0, 0.0, 0.0), (0.0, 0.0, 0.0)
-    fwd = (0.0, 0.5, 0.5) if plan.get("fwd_pair") else (0.5 * plan["fwd_split_scores"], 0.0, 0.0)
+    if plan.get("fwd_pair"):
+        nb = (slots + 15) // 16
+        alone = nb - 2 * ((nb - 1) // 2)
+        fwd = (0.0, 0.5 + 0.5 * (nb - alone) / nb, 0.5 * alone / nb)
+    else:
+        fwd = (0.5 * plan["fwd_split_scores"], 0.0, 0.0)
     bwd = (0.0, 0.4, 0.6) if plan.get("bwd_pair") else (0.2 * plan["bwd_split_dp"], 0.0, 0.0)
     return fwd, bwd
 
@@ -194,7 +200,7 @@ def other_configs(device, reps):
         b_us = _timed(lambda: A.attn_bwd(qkv, off, dm, merged, ml, cf, H, hd, cf_seq_adj=ca, qkv_adj=qa, cfh=cfh), reps)
         alg = algorithmic(tk, D, H)
         plan = _lib.describe(N, T, S, H, hd)
-        fsh, bsh = split_shares(plan)
+        fsh, bsh = split_shares(plan, S)
         bound = max(mixed_seconds(alg["fwd_flops"], *fsh) + mixed_seconds(alg["bwd_flops"], *bsh),
                     (alg["fwd_bytes"] + alg["bwd_bytes"]) / PEAK_HBM) * 1e6
         res[name] = dict(workload=conf.name, atoms=N, tokens=T, head_dim=hd, fwd_us=f_us, bwd_us=b_us,
@@ -346,7 +352,7 @@ def main():
     alg = algorithmic(tk, D, H)
     fwd_avg, bwd_avg = statistics.fmean(fwd_us), statistics.fmean(bwd_us)
     plan = _lib.describe(N, T, S, H, hd)
-    fsh, bsh = split_shares(plan)
+    fsh, bsh = split_shares(plan, S)
     core_bytes = alg["fwd_bytes"] + alg["bwd_bytes"]
     # the core's bound at the ceilings of the instructions that run
     core_mfma_s = mixed_seconds(alg["fwd_flops"], *fsh) + mixed_seconds(alg["bwd_flops"], *bsh)
@@ -387,6 +393,22 @@ def main():
                          fwd_mb=alg["fwd_bytes"] / 1e6, bwd_mb=alg["bwd_bytes"] / 1e6),
         wall_s=wall,
     )
+    # the box's achievable streaming rate, for scale: a plain 1 GiB device copy
+    # (read + write) timed the same way; the roofline stays against 8 TB/s
+    src = torch.empty(1 << 28, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    c1.record()
+    torch.cuda.synchronize()
+    copy_tbps = 2 * src.numel() * 4 * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e12
+    extra["hbm_copy_tbps"] = copy_tbps
+    extra["core_frac_of_copy_rate"] = core_bytes / (copy_tbps * 1e12) / (us_per_step * 1e-6)
+    del src, dst
 
     if not args.no_op_level:
         # attention() + attention_bwd(): the core plus the W_out / W_in linears.
@@ -411,14 +433,22 @@ def main():
         s1.record()
         torch.cuda.synchronize()
         extra["op_level_us"] = s0.elapsed_time(s1) * 1e3 / reps
-        # its contraction bound: the core's, plus the output linear (2 T D^2,
-        # W_out split as it is staged: bf16 parts), dmerged (2 T D^2, K = D) and
-        # the input adjoint (6 T D^2, K = 3D), each on the split-product kernel
-        # where it is large enough (fp16 pairs from K = 256), else rocBLAS fp32
-        big = T * D * D >= 2 ** 32
-        pair = (2.0 * (D >= 256) + 6.0 * (3 * D >= 256)) / 10.0 if big else 0.0
-        gemm_s = mixed_seconds(10.0 * T * D * D, (1.0 - pair) if big else 0.0, pair)
-        extra["op_level_bound_us"] = (core_mfma_s + gemm_s) * 1e6
+        # its bound: the core's (the larger of its HBM and matrix-core times)
+        # plus each dense product's larger of its own HBM bytes and its FLOPs
+        # at the ceiling of the instruction it runs on: the output linear
+        # out = merged W_out^T + b (2 T D^2 FLOP; merged and out, 8 T D + 4 D^2
+        # bytes), dmerged = out_adj W_out (2 T D^2; 8 T D + 4 D^2) and the input
+        # adjoint qkv_adj W_in (6 T D^2; 16 T D + 12 D^2), each on the
+        # split-product kernel: fp16 pairs from K = 256, bf16 parts below
+        def gemm_s(flops, nbytes, k):
+            pair = k >= 256
+            return max(nbytes / PEAK_HBM, mixed_seconds(flops, 0.0 if pair else 1.0, 1.0 if pair else 0.0))
+        gemms = [gemm_s(2.0 * T * D * D, 8.0 * T * D + 4.0 * D * D, D),
+                 gemm_s(2.0 * T * D * D, 8.0 * T * D + 4.0 * D * D, D),
+                 gemm_s(6.0 * T * D * D, 16.0 * T * D + 12.0 * D * D, 3 * D)]
+        extra["op_level_bound_us"] = (bound_us * 1e-6 + sum(gemms)) * 1e6
+        extra["op_level_bound_parts_us"] = dict(core=bound_us, out_linear=gemms[0] * 1e6, dmerged=gemms[1] * 1e6,
+                                                in_adj=gemms[2] * 1e6)
         extra["op_level_frac_of_roofline"] = extra["op_level_bound_us"] / extra["op_level_us"]
         extra["op_level_note"] = ("attention()+attention_bwd(): core + the output linear (split-product kernel, W_out "
                                   "split as it is staged, bias in its epilogue), dmerged = out_adj W_out and the input "

@@ -58,18 +58,19 @@ __device__ __forceinline__ f4 mfma6(const u4* a, const u4* b, f4 c) {
 
 // ---- fp32 products from fp16 pairs on the 16-bit matrix cores --------------
 // A row of a matrix, scaled by a power of two s that puts its largest |x| in
-// [2^14, 2^15), splits into two fp16 values per element: hi = x s with its
-// low 13 significand bits cleared (its leading 11 bits, exact in fp16) and
-// lo = x s - hi (exact in fp32) rounded to the nearest fp16. hi + lo holds 22
-// of x's 24 significand bits, the rounding of lo within 2^-22 |x| (and within
-// 2^-37 of the row's largest element where x s leaves fp16's normal range). A product a.b over k is then (a_hi b_hi + a_hi b_lo + a_lo b_hi) /
-// (s_a s_b) with the three part products accumulated in fp32 by
-// v_mfma_f32_16x16x32_f16 and the scales undone in the epilogue; the dropped
-// a_lo b_lo is below 2^-22 |a||b|. Measured error on fp32 operands spread over
-// many octaves per row: 2.9e-8 of sum |a_k b_k| before the fp32 accumulation
-// (three bf16 parts with six products: 2.1e-8; the fp32 instruction's
-// accumulation alone: 1.6e-7). Three matrix instructions where the bf16 form
-// takes six.
+// [2^14, 2^15), splits into two fp16 values per element, both rounded to
+// nearest: hi = x s rounded to fp16 (its leading 11 bits) and lo = x s - hi
+// (exact in fp32) rounded to fp16. hi + lo holds x to 2^-23 |x| (2^-25 of the
+// row's largest where x s leaves fp16's normal range). A product a.b over k is
+// then (a_hi b_hi + a_hi b_lo + a_lo b_hi) / (s_a s_b) with the three part
+// products accumulated in fp32 by v_mfma_f32_16x16x32_f16 and the scales
+// undone in the epilogue; the dropped a_lo b_lo is below 2^-22 |a||b| and,
+// the lo parts of round-to-nearest splits having either sign, does not add
+// up along k. (A truncated hi, whose lo always has x's sign, made the dropped
+// terms share the product's sign: a bias along k of about 2^-21 of sum |a b|,
+// which moved a d = 512 model's 648-atom energy 8.5e-6 from the float64
+// oracle, against 1.5e-6 for the float32 oracle.) Three matrix instructions
+// where the bf16 form takes six.
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
@@ -77,8 +78,7 @@ __device__ __forceinline__ f4 mfma_h(const u4& a, const u4& b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
 }
 // c += a.b with the fourth part product a_lo b_lo too: the error left is the
-// rounding of the lo parts (2^-22 |a||b| at most, fp32's own order), where
-// mfma3 also drops a_lo b_lo (up to 2^-20 |a||b|)
+// rounding of the lo parts (2^-23 |a||b| at most, fp32's own order)
 __device__ __forceinline__ f4 mfma4(const u4* a, const u4* b, f4 c) {
   c = mfma_h(a[1], b[1], c);
   c = mfma_h(a[1], b[0], c);
@@ -91,12 +91,13 @@ __device__ __forceinline__ f4 mfma3(const u4* a, const u4* b, f4 c) {
   c = mfma_h(a[0], b[1], c);
   return mfma_h(a[0], b[0], c);
 }
-// two scaled values as a register of hi parts and a register of lo parts
+// two scaled values (exact products of a value and a power of two, or values
+// as computed) as a register of hi parts and a register of lo parts, both to
+// nearest
 __device__ __forceinline__ void pair2(float x, float y, unsigned& hi, unsigned& lo) {
-  const float hx = __uint_as_float(__float_as_uint(x) & 0xffffe000u);
-  const float hy = __uint_as_float(__float_as_uint(y) & 0xffffe000u);
-  hi = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(hx, hy));  // exact
-  const h2v l = {(_Float16)(x - hx), (_Float16)(y - hy)};                 // to nearest
+  const h2v h = {(_Float16)x, (_Float16)y};
+  const h2v l = {(_Float16)(x - float(h[0])), (_Float16)(y - float(h[1]))};
+  hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
 }
 // The row scale 2^(15 - e) for a largest |x| m = f 2^e (f in [0.5, 1)); 1 for
