@@ -221,6 +221,7 @@ def time_ef(device, reps, cpu: bool):
     import numpy as np
     import torch
 
+    from pet_kokkos_amd import _lib
     from pet_kokkos_amd.model import PetModel, ef_flops, ef_workload, structures_input
 
     res, cpu_cases = {}, []
@@ -245,7 +246,19 @@ def time_ef(device, reps, cpu: bool):
                          d_pet=h.d_pet, heads=h.num_heads, ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
                          ef_bound_ms=bound_ms, ef_frac_of_roofline=bound_ms / ef_ms,
                          ef_split_share=fl["split"] / fl["forces"], ef_pair_share=fl["pair"] / fl["forces"],
-                         workspace_gb=m.workspace_bytes / 1e9)
+                         workspace_gb=m.workspace_bytes / 1e9, tier=m.last_tier,
+                         pairs_scratch_gb=m.pairs_scratch_bytes / 1e9)
+        if name == "c5":
+            # the "wide" memory tier (qkv and the edge MLP's pre-activation
+            # remade in the backward, the edge MLP over 64k-row chunks): the
+            # same bits, a fresh model so its workspace is its own
+            del m, o
+            torch.cuda.empty_cache()
+            m = PetModel(h, w, comp)
+            with _lib.options(model_recompute=2):
+                o = m.compute(x, True)
+                wide_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
+            res[name]["wide"] = dict(ef_ms=wide_ms, workspace_gb=m.workspace_bytes / 1e9, tier=m.last_tier)
         if name in ("c2", "c2-residual") and cpu:
             cpu_cases.append((name, h, w, comp, x.species.cpu().numpy(), x.host))
         del m, x, o

@@ -74,6 +74,7 @@ class PetModel {
   const pet_model_hypers& hypers() const { return h_; }
   size_t workspace_bytes() const { return pet_model_workspace_bytes(m_); }
   size_t pairs_scratch_bytes() const { return pet_model_pairs_scratch_bytes(m_); }
+  int last_tier() const { return pet_model_last_tier(m_); }
 
   // energy_forces_batch on the device (src/model.cpp:795-811).
   void compute(const pet_model_edges& edges, bool forces, const DeviceOut& out, hipStream_t stream = nullptr) {

@@ -105,7 +105,12 @@ enum {
   PET_OPT_ATTN_STREAM = 6, /* 0 (default): the LDS-staged kernels where they hold the shape; 1: the streaming kernels always */
   PET_OPT_BWD_KERNEL = 7,  /* 0 (default): at head_dim 32 and 64 the fp16-pair backward (every product on the 16-bit
                               matrix cores) where it fits, with PET_OPT_SPLIT 1; 1: the tile-exchange backward */
-  PET_OPT_COUNT = 8
+  PET_OPT_MODEL_RECOMPUTE = 8, /* the whole evaluation's memory tier (pet_model_compute): 0 (default) chosen from the
+                              shapes and the device's free memory; 1 "never": every activation of the forward kept
+                              for the backward; 2 "wide": the attention's qkv and the edge MLP's pre-activation not
+                              kept but recomputed in the backward, the edge MLP run over chunks of edge rows (the
+                              reference's Recompute::Wide, src/model.cpp:819-860) -- the same results */
+  PET_OPT_COUNT = 9
 };
 
 /* Sets an option; PET_ATTN_EINVAL for an unknown option or a value out of range. */

@@ -179,6 +179,11 @@ PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
  * device has room; 0 when it has none, and then those products split A as
  * they stage it instead (the same bits, more work per product). */
 PET_ATTN_API size_t pet_model_pairs_scratch_bytes(const pet_model* model);
+/* The memory tier the model's last evaluation with forces ran (option
+ * PET_OPT_MODEL_RECOMPUTE): 1 "never" (every activation kept), 2 "wide" (qkv
+ * and the edge MLP's pre-activation remade in the backward, the edge MLP over
+ * chunks of edge rows); 0 before any. The residual featurizer runs "never". */
+PET_ATTN_API int pet_model_last_tier(const pet_model* model);
 
 #ifdef __cplusplus
 }

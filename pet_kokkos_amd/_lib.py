@@ -47,6 +47,7 @@ EXPORTS = (
     "pet_model_compute",
     "pet_model_workspace_bytes",
     "pet_model_pairs_scratch_bytes",
+    "pet_model_last_tier",
     "pet_linear_fused",
     "pet_linear_split_weights",
     "pet_linear_split_weights_transposed",
@@ -228,11 +229,14 @@ def load() -> ctypes.CDLL:
     lib.pet_model_workspace_bytes.argtypes = [_P]
     lib.pet_model_pairs_scratch_bytes.restype = ctypes.c_size_t
     lib.pet_model_pairs_scratch_bytes.argtypes = [_P]
+    lib.pet_model_last_tier.restype = ctypes.c_int
+    lib.pet_model_last_tier.argtypes = [_P]
     _lib = lib
     return lib
 
 
-OPTIONS = {"split": 1, "fwd_kernel": 2, "bwd_vlds": 3, "bwd_nbuf": 4, "model_gemm": 5, "attn_stream": 6, "bwd_kernel": 7}
+OPTIONS = {"split": 1, "fwd_kernel": 2, "bwd_vlds": 3, "bwd_nbuf": 4, "model_gemm": 5, "attn_stream": 6, "bwd_kernel": 7,
+           "model_recompute": 8}
 
 
 def set_option(name: str, value: int) -> None:

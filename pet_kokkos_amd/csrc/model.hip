@@ -479,6 +479,7 @@ struct pet_model {
   pet_model_hypers h{};
   int hd = 0, cw = 0, ew = 0;  // head_dim, center / edge MLP pre-activation widths
   int gemm_mode = 4;           // PET_OPT_MODEL_GEMM for the evaluation in progress
+  int tier = 1;                // the memory tier of the last evaluation: 1 never, 2 wide
   std::unordered_map<std::string, Mat> m;
   std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
   // layers whose saved pre-activation holds its bias (made by the split-product
@@ -770,7 +771,9 @@ void fill0(float* x, int64_t n, hipStream_t st) {
 }
 
 // What one GNN layer keeps for its backward (the reference's LayerSaves,
-// include/pet/model.hpp:183-198), every block's wide activations included.
+// include/pet/model.hpp:183-198): under the "never" tier every block's wide
+// activations too (qkv, the edge MLP's pre-activation pre_e); under "wide"
+// those two are null and the backward remakes them.
 struct Block {
   float *tok, *inv, *qkv, *merged, *ml, *eps, *node_res, *pre_c, *pre_e;
 };
@@ -786,17 +789,38 @@ struct Pass {
   int N, E, T, S, D, Dn, Dh, A, G;
   pet_attn_shape sh{};
   float* cf_seq = nullptr;
+  bool wide = false;  // the "wide" memory tier (recompute_tier)
+  int chunk = 0;      // edge rows of an edge-MLP chunk under it
 
   Pass(pet_model& m, const pet_model_edges& ed, hipStream_t s) : md(m), e(ed), st(s) {
     N = e.n_atoms, E = e.n_edges, T = N + E, S = e.max_neighbors + 1;
     D = md.h.d_pet, Dn = md.h.d_node, Dh = md.h.d_head, A = md.h.num_attention_layers, G = md.h.num_gnn_layers;
+    // the reference's chunk (PetModel::edge_chunk_rows, src/model.cpp:812-817):
+    // an eighth of the edges and at least 64k rows, where the products run at
+    // full speed and (at or above 2^32 multiply-adds) on the split-product
+    // kernel, whose rows do not depend on how many there are
+    chunk = std::max(65536, (E + 7) / 8);
     sh.n_atoms = N, sh.n_rows = T, sh.slots = S, sh.heads = md.h.num_heads, sh.head_dim = md.hd, sh.dead = 0;
     sh.scale = pet_attn_scale(md.hd, md.h.attention_temperature);
   }
   std::string g(int L) const { return "gnn_layers." + std::to_string(L); }
   std::string t(int L, int a) const { return g(L) + ".trans.layers." + std::to_string(a); }
 
-  // One GNN layer forward (ff_layer, src/feedforward.cpp:34-198, every save kept).
+  // The edge MLP's SwiGLU of rows of its normed input en (rows x D) into he
+  // (rows x ew / 2), its pre-activation into a temporary the caller's scope
+  // releases, which it returns: the forward's product and activation, so
+  // the backward of the "wide" tier remakes the same bits.
+  float* edge_pre(float* he, const float* en, int rows, const std::string& tl) {
+    float* pre = md.f(int64_t(rows) * md.ew);
+    if (!linear_act(md, he, pre, en, rows, D, tl + ".mlp.w_in", 2, st)) {
+      linear_pre(md, pre, en, rows, D, tl + ".mlp.w_in", st);
+      swiglu(md, he, pre, rows, tl + ".mlp.w_in", st);
+    }
+    return pre;
+  }
+
+  // One GNN layer forward (ff_layer, src/feedforward.cpp:34-198; under the
+  // "wide" tier without its qkv and edge pre-activation saves).
   void layer_fwd(int L, float*& node, float* input_edge, Layer& sv) {
     sv.cpre = md.f(int64_t(E) * D);
     sv.b.resize(A);
@@ -808,9 +832,10 @@ struct Pass {
     for (int a = 0; a < A; ++a) {
       const std::string tl = t(L, a);
       Block& b = sv.b[a];
-      b.qkv = md.f(int64_t(T) * 3 * D), b.merged = md.f(int64_t(T) * D), b.ml = md.f(int64_t(N) * md.h.num_heads * S * 2);
+      b.qkv = wide ? nullptr : md.f(int64_t(T) * 3 * D), b.merged = md.f(int64_t(T) * D);
+      b.ml = md.f(int64_t(N) * md.h.num_heads * S * 2);
       b.eps = md.f(int64_t(E) * D), b.node_res = md.f(int64_t(N) * Dn), b.inv = md.f(T);
-      b.pre_c = md.f(int64_t(N) * md.cw), b.pre_e = md.f(int64_t(E) * md.ew);
+      b.pre_c = md.f(int64_t(N) * md.cw), b.pre_e = wide ? nullptr : md.f(int64_t(E) * md.ew);
       float* node_next = md.f(int64_t(N) * Dn);
       float* edge_next = a + 1 < A ? sv.b[a + 1].tok + int64_t(N) * D : out_edge;
       auto scope = md.ws.mark();
@@ -818,8 +843,9 @@ struct Pass {
       // the fused QKV projection: qkv = tok (W_in diag(norm weight))^T, the
       // attention applying 1/rms and the bias as it loads it
       ok(pet_rows_rms_inv(T, D, b.tok, D, b.inv, st));
-      linear_pre(md, b.qkv, b.tok, T, D, tl + ".attention.input_linear@fold", st);
-      ok(pet_attn_fwd_xf(&sh, b.qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, cf_seq, S,
+      float* qkv = wide ? md.f(int64_t(T) * 3 * D) : b.qkv;
+      linear_pre(md, qkv, b.tok, T, D, tl + ".attention.input_linear@fold", st);
+      ok(pet_attn_fwd_xf(&sh, qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, cf_seq, S,
                          b.merged, D, b.ml, st));
       float* attn_out = md.f(int64_t(T) * D);
       linear(md, attn_out, b.merged, T, D, tl + ".attention.output_linear", st);
@@ -844,13 +870,26 @@ struct Pass {
       }
       linear_acc(md, node_next, hc, N, md.cw / 2, tl + ".center_mlp.w_out", st);
       float* en = attn_out;  // consumed: its edge rows were read by the residual pass
-      norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
-      float* he = md.f(int64_t(E) * md.ew / 2);
-      if (!linear_act(md, he, b.pre_e, en, E, D, tl + ".mlp.w_in", 2, st)) {
-        linear_pre(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
-        swiglu(md, he, b.pre_e, E, tl + ".mlp.w_in", st);
+      if (!wide) {
+        norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
+        float* he = md.f(int64_t(E) * md.ew / 2);
+        if (!linear_act(md, he, b.pre_e, en, E, D, tl + ".mlp.w_in", 2, st)) {
+          linear_pre(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
+          swiglu(md, he, b.pre_e, E, tl + ".mlp.w_in", st);
+        }
+        linear_acc(md, edge_next, he, E, md.ew / 2, tl + ".mlp.w_out", st);
+      } else {  // a chunk of edge rows at a time, its pre-activation a temporary
+        for (int e0 = 0; e0 < E; e0 += chunk) {
+          const int rows = std::min(chunk, E - e0);
+          auto sc = md.ws.mark();
+          float* enc = en + int64_t(e0) * D;
+          norm(md, enc, b.eps + int64_t(e0) * D, rows, D, tl + ".norm_mlp", false, st);
+          float* he = md.f(int64_t(rows) * md.ew / 2);
+          edge_pre(he, enc, rows, tl);
+          linear_acc(md, edge_next + int64_t(e0) * D, he, rows, md.ew / 2, tl + ".mlp.w_out", st);
+          md.ws.release(sc);
+        }
       }
-      linear_acc(md, edge_next, he, E, md.ew / 2, tl + ".mlp.w_out", st);
       md.ws.release(scope);
       node_cur = node_next;
       edge_cur = edge_next;
@@ -911,15 +950,35 @@ struct Pass {
       const Block& b = sv.b[a];
       auto s2 = md.ws.mark();
       {  // the two MLPs: edge_adj and node_adj become eps's and node_res's
-        float* h_adj = md.f(int64_t(E) * md.ew / 2);
-        float* pre_adj = md.f(int64_t(E) * md.ew);
-        float* en_adj = md.f(int64_t(E) * D);
-        if (!linear_bwd_act(md, pre_adj, edge_adj, E, tl + ".mlp.w_out", b.pre_e, tl + ".mlp.w_in", 2, st)) {
-          linear_bwd(md, h_adj, edge_adj, E, tl + ".mlp.w_out", 0.0f, st);
-          swiglu_bwd(md, pre_adj, h_adj, b.pre_e, E, tl + ".mlp.w_in", st);
+        // the edge MLP over edge rows [e0, e0 + rows): all of them, or (wide) a
+        // chunk at a time with its normed input and pre-activation remade
+        auto edge_mlp_bwd = [&](int e0, int rows, const float* pre) {
+          float* ea = edge_adj + int64_t(e0) * D;
+          float* h_adj = md.f(int64_t(rows) * md.ew / 2);
+          float* pre_adj = md.f(int64_t(rows) * md.ew);
+          float* en_adj = md.f(int64_t(rows) * D);
+          if (!linear_bwd_act(md, pre_adj, ea, rows, tl + ".mlp.w_out", pre, tl + ".mlp.w_in", 2, st)) {
+            linear_bwd(md, h_adj, ea, rows, tl + ".mlp.w_out", 0.0f, st);
+            swiglu_bwd(md, pre_adj, h_adj, pre, rows, tl + ".mlp.w_in", st);
+          }
+          linear_bwd(md, en_adj, pre_adj, rows, tl + ".mlp.w_in", 0.0f, st);
+          ok(pet_norm_rows_bwd(rows, D, ea, D, 1.0f, en_adj, D, b.eps + int64_t(e0) * D, D,
+                               md.p(tl + ".norm_mlp.weight"), 0, st));
+        };
+        if (!wide) {
+          edge_mlp_bwd(0, E, b.pre_e);
+        } else {
+          for (int e0 = 0; e0 < E; e0 += chunk) {
+            const int rows = std::min(chunk, E - e0);
+            auto sc = md.ws.mark();
+            float* en = md.f(int64_t(rows) * D);
+            norm(md, en, b.eps + int64_t(e0) * D, rows, D, tl + ".norm_mlp", false, st);
+            float* he = md.f(int64_t(rows) * md.ew / 2);
+            const float* pre = edge_pre(he, en, rows, tl);
+            edge_mlp_bwd(e0, rows, pre);
+            md.ws.release(sc);
+          }
         }
-        linear_bwd(md, en_adj, pre_adj, E, tl + ".mlp.w_in", 0.0f, st);
-        ok(pet_norm_rows_bwd(E, D, edge_adj, D, 1.0f, en_adj, D, b.eps, D, md.p(tl + ".norm_mlp.weight"), 0, st));
         float* hc_adj = md.f(int64_t(N) * md.cw / 2);
         float* prec_adj = md.f(int64_t(N) * md.cw);
         float* cn_adj = md.f(int64_t(N) * Dn);
@@ -941,7 +1000,12 @@ struct Pass {
       float* cfh = md.f(int64_t(N) * md.h.num_heads * S);
       float* in_adj = dmerged;
       linear_bwd(md, dmerged, tok_adj, T, tl + ".attention.output_linear", 0.0f, st);
-      ok(pet_attn_bwd_xf(&sh, b.qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, dmerged, D,
+      float* qkv = b.qkv;
+      if (wide) {  // remade as the forward made it
+        qkv = md.f(int64_t(T) * 3 * D);
+        linear_pre(md, qkv, b.tok, T, D, tl + ".attention.input_linear@fold", st);
+      }
+      ok(pet_attn_bwd_xf(&sh, qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, dmerged, D,
                          b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh, cf_seq_adj, S, st));
       linear_bwd(md, in_adj, qkv_adj, T, tl + ".attention.input_linear", 0.0f, st);
       // through the norm: atom rows set (input_node's adjoint), edge rows onto edge_adj
@@ -1461,6 +1525,31 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
 
 void pet_model_destroy(pet_model* model) { delete model; }
 
+namespace {
+// The memory tier of an evaluation with forces (PetModel::recompute_tier,
+// src/model.cpp:819-860, for the feedforward featurizer): option
+// PET_OPT_MODEL_RECOMPUTE 1 or 2 forces "never" or "wide"; 0 takes "never"
+// unless its estimate -- what the forward keeps plus the backward's largest
+// temporaries, in floats: per block the token rows, qkv, merged, the edge MLP's
+// pre-activation (E x ew) and the node/edge residual rows; per layer the
+// combination's three 2D-wide edge arrays; the backward's E x ew and 1.5 T x
+// 3D work -- passes 85% of what the device has free plus what the model's
+// workspace already holds.
+bool recompute_wide(const pet_model& md, const pet_model_edges& e) {
+  const int opt = pet_attn_get_option(PET_OPT_MODEL_RECOMPUTE);
+  if (opt) return opt == 2;
+  const double N = e.n_atoms, E = e.n_edges, T = N + E, D = md.h.d_pet, Dn = md.h.d_node;
+  const double G = md.h.num_gnn_layers, A = md.h.num_attention_layers;
+  const double block = 5 * T * D + E * D + E * md.ew + N * (2 * Dn + md.cw) + T;
+  const double never = 4.0 * (G * A * block + G * 5 * E * D + 1.5 * E * md.ew + 6 * T * D);
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return false;
+  return never > 0.85 * (double(free_b) + double(md.ws.bytes()));
+}
+}  // namespace
+
+int pet_model_last_tier(const pet_model* model) { return model ? model->tier : 0; }
+
 size_t pet_model_workspace_bytes(const pet_model* model) { return model ? model->ws.bytes() : 0; }
 
 size_t pet_model_pairs_scratch_bytes(const pet_model* model) {
@@ -1482,6 +1571,8 @@ int pet_model_compute(pet_model* md, const pet_model_edges* e, int forces, doubl
     return PET_ATTN_EINDEX;
   try {
     Pass p(*md, *e, reinterpret_cast<hipStream_t>(stream));
+    p.wide = forces != 0 && md->h.featurizer == 0 && recompute_wide(*md, *e);
+    md->tier = p.wide ? 2 : 1;
     p.run(forces != 0, energy, per_atom, forces_out, virial, edge_grad);
   } catch (const Error& err) {
     return err.code;

@@ -127,6 +127,11 @@ class PetModel:
         return int(self._lib.pet_model_workspace_bytes(self._handle))
 
     @property
+    def last_tier(self) -> str:
+        """The memory tier of the last evaluation with forces: "never" or "wide" (option model_recompute)."""
+        return {0: "none", 1: "never", 2: "wide"}[int(self._lib.pet_model_last_tier(self._handle))]
+
+    @property
     def pairs_scratch_bytes(self) -> int:
         """Bytes of the model's pairs scratch (0: the large products split A as they stage it)."""
         return int(self._lib.pet_model_pairs_scratch_bytes(self._handle))

@@ -209,9 +209,9 @@ def test_split_weights_exact(device):
 def test_pair_weights_exact(transposed, device):
     """From K = 256 the split is fp16 pairs: per row a power-of-two scale s
     with max |w| s in [2^14, 2^15), then per 8-element k group a hi part (w s
-    with its low 13 significand bits cleared, exact in fp16) and a lo part
-    (the rest, rounded to the nearest fp16: hi + lo within 2^-22 |w s|, or
-    1.5 fp16 subnormal steps below fp16's normal range), and after the N K 4 bytes of parts the rows' 1 / s.
+    rounded to the nearest fp16) and a lo part (the rest, rounded to the
+    nearest fp16: hi + lo within 2^-23 |w s|, or half an fp16 subnormal step
+    below fp16's normal range), and after the N K 4 bytes of parts the rows' 1 / s.
     The split of W^T from W equals that of W^T made contiguous."""
     N, K = 40, 256
     g = torch.Generator(device=device).manual_seed(6)
@@ -238,10 +238,12 @@ def test_pair_weights_exact(transposed, device):
     ws = w * s[:, None, None]
     hi, lo = parts[:, :, 0, :], parts[:, :, 1, :]
     normal = np.abs(ws) >= 2.0 ** -14
-    hi_ref = (ws.astype(np.float32).view(np.uint32) & 0xFFFFE000).view(np.float32).astype(np.float64)
+    hi_ref = ws.astype(np.float32).astype(np.float16).astype(np.float64)  # to nearest (even)
     assert np.array_equal(hi[normal], hi_ref[normal])
-    # below fp16's normal range hi is truncated to the subnormal step (2^-24) and lo rounded to it
-    assert np.all(np.abs(hi + lo - ws) <= 2.0 ** -22 * np.abs(ws) + 1.5 * 2.0 ** -24)
+    # lo of either sign (round to nearest), |lo| within half of hi's ulp
+    assert np.any(lo[normal] < 0) and np.any(lo[normal] > 0)
+    # below fp16's normal range hi and lo are rounded to the subnormal step (2^-24)
+    assert np.all(np.abs(hi + lo - ws) <= 2.0 ** -23 * np.abs(ws) + 2.0 ** -25)
 
 
 def test_split_rejects(device):
