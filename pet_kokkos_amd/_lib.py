@@ -53,6 +53,8 @@ EXPORTS = (
     "pet_linear_split_weights_transposed",
     "pet_linear_fused_split",
     "pet_linear_fused_split_ws",
+    "pet_linear_pair_weights",
+    "pet_linear_fused_smallk",
     "pet_linear_pair_rows",
     "pet_linear_fused_pairs",
 )
@@ -218,6 +220,10 @@ def load() -> ctypes.CDLL:
     lib.pet_linear_split_weights_transposed.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_split.restype = ctypes.c_int
     lib.pet_linear_fused_split.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
+    lib.pet_linear_pair_weights.restype = ctypes.c_int
+    lib.pet_linear_pair_weights.argtypes = [_P, _I, _I, _I64, _P, _P]
+    lib.pet_linear_fused_smallk.restype = ctypes.c_int
+    lib.pet_linear_fused_smallk.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_linear_fused_split_ws.restype = ctypes.c_int
     lib.pet_linear_fused_split_ws.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I,
                                               _P, ctypes.c_size_t, _P]

@@ -798,18 +798,24 @@ __device__ __forceinline__ void wait_vm() {
 template <int BM, int BN, int WGM, int WGN, int ST>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_pp_kernel(int M, int N, int K, const u4* __restrict__ Ap,
                                                                   const u4* __restrict__ Bs, float* C, int64_t ldc,
-                                                                  Epi epi) {
+                                                                  Epi epi, int WR) {
   constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
   constexpr int SR = BM + BN, LPW = SR / 8 / NW;  // rows a stage; load instructions a wave a step
   static_assert(LPW * 8 * NW == SR && ST >= 2 && ST <= 6, "a stage's rows divide over the waves");
   extern __shared__ u4 ring[];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
   const int wm = w / WGN, wn = w % WGN;
-  // the XCD-contiguous tile order of gemm_nt_pair_kernel, one tile an item
-  const int NT = (N + BN - 1) / BN, total = gridDim.x, L = blockIdx.x;
+  // the XCD-contiguous tile order of gemm_nt_pair_kernel, one tile an item;
+  // within an XCD's run, windows of WR row blocks, each swept column tile by
+  // column tile with its row blocks fastest: the tiles in flight at once are
+  // a few row blocks by a few column tiles, whose A rows and B strip both
+  // stay in the XCD's L2 (row-block order instead streamed all of B, 4 MB at
+  // N 2048, through each row block: 2.6 times the product's bytes)
+  const int NT = (N + BN - 1) / BN, RB = (M + BM - 1) / BM, total = gridDim.x, L = blockIdx.x;
   const int q = total / 8, r = total % 8, x = L % 8;
   const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + L / 8;
-  const int m0 = (t / NT) * BM, n0 = (t % NT) * BN, KG = K / 8;
+  const int wi = t / (WR * NT), wr = min(WR, RB - wi * WR), within = t - wi * WR * NT;
+  const int m0 = (wi * WR + within % wr) * BM, n0 = (within / wr) * BN, KG = K / 8;
 
   // this lane's source for each of the wave's load instructions: stage row
   // R = 8 (w LPW + i) + l / 8 (A rows first, then B), part (l % 8) ^ (l / 8)
@@ -888,6 +894,132 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_pp_kernel(int M, int N, i
   static_assert(ST * (BM + BN) * 128 >= BM * BN * 4, "the ring holds the result tile");
   if (staged_epilogue<BM, BN, WGM, WGN>(acc, reinterpret_cast<float*>(ring), m0, n0, M, N, C, ldc, epi)) return;
   epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+}
+
+// Small K (at most 128): A resident in the waves' registers. A workgroup of
+// four waves takes 128 rows of A (32 a wave), loads them once, finds each
+// row's largest |x| across the four lanes that hold it, and keeps the rows as
+// fp16 pairs in the matrix instruction's a layout (lane (c, g): row c of a
+// 16-row block, k 32 kk + 8 g .. + 7); then for each of its column tiles (BN
+// columns) it stages B's pair rows (pet_gemm_pair_weights' layout: per column
+// n its k groups' hi and lo, then the inverse scales) into LDS, rows padded by
+// 16 bytes so that a 16-lane read of 16 columns meets 16 distinct bank
+// quads, and runs all four part products (hi hi, hi lo, lo hi, lo lo: the
+// dropped term of three is not negligible against the products' own fp32
+// rounding at so short a K), k groups in order. A row's results depend on
+// that row alone: neither the tile shape nor M changes them. Epilogue as the
+// other kernels'.
+template <int KB, int BN, int NWV, int TM>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4)))
+gemm_sk_kernel(int M, int N, const float* __restrict__ A, int64_t lda, const u4* __restrict__ Bp, float* C,
+               int64_t ldc, Epi epi, int cpw) {
+  constexpr int BM = 16 * NWV * TM, TN = BN / 16, KG = 4 * KB, RPB = 2 * KG + 1;
+  constexpr int BT = BN * RPB * 16, ET = BM * BN * 4;  // bytes: the B tile, the staged epilogue's tile
+  __shared__ u4 lds_b[(BT > ET ? BT : ET) / 16];
+  __shared__ float sinv[BM];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  // work items: (row block, cpw of its column tiles), XCD-contiguous as in
+  // gemm_nt_pair_kernel
+  const int NT = (N + BN - 1) / BN, NG = (NT + cpw - 1) / cpw, total = gridDim.x, L = blockIdx.x;
+  const int q = total / 8, r = total % 8, x = L % 8;
+  const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + L / 8;
+  const int tm = t / NG, tn0 = (t % NG) * cpw, tn1 = min(tn0 + cpw, NT);
+  const int m0 = tm * BM;
+
+  u4 av[TM][KB][2];
+  {
+    float4 v[TM][KB][2];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const float* row = A + int64_t(min(m0 + 16 * TM * w + 16 * a + c, M - 1)) * lda + 8 * g;
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) {
+        v[a][kk][0] = *reinterpret_cast<const float4*>(row + 32 * kk);
+        v[a][kk][1] = *reinterpret_cast<const float4*>(row + 32 * kk + 4);
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      float m = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4 u = v[a][kk][h];
+          m = fmaxf(m, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+        }
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      const float sc = pair_scale(m);
+      if (g == 0) sinv[16 * TM * w + 16 * a + c] = 1.f / sc;
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) {
+        unsigned h[4], lo[4];
+        pair2(v[a][kk][0].x * sc, v[a][kk][0].y * sc, h[0], lo[0]);
+        pair2(v[a][kk][0].z * sc, v[a][kk][0].w * sc, h[1], lo[1]);
+        pair2(v[a][kk][1].x * sc, v[a][kk][1].y * sc, h[2], lo[2]);
+        pair2(v[a][kk][1].z * sc, v[a][kk][1].w * sc, h[3], lo[3]);
+        av[a][kk][0] = u4{h[0], h[1], h[2], h[3]};
+        av[a][kk][1] = u4{lo[0], lo[1], lo[2], lo[3]};
+      }
+    }
+  }
+  const float* inv_b = reinterpret_cast<const float*>(Bp + int64_t(N) * KG * 2);
+  for (int tn = tn0; tn < tn1; ++tn) {
+    const int n0 = tn * BN;
+    __syncthreads();  // the last tile's reads and epilogue are done with the LDS
+    for (int i = tid; i < BN * 2 * KG; i += 64 * NWV) {
+      const int rr = i / (2 * KG), o = i - rr * (2 * KG);
+      lds_b[rr * RPB + o] = Bp[int64_t(min(n0 + rr, N - 1)) * (2 * KG) + o];
+    }
+    __syncthreads();
+    f4 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) {
+        const u4* br = lds_b + (16 * b + c) * RPB + (4 * kk + g) * 2;
+        const u4 bh = br[0], bl = br[1];
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+          acc[a][b] = pet_split::mfma_h(av[a][kk][1], bl, acc[a][b]);
+          acc[a][b] = pet_split::mfma_h(av[a][kk][1], bh, acc[a][b]);
+          acc[a][b] = pet_split::mfma_h(av[a][kk][0], bl, acc[a][b]);
+          acc[a][b] = pet_split::mfma_h(av[a][kk][0], bh, acc[a][b]);
+        }
+      }
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const float ib = inv_b[min(n0 + 16 * b + c, N - 1)];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) acc[a][b][rr] = acc[a][b][rr] * sinv[16 * TM * w + 16 * a + 4 * g + rr] * ib;
+    }
+    if (!staged_epilogue<BM, BN, NWV, 1>(acc, reinterpret_cast<float*>(lds_b), m0, n0, M, N, C, ldc, epi)) {
+      // a partial column tile or unaligned operands: the tile through LDS as
+      // well, then one element a thread a row at a time (a SwiGLU pair in
+      // neighbouring lanes), so no lane holds the addresses of all its
+      // results at once
+      float* tile = reinterpret_cast<float*>(lds_b);
+      __syncthreads();
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) tile[(16 * TM * w + 16 * a + 4 * g + rr) * BN + 16 * b + c] = acc[a][b][rr];
+      __syncthreads();
+      for (int e = tid; e < BM * BN; e += 64 * NWV) {
+        const int R = e / BN, cc = e - R * BN;
+        epi_elem(tile[e], m0 + R, n0 + cc, cc & 15, M, N, C, ldc, epi);
+      }
+    }
+  }
 }
 
 }  // namespace pet_gemm
@@ -1139,7 +1271,7 @@ int pet_gemm_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, hip
 
 // The pairs-by-pairs kernel's shapes: tile, waves, LDS stages.
 struct PPShape {
-  void (*kern)(int, int, int, const u4*, const u4*, float*, int64_t, Epi);
+  void (*kern)(int, int, int, const u4*, const u4*, float*, int64_t, Epi, int);
   int bm, bn, threads, stages;
   size_t lds() const { return size_t(stages) * (bm + bn) * 128; }
 };
@@ -1182,9 +1314,66 @@ int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
   const PPShape& k = kPP[N >= 128 && t128 >= 1024 ? 0 : N >= 64 ? 1 : 2];
   const int64_t tiles = int64_t((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
+  const char* wre = getenv("PET_EXP_WR");
+  const int wr = wre ? atoi(wre) : 8;
   hipLaunchKernelGGL(k.kern, dim3(unsigned(tiles)), dim3(k.threads), k.lds(), st, M, N, K,
-                     static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e);
+                     static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e, wr);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// B's pair rows at any K (a multiple of 32): the pair form of
+// pet_gemm_split_weights, which takes it from K = 256 only.
+int pet_gemm_pair_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st) {
+  if (N < 0 || K < 0 || K % 32 || (reinterpret_cast<uintptr_t>(out) & 15)) return PET_ATTN_EINVAL;
+  if (N == 0 || K == 0) return PET_ATTN_OK;
+  hipLaunchKernelGGL(pair_rows_kernel, dim3(unsigned(N)), dim3(256), 0, st, W, N, K, ldw, transposed,
+                     static_cast<u4*>(out));
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// C = epi(A B^T) for K at most 128 (a multiple of 32), B as pair rows
+// (pet_gemm_pair_weights): gemm_sk_kernel.
+int pet_gemm_nt_sk(int M, int N, int K, const float* A, int64_t lda, const void* Bp, float* C, int64_t ldc,
+                   const Epi& e, hipStream_t st) {
+  if (M < 0 || N < 0 || K < 32 || K > 128 || K % 32) return PET_ATTN_EINVAL;
+  if (M == 0 || N == 0) return PET_ATTN_OK;
+  if (lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(Bp) & 15))
+    return PET_ATTN_EALIGN;
+  constexpr int BN = 64, NWV = 4, TM = 1, BM = 16 * NWV * TM;
+  const int64_t rb = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+  if (rb * nt >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
+  // column tiles an item: about 2048 items, so A is loaded as few times as
+  // that allows
+  const int64_t cpw = std::max<int64_t>(1, std::min<int64_t>(nt, rb * nt / 2048));
+  const int64_t items = rb * ((nt + cpw - 1) / cpw);
+  const u4* B = static_cast<const u4*>(Bp);
+  const dim3 grid{unsigned(items)}, block{unsigned(64 * NWV)};
+  switch (K / 32) {
+    case 1: hipLaunchKernelGGL((gemm_sk_kernel<1, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
+    case 2: hipLaunchKernelGGL((gemm_sk_kernel<2, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
+    case 3: hipLaunchKernelGGL((gemm_sk_kernel<3, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
+    default: hipLaunchKernelGGL((gemm_sk_kernel<4, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
+  }
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+extern "C" int pet_linear_pair_weights(const float* W, int N, int K, int64_t ldw, void* out, void* stream) {
+  if (N < 0 || K < 0 || K % 32 || ldw < K || ((N > 0 && K > 0) && (!W || !out))) return PET_ATTN_EINVAL;
+  if (reinterpret_cast<uintptr_t>(out) & 15) return PET_ATTN_EALIGN;
+  return pet_gemm_pair_weights(W, N, K, ldw, false, out, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pet_linear_fused_smallk(int M, int N, int K, const float* A, int64_t lda, const void* Wpairs, float* C,
+                                       int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                       int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream) {
+  if ((M > 0 && N > 0) && (!A || !Wpairs || !C || lda < K || !epi_args_ok(N, C, ldc, row_scale, cin, ldcin, pre,
+                                                                              ldpre, act)))
+    return PET_ATTN_EINVAL;
+  if (act == 2 && N % 2) return PET_ATTN_EINVAL;
+  Epi e;
+  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
+  e.act = act;
+  return pet_gemm_nt_sk(M, N, K, A, lda, Wpairs, C, ldc, e, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pet_linear_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, void* stream) {

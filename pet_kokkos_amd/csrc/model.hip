@@ -47,6 +47,11 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
                       float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch = nullptr,
                       size_t scratch_bytes = 0);
 
+extern "C" int pet_linear_fused_smallk(int M, int N, int K, const float* A, int64_t lda, const void* Wpairs, float* C,
+                                       int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                       int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
+int pet_gemm_pair_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st);
+
 namespace pet_model_impl {
 
 using pet_attn::gemm_nn;
@@ -482,11 +487,13 @@ struct pet_model {
   int tier = 1;                // the memory tier of the last evaluation: 1 never, 2 wide
   std::unordered_map<std::string, Mat> m;
   std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
+  std::unordered_map<const float*, const void*> psplit;  // its fp16 pair rows at K <= 128 (the short-K kernel)
   // layers whose saved pre-activation holds its bias (made by the split-product
   // kernel's epilogue in the forward in progress), read by their backward
   std::unordered_map<std::string, bool> pre_biased;
   void* weights = nullptr;
   void* wsplit = nullptr;
+  void* wpair = nullptr;
   double* comp = nullptr;
   // A's fp16 pairs for the split-product kernel's pairs-by-pairs path, a row
   // chunk at a time (null: that path is not taken)
@@ -495,9 +502,10 @@ struct pet_model {
   Arena ws;
 
   ~pet_model() {
-    if (weights || wsplit || comp || ws.bytes()) (void) hipDeviceSynchronize();
+    if (weights || wsplit || wpair || comp || ws.bytes()) (void) hipDeviceSynchronize();
     if (weights) (void) hipFree(weights);
     if (wsplit) (void) hipFree(wsplit);
+    if (wpair) (void) hipFree(wpair);
     if (comp) (void) hipFree(comp);
     if (pairs) (void) hipFree(pairs);
   }
@@ -528,28 +536,57 @@ bool own_gemm(const pet_model& md, int M, int K) {
 }
 
 // out[M, N] = in W^T + beta out, W a model matrix [N, K]: rocBLAS fp32, or
-// this library's split-product kernel (gemm.hip) where W has a split copy (K a
-// multiple of 32) and in is 16-byte aligned rows -- by default for the large
-// products (M N K >= 2^32), every one with PET_OPT_MODEL_GEMM 3, none with
-// PET_OPT_MODEL_GEMM 0. Measured on MI355X (energy+forces, ms, same process):
-// C2 2.98 / 2.15 (residual) with rocBLAS, the same by default (no C2 product is
-// that large), 3.59 / 2.40 with all split; C5 276-279 with rocBLAS, 244 by
-// default and with all split.
-// W's split copy when in W^T takes the split-product kernel, else null.
-const void* split_for(const pet_model& md, const float* in, int64_t ldi, const float* W, int M, int N, int K) {
+// this library's kernels where W has a copy in their form and in is 16-byte
+// aligned rows. By PET_OPT_MODEL_GEMM: 4 (the default) the split-product
+// kernel for the large products (M N K >= 2^32), rocBLAS for the rest; 5
+// every product on this library's kernels -- the short-K kernel
+// (pet_linear_fused_smallk: A's rows as fp16 pairs in registers, four part
+// products) for K at most 128, the split-product kernel above -- so that no
+// result depends on how many rows come with it and every bias and activation
+// rides in an epilogue; 3 the split-product kernel for every product; 0
+// rocBLAS only. Measured on MI355X (energy+forces, ms): C2 2.81 / 2.06
+// (residual) with mode 4 (no C2 product is large), 2.88 / 1.92 with mode 5
+// (its kernels 2.25 ms of dense products against rocBLAS's 1.78, the
+// activation and bias passes gone), 3.59 / 2.40 with mode 3; C5 171 with mode
+// 4, 170 with mode 5. Mode 5's three-product split above K = 128 leaves C2's
+// energy 5.1e-7 from the float64 oracle (mode 4: 0.7e-7; the float32 oracle
+// 3.3e-7), so mode 4 stays the default.
+// The kernel a product takes (null: rocBLAS): the copy of W it reads and
+// whether it is the short-K kernel.
+struct Sel {
+  const void* p = nullptr;
+  bool sk = false;
+  explicit operator bool() const { return p != nullptr; }
+};
+Sel split_for(const pet_model& md, const float* in, int64_t ldi, const float* W, int M, int N, int K) {
   const int mode = md.gemm_mode;
   const bool big = double(M) * N * K >= 4294967296.0;
-  if ((mode == 3 || (mode == 4 && big)) && ldi % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
-    auto it = md.split.find(W);
-    if (it != md.split.end()) return it->second;
+  if (ldi % 4 || (reinterpret_cast<uintptr_t>(in) & 15)) return {};
+  if (mode == 5 && K <= 128 && K % 32 == 0) {
+    auto it = md.psplit.find(W);
+    if (it != md.psplit.end()) return {it->second, true};
   }
-  return nullptr;
+  if (mode == 3 || mode == 5 || (mode == 4 && big)) {
+    auto it = md.split.find(W);
+    if (it != md.split.end()) return {it->second, false};
+  }
+  return {};
+}
+// C = epilogue(in W^T) on the kernel sel names
+int own_nt(const pet_model& md, const Sel& sel, int M, int N, int K, const float* in, int64_t ldi, float* C,
+           int64_t ldc, const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+           float* pre, int64_t ldpre, int act, hipStream_t st) {
+  if (sel.sk)
+    return pet_linear_fused_smallk(M, N, K, in, ldi, sel.p, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre,
+                                   act, st);
+  return pet_gemm_nt_split(M, N, K, in, ldi, sel.p, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre, act, st,
+                           md.pairs, md.pairs ? md.kPairsBytes : 0);
 }
 int gemm_w(const pet_model& md, float* out, int64_t ldo, const float* in, int64_t ldi, const float* W, int M, int N,
            int K, float beta, hipStream_t st) {
-  if (const void* sp = split_for(md, in, ldi, W, M, N, K))
-    return pet_gemm_nt_split(M, N, K, in, ldi, sp, out, ldo, nullptr, nullptr, beta != 0.f ? out : nullptr, ldo, beta,
-                             nullptr, 0, 0, st, md.pairs, md.pairs ? md.kPairsBytes : 0);
+  if (const Sel sp = split_for(md, in, ldi, W, M, N, K))
+    return own_nt(md, sp, M, N, K, in, ldi, out, ldo, nullptr, nullptr, beta != 0.f ? out : nullptr, ldo, beta,
+                  nullptr, 0, 0, st);
   return gemm_nt(out, ldo, in, ldi, W, M, N, K, beta, st);
 }
 
@@ -564,9 +601,8 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
-  if (const void* sp = split_for(md, in, K, W.p, M, W.rows, K)) {  // the bias in the epilogue
-    ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st,
-                         md.pairs, md.pairs ? md.kPairsBytes : 0));
+  if (const Sel sp = split_for(md, in, K, W.p, M, W.rows, K)) {  // the bias in the epilogue
+    ok(own_nt(md, sp, M, W.rows, K, in, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
   if (rows4_ok(W.rows, {out, b}))
@@ -597,9 +633,9 @@ void linear_acc_bias(pet_model& md, float* out, const float* in, int M, int K, c
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   if (M == 0) return;
-  if (const void* sp = own_gemm(md, M, K) ? nullptr : split_for(md, in, K, W.p, M, W.rows, K)) {
-    ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, W.rows, nullptr, md.p(key + ".bias"), out, W.rows, 1.f,
-                         nullptr, 0, 0, st, md.pairs, md.pairs ? md.kPairsBytes : 0));
+  if (const Sel sp = own_gemm(md, M, K) ? Sel{} : split_for(md, in, K, W.p, M, W.rows, K)) {
+    ok(own_nt(md, sp, M, W.rows, K, in, K, out, W.rows, nullptr, md.p(key + ".bias"), out, W.rows, 1.f, nullptr, 0, 0,
+              st));
     return;
   }
   add_bias_pass(out, md.p(key + ".bias"), int64_t(M), W.rows, st);
@@ -622,11 +658,11 @@ const float* pass_bias(const pet_model& md, const std::string& key);
 bool linear_bwd_act(pet_model& md, float* out, const float* adj, int M, const std::string& key_out, const float* z,
                     const std::string& key_act, int act, hipStream_t st) {
   const Mat& WT = md.w(key_out + ".weight^T");
-  const void* sp = M ? split_for(md, adj, WT.cols, WT.p, M, WT.rows, WT.cols) : nullptr;
+  const Sel sp = M ? split_for(md, adj, WT.cols, WT.p, M, WT.rows, WT.cols) : Sel{};
   if (!sp) return false;
   const int64_t w = act == 2 ? 2 * int64_t(WT.rows) : WT.rows;
-  ok(pet_gemm_nt_split(M, WT.rows, WT.cols, adj, WT.cols, sp, out, w, nullptr, pass_bias(md, key_act), z, w, 0.f,
-                       nullptr, 0, act == 2 ? 4 : 3, st, md.pairs, md.pairs ? md.kPairsBytes : 0));
+  ok(own_nt(md, sp, M, WT.rows, WT.cols, adj, WT.cols, out, w, nullptr, pass_bias(md, key_act), z, w, 0.f, nullptr, 0,
+            act == 2 ? 4 : 3, st));
   return true;
 }
 // z[M, Nout] = in W^T, no bias: the pre-activation an activation pass reads with its bias
@@ -648,18 +684,18 @@ void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const st
 // Whether linear_act fuses the layer (then out must be a buffer other than in).
 bool act_fuses(const pet_model& md, const float* in, int M, int K, const std::string& key) {
   const Mat& W = md.w(key + ".weight");
-  return !own_gemm(md, M, K) && split_for(md, in, K, W.p, M, W.rows, K) != nullptr;
+  return !own_gemm(md, M, K) && bool(split_for(md, in, K, W.p, M, W.rows, K));
 }
 bool linear_act(pet_model& md, float* out, float* z, const float* in, int M, int K, const std::string& key, int act,
                 hipStream_t st) {
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   // (out must not be the GEMM's input: other workgroups still read its rows)
-  const void* sp = own_gemm(md, M, K) || out == in ? nullptr : split_for(md, in, K, W.p, M, W.rows, K);
-  md.pre_biased[key] = sp != nullptr;
+  const Sel sp = own_gemm(md, M, K) || out == in ? Sel{} : split_for(md, in, K, W.p, M, W.rows, K);
+  md.pre_biased[key] = bool(sp);
   if (!sp || M == 0) return false;
-  ok(pet_gemm_nt_split(M, W.rows, K, in, K, sp, out, act == 2 ? W.rows / 2 : W.rows, nullptr, md.p(key + ".bias"),
-                       nullptr, 0, 0.f, z, W.rows, act, st, md.pairs, md.pairs ? md.kPairsBytes : 0));
+  ok(own_nt(md, sp, M, W.rows, K, in, K, out, act == 2 ? W.rows / 2 : W.rows, nullptr, md.p(key + ".bias"), nullptr, 0,
+            0.f, z, W.rows, act, st));
   return true;
 }
 // the bias the activation passes add to a saved pre-activation: none where the
@@ -1501,6 +1537,21 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
         void* dst = static_cast<char*>(md->wsplit) + o;
         ok(pet_linear_split_weights(mt->p, mt->rows, mt->cols, mt->cols, dst, nullptr));
         md->split[mt->p] = dst;
+      }
+      if (hipDeviceSynchronize() != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
+    }
+    // fp16 pair rows of the matrices with K at most 128, for the short-K kernel
+    std::vector<std::pair<const Mat*, size_t>> pat;
+    size_t ptotal = 0;
+    for (auto& [n, mt] : md->m)
+      if (mt.cols > 0 && mt.cols <= 128 && mt.cols % 32 == 0)
+        pat.push_back({&mt, ptotal}), ptotal += (size_t(4) * mt.rows * mt.cols + size_t(4) * mt.rows + 255) & ~size_t(255);
+    if (ptotal) {
+      if (hipMalloc(&md->wpair, ptotal) != hipSuccess) throw Error{PET_MODEL_EMEMORY};
+      for (auto& [mt, o] : pat) {
+        void* dst = static_cast<char*>(md->wpair) + o;
+        ok(pet_gemm_pair_weights(mt->p, mt->rows, mt->cols, mt->cols, false, dst, nullptr));
+        md->psplit[mt->p] = dst;
       }
       if (hipDeviceSynchronize() != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
     }

@@ -33,6 +33,24 @@ class SplitWeights:
                    "pet_linear_split_weights" + ("_transposed" if transposed else ""))
 
 
+class PairWeights:
+    """W [N, K] (K a multiple of 32) as fp16 pair rows at any K (each row
+    scaled by a power of two, hi and lo parts both rounded to nearest),
+    N K 4 + N 4 bytes: the weights of the short-contraction layer
+    (pet_linear_fused_smallk, K at most 128)."""
+
+    def __init__(self, W: torch.Tensor):
+        _check(W, "W")
+        N, K = W.shape
+        if K % 32:
+            raise ValueError(f"W has K = {K}: pair weights need K a multiple of 32")
+        self.shape = (N, K)
+        self.data = torch.empty(N * K * 2 + 2 * N + 8, dtype=torch.int16, device=W.device)
+        _lib.check(_lib.load().pet_linear_pair_weights(W.data_ptr(), N, K, W.stride(0), self.data.data_ptr(),
+                                                       torch.cuda.current_stream().cuda_stream),
+                   "pet_linear_pair_weights")
+
+
 class PairRows:
     """A [M, K] (K a multiple of 32 and at least 256) as fp16 pairs of
     power-of-two-scaled rows, M K 4 + M 4 bytes of device memory: made once
@@ -89,7 +107,7 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
         _check(A, "A")
         M, K = A.shape
         dev = A.device
-    if isinstance(W, SplitWeights):
+    if isinstance(W, (SplitWeights, PairWeights)):
         N, Kw = W.shape
         if W.data.device != dev:
             raise ValueError(f"W: on {W.data.device}, A on {dev}")
@@ -117,7 +135,13 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
     ld = lambda t: 0 if t is None else t.stride(0)
     st = torch.cuda.current_stream().cuda_stream
     lib = _lib.load()
-    if isinstance(A, PairRows):
+    if isinstance(W, PairWeights):
+        if isinstance(A, PairRows) or K > 128:
+            raise ValueError("pair weights take fp32 A and K at most 128 (pet_linear_fused_smallk)")
+        _lib.check(lib.pet_linear_fused_smallk(M, N, K, p(A), A.stride(0), W.data.data_ptr(), p(C), C.stride(0),
+                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
+                   "pet_linear_fused_smallk")
+    elif isinstance(A, PairRows):
         _lib.check(lib.pet_linear_fused_pairs(M, N, K, A.data.data_ptr(), W.data.data_ptr(), p(C), C.stride(0),
                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
                    "pet_linear_fused_pairs")

@@ -23,7 +23,9 @@ def split_weights(W):
 
 
 def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, split=False):
-    L.fused(A, split_weights(W) if split else W, C, row_scale, bias, cin, beta, pre, act)
+    # split: False (fp32 products), True (split weights), "smallk" (pair weights, K <= 128)
+    Wf = L.PairWeights(W) if split == "smallk" else split_weights(W) if split else W
+    L.fused(A, Wf, C, row_scale, bias, cin, beta, pre, act)
 
 
 # the last two are large enough for the split form's 128 x 128 and 128 x 64 tiles
@@ -31,11 +33,13 @@ SHAPES = [(1, 16, 16), (37, 40, 32), (300, 128, 128), (2049, 96, 256), (5000, 38
           (129, 64, 1024), (16385, 1024, 64), (131071, 96, 64)]
 
 
-@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
+@pytest.mark.parametrize("split", [False, True, "smallk"], ids=["fp32", "split", "smallk"])
 @pytest.mark.parametrize("M,N,K", SHAPES)
 def test_plain_and_bias(M, N, K, split, device):
     if split and K % 32:
         pytest.skip("the split form needs K a multiple of 32")
+    if split == "smallk" and K > 128:
+        pytest.skip("the short-contraction layer takes K at most 128")
     g = torch.Generator(device=device).manual_seed(M + N + K)
     A = torch.randn(M, K, device=device, generator=g)
     W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
@@ -50,7 +54,7 @@ def test_plain_and_bias(M, N, K, split, device):
     assert torch.equal(C, C2)
 
 
-@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
+@pytest.mark.parametrize("split", [False, True, "smallk"], ids=["fp32", "split", "smallk"])
 def test_epilogues(split, device):
     M, N, K = 777, 256, 128
     g = torch.Generator(device=device).manual_seed(5)
@@ -348,3 +352,35 @@ def test_split_scratch_chunks_same_bits(device):
         assert torch.equal(outs[0][0], outs[1][0]), kw.keys()
         if outs[0][1] is not None:
             assert torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("K", [32, 64, 96, 128])
+def test_smallk_rows_independent_of_M(K, device):
+    # pet_linear_fused_smallk: a row's results are the same bits whatever
+    # rows come with it (M, and where the row falls in a tile): the full
+    # product against the product of rows 77 .. 77 + 301 alone, with SwiGLU and
+    # the kept pre-activation, N 384 (six column tiles) and N 72 (a partial one)
+    for N in (384, 72):
+        M = 1000
+        g = torch.Generator(device=device).manual_seed(K + N)
+        A = torch.randn(M, K, device=device, generator=g) * torch.logspace(-3, 3, M, device=device)[:, None]
+        W = L.PairWeights(torch.randn(N, K, device=device, generator=g) / K ** 0.5)
+        b = torch.randn(N, device=device, generator=g)
+        C, pre = torch.empty(M, N // 2, device=device), torch.empty(M, N, device=device)
+        L.fused(A, W, C, bias=b, pre=pre, act=2)
+        A2 = A[77:378].clone()
+        C2, pre2 = torch.empty(301, N // 2, device=device), torch.empty(301, N, device=device)
+        L.fused(A2, W, C2, bias=b, pre=pre2, act=2)
+        assert torch.equal(C[77:378], C2) and torch.equal(pre[77:378], pre2)
+        z = A.double() @ W_ref(W, device).T + b.double()
+        assert (pre.double() - z).abs().max().item() <= 1e-5 * z.abs().max().item()
+
+
+def W_ref(W, device):
+    """The fp64 matrix of pair weights: hi + lo over each row's scale."""
+    N, K = W.shape
+    raw = W.data.cpu().numpy().view(np.uint8)
+    parts = raw[: N * K * 4].view(np.float16).reshape(N, K // 8, 2, 8).astype(np.float64)
+    inv = raw[N * K * 4: N * K * 4 + 4 * N].view(np.float32).astype(np.float64)
+    w = (parts[:, :, 0, :] + parts[:, :, 1, :]).reshape(N, K) * inv[:, None]
+    return torch.from_numpy(w).to(device)
