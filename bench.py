@@ -406,6 +406,37 @@ def main():
                          fwd_mb=alg["fwd_bytes"] / 1e6, bwd_mb=alg["bwd_bytes"] / 1e6),
         wall_s=wall,
     )
+    # the kernels' own access pattern with no arithmetic (pet_attn_access_floor,
+    # head_dim 32): the floor their HBM traffic sets on this device
+    if hd == 32 and S <= 128:
+        lib = _lib.load()
+        shp = _lib.Shape(N, T, S, H, hd, 0, lib.pet_attn_scale(hd, 1.0))
+        mp, mlp = torch.empty_like(merged), torch.empty_like(ml)
+        qap, cfhp = torch.empty_like(qkv_adj), torch.empty_like(cfh)
+        st = torch.cuda.current_stream().cuda_stream
+        import ctypes
+
+        def floor_call(bwd):
+            _lib.check(lib.pet_attn_access_floor(ctypes.byref(shp), bwd, qkv.data_ptr(), 3 * D, off.data_ptr(),
+                                                 dm.data_ptr(), D, (merged if bwd else mp).data_ptr(), D,
+                                                 mlp.data_ptr(), qap.data_ptr(), 3 * D, cfhp.data_ptr(), st),
+                       "pet_attn_access_floor")
+        fl = {}
+        for bwd in (0, 1):
+            for _ in range(5):
+                floor_call(bwd)
+            f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            f0.record()
+            for _ in range(20):
+                floor_call(bwd)
+            f1.record()
+            torch.cuda.synchronize()
+            fl["bwd" if bwd else "fwd"] = f0.elapsed_time(f1) * 1e3 / 20
+        extra["access_floor_us"] = fl
+        extra["core_frac_of_access_floor"] = (fl["fwd"] + fl["bwd"]) / us_per_step
+        extra["access_floor_note"] = ("pet_attn_access_floor: the fp16-pair kernels' grid, item order and bytes with "
+                                      "no arithmetic; the floor their traffic sets on this device")
+        del mp, mlp, qap, cfhp
     # the box's achievable streaming rate, for scale: a plain 1 GiB device copy
     # (read + write) timed the same way; the roofline stays against 8 TB/s
     src = torch.empty(1 << 28, device=device)

@@ -185,6 +185,17 @@ PET_ATTN_API int pet_attn_bwd_noalloc(const pet_attn_shape* shape, const float* 
                                       const float* ml, const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda,
                                       float* cf_seq_adj, int64_t ldca, void* stream);
 
+/* For measurement: the HBM access pattern of the head_dim-32 fp16-pair kernels
+ * alone -- their grid, item order and bytes (forward: q, k, v read, merged and
+ * ml written; backward nonzero: q, k, v, dO, O read, qkv_adj and cfh
+ * written) with no arithmetic between -- into the buffers given (values
+ * meaningless). Its duration is the floor the kernels' traffic sets on the
+ * device. Head_dim 32 and at most 128 slots only. No counterpart in the
+ * reference: it calibrates the roofline. */
+PET_ATTN_API int pet_attn_access_floor(const pet_attn_shape* shape, int backward, const float* qkv, int64_t ldq,
+                                       const int* off, const float* dmerged, int64_t ldg, float* merged, int64_t ldm,
+                                       float* ml, float* qkv_adj, int64_t lda, float* cfh, void* stream);
+
 /* ---- runs of atoms: the kernels of attention_chunked / _bwd_chunked ------ */
 
 /* pet_attn_fwd / pet_attn_bwd on qkv given as raw + transform: the attention

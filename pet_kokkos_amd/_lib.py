@@ -54,6 +54,7 @@ EXPORTS = (
     "pet_linear_fused_split",
     "pet_linear_fused_split_ws",
     "pet_linear_pair_weights",
+    "pet_attn_access_floor",
     "pet_linear_fused_smallk",
     "pet_linear_pair_rows",
     "pet_linear_fused_pairs",
@@ -220,6 +221,9 @@ def load() -> ctypes.CDLL:
     lib.pet_linear_split_weights_transposed.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_split.restype = ctypes.c_int
     lib.pet_linear_fused_split.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
+    lib.pet_attn_access_floor.restype = ctypes.c_int
+    lib.pet_attn_access_floor.argtypes = [ctypes.POINTER(Shape), _I, _P, _I64, _P, _P, _I64, _P, _I64, _P, _P, _I64,
+                                          _P, _P]
     lib.pet_linear_pair_weights.restype = ctypes.c_int
     lib.pet_linear_pair_weights.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_smallk.restype = ctypes.c_int

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpet_attn.so")
-SOURCES = ["attention.hip", "attention_pair.hip", "attention_stream.hip", "ops.hip", "rows.hip", "forces.hip", "model.hip", "gemm.hip"]
+SOURCES = ["attention.hip", "attention_pair.hip", "attention_stream.hip", "ops.hip", "rows.hip", "forces.hip", "model.hip", "gemm.hip", "probe.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
