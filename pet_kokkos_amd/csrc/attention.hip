@@ -638,10 +638,19 @@ __global__ void attn_cf_adjoint_kernel(const float* __restrict__ cfh, const floa
   if (i >= int64_t(N) * S) return;
   const int n = int(i / S), k = int(i - int64_t(n) * S);
   const float cf = cf_seq[int64_t(n) * ldc + k];
-  if (cf <= 0.f) return;
+  // the heads' loads issued eight at a time (with cf's), then summed in head order
+  const float* p = cfh + int64_t(n) * H * S + k;
   float total = 0.f;
-  for (int hh = 0; hh < H; ++hh) total += cfh[(int64_t(n) * H + hh) * S + k];
-  cf_seq_adj[int64_t(n) * ldca + k] += total / cf;
+  int hh = 0;
+  for (; hh + 8 <= H; hh += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[int64_t(hh + u) * S];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) total += v[u];
+  }
+  for (; hh < H; ++hh) total += p[int64_t(hh) * S];
+  if (cf > 0.f) cf_seq_adj[int64_t(n) * ldca + k] += total / cf;
 }
 
 // A capacity's dead rows, N + off[N] .. T-1, of x[T, width] set to zero
