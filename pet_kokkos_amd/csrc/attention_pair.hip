@@ -124,16 +124,21 @@ __device__ __forceinline__ void pair2s(float x, float y, float s, unsigned& hi, 
   lo = __builtin_bit_cast(unsigned, l);
 }
 
-// The largest x over a row of 16 lanes, in every lane of the row (DPP row
-// rotations by 1, 2, 4, 8: vector instructions, no LDS).
+// The largest x over a row of 16 lanes, in every lane of the row, for x >= 0
+// (norms): DPP row rotations by 1, 2, 4, 8, each folded into an integer max
+// of the bit patterns (which order non-negative floats as their values do;
+// fmaxf would canonicalize each operand first, an instruction more a step).
+// A rotation within a full row reads a live lane everywhere, so the DPP's old
+// value (0) is never taken.
 __device__ __forceinline__ float row_max16(float x) {
-#define PET_ROR(n) x = fmaxf(x, __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(x), 0x120 + (n), 0xf, 0xf, false)))
+  int v = __float_as_int(x);
+#define PET_ROR(n) v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x120 + (n), 0xf, 0xf, true))
   PET_ROR(1);
   PET_ROR(2);
   PET_ROR(4);
   PET_ROR(8);
 #undef PET_ROR
-  return x;
+  return __int_as_float(v);
 }
 // The exponent k of the pair scale 2^k that puts m = f 2^e (f in [0.5, 1))
 // at [2^14, 2^15): 15 - e; 0 for a zero (or non-finite) m.
