@@ -108,10 +108,46 @@ def test_batched_equals_alone_c5(device):
         print(f"    structure {k} ({b - a} atoms): energy {de:.1e} relative, per-atom {dpa:.1e}, forces {df:.1e} eV/A",
               flush=True)
         # the batch's large dense products run on the split-product kernel and
-        # a lone structure's on rocBLAS: the two differ by fp32 roundings (on
-        # C2-size products a per-atom energy differs from the float64 oracle
-        # by about 1e-6 of the largest)
+        # a lone structure's on rocBLAS (the default model_gemm 4): the two
+        # differ by fp32 roundings (on C2-size products a per-atom energy
+        # differs from the float64 oracle by about 1e-6 of the largest;
+        # measured here up to 5.3e-5 eV/A on forces). With every product on
+        # this library's kernels the two are the same bits
+        # (test_batched_equals_alone_c5_own_kernels)
         assert de <= 5e-6 and dpa <= 5e-6 and df <= 1e-4
+
+
+def test_batched_equals_alone_c5_own_kernels(device):
+    """Under PET_OPT_MODEL_GEMM 5 every dense product runs on this library's
+    kernels, whose results for a row do not depend on the other rows; the
+    attention, norms and folds are per item, row or atom. So a structure's
+    per-atom energies and forces in the 32-structure C5 batch are the same
+    bits as the structure's alone, and its energy (a per-structure sum of the
+    same per-atom values) too."""
+    from pet_kokkos_amd import _lib
+    h, w, comp, sts = ef_workload("c5")
+    old = _lib.get_option("model_gemm")
+    _lib.set_option("model_gemm", 5)
+    try:
+        m = PetModel(h, w, comp)
+        print(f"[gpu] c5 batch of {len(sts)} structures against four of them alone, model_gemm 5", flush=True)
+        x = structures_input(h, sts, device)
+        got = m.compute(x, forces=True)
+        torch.cuda.synchronize()
+        pa_all, f_all, e_all = (got[k].cpu().numpy() for k in ("per_atom", "forces", "energy"))
+        soff = x.struct_off.cpu().numpy()
+        del x, got
+        for k in (0, 1, 16, 31):
+            alone = m.compute(structures_input(h, [sts[k]], device), forces=True)
+            torch.cuda.synchronize()
+            a, b = soff[k], soff[k + 1]
+            pa, f = alone["per_atom"].cpu().numpy(), alone["forces"].cpu().numpy()
+            e = float(alone["energy"][0])
+            print(f"    structure {k} ({b - a} atoms): per-atom max diff {np.abs(pa - pa_all[a:b]).max():.1e}, "
+                  f"forces {np.abs(f - f_all[a:b]).max():.1e}, energy {abs(e - e_all[k]):.1e}", flush=True)
+            assert np.array_equal(pa, pa_all[a:b]) and np.array_equal(f, f_all[a:b]) and e == e_all[k]
+    finally:
+        _lib.set_option("model_gemm", old)
 
 
 def test_supercell_is_extensive(device):
