@@ -112,7 +112,11 @@ enum {
                               for the backward; 2 "wide": the attention's qkv and the edge MLP's pre-activation not
                               kept but recomputed in the backward, the edge MLP run over chunks of edge rows (the
                               reference's Recompute::Wide, src/model.cpp:819-860) -- the same results */
-  PET_OPT_COUNT = 9
+  PET_OPT_MODEL_PAIRS = 9, /* the whole evaluation's MLPs: 1 (default) an activation, or its adjoint, that only the
+                              next product reads passes to it as block pairs (pet_linear_fused_split_blocks /
+                              pet_linear_fused_blocks) where both products take the pairs-by-pairs kernel; 0 as
+                              fp32 and a split pass */
+  PET_OPT_COUNT = 10
 };
 
 /* Sets an option; PET_ATTN_EINVAL for an unknown option or a value out of range. */

@@ -187,6 +187,34 @@ PET_ATTN_API int pet_linear_fused_pairs(int M, int N, int K, const void* Apairs,
                                         int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                         int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
 
+/* Block pairs: a product's output made directly as the fp16 pairs the next
+ * product reads, with no fp32 round trip and no separate split pass.
+ * pet_linear_fused_split_blocks is pet_linear_fused_split_ws (the pairs-by-pairs
+ * path: K a multiple of 32 and at least 256, N >= 512 and a multiple of 128,
+ * a scratch of at least 128 rows of A's pairs) with the epilogue's output
+ * act(...) written into `out` instead of C: M rows of out_cols fp16 pairs
+ * (out_cols = N / 2 for SwiGLU, 2 N for its backward, else N; a multiple of
+ * 32), each row's 128-column tiles of the product scaled by their own power of
+ * two (the largest |value| of the block at [2^14, 2^15)), then the blocks'
+ * inverse scales [out_cols / kb][M]: M * out_cols * 4 + M * (out_cols / kb) * 4
+ * bytes, 16-byte aligned. *kb receives the block width in output columns (64
+ * for SwiGLU, 256 for its backward, 128 otherwise). Every epilogue operand
+ * 16-byte aligned, leading dimensions multiples of 4.
+ * pet_linear_fused_blocks is pet_linear_fused_pairs with A as such blocks (K =
+ * out_cols, kb as returned, at most 32 blocks): each block's products summed
+ * on their own, then into the total times the block's inverse scale. No
+ * counterpart in the reference, whose fused layers (src/fused_gemm_hip.cpp:345-400)
+ * write fp32. */
+PET_ATTN_API int pet_linear_fused_split_blocks(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit,
+                                               void* out, const float* row_scale, const float* bias,
+                                               const float* cin, int64_t ldcin, float beta, float* pre,
+                                               int64_t ldpre, int act, void* scratch, size_t scratch_bytes, int* kb,
+                                               void* stream);
+PET_ATTN_API int pet_linear_fused_blocks(int M, int N, int K, const void* Ablocks, int kb, const void* Wsplit,
+                                         float* C, int64_t ldc, const float* row_scale, const float* bias,
+                                         const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre,
+                                         int act, void* stream);
+
 /* Bytes of device workspace the model holds now (its high-water mark). */
 PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
 /* Bytes of the model's pairs scratch (the large products' A operands as fp16

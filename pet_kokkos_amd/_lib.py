@@ -58,6 +58,8 @@ EXPORTS = (
     "pet_linear_fused_smallk",
     "pet_linear_pair_rows",
     "pet_linear_fused_pairs",
+    "pet_linear_fused_split_blocks",
+    "pet_linear_fused_blocks",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX, ESCRATCH = range(10)
@@ -235,6 +237,11 @@ def load() -> ctypes.CDLL:
     lib.pet_linear_pair_rows.argtypes = [_P, _I, _I, _I64, _P, _P]
     lib.pet_linear_fused_pairs.restype = ctypes.c_int
     lib.pet_linear_fused_pairs.argtypes = [_I, _I, _I, _P, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
+    lib.pet_linear_fused_split_blocks.restype = ctypes.c_int
+    lib.pet_linear_fused_split_blocks.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _P, _P, _P, _I64, _F, _P, _I64, _I,
+                                                  _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), _P]
+    lib.pet_linear_fused_blocks.restype = ctypes.c_int
+    lib.pet_linear_fused_blocks.argtypes = [_I, _I, _I, _P, _I, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_model_workspace_bytes.restype = ctypes.c_size_t
     lib.pet_model_workspace_bytes.argtypes = [_P]
     lib.pet_model_pairs_scratch_bytes.restype = ctypes.c_size_t
@@ -246,11 +253,11 @@ def load() -> ctypes.CDLL:
 
 
 OPTIONS = {"split": 1, "fwd_kernel": 2, "bwd_vlds": 3, "bwd_nbuf": 4, "model_gemm": 5, "attn_stream": 6, "bwd_kernel": 7,
-           "model_recompute": 8}
+           "model_recompute": 8, "model_pairs": 9}
 
 
 def set_option(name: str, value: int) -> None:
-    """pet_attn_set_option by name (split, fwd_kernel, bwd_vlds, bwd_nbuf, model_gemm, attn_stream, bwd_kernel)."""
+    """pet_attn_set_option by name (the keys of OPTIONS)."""
     check(load().pet_attn_set_option(OPTIONS[name], int(value)), f"pet_attn_set_option({name}={value})")
 
 

@@ -705,7 +705,7 @@ int waves_for(int S) { return (S + 15) / 16; }
 
 // Process-wide tuning options (pet_attn_set_option): each an atomic read
 // once per launch, never the environment.
-std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {4}, {0}, {0}, {0}};
+std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {4}, {0}, {0}, {0}, {1}};
 int option(int o) { return g_options[o].load(std::memory_order_relaxed); }
 bool split_enabled() { return option(PET_OPT_SPLIT) != 0; }
 
@@ -1004,7 +1004,7 @@ const char* pet_attn_strerror(int code) {
 
 int pet_attn_set_option(int opt, int value) {
   if (opt <= 0 || opt >= PET_OPT_COUNT) return PET_ATTN_EINVAL;
-  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 5, 1, 1, 2};
+  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 5, 1, 1, 2, 1};
   if (value < lo[opt] || value > hi[opt]) return PET_ATTN_EINVAL;
   g_options[opt].store(value, std::memory_order_relaxed);
   return PET_ATTN_OK;

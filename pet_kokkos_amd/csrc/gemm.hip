@@ -41,6 +41,7 @@ using pet_split::pack_hi;
 using pet_split::split3;
 using pet_split::split8;
 using pet_split::u4;
+using pet_split::u2;
 using pet_split::mfma3;
 using pet_split::mfma_h;
 using pet_split::pair2;
@@ -61,6 +62,15 @@ struct Epi {
   int64_t ldpre = 0;
   int act = 0;                       // 0 none, 1 SiLU, 2 SwiGLU (C has N/2 columns),
                                      // 3 / 4 the backward of SiLU / SwiGLU (below)
+  // Block pairs in place of C (staged epilogue only): the output row i as
+  // fp16 pairs in pair_act_kernel's layout (kgo k groups of 8 a row, each
+  // group's hi then lo 16 bytes), scaled per (row, column tile) -- the tile's
+  // output columns are one K block of the product that reads them -- with the
+  // block's inverse scale at pinv[block ldinv + i].
+  u4* pout = nullptr;
+  float* pinv = nullptr;
+  int64_t ldinv = 0;
+  int kgo = 0;
 };
 
 // The epilogue of one result element v at (i, j), shared by the kernels. Every
@@ -121,7 +131,7 @@ __device__ __forceinline__ void epilogue(const f4 (&acc)[WM / 16][WN / 16], int 
 // stores to four rows. False (nothing written) where a pointer or leading
 // dimension does not allow the 16-byte accesses; the caller then uses
 // epilogue(). tile: BM BN floats of LDS no wave still reads.
-template <int BM, int BN, int WGM, int WGN, int PASSES = 1>
+template <int BM, int BN, int WGM, int WGN, int PASSES = 1, bool PO = false>
 __device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][BN / WGN / 16], float* tile, int m0,
                                                 int n0, int M, int N, float* C, int64_t ldc, const Epi& epi) {
   constexpr int T = 64 * WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16, F = BN / 4;
@@ -130,7 +140,7 @@ __device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][B
   auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   const bool act4 = epi.act == 4, act2 = epi.act == 2;
   // C's columns: 2 N (act 4), N / 2 (act 2), else N; j stays a multiple of 4
-  const bool ok = n0 + BN <= N && a16(C) && ldc % 4 == 0 && (!epi.bias || a16(epi.bias)) &&
+  const bool ok = n0 + BN <= N && (PO || (a16(C) && ldc % 4 == 0)) && (!epi.bias || a16(epi.bias)) &&
                   (!epi.cin || (a16(epi.cin) && epi.ldcin % 4 == 0)) && (!epi.pre || (a16(epi.pre) && epi.ldpre % 4 == 0));
   if (!ok) return false;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
@@ -138,6 +148,51 @@ __device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][B
   auto slot = [](int R, int q) { return R * BN + 4 * (q ^ ((4 * (R >> 2)) & (F - 1))); };
   const int q = tid % F;
   const int j = n0 + 4 * q;
+  // a thread's NO outputs of row i from output column jo on: to C, or (block
+  // pairs) split by the power of two that puts the largest |output| of the
+  // row's BN-column tile at [2^14, 2^15) -- the row's F threads are
+  // consecutive lanes, F 16 or 32 -- with one thread a row writing the
+  // inverse scale
+  auto put = [&](int i, int jo, const float* o, auto no_c) {
+    constexpr int NO = decltype(no_c)::value;
+    if constexpr (!PO) {
+      float* dst = C + int64_t(i) * ldc + jo;
+      if constexpr (NO == 2) *reinterpret_cast<float2*>(dst) = make_float2(o[0], o[1]);
+      if constexpr (NO >= 4) *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+      if constexpr (NO == 8) *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    } else {
+    static_assert(F == 16 || F == 32, "a row's threads one or two DPP rows");
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < NO; ++e) m = fmaxf(m, fabsf(o[e]));
+    int mb = __float_as_int(m);  // |values|: the bit patterns order as the values
+#define PET_ROR(n) mb = max(mb, __builtin_amdgcn_update_dpp(0, mb, 0x120 + (n), 0xf, 0xf, true))
+    PET_ROR(1);
+    PET_ROR(2);
+    PET_ROR(4);
+    PET_ROR(8);
+#undef PET_ROR
+    if constexpr (F == 32) mb = max(mb, __shfl_xor(mb, 16));
+    const float sc = pair_scale(__int_as_float(mb));
+    unsigned h[NO / 2], lw[NO / 2];
+#pragma unroll
+    for (int e = 0; e < NO / 2; ++e) pair2(o[2 * e] * sc, o[2 * e + 1] * sc, h[e], lw[e]);
+    unsigned* hi = reinterpret_cast<unsigned*>(epi.pout + (int64_t(i) * epi.kgo + jo / 8) * 2) + (jo % 8) / 2;
+    if constexpr (NO == 2) hi[0] = h[0], hi[4] = lw[0];
+    if constexpr (NO == 4) {
+      *reinterpret_cast<u2*>(hi) = u2{h[0], h[1]};
+      *reinterpret_cast<u2*>(hi + 4) = u2{lw[0], lw[1]};
+    }
+    if constexpr (NO == 8) {
+      *reinterpret_cast<u4*>(hi) = u4{h[0], h[1], h[2], h[3]};
+      *reinterpret_cast<u4*>(hi + 4) = u4{lw[0], lw[1], lw[2], lw[3]};
+    }
+    if (q == 0) epi.pinv[int64_t(n0 / BN) * epi.ldinv + i] = 1.f / sc;
+    }
+  };
+  using c2 = std::integral_constant<int, 2>;
+  using c4 = std::integral_constant<int, 4>;
+  using c8 = std::integral_constant<int, 8>;
   float4 bj = make_float4(0.f, 0.f, 0.f, 0.f), bj2 = bj;
   if (epi.bias) {
     if (act4) {
@@ -177,7 +232,7 @@ __device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][B
           const float x = zz[e] + (epi.bias ? bb[e] : 0.f), sg = sig_fast(x);
           o[e] = v[e] * (sg * (1.0f + x * (1.0f - sg)));
         }
-        *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(o[0], o[1], o[2], o[3]);
+        put(i, j, o, c4{});
       } else {
         const float4 z0 = *reinterpret_cast<const float4*>(z + 2 * j), z1 = *reinterpret_cast<const float4*>(z + 2 * j + 4);
         const float zz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
@@ -189,9 +244,7 @@ __device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][B
           const float sg = sig_fast(zz[2 * e + 1] + (epi.bias ? bb[2 * e + 1] : 0.f));
           o[2 * e] = v[e] * sg, o[2 * e + 1] = v[e] * u * sg * (1.0f - sg);
         }
-        float* dst = C + int64_t(i) * ldc + 2 * j;
-        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        put(i, 2 * j, o, c8{});
       }
       continue;
     }
@@ -207,12 +260,13 @@ __device__ __forceinline__ bool staged_epilogue(const f4 (&acc)[BM / WGM / 16][B
     }
     if (epi.pre) *reinterpret_cast<float4*>(epi.pre + int64_t(i) * epi.ldpre + j) = make_float4(v[0], v[1], v[2], v[3]);
     if (act2) {
-      *reinterpret_cast<float2*>(C + int64_t(i) * ldc + j / 2) = make_float2(v[0] * sig_fast(v[1]), v[2] * sig_fast(v[3]));
+      const float o[2] = {v[0] * sig_fast(v[1]), v[2] * sig_fast(v[3])};
+      put(i, j / 2, o, c2{});
     } else {
       if (epi.act == 1)
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = v[e] * sig_fast(v[e]);
-      *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(v[0], v[1], v[2], v[3]);
+      put(i, j, v, c4{});
     }
   }
   }
@@ -795,8 +849,16 @@ __device__ __forceinline__ void wait_vm() {
 // (lane L of an instruction loads the part its slot L % 8 holds). The k order and the
 // epilogue's unscaling are gemm_nt_pair_kernel's, so the two give the same bits.
 // Tiles of WGM x WGN waves; K a multiple of 32.
-template <int BM, int BN, int WGM, int WGN, int ST>
-__global__ void __launch_bounds__(64 * WGM * WGN) gemm_pp_kernel(int M, int N, int K, const u4* __restrict__ Ap,
+// KBS > 0: A as block pairs (a staged epilogue's pout): A's scale is per (row,
+// K block of 32 KBS), the inverse scales [K / (32 KBS)][M] after the pairs.
+// Each block's products go to their own accumulators (cleared at the block's
+// start), which are then added into the total times the rows'
+// inverse scales for the block (staged in LDS after the ring at the start);
+// B's column scales are undone at the end.
+// PO: the output as block pairs (Epi::pout) from the staged epilogue.
+template <int BM, int BN, int WGM, int WGN, int ST, int KBS = 0, bool PO = false>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+__attribute__((amdgpu_waves_per_eu(BM == 128 && BN == 128 ? 4 : 1))) gemm_pp_kernel(int M, int N, int K, const u4* __restrict__ Ap,
                                                                   const u4* __restrict__ Bs, float* C, int64_t ldc,
                                                                   Epi epi, int WR) {
   constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
@@ -838,13 +900,36 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_pp_kernel(int M, int N, i
   for (int a = 0; a < TM; ++a)
 #pragma unroll
     for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+  // block pairs: the tile's rows' inverse scales of every K block into LDS
+  // after the ring (the loads issued before the ring's first steps, the
+  // stores after them)
+  constexpr int SPT = KBS > 0 ? (32 * BM + 64 * NW - 1) / (64 * NW) : 1;  // scales a thread, at most 32 blocks
+  float* scl = reinterpret_cast<float*>(ring + ST * SR * 8);
+  const int nblk = KBS > 0 ? steps / KBS : 0;
+  float sv[SPT];
+  if constexpr (KBS > 0) {
+    const float* inv_a = reinterpret_cast<const float*>(Ap + int64_t(M) * KG * 2);
+#pragma unroll
+    for (int u = 0; u < SPT; ++u) {
+      const int ti = tid + 64 * NW * u, kb = ti / BM, rw = ti % BM;
+      sv[u] = kb < nblk ? inv_a[int64_t(kb) * M + min(m0 + rw, M - 1)] : 0.f;
+    }
+  }
 #pragma unroll
   for (int s = 0; s < ST - 1; ++s)
     if (s < steps) issue(s);
+  if constexpr (KBS > 0) {
+#pragma unroll
+    for (int u = 0; u < SPT; ++u) {
+      const int ti = tid + 64 * NW * u;
+      if (ti < nblk * BM) scl[ti] = sv[u];
+    }
+  }
   const int fc = ((c >> 2) & 1) | ((c >> 1) & 4);  // f(row), row & 15 = c
   const int sw0 = (2 * g) ^ fc, sw1 = (2 * g + 1) ^ fc;
-  for (int s = 0; s < steps; ++s) {
-    // step s's loads done (those after it may still fly), then every wave's
+  // step s: its loads done (those after it may still fly), every wave's
+  // reads of the stage it refills done, the refill issued, the products
+  auto step = [&](int s) {
     const int after = min(ST - 2, steps - 1 - s);
     if (after >= ST - 2) wait_vm<(ST - 2) * LPW>();
     else if constexpr (ST >= 4) {
@@ -879,21 +964,56 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_pp_kernel(int M, int N, i
 #pragma unroll
         for (int b = 0; b < TN; ++b)
           acc[a][b] = pet_split::mfma_h(av[a][p == 0 ? 1 : 0], bv[b][p == 1 ? 1 : 0], acc[a][b]);
-  }
-  const float* inv_a = reinterpret_cast<const float*>(Ap + int64_t(M) * KG * 2);
+  };
   const float* inv_b = reinterpret_cast<const float*>(Bs + int64_t(N) * KG * 2);
+  if constexpr (KBS == 0) {
+    for (int s = 0; s < steps; ++s) step(s);
+    const float* inv_a = reinterpret_cast<const float*>(Ap + int64_t(M) * KG * 2);
 #pragma unroll
-  for (int b = 0; b < TN; ++b) {
-    const float ib = inv_b[min(n0 + wn * WN + 16 * b + c, N - 1)];
+    for (int b = 0; b < TN; ++b) {
+      const float ib = inv_b[min(n0 + wn * WN + 16 * b + c, N - 1)];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          acc[a][b][rr] = acc[a][b][rr] * inv_a[min(m0 + wm * WM + 16 * a + 4 * g + rr, M - 1)] * ib;
+    }
+  } else {
+    f4 tot[TM][TN];
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        acc[a][b][rr] = acc[a][b][rr] * inv_a[min(m0 + wm * WM + 16 * a + 4 * g + rr, M - 1)] * ib;
+      for (int b = 0; b < TN; ++b) tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nblk; ++kb) {
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+      for (int ss = 0; ss < KBS; ++ss) step(kb * KBS + ss);
+      // the block into the total, times its rows' inverse scales (rows 4g .. 4g + 3 of each tile)
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+        const float4 ia = *reinterpret_cast<const float4*>(scl + kb * BM + wm * WM + 16 * a + 4 * g);
+        const float iar[4] = {ia.x, ia.y, ia.z, ia.w};
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) tot[a][b][rr] = fmaf(acc[a][b][rr], iar[rr], tot[a][b][rr]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const float ib = inv_b[min(n0 + wn * WN + 16 * b + c, N - 1)];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) acc[a][b][rr] = tot[a][b][rr] * ib;
+    }
   }
   static_assert(ST * (BM + BN) * 128 >= BM * BN * 4, "the ring holds the result tile");
-  if (staged_epilogue<BM, BN, WGM, WGN>(acc, reinterpret_cast<float*>(ring), m0, n0, M, N, C, ldc, epi)) return;
-  epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);
+  if (staged_epilogue<BM, BN, WGM, WGN, 1, PO>(acc, reinterpret_cast<float*>(ring), m0, n0, M, N, C, ldc, epi)) return;
+  if constexpr (!PO) epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);  // (block pairs: the host makes sure of the staged one)
 }
 
 // Small K (at most 128): A resident in the waves' registers. A workgroup of
@@ -1090,7 +1210,7 @@ extern "C" int pet_linear_fused(int M, int N, int K, const float* A, int64_t lda
 }
 
 int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C, int64_t ldc, const Epi& e,
-                   hipStream_t st);
+                   hipStream_t st, bool tile128 = false);
 int pet_gemm_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, hipStream_t st);
 
 // The pairs-by-pairs path's threshold: from N = 512 the products' gain
@@ -1100,31 +1220,35 @@ int pet_gemm_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, hip
 // 4634 against 342 + 3443; with a kept pre-activation 5760 against 4244).
 constexpr int kPairsMinN = 512;
 
-int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
-                      const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
-                      float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch, size_t scratch_bytes) {
+// The split-product GEMM with the epilogue e (block pairs out where e.pout:
+// then 128 x 128 tiles, so that an output row's K blocks are 128 columns of
+// the product wide).
+int split_impl(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc, Epi e,
+               hipStream_t st, void* scratch, size_t scratch_bytes) {
   if (M < 0 || N < 0 || K < 0) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
   if (K == 0) return PET_ATTN_EINVAL;
   if (int64_t((M + 63) / 64) * ((N + 63) / 64) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;  // 1-D grid of tiles
   if (K % 32 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15))
     return PET_ATTN_EALIGN;
-  if (act == 2 && N % 2) return PET_ATTN_EINVAL;
-  Epi e;
-  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
-  e.act = act;
+  if (e.act == 2 && N % 2) return PET_ATTN_EINVAL;
+  const int64_t ldcin = e.ldcin, ldpre = e.ldpre;
+  const bool t128 = e.pout != nullptr;
   // A's rows split into the scratch a chunk at a time (as many rows as it
   // holds, a multiple of 128), each chunk's product from the pairs
   const int64_t chunk = scratch ? int64_t(scratch_bytes / (size_t(K) * 4 + 4)) / 128 * 128 : 0;
-  if (pair_form(K) && N >= kPairsMinN && chunk >= 128 && (reinterpret_cast<uintptr_t>(scratch) & 15) == 0) {
+  const bool pp = pair_form(K) && N >= kPairsMinN && chunk >= 128 && (reinterpret_cast<uintptr_t>(scratch) & 15) == 0;
+  if (t128 && !pp) return PET_ATTN_EINVAL;  // block pairs out: the pairs-by-pairs kernel only
+  if (pp) {
     for (int64_t r0 = 0; r0 < M; r0 += chunk) {
       const int m = int(std::min<int64_t>(chunk, M - r0));
       Epi ec = e;
       if (ec.row_scale) ec.row_scale += r0;
       if (ec.cin) ec.cin += r0 * ldcin;
       if (ec.pre) ec.pre += r0 * ldpre;
+      if (ec.pout) ec.pout += r0 * ec.kgo * 2, ec.pinv += r0;
       int rc = pet_gemm_pair_rows(A + r0 * lda, m, K, lda, scratch, st);
-      if (rc == PET_ATTN_OK) rc = pet_gemm_nt_pp(m, N, K, scratch, Bs, C + r0 * ldc, ldc, ec, st);
+      if (rc == PET_ATTN_OK) rc = pet_gemm_nt_pp(m, N, K, scratch, Bs, C ? C + r0 * ldc : C, ldc, ec, st, t128);
       if (rc != PET_ATTN_OK) return rc;
     }
     return PET_ATTN_OK;
@@ -1146,23 +1270,60 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
   // 1535 for 64 x 64; 256 x 128 and 128 x 256 tiles of 16 waves were no
   // faster), 64 x 64 otherwise (27318 x 128 x 128: 16.1 against 18.4 us); one
   // LDS buffer beat two in every shape
-  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
+  const int64_t tiles128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
   if (pair_form(K)) {
-    if (N >= 128 && t128 >= 2048)
+    if (t128 || (N >= 128 && tiles128 >= 2048))
       go(gemm_nt_pair_kernel<128, 128, 2, 4>, 128, 128, 512, true);
-    else if (t128 >= 2048)
+    else if (tiles128 >= 2048)
       go(gemm_nt_pair_kernel<128, 64>, 128, 64, 256, true);
     else
       go(gemm_nt_pair_kernel<64, 64>, 64, 64, 256, true);
   } else {
-    if (N >= 128 && t128 >= 2048)
+    if (t128 || (N >= 128 && tiles128 >= 2048))
       go(gemm_nt_split_kernel<128, 128, 2, 4>, 128, 128, 512, false);
-    else if (t128 >= 2048)
+    else if (tiles128 >= 2048)
       go(gemm_nt_split_kernel<128, 64>, 128, 64, 256, false);
     else
       go(gemm_nt_split_kernel<64, 64>, 64, 64, 256, false);
   }
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const void* Bs, float* C, int64_t ldc,
+                      const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                      float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch, size_t scratch_bytes) {
+  Epi e;
+  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
+  e.act = act;
+  return split_impl(M, N, K, A, lda, Bs, C, ldc, e, st, scratch, scratch_bytes);
+}
+
+// The output columns of a product of N columns under activation act.
+int out_cols(int N, int act) { return act == 2 ? N / 2 : act == 4 ? 2 * N : N; }
+
+// Block pairs out: the split-product GEMM's output epi(A B^T) as fp16 pairs
+// scaled per (row, 128-column tile of the product) into pout -- M rows of
+// out_cols(N, act) / 8 k groups (pair_act_kernel's layout), then the inverse
+// scales [out_cols(N, act) / kb][M] -- for a product that reads them as its A
+// (pet_gemm_nt_pp_blocks with that kb, returned in *kb: 64 for SwiGLU, 256
+// for its backward, 128 otherwise). N a multiple of 128, the output's columns
+// of 32, every epilogue operand 16-byte aligned with leading dimensions of 4.
+int pet_gemm_nt_split_pairs(int M, int N, int K, const float* A, int64_t lda, const void* Bs, void* pout,
+                            const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                            float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch, size_t scratch_bytes,
+                            int* kb) {
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const int no = out_cols(N, act);
+  if (!pout || !a16(pout) || N % 128 || no % 32 || (bias && !a16(bias)) || (cin && (!a16(cin) || ldcin % 4)) ||
+      (pre && (!a16(pre) || ldpre % 4)))
+    return PET_ATTN_EINVAL;
+  Epi e;
+  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
+  e.act = act;
+  e.pout = static_cast<u4*>(pout), e.kgo = no / 8, e.ldinv = M;
+  e.pinv = reinterpret_cast<float*>(e.pout + int64_t(M) * e.kgo * 2);
+  if (kb) *kb = out_cols(128, act);
+  return split_impl(M, N, K, A, lda, Bs, nullptr, 0, e, st, scratch, scratch_bytes);
 }
 
 // The same product from fp32 B [N, K] (ld ldb), split as it is staged: for
@@ -1285,11 +1446,13 @@ const PPShape kPP[] = {
     {gemm_pp_kernel<128, 64, 2, 2, 4>, 128, 64, 256, 4},    // fewer tiles, N >= 64
     {gemm_pp_kernel<64, 64, 2, 2, 4>, 64, 64, 256, 4},      // the rest
 };
+// the first shape with block pairs out (Epi::pout)
+const PPShape kPPOut = {gemm_pp_kernel<128, 128, 2, 4, 2, 0, true>, 128, 128, 512, 2};
 
 // C = epi(A B^T) from the pairs of A (pet_gemm_pair_rows) and of B
 // (pet_gemm_split_weights), K of the pair form.
 int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C, int64_t ldc, const Epi& e,
-                   hipStream_t st) {
+                   hipStream_t st, bool tile128) {
   if (M < 0 || N < 0 || !pair_form(K) || K % 32) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
   if ((reinterpret_cast<uintptr_t>(Ap) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15)) return PET_ATTN_EALIGN;
@@ -1308,11 +1471,14 @@ int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(k.kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 int(k.lds())) != hipSuccess)
           set_on[dev] = -1;
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kPPOut.kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              int(kPPOut.lds())) != hipSuccess)
+        set_on[dev] = -1;
     }
     if (set_on[dev] < 0) return PET_ATTN_ELAUNCH;
   }
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
-  const PPShape& k = kPP[N >= 128 && t128 >= 1024 ? 0 : N >= 64 ? 1 : 2];
+  const PPShape& k = e.pout ? kPPOut : kPP[tile128 || (N >= 128 && t128 >= 1024) ? 0 : N >= 64 ? 1 : 2];
   const int64_t tiles = int64_t((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
   // windows of 8 row blocks (498338 x 2048 x 512 on MI355X: L2-miss reads
   // 4.55 -> 2.71 GiB a product, 3587 -> 3428 us; 16 the same time, 2 and 4
@@ -1320,6 +1486,71 @@ int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C
   constexpr int wr = 8;
   hipLaunchKernelGGL(k.kern, dim3(unsigned(tiles)), dim3(k.threads), k.lds(), st, M, N, K,
                      static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e, wr);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// The block-pairs product's kernels: kPP's shapes, by K block of 32, 64, 128
+// or 256 (KBS 1, 2, 4, 8 steps); each takes at most 32 blocks' scales in LDS
+// after its ring.
+using PPKern = void (*)(int, int, int, const u4*, const u4*, float*, int64_t, Epi, int);
+constexpr int kMaxBlocks = 32;
+PPKern pp_blocks_kernel(int shape, int kbs) {
+  switch (shape * 16 + kbs) {
+    case 1: return gemm_pp_kernel<128, 128, 2, 4, 2, 1>;
+    case 2: return gemm_pp_kernel<128, 128, 2, 4, 2, 2>;
+    case 4: return gemm_pp_kernel<128, 128, 2, 4, 2, 4>;
+    case 8: return gemm_pp_kernel<128, 128, 2, 4, 2, 8>;
+    case 17: return gemm_pp_kernel<128, 64, 2, 2, 4, 1>;
+    case 18: return gemm_pp_kernel<128, 64, 2, 2, 4, 2>;
+    case 20: return gemm_pp_kernel<128, 64, 2, 2, 4, 4>;
+    case 24: return gemm_pp_kernel<128, 64, 2, 2, 4, 8>;
+    case 33: return gemm_pp_kernel<64, 64, 2, 2, 4, 1>;
+    case 34: return gemm_pp_kernel<64, 64, 2, 2, 4, 2>;
+    case 36: return gemm_pp_kernel<64, 64, 2, 2, 4, 4>;
+    case 40: return gemm_pp_kernel<64, 64, 2, 2, 4, 8>;
+    default: return nullptr;
+  }
+}
+
+// C = epi(A B^T) with A as block pairs (pet_gemm_nt_split_pairs' pout: M
+// rows of pairs, then the inverse scales [K / kb][M]) and B's pair rows; kb 32,
+// 64, 128 or 256, dividing K, at most 32 blocks.
+int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const void* Bs, float* C, int64_t ldc,
+                          const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                          float* pre, int64_t ldpre, int act, hipStream_t st) {
+  if (M < 0 || N < 0 || K <= 0 || K % 32 || !(kb == 32 || kb == 64 || kb == 128 || kb == 256) || K % kb ||
+      K / kb > kMaxBlocks || (act == 2 && N % 2))
+    return PET_ATTN_EINVAL;
+  if (M == 0 || N == 0) return PET_ATTN_OK;
+  if ((reinterpret_cast<uintptr_t>(Ap) & 15) || (reinterpret_cast<uintptr_t>(Bs) & 15)) return PET_ATTN_EALIGN;
+  if (int64_t((M + 63) / 64) * ((N + 63) / 64) >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
+  static std::mutex mu;
+  static signed char set_on[64] = {};  // 0 not yet, 1 set, -1 failed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return PET_ATTN_ELAUNCH;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (set_on[dev] == 0) {
+      set_on[dev] = 1;
+      for (int sh = 0; sh < 3; ++sh)
+        for (int kbs : {1, 2, 4, 8})
+          if (hipFuncSetAttribute(reinterpret_cast<const void*>(pp_blocks_kernel(sh, kbs)),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  int(kPP[sh].lds() + size_t(kMaxBlocks) * kPP[sh].bm * 4)) != hipSuccess)
+            set_on[dev] = -1;
+    }
+    if (set_on[dev] < 0) return PET_ATTN_ELAUNCH;
+  }
+  Epi e;
+  e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
+  e.act = act;
+  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
+  const int sh = N >= 128 && t128 >= 1024 ? 0 : N >= 64 ? 1 : 2;
+  const PPShape& k = kPP[sh];
+  const int64_t tiles = int64_t((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
+  const size_t lds = k.lds() + size_t(K / kb) * k.bm * 4;
+  hipLaunchKernelGGL(pp_blocks_kernel(sh, kb / 32), dim3(unsigned(tiles)), dim3(k.threads), lds, st, M, N, K,
+                     static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e, 8);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -1381,6 +1612,35 @@ extern "C" int pet_linear_fused_smallk(int M, int N, int K, const float* A, int6
 extern "C" int pet_linear_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, void* stream) {
   if (M < 0 || K < 0 || ldx < K || (M > 0 && K > 0 && (!X || !out))) return PET_ATTN_EINVAL;
   return pet_gemm_pair_rows(X, M, K, ldx, out, reinterpret_cast<hipStream_t>(stream));
+}
+
+// the epilogue's operands for a product with no C (block pairs out)
+static bool epi_args_nc_ok(int N, const float* row_scale, const float* cin, int64_t ldcin, const float* pre,
+                           int64_t ldpre, int act) {
+  if (act < 0 || act > 4) return false;
+  if (act >= 3) return cin && ldcin >= (act == 4 ? 2 * int64_t(N) : N) && !row_scale && !pre;
+  return (!cin || ldcin >= N) && (!pre || ldpre >= N);
+}
+
+extern "C" int pet_linear_fused_split_blocks(int M, int N, int K, const float* A, int64_t lda, const void* Wsplit,
+                                             void* out, const float* row_scale, const float* bias, const float* cin,
+                                             int64_t ldcin, float beta, float* pre, int64_t ldpre, int act,
+                                             void* scratch, size_t scratch_bytes, int* kb, void* stream) {
+  if (!kb || (M > 0 && N > 0 && (!A || !Wsplit || !out || lda < K ||
+                                  !epi_args_nc_ok(N, row_scale, cin, ldcin, pre, ldpre, act))))
+    return PET_ATTN_EINVAL;
+  return pet_gemm_nt_split_pairs(M, N, K, A, lda, Wsplit, out, row_scale, bias, cin, ldcin, beta, pre, ldpre, act,
+                                 reinterpret_cast<hipStream_t>(stream), scratch, scratch_bytes, kb);
+}
+
+extern "C" int pet_linear_fused_blocks(int M, int N, int K, const void* Ablocks, int kb, const void* Wsplit, float* C,
+                                       int64_t ldc, const float* row_scale, const float* bias, const float* cin,
+                                       int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream) {
+  if ((M > 0 && N > 0) && (!Ablocks || !Wsplit || !C || !epi_args_ok(N, C, ldc, row_scale, cin, ldcin, pre,
+                                                                       ldpre, act)))
+    return PET_ATTN_EINVAL;
+  return pet_gemm_nt_pp_blocks(M, N, K, Ablocks, kb, Wsplit, C, ldc, row_scale, bias, cin, ldcin, beta, pre, ldpre,
+                               act, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pet_linear_fused_pairs(int M, int N, int K, const void* Apairs, const void* Wsplit, float* C,

@@ -47,6 +47,15 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
                       float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch = nullptr,
                       size_t scratch_bytes = 0);
 
+// gemm.hip: block pairs out of one product, into the next
+int pet_gemm_nt_split_pairs(int M, int N, int K, const float* A, int64_t lda, const void* Bs, void* pout,
+                            const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                            float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch, size_t scratch_bytes,
+                            int* kb);
+int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const void* Bs, float* C, int64_t ldc,
+                          const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                          float* pre, int64_t ldpre, int act, hipStream_t st);
+
 extern "C" int pet_linear_fused_smallk(int M, int N, int K, const float* A, int64_t lda, const void* Wpairs, float* C,
                                        int64_t ldc, const float* row_scale, const float* bias, const float* cin,
                                        int64_t ldcin, float beta, float* pre, int64_t ldpre, int act, void* stream);
@@ -484,6 +493,7 @@ struct pet_model {
   pet_model_hypers h{};
   int hd = 0, cw = 0, ew = 0;  // head_dim, center / edge MLP pre-activation widths
   int gemm_mode = 4;           // PET_OPT_MODEL_GEMM for the evaluation in progress
+  bool blocks = true;          // PET_OPT_MODEL_PAIRS for the evaluation in progress
   int tier = 1;                // the memory tier of the last evaluation: 1 never, 2 wide
   std::unordered_map<std::string, Mat> m;
   std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
@@ -698,6 +708,56 @@ bool linear_act(pet_model& md, float* out, float* z, const float* in, int M, int
             0.f, z, W.rows, act, st));
   return true;
 }
+// ---- block pairs between two products ----------------------------------------
+//
+// Where an activation (SiLU, SwiGLU) or its adjoint is read by the next
+// product alone, and both products take the split kernel's pairs-by-pairs
+// form, the first writes it as block pairs (pet_gemm_nt_split_pairs: fp16
+// pairs scaled per row and 128-column tile of the product) and the second
+// reads them as its A (pet_gemm_nt_pp_blocks), in place of an fp32 round trip
+// and a split pass (C5 energy+forces on MI355X: see pet_gemm_nt_split_pairs).
+// The pre-activation the backward reads is the same bits either way.
+int out_cols(int N, int act) { return act == 2 ? N / 2 : act == 4 ? 2 * N : N; }
+struct Blocks {
+  void* p = nullptr;
+  int kb = 0, cols = 0;
+};
+// the split copy of W when the product (M x N x K) takes the pairs-by-pairs form
+const void* pp_split(const pet_model& md, const Mat& W, int M, int N, int K) {
+  const int mode = md.gemm_mode;
+  const bool big = double(M) * N * K >= 4294967296.0;
+  if (!(mode == 3 || mode == 5 || (mode == 4 && big)) || (mode == 5 && K <= 128)) return nullptr;
+  if (K < 256 || K % 32 || N < 512) return nullptr;
+  auto it = md.split.find(W.p);
+  return it == md.split.end() ? nullptr : it->second;
+}
+// Whether out = act(in Wa^T ...) (M x Wa.rows x K) and the product out Wb^T
+// chain as block pairs (Wa, Wb as the products read them: row-major [N, K]).
+bool chains(const pet_model& md, int M, int K, const Mat& Wa, int act, const Mat& Wb) {
+  if (!md.blocks || !md.pairs || M <= 0) return false;
+  const int N = Wa.rows, no = out_cols(N, act), kb = out_cols(128, act);
+  if (N % 128 || no % kb || no / kb > 32 || Wb.cols != no) return false;
+  return pp_split(md, Wa, M, N, K) && pp_split(md, Wb, M, Wb.rows, no);
+}
+// the producer: act(in W^T + bias) as block pairs (act 1 / 2, pre kept and
+// biased), or (act 3 / 4) the adjoint adj W^T through the saved pre-activation z
+Blocks blocks_out(pet_model& md, const float* in, int M, int K, const Mat& W, int act, const float* bias,
+                  const float* z, float* pre, hipStream_t st) {
+  Blocks b;
+  b.cols = out_cols(W.rows, act);
+  b.p = md.f(int64_t(M) * b.cols + int64_t(M) * (b.cols / 32) + 4);
+  const int64_t ldz = act == 4 ? 2 * int64_t(W.rows) : W.rows;
+  ok(pet_gemm_nt_split_pairs(M, W.rows, K, in, K, pp_split(md, W, M, W.rows, K), b.p, nullptr, bias, z,
+                             z ? ldz : 0, 0.f, pre, pre ? W.rows : 0, act, st, md.pairs, md.kPairsBytes, &b.kb));
+  return b;
+}
+// the consumer: C = B W^T + bias + beta cin
+void blocks_in(pet_model& md, float* C, const Blocks& b, int M, const Mat& W, const float* bias, const float* cin,
+               float beta, hipStream_t st) {
+  ok(pet_gemm_nt_pp_blocks(M, W.rows, b.cols, b.p, b.kb, pp_split(md, W, M, W.rows, b.cols), C, W.rows, nullptr,
+                           bias, cin, cin ? W.rows : 0, beta, nullptr, 0, 0, st));
+}
+
 // the bias the activation passes add to a saved pre-activation: none where the
 // forward's epilogue put it in already
 const float* pass_bias(const pet_model& md, const std::string& key) {
@@ -906,23 +966,36 @@ struct Pass {
       }
       linear_acc(md, node_next, hc, N, md.cw / 2, tl + ".center_mlp.w_out", st);
       float* en = attn_out;  // consumed: its edge rows were read by the residual pass
+      const Mat& wi = md.w(tl + ".mlp.w_in.weight");
+      const Mat& wo = md.w(tl + ".mlp.w_out.weight");
+      // edge_next += SwiGLU(en W_in^T + b_in) W_out^T over rows [e0, e0 + rows),
+      // the pre-activation into pre: the SwiGLU output as block pairs where the
+      // two products chain so
+      auto edge_mlp = [&](int e0, int rows, const float* enr, float* pre) {
+        float* out = edge_next + int64_t(e0) * D;
+        if (chains(md, rows, D, wi, 2, wo)) {
+          md.pre_biased[tl + ".mlp.w_in"] = true;
+          const Blocks hb = blocks_out(md, enr, rows, D, wi, 2, md.p(tl + ".mlp.w_in.bias"), nullptr, pre, st);
+          blocks_in(md, out, hb, rows, wo, nullptr, out, 1.f, st);
+          return;
+        }
+        float* he = md.f(int64_t(rows) * md.ew / 2);
+        if (!linear_act(md, he, pre, enr, rows, D, tl + ".mlp.w_in", 2, st)) {
+          linear_pre(md, pre, enr, rows, D, tl + ".mlp.w_in", st);
+          swiglu(md, he, pre, rows, tl + ".mlp.w_in", st);
+        }
+        linear_acc(md, out, he, rows, md.ew / 2, tl + ".mlp.w_out", st);
+      };
       if (!wide) {
         norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
-        float* he = md.f(int64_t(E) * md.ew / 2);
-        if (!linear_act(md, he, b.pre_e, en, E, D, tl + ".mlp.w_in", 2, st)) {
-          linear_pre(md, b.pre_e, en, E, D, tl + ".mlp.w_in", st);
-          swiglu(md, he, b.pre_e, E, tl + ".mlp.w_in", st);
-        }
-        linear_acc(md, edge_next, he, E, md.ew / 2, tl + ".mlp.w_out", st);
+        edge_mlp(0, E, en, b.pre_e);
       } else {  // a chunk of edge rows at a time, its pre-activation a temporary
         for (int e0 = 0; e0 < E; e0 += chunk) {
           const int rows = std::min(chunk, E - e0);
           auto sc = md.ws.mark();
           float* enc = en + int64_t(e0) * D;
           norm(md, enc, b.eps + int64_t(e0) * D, rows, D, tl + ".norm_mlp", false, st);
-          float* he = md.f(int64_t(rows) * md.ew / 2);
-          edge_pre(he, enc, rows, tl);
-          linear_acc(md, edge_next + int64_t(e0) * D, he, rows, md.ew / 2, tl + ".mlp.w_out", st);
+          edge_mlp(e0, rows, enc, md.f(int64_t(rows) * md.ew));
           md.ws.release(sc);
         }
       }
@@ -942,14 +1015,22 @@ struct Pass {
     }
     float* cn = md.f(int64_t(E) * 2 * D);
     norm(md, cn, sv.concat, E, 2 * D, "combination_norms." + ls, true, st);
+    const std::string c0 = "combination_mlps." + ls + ".0", c2 = "combination_mlps." + ls + ".2";
+    if (chains(md, E, 2 * D, md.w(c0 + ".weight"), 1, md.w(c2 + ".weight"))) {  // the SiLU's output as block pairs
+      md.pre_biased[c0] = true;
+      const Blocks cb = blocks_out(md, cn, E, 2 * D, md.w(c0 + ".weight"), 1, md.p(c0 + ".bias"), nullptr, sv.cph, st);
+      blocks_in(md, input_edge, cb, E, md.w(c2 + ".weight"), md.p(c2 + ".bias"), input_edge, 1.f, st);
+      md.ws.release(scope);
+      return;
+    }
     // the SiLU's output: in place, or a buffer of its own for the fused GEMM
     // (which cannot write its input)
-    float* ca = act_fuses(md, cn, E, 2 * D, "combination_mlps." + ls + ".0") ? md.f(int64_t(E) * 2 * D) : cn;
-    if (!linear_act(md, ca, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", 1, st)) {
-      linear_pre(md, sv.cph, cn, E, 2 * D, "combination_mlps." + ls + ".0", st);
-      silu(md, ca, sv.cph, E, "combination_mlps." + ls + ".0", st);
+    float* ca = act_fuses(md, cn, E, 2 * D, c0) ? md.f(int64_t(E) * 2 * D) : cn;
+    if (!linear_act(md, ca, sv.cph, cn, E, 2 * D, c0, 1, st)) {
+      linear_pre(md, sv.cph, cn, E, 2 * D, c0, st);
+      silu(md, ca, sv.cph, E, c0, st);
     }
-    linear_acc_bias(md, input_edge, ca, E, 2 * D, "combination_mlps." + ls + ".2", st);
+    linear_acc_bias(md, input_edge, ca, E, 2 * D, c2, st);
     md.ws.release(scope);
   }
 
@@ -965,12 +1046,18 @@ struct Pass {
       auto s2 = md.ws.mark();
       float* cph_adj = md.f(int64_t(E) * 2 * D);
       float* cn_adj = md.f(int64_t(E) * 2 * D);
-      if (!linear_bwd_act(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", sv.cph,
-                          "combination_mlps." + ls + ".0", 1, st)) {
-        linear_bwd(md, cph_adj, ie_adj, E, "combination_mlps." + ls + ".2", 0.0f, st);
-        silu_bwd(md, cph_adj, sv.cph, E, "combination_mlps." + ls + ".0", st);
+      const std::string c0 = "combination_mlps." + ls + ".0", c2 = "combination_mlps." + ls + ".2";
+      const Mat& c2t = md.w(c2 + ".weight^T");
+      if (chains(md, E, c2t.cols, c2t, 3, md.w(c0 + ".weight^T"))) {  // the SiLU adjoint as block pairs
+        const Blocks cb = blocks_out(md, ie_adj, E, c2t.cols, c2t, 3, pass_bias(md, c0), sv.cph, nullptr, st);
+        blocks_in(md, cn_adj, cb, E, md.w(c0 + ".weight^T"), nullptr, nullptr, 0.f, st);
+      } else {
+        if (!linear_bwd_act(md, cph_adj, ie_adj, E, c2, sv.cph, c0, 1, st)) {
+          linear_bwd(md, cph_adj, ie_adj, E, c2, 0.0f, st);
+          silu_bwd(md, cph_adj, sv.cph, E, c0, st);
+        }
+        linear_bwd(md, cn_adj, cph_adj, E, c0, 0.0f, st);
       }
-      linear_bwd(md, cn_adj, cph_adj, E, "combination_mlps." + ls + ".0", 0.0f, st);
       float* ca = cph_adj;  // consumed
       ok(pet_norm_rows_bwd(E, 2 * D, ca, 2 * D, 0.0f, cn_adj, 2 * D, sv.concat, 2 * D,
                            md.p("combination_norms." + ls + ".weight"), 1, st));
@@ -990,14 +1077,21 @@ struct Pass {
         // chunk at a time with its normed input and pre-activation remade
         auto edge_mlp_bwd = [&](int e0, int rows, const float* pre) {
           float* ea = edge_adj + int64_t(e0) * D;
-          float* h_adj = md.f(int64_t(rows) * md.ew / 2);
-          float* pre_adj = md.f(int64_t(rows) * md.ew);
           float* en_adj = md.f(int64_t(rows) * D);
-          if (!linear_bwd_act(md, pre_adj, ea, rows, tl + ".mlp.w_out", pre, tl + ".mlp.w_in", 2, st)) {
-            linear_bwd(md, h_adj, ea, rows, tl + ".mlp.w_out", 0.0f, st);
-            swiglu_bwd(md, pre_adj, h_adj, pre, rows, tl + ".mlp.w_in", st);
+          const Mat& wot = md.w(tl + ".mlp.w_out.weight^T");
+          if (chains(md, rows, wot.cols, wot, 4, md.w(tl + ".mlp.w_in.weight^T"))) {  // SwiGLU's adjoint as block pairs
+            const Blocks pb = blocks_out(md, ea, rows, wot.cols, wot, 4, pass_bias(md, tl + ".mlp.w_in"), pre, nullptr,
+                                         st);
+            blocks_in(md, en_adj, pb, rows, md.w(tl + ".mlp.w_in.weight^T"), nullptr, nullptr, 0.f, st);
+          } else {
+            float* h_adj = md.f(int64_t(rows) * md.ew / 2);
+            float* pre_adj = md.f(int64_t(rows) * md.ew);
+            if (!linear_bwd_act(md, pre_adj, ea, rows, tl + ".mlp.w_out", pre, tl + ".mlp.w_in", 2, st)) {
+              linear_bwd(md, h_adj, ea, rows, tl + ".mlp.w_out", 0.0f, st);
+              swiglu_bwd(md, pre_adj, h_adj, pre, rows, tl + ".mlp.w_in", st);
+            }
+            linear_bwd(md, en_adj, pre_adj, rows, tl + ".mlp.w_in", 0.0f, st);
           }
-          linear_bwd(md, en_adj, pre_adj, rows, tl + ".mlp.w_in", 0.0f, st);
           ok(pet_norm_rows_bwd(rows, D, ea, D, 1.0f, en_adj, D, b.eps + int64_t(e0) * D, D,
                                md.p(tl + ".norm_mlp.weight"), 0, st));
         };
@@ -1612,6 +1706,7 @@ int pet_model_compute(pet_model* md, const pet_model_edges* e, int forces, doubl
   if (!md || !e || e->n_atoms < 0 || e->n_edges < 0 || e->max_neighbors < 0 || e->n_struct < 0) return PET_ATTN_EINVAL;
   if (e->n_atoms == 0) return PET_ATTN_OK;
   md->gemm_mode = pet_attn_get_option(PET_OPT_MODEL_GEMM);
+  md->blocks = pet_attn_get_option(PET_OPT_MODEL_PAIRS) == 1;
   if (!e->species || !e->off || (e->n_edges > 0 && (!e->center || !e->neigh_species || !e->reverse || !e->vec ||
                                                     !e->dist || !e->pcut || !e->cut)))
     return PET_ATTN_EINVAL;

@@ -11,6 +11,8 @@ false, since there is no other path here to fall back to.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -69,6 +71,60 @@ class PairRows:
                    "pet_linear_pair_rows")
 
 
+class BlockPairs:
+    """A product's output [M, cols] (cols a multiple of 32) as block pairs, made
+    by fused_to_blocks (pet_linear_fused_split_blocks): fp16 pairs scaled per
+    (row, block of kb columns), then the blocks' inverse scales. Read in place
+    of A by fused() with SplitWeights (pet_linear_fused_blocks)."""
+
+    def __init__(self, M: int, cols: int, device):
+        if cols % 32:
+            raise ValueError(f"block pairs need a multiple of 32 columns, not {cols}")
+        self.shape = (M, cols)
+        self.kb = None  # set by the product that writes them
+        self.data = torch.empty(M * cols * 2 + 2 * M * (cols // 32) + 8, dtype=torch.int16, device=device)
+
+
+def _out_cols(N, act):
+    return N // 2 if act == 2 else 2 * N if act == 4 else N
+
+
+def fused_to_blocks(A, W, out, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, scratch=None):
+    """fused() with the output act(...) written as block pairs into `out`
+    (BlockPairs [M, N / 2 | 2 N | N] by act) instead of an fp32 C: W as
+    SplitWeights, K a multiple of 32 and at least 256, N >= 512 and a multiple
+    of 128, `scratch` the workspace A's rows are split into a chunk at a time."""
+    _check(A, "A")
+    if not isinstance(W, SplitWeights) or not isinstance(out, BlockPairs):
+        raise ValueError("block pairs out need W as SplitWeights and out as BlockPairs")
+    M, K = A.shape
+    N = W.shape[0]
+    if W.shape[1] != K:
+        raise ValueError(f"A has K = {K}, W has K = {W.shape[1]}")
+    if out.shape != (M, _out_cols(N, act)):
+        raise ValueError(f"out is {out.shape}, the product gives {(M, _out_cols(N, act))}")
+    if scratch is None or scratch.device != A.device or not scratch.is_contiguous():
+        raise ValueError("scratch: a contiguous tensor on A's device")
+    dev = A.device
+    width = 2 * N if act == 4 else N
+    if row_scale is not None:
+        _check(row_scale, "row_scale", M, vector=True, device=dev)
+    if bias is not None:
+        _check(bias, "bias", width, vector=True, device=dev)
+    if cin is not None:
+        _check(cin, "cin", M, width, device=dev)
+    if pre is not None:
+        _check(pre, "pre", M, N, device=dev)
+    p = lambda t: None if t is None else t.data_ptr()
+    ld = lambda t: 0 if t is None else t.stride(0)
+    kb = ctypes.c_int(0)
+    _lib.check(_lib.load().pet_linear_fused_split_blocks(
+        M, N, K, p(A), A.stride(0), W.data.data_ptr(), out.data.data_ptr(), p(row_scale), p(bias), p(cin), ld(cin),
+        beta, p(pre), ld(pre), act, scratch.data_ptr(), scratch.numel() * scratch.element_size(), ctypes.byref(kb),
+        torch.cuda.current_stream().cuda_stream), "pet_linear_fused_split_blocks")
+    out.kb = kb.value
+
+
 def _check(t, name, rows=None, cols=None, vector=False, device=None):
     """A float32 CUDA tensor, unit stride along its last axis, of the stated
     extents (a row may be longer than `cols` in a 2-D view: the leading
@@ -98,9 +154,11 @@ def _check(t, name, rows=None, cols=None, vector=False, device=None):
 def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=0, scratch=None):
     if act not in (0, 1, 2, 3, 4):
         raise ValueError(f"act {act}: 0 (none), 1 (SiLU), 2 (SwiGLU), 3 / 4 (their backward)")
-    if isinstance(A, PairRows):
+    if isinstance(A, (PairRows, BlockPairs)):
         if not isinstance(W, SplitWeights):
-            raise ValueError("A as pair rows needs W as SplitWeights")
+            raise ValueError("A as pair rows or block pairs needs W as SplitWeights")
+        if isinstance(A, BlockPairs) and A.kb is None:
+            raise ValueError("A: block pairs no product has written")
         M, K = A.shape
         dev = A.data.device
     else:
@@ -141,6 +199,10 @@ def _call(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=None, act=
         _lib.check(lib.pet_linear_fused_smallk(M, N, K, p(A), A.stride(0), W.data.data_ptr(), p(C), C.stride(0),
                                                p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
                    "pet_linear_fused_smallk")
+    elif isinstance(A, BlockPairs):
+        _lib.check(lib.pet_linear_fused_blocks(M, N, K, A.data.data_ptr(), A.kb, W.data.data_ptr(), p(C), C.stride(0),
+                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),
+                   "pet_linear_fused_blocks")
     elif isinstance(A, PairRows):
         _lib.check(lib.pet_linear_fused_pairs(M, N, K, A.data.data_ptr(), W.data.data_ptr(), p(C), C.stride(0),
                                               p(row_scale), p(bias), p(cin), ld(cin), beta, p(pre), ld(pre), act, st),

@@ -384,3 +384,115 @@ def W_ref(W, device):
     inv = raw[N * K * 4: N * K * 4 + 4 * N].view(np.float32).astype(np.float64)
     w = (parts[:, :, 0, :] + parts[:, :, 1, :]).reshape(N, K) * inv[:, None]
     return torch.from_numpy(w).to(device)
+
+
+def blocks_ref(B, device):
+    """The fp64 matrix of block pairs: (hi + lo) times each (row, block)'s
+    inverse scale; and the scaled parts' largest |hi| per (row, block)."""
+    M, cols = B.shape
+    raw = B.data.cpu().numpy().view(np.uint8)
+    parts = raw[: M * cols * 4].view(np.float16).reshape(M, cols // 8, 2, 8).astype(np.float64)
+    nblk = cols // B.kb
+    inv = raw[M * cols * 4: M * cols * 4 + 4 * M * nblk].view(np.float32).reshape(nblk, M).astype(np.float64)
+    hi, lo = parts[:, :, 0, :].reshape(M, cols), parts[:, :, 1, :].reshape(M, cols)
+    x = (hi + lo) * np.repeat(inv.T, B.kb, axis=1)
+    hmax = np.abs(hi).reshape(M, nblk, B.kb).max(axis=2)
+    return torch.from_numpy(x).to(device), hmax
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4])
+def test_block_pairs_out(act, device):
+    # pet_linear_fused_split_blocks: the output act(...) as block pairs equals
+    # the fp32 output of the same product (pet_linear_fused_split_ws, the same
+    # kernel and epilogue arithmetic) within the split's rounding (hi and lo
+    # both to nearest: 2^-22 of the value, or 2^-25 of the block's largest
+    # below fp16's normal range), each block scaled so that its largest |hi|
+    # lies in [2^14, 2^15]; rows 10^-3 .. 10^3 apart and one all-zero row;
+    # the same bits whatever the scratch's chunking
+    M, N, K = 1000, 512, 256
+    print(f"[gpu] block pairs out, act {act}, M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(40 + act)
+    A = torch.randn(M, K, device=device, generator=g) * torch.logspace(-3, 3, M, device=device)[:, None]
+    A[500] = 0.0
+    W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
+    Ws = L.SplitWeights(W)
+    width = 2 * N if act == 4 else N
+    kw = dict(bias=torch.randn(width, device=device, generator=g), act=act)
+    if act >= 3:
+        kw["cin"] = torch.randn(M, width, device=device, generator=g)
+    else:
+        kw["pre"] = torch.empty(M, N, device=device)
+    if act == 0:
+        kw["row_scale"] = torch.rand(M, device=device, generator=g) + 0.5
+        kw["cin"], kw["beta"] = torch.randn(M, N, device=device, generator=g), 0.5
+    cols = N // 2 if act == 2 else width
+    big = torch.empty(M * (K * 4 + 4) // 4 + 64, device=device)
+    small = torch.empty(128 * (K * 4 + 4) // 4, device=device)
+    C = torch.empty(M, cols, device=device)
+    L.fused(A, Ws, C, **kw, scratch=big)
+    pre_ref = kw["pre"].clone() if "pre" in kw else None
+    outs = []
+    for sc in (big, small):
+        B = L.BlockPairs(M, cols, device)
+        L.fused_to_blocks(A, Ws, B, **kw, scratch=sc)
+        torch.cuda.synchronize()
+        outs.append(B)
+        if pre_ref is not None:
+            assert torch.equal(kw["pre"], pre_ref)
+    assert outs[0].kb == (64 if act == 2 else 256 if act == 4 else 128)
+    used = M * cols * 2 + 2 * M * (cols // outs[0].kb)  # int16s written: the pairs, then the inverse scales
+    assert torch.equal(outs[0].data[:used], outs[1].data[:used])
+    x, hmax = blocks_ref(outs[0], device)
+    c = C.double()
+    bmax = c.abs().reshape(M, cols // outs[0].kb, outs[0].kb).amax(dim=2)
+    tol = 2.0 ** -22 * c.abs() + 2.0 ** -25 * bmax.repeat_interleave(outs[0].kb, dim=1)
+    assert ((x - c).abs() <= tol).all(), (x - c).abs().max().item()
+    live = bmax.cpu().numpy() > 0
+    assert (hmax[live] >= 2.0 ** 14).all() and (hmax[live] <= 2.0 ** 15).all()
+    assert (hmax[~live] == 0).all()
+
+
+@pytest.mark.parametrize("act", [2, 4, 1])
+def test_block_pairs_product(act, device):
+    # pet_linear_fused_blocks: the product of block pairs (as the producer of
+    # the test above made them) with split weights, against the fp64 product of
+    # the decoded blocks and weights, per element within the fp32
+    # accumulation's bound and the dropped lo * lo terms (below);
+    # rows independent of M (a slice alone gives the same bits); epilogue with
+    # bias and a residual from C itself
+    M, N0, K0 = 3000, 512, 256
+    g = torch.Generator(device=device).manual_seed(60 + act)
+    A = torch.randn(M, K0, device=device, generator=g) * torch.logspace(-2, 2, M, device=device)[:, None]
+    W0 = L.SplitWeights(torch.randn(N0, K0, device=device, generator=g) / K0 ** 0.5)
+    width = 2 * N0 if act == 4 else N0
+    kw = dict(bias=torch.randn(width, device=device, generator=g))
+    if act >= 3:
+        kw["cin"] = torch.randn(M, width, device=device, generator=g)
+    cols = N0 // 2 if act == 2 else width
+    scratch = torch.empty(M * (K0 * 4 + 4) // 4 + 64, device=device)
+    B = L.BlockPairs(M, cols, device)
+    L.fused_to_blocks(A, W0, B, **kw, act=act, scratch=scratch)
+    N = 384
+    print(f"[gpu] block pairs product, K={cols} (kb {B.kb}), N={N}", flush=True)
+    W = L.SplitWeights(torch.randn(N, cols, device=device, generator=g) / cols ** 0.5)
+    b = torch.randn(N, device=device, generator=g)
+    res = torch.randn(M, N, device=device, generator=g)
+    C = res.clone()
+    L.fused(B, W, C, bias=b, cin=C, beta=1.0)
+    torch.cuda.synchronize()
+    x, _ = blocks_ref(B, device)
+    w = W_ref(W, device)
+    ref = x @ w.T + b.double() + res.double()
+    bound = x.abs() @ w.abs().T + res.double().abs()
+    # fp32 accumulation: one rounding a 32-wide K step (the matrix instruction
+    # sums its 32 products), one a block's addition into the total, a few in
+    # the epilogue; the dropped lo * lo terms 2^-22 of |a| |w|
+    rel = (cols // 32 + cols // B.kb + 4) * 2.0 ** -24 + 2.0 ** -22
+    assert ((C.double() - ref).abs() <= rel * bound + 1e-30).all(), ((C.double() - ref).abs() / bound).max().item()
+    # a slice of the rows alone: block pairs of those rows only
+    B2 = L.BlockPairs(1000, cols, device)
+    L.fused_to_blocks(A[1000:2000].contiguous(), W0, B2, **{k: (v[1000:2000].contiguous() if v.dim() == 2 else v)
+                                                           for k, v in kw.items()}, act=act, scratch=scratch)
+    C2 = res[1000:2000].clone()
+    L.fused(B2, W, C2, bias=b, cin=C2, beta=1.0)
+    assert torch.equal(C2, C[1000:2000])
