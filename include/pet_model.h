@@ -180,6 +180,12 @@ PET_ATTN_API int pet_linear_fused_smallk(int M, int N, int K, const float* A, in
  * split into a high part exact in fp16 and the rest rounded to fp16, then the
  * rows' inverse scales). Split once, an activation feeds any number of products. */
 PET_ATTN_API int pet_linear_pair_rows(const float* X, int M, int K, int64_t ldx, void* out, void* stream);
+/* pet_norm_rows (RMSNorm, or LayerNorm with a bias) with its output as pair
+ * rows: the bits pet_linear_pair_rows gives for pet_norm_rows' output, without
+ * the fp32 round trip. width a multiple of 8 and at most 2048; out 16-byte
+ * aligned, rows * width * 4 + rows * 4 bytes. */
+PET_ATTN_API int pet_norm_rows_pairs(int rows, int width, void* out, const float* in, int64_t ldi,
+                                     const float* weight, const float* bias, void* stream);
 /* pet_linear_fused_split with A as pet_linear_pair_rows made it: the same bits,
  * with no arithmetic but the products in the K loop. No counterpart in the
  * reference (src/fused_gemm_hip.cpp runs its layers in fp32). */

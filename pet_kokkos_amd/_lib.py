@@ -60,6 +60,7 @@ EXPORTS = (
     "pet_linear_fused_pairs",
     "pet_linear_fused_split_blocks",
     "pet_linear_fused_blocks",
+    "pet_norm_rows_pairs",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX, ESCRATCH = range(10)
@@ -240,6 +241,8 @@ def load() -> ctypes.CDLL:
     lib.pet_linear_fused_split_blocks.restype = ctypes.c_int
     lib.pet_linear_fused_split_blocks.argtypes = [_I, _I, _I, _P, _I64, _P, _P, _P, _P, _P, _I64, _F, _P, _I64, _I,
                                                   _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), _P]
+    lib.pet_norm_rows_pairs.restype = ctypes.c_int
+    lib.pet_norm_rows_pairs.argtypes = [_I, _I, _P, _P, _I64, _P, _P, _P]
     lib.pet_linear_fused_blocks.restype = ctypes.c_int
     lib.pet_linear_fused_blocks.argtypes = [_I, _I, _I, _P, _I, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_model_workspace_bytes.restype = ctypes.c_size_t

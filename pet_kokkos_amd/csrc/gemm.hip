@@ -1299,7 +1299,7 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
 }
 
 // The output columns of a product of N columns under activation act.
-int out_cols(int N, int act) { return act == 2 ? N / 2 : act == 4 ? 2 * N : N; }
+static int out_cols(int N, int act) { return act == 2 ? N / 2 : act == 4 ? 2 * N : N; }
 
 // Block pairs out: the split-product GEMM's output epi(A B^T) as fp16 pairs
 // scaled per (row, 128-column tile of the product) into pout -- M rows of
@@ -1487,6 +1487,25 @@ int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C
   hipLaunchKernelGGL(k.kern, dim3(unsigned(tiles)), dim3(k.threads), k.lds(), st, M, N, K,
                      static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e, wr);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
+
+// Block pairs out (as pet_gemm_nt_split_pairs) from A already as pair rows
+// (pet_gemm_pair_rows' layout, K of the pair form): the pairs-by-pairs kernel
+// alone, every row at once.
+int pet_gemm_nt_pp_to_blocks(int M, int N, int K, const void* Ap, const void* Bs, void* pout, const float* bias,
+                             const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre, int act,
+                             hipStream_t st, int* kb) {
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const int no = out_cols(N, act);
+  if (!pout || !a16(pout) || N % 128 || no % 32 || (bias && !a16(bias)) || (cin && (!a16(cin) || ldcin % 4)) ||
+      (pre && (!a16(pre) || ldpre % 4)) || act < 0 || act > 4 || (act == 2 && N % 2))
+    return PET_ATTN_EINVAL;
+  Epi e;
+  e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre, e.act = act;
+  e.pout = static_cast<u4*>(pout), e.kgo = no / 8, e.ldinv = M;
+  e.pinv = reinterpret_cast<float*>(e.pout + int64_t(M) * e.kgo * 2);
+  if (kb) *kb = out_cols(128, act);
+  return pet_gemm_nt_pp(M, N, K, Ap, Bs, nullptr, 0, e, st, true);
 }
 
 // The block-pairs product's kernels: kPP's shapes, by K block of 32, 64, 128

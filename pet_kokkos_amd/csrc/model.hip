@@ -52,6 +52,9 @@ int pet_gemm_nt_split_pairs(int M, int N, int K, const float* A, int64_t lda, co
                             const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
                             float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch, size_t scratch_bytes,
                             int* kb);
+int pet_gemm_nt_pp_to_blocks(int M, int N, int K, const void* Ap, const void* Bs, void* pout, const float* bias,
+                             const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre, int act,
+                             hipStream_t st, int* kb);
 int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const void* Bs, float* C, int64_t ldc,
                           const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
                           float* pre, int64_t ldpre, int act, hipStream_t st);
@@ -751,6 +754,20 @@ Blocks blocks_out(pet_model& md, const float* in, int M, int K, const Mat& W, in
                              z ? ldz : 0, 0.f, pre, pre ? W.rows : 0, act, st, md.pairs, md.kPairsBytes, &b.kb));
   return b;
 }
+// the producer from the norm of rows `in` (width K: RMSNorm, or LayerNorm with
+// a bias) made directly as pair rows (pet_norm_rows_pairs: the bits the split
+// pass gives for the fp32 norm), act 1 / 2 with the pre-activation kept
+Blocks blocks_out_normed(pet_model& md, const float* in, int M, int K, const std::string& norm_key, bool ln,
+                         const Mat& W, int act, const float* bias, float* pre, hipStream_t st) {
+  void* ap = md.f(int64_t(M) * K + M + 4);
+  ok(pet_norm_rows_pairs(M, K, ap, in, K, md.p(norm_key + ".weight"), ln ? md.p(norm_key + ".bias") : nullptr, st));
+  Blocks b;
+  b.cols = out_cols(W.rows, act);
+  b.p = md.f(int64_t(M) * b.cols + int64_t(M) * (b.cols / 32) + 4);
+  ok(pet_gemm_nt_pp_to_blocks(M, W.rows, K, ap, pp_split(md, W, M, W.rows, K), b.p, bias, nullptr, 0, 0.f, pre,
+                              pre ? W.rows : 0, act, st, &b.kb));
+  return b;
+}
 // the consumer: C = B W^T + bias + beta cin
 void blocks_in(pet_model& md, float* C, const Blocks& b, int M, const Mat& W, const float* bias, const float* cin,
                float beta, hipStream_t st) {
@@ -971,14 +988,18 @@ struct Pass {
       // edge_next += SwiGLU(en W_in^T + b_in) W_out^T over rows [e0, e0 + rows),
       // the pre-activation into pre: the SwiGLU output as block pairs where the
       // two products chain so
-      auto edge_mlp = [&](int e0, int rows, const float* enr, float* pre) {
+      // (en = norm(eps) rows into enr, or as pair rows straight from the norm)
+      auto edge_mlp = [&](int e0, int rows, float* enr, float* pre) {
         float* out = edge_next + int64_t(e0) * D;
+        const float* epsr = b.eps + int64_t(e0) * D;
         if (chains(md, rows, D, wi, 2, wo)) {
           md.pre_biased[tl + ".mlp.w_in"] = true;
-          const Blocks hb = blocks_out(md, enr, rows, D, wi, 2, md.p(tl + ".mlp.w_in.bias"), nullptr, pre, st);
+          const Blocks hb = blocks_out_normed(md, epsr, rows, D, tl + ".norm_mlp", false, wi, 2,
+                                             md.p(tl + ".mlp.w_in.bias"), pre, st);
           blocks_in(md, out, hb, rows, wo, nullptr, out, 1.f, st);
           return;
         }
+        norm(md, enr, epsr, rows, D, tl + ".norm_mlp", false, st);
         float* he = md.f(int64_t(rows) * md.ew / 2);
         if (!linear_act(md, he, pre, enr, rows, D, tl + ".mlp.w_in", 2, st)) {
           linear_pre(md, pre, enr, rows, D, tl + ".mlp.w_in", st);
@@ -987,15 +1008,12 @@ struct Pass {
         linear_acc(md, out, he, rows, md.ew / 2, tl + ".mlp.w_out", st);
       };
       if (!wide) {
-        norm(md, en, b.eps, E, D, tl + ".norm_mlp", false, st);
         edge_mlp(0, E, en, b.pre_e);
       } else {  // a chunk of edge rows at a time, its pre-activation a temporary
         for (int e0 = 0; e0 < E; e0 += chunk) {
           const int rows = std::min(chunk, E - e0);
           auto sc = md.ws.mark();
-          float* enc = en + int64_t(e0) * D;
-          norm(md, enc, b.eps + int64_t(e0) * D, rows, D, tl + ".norm_mlp", false, st);
-          edge_mlp(e0, rows, enc, md.f(int64_t(rows) * md.ew));
+          edge_mlp(e0, rows, en + int64_t(e0) * D, md.f(int64_t(rows) * md.ew));
           md.ws.release(sc);
         }
       }
@@ -1013,16 +1031,18 @@ struct Pass {
                          e.reverse, int64_t(E), D);
       launched();
     }
-    float* cn = md.f(int64_t(E) * 2 * D);
-    norm(md, cn, sv.concat, E, 2 * D, "combination_norms." + ls, true, st);
     const std::string c0 = "combination_mlps." + ls + ".0", c2 = "combination_mlps." + ls + ".2";
-    if (chains(md, E, 2 * D, md.w(c0 + ".weight"), 1, md.w(c2 + ".weight"))) {  // the SiLU's output as block pairs
+    if (chains(md, E, 2 * D, md.w(c0 + ".weight"), 1, md.w(c2 + ".weight"))) {
+      // the norm as pair rows, the SiLU's output as block pairs
       md.pre_biased[c0] = true;
-      const Blocks cb = blocks_out(md, cn, E, 2 * D, md.w(c0 + ".weight"), 1, md.p(c0 + ".bias"), nullptr, sv.cph, st);
+      const Blocks cb = blocks_out_normed(md, sv.concat, E, 2 * D, "combination_norms." + ls, true,
+                                          md.w(c0 + ".weight"), 1, md.p(c0 + ".bias"), sv.cph, st);
       blocks_in(md, input_edge, cb, E, md.w(c2 + ".weight"), md.p(c2 + ".bias"), input_edge, 1.f, st);
       md.ws.release(scope);
       return;
     }
+    float* cn = md.f(int64_t(E) * 2 * D);
+    norm(md, cn, sv.concat, E, 2 * D, "combination_norms." + ls, true, st);
     // the SiLU's output: in place, or a buffer of its own for the fused GEMM
     // (which cannot write its input)
     float* ca = act_fuses(md, cn, E, 2 * D, c0) ? md.f(int64_t(E) * 2 * D) : cn;

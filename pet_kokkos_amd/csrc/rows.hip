@@ -14,7 +14,8 @@
 #include <cstdint>
 #include <type_traits>
 
-#include "../../include/pet_attn.h"
+#include "../../include/pet_model.h"
+#include "split_bf16.h"
 
 namespace pet_rows {
 
@@ -185,7 +186,12 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
-template <int LPR, int C4>
+// PAIRS: the row as fp16 pairs (pair rows: each row scaled by the power of two
+// that puts its largest |value| at [2^14, 2^15), 8-value groups of hi then lo
+// 16 bytes, the rows' inverse scales after all rows' pairs) into `out`
+// instead of fp32: the same values, split as the pair-rows pass would split
+// them.
+template <int LPR, int C4, bool PAIRS = false>
 __global__ void __launch_bounds__(256) norm_fwd4_kernel(int rows, int width, float* __restrict__ out, int64_t ldo,
                                                         const float* __restrict__ in, int64_t ldi,
                                                         const float* __restrict__ weight,
@@ -222,14 +228,41 @@ __global__ void __launch_bounds__(256) norm_fwd4_kernel(int rows, int width, flo
   float4* o_row = reinterpret_cast<float4*>(out + int64_t(r) * ldo);
   const float4* w4p = reinterpret_cast<const float4*>(weight);
   const float4* b4p = reinterpret_cast<const float4*>(bias);
+  float4 o[C4];
 #pragma unroll
   for (int j = 0; j < C4; ++j) {
     const int q = t + LPR * j;
     if (q < w4) {
       const float4 wq = w4p[q], bq = ln ? b4p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-      o_row[q] = make_float4((x[j].x - mu) * inv * wq.x + bq.x, (x[j].y - mu) * inv * wq.y + bq.y,
-                             (x[j].z - mu) * inv * wq.z + bq.z, (x[j].w - mu) * inv * wq.w + bq.w);
+      o[j] = make_float4((x[j].x - mu) * inv * wq.x + bq.x, (x[j].y - mu) * inv * wq.y + bq.y,
+                         (x[j].z - mu) * inv * wq.z + bq.z, (x[j].w - mu) * inv * wq.w + bq.w);
+      if constexpr (!PAIRS) o_row[q] = o[j];
+    } else {
+      o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
+  }
+  if constexpr (PAIRS) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < C4; ++j) m = fmaxf(m, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
+#pragma unroll
+    for (int k = LPR / 2; k > 0; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
+    const float s = pet_split::pair_scale(m);
+    const int KG = width / 8;
+    unsigned* base = reinterpret_cast<unsigned*>(out) + int64_t(r) * KG * 8;
+#pragma unroll
+    for (int j = 0; j < C4; ++j) {
+      const int q = t + LPR * j;
+      if (q < w4) {
+        unsigned h0, h1, l0, l1;
+        pet_split::pair2(o[j].x * s, o[j].y * s, h0, l0);
+        pet_split::pair2(o[j].z * s, o[j].w * s, h1, l1);
+        unsigned* hi = base + (q >> 1) * 8 + (q & 1) * 2;  // group q / 2: hi words 0-3, lo words 4-7
+        *reinterpret_cast<uint2*>(hi) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(hi + 4) = make_uint2(l0, l1);
+      }
+    }
+    if (t == 0) (out + int64_t(rows) * width)[r] = 1.f / s;
   }
 }
 
@@ -432,6 +465,22 @@ int pet_norm_rows(int rows, int width, float* out, int64_t ldo, const float* in,
                        in, ldi, weight, bias);
     return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
   });
+}
+
+int pet_norm_rows_pairs(int rows, int width, void* out, const float* in, int64_t ldi, const float* weight,
+                        const float* bias, void* stream) {
+  if (rows < 0 || width < 8 || width % 8 || !out || !in || !weight || ldi < width) return PET_ATTN_EINVAL;
+  if (rows == 0) return PET_ATTN_OK;
+  if (!aligned16(out, 4) || !aligned16(in, ldi) || !aligned16(weight, 4) || (bias && !aligned16(bias, 4)))
+    return PET_ATTN_EALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int e = with_vec(width, [&](auto lc, auto cc) {
+    constexpr int LPR = decltype(lc)::value, C4 = decltype(cc)::value, RPB = 4 * (64 / LPR);
+    hipLaunchKernelGGL((norm_fwd4_kernel<LPR, C4, true>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st,
+                       rows, width, static_cast<float*>(out), int64_t(width), in, ldi, weight, bias);
+    return hipGetLastError() == hipSuccess ? int(PET_ATTN_OK) : int(PET_ATTN_ELAUNCH);
+  });
+  return e >= 0 ? e : int(PET_ATTN_EINVAL);  // wider than the row kernels take
 }
 
 int pet_norm_rows_bwd(int rows, int width, float* in_adj, int64_t lda, float beta, const float* out_adj, int64_t ldg,

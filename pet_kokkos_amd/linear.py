@@ -125,6 +125,27 @@ def fused_to_blocks(A, W, out, row_scale=None, bias=None, cin=None, beta=0.0, pr
     out.kb = kb.value
 
 
+def norm_pair_rows(X, weight, bias=None):
+    """norm(X) (RMSNorm, or LayerNorm with a bias: pet_norm_rows) made
+    directly as PairRows (pet_norm_rows_pairs): the same bits as PairRows of
+    the fp32 norm, with no fp32 round trip. X [M, K], K a multiple of 32 from
+    256 to 2048."""
+    _check(X, "X")
+    M, K = X.shape
+    if K % 32 or K < 256 or K > 2048:
+        raise ValueError(f"X has K = {K}: the norm's pair rows need K a multiple of 32 from 256 to 2048")
+    _check(weight, "weight", K, vector=True, device=X.device)
+    if bias is not None:
+        _check(bias, "bias", K, vector=True, device=X.device)
+    out = PairRows.__new__(PairRows)
+    out.shape = (M, K)
+    out.data = torch.empty(M * K * 2 + 2 * M + 8, dtype=torch.int16, device=X.device)
+    _lib.check(_lib.load().pet_norm_rows_pairs(M, K, out.data.data_ptr(), X.data_ptr(), X.stride(0),
+                                               weight.data_ptr(), None if bias is None else bias.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream), "pet_norm_rows_pairs")
+    return out
+
+
 def _check(t, name, rows=None, cols=None, vector=False, device=None):
     """A float32 CUDA tensor, unit stride along its last axis, of the stated
     extents (a row may be longer than `cols` in a 2-D view: the leading

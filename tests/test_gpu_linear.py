@@ -496,3 +496,25 @@ def test_block_pairs_product(act, device):
     C2 = res[1000:2000].clone()
     L.fused(B2, W, C2, bias=b, cin=C2, beta=1.0)
     assert torch.equal(C2, C[1000:2000])
+
+
+@pytest.mark.parametrize("K", [256, 512, 1024, 2048])
+def test_norm_pair_rows_same_bits(K, device):
+    # pet_norm_rows_pairs: the norm's output made directly as pair rows is the
+    # same bits as pet_norm_rows then pet_linear_pair_rows, for RMSNorm and
+    # LayerNorm, rows 10^-3 .. 10^3 apart, and a product from either the same
+    from pet_kokkos_amd import attention as A_
+    M = 777
+    print(f"[gpu] norm as pair rows, K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(K)
+    X = torch.randn(M, K, device=device, generator=g) * torch.logspace(-3, 3, M, device=device)[:, None]
+    w = torch.rand(K, device=device, generator=g) + 0.5
+    for bias in (None, torch.randn(K, device=device, generator=g)):
+        Y = torch.empty(M, K, device=device)
+        _lib.check(_lib.load().pet_norm_rows(M, K, Y.data_ptr(), K, X.data_ptr(), K, w.data_ptr(),
+                                             None if bias is None else bias.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream), "pet_norm_rows")
+        ref = L.PairRows(Y)
+        got = L.norm_pair_rows(X, w, bias)
+        used = M * K * 2 + 2 * M
+        assert torch.equal(ref.data[:used], got.data[:used]), bias is None
