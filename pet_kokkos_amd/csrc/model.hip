@@ -757,9 +757,13 @@ Blocks blocks_out(pet_model& md, const float* in, int M, int K, const Mat& W, in
 // the producer from the norm of rows `in` (width K: RMSNorm, or LayerNorm with
 // a bias) made directly as pair rows (pet_norm_rows_pairs: the bits the split
 // pass gives for the fp32 norm), act 1 / 2 with the pre-activation kept
+// (the pair rows into `room` where it holds them: room_floats floats no one
+// reads any more)
 Blocks blocks_out_normed(pet_model& md, const float* in, int M, int K, const std::string& norm_key, bool ln,
-                         const Mat& W, int act, const float* bias, float* pre, hipStream_t st) {
-  void* ap = md.f(int64_t(M) * K + M + 4);
+                         const Mat& W, int act, const float* bias, float* pre, hipStream_t st, float* room = nullptr,
+                         int64_t room_floats = 0) {
+  const int64_t apf = int64_t(M) * K + M + 4;
+  void* ap = room && room_floats >= apf ? static_cast<void*>(room) : md.f(apf);
   ok(pet_norm_rows_pairs(M, K, ap, in, K, md.p(norm_key + ".weight"), ln ? md.p(norm_key + ".bias") : nullptr, st));
   Blocks b;
   b.cols = out_cols(W.rows, act);
@@ -989,13 +993,17 @@ struct Pass {
       // the pre-activation into pre: the SwiGLU output as block pairs where the
       // two products chain so
       // (en = norm(eps) rows into enr, or as pair rows straight from the norm)
+      // (attn_out is dead by then: all of it is room for the norm's pair rows
+      // of the whole edge MLP)
       auto edge_mlp = [&](int e0, int rows, float* enr, float* pre) {
         float* out = edge_next + int64_t(e0) * D;
         const float* epsr = b.eps + int64_t(e0) * D;
         if (chains(md, rows, D, wi, 2, wo)) {
           md.pre_biased[tl + ".mlp.w_in"] = true;
+          const bool all = rows == E;
           const Blocks hb = blocks_out_normed(md, epsr, rows, D, tl + ".norm_mlp", false, wi, 2,
-                                             md.p(tl + ".mlp.w_in.bias"), pre, st);
+                                             md.p(tl + ".mlp.w_in.bias"), pre, st, all ? attn_out : nullptr,
+                                             all ? int64_t(T) * D : 0);
           blocks_in(md, out, hb, rows, wo, nullptr, out, 1.f, st);
           return;
         }
@@ -1064,21 +1072,23 @@ struct Pass {
     float* edge_adj = tok_adj + int64_t(N) * D;
     {
       auto s2 = md.ws.mark();
-      float* cph_adj = md.f(int64_t(E) * 2 * D);
       float* cn_adj = md.f(int64_t(E) * 2 * D);
       const std::string c0 = "combination_mlps." + ls + ".0", c2 = "combination_mlps." + ls + ".2";
       const Mat& c2t = md.w(c2 + ".weight^T");
+      float* ca;  // the norm's input adjoint, in the buffer of the SiLU adjoint, consumed by then
       if (chains(md, E, c2t.cols, c2t, 3, md.w(c0 + ".weight^T"))) {  // the SiLU adjoint as block pairs
         const Blocks cb = blocks_out(md, ie_adj, E, c2t.cols, c2t, 3, pass_bias(md, c0), sv.cph, nullptr, st);
         blocks_in(md, cn_adj, cb, E, md.w(c0 + ".weight^T"), nullptr, nullptr, 0.f, st);
+        ca = static_cast<float*>(cb.p);  // E (2D + 2D / 32) floats
       } else {
+        float* cph_adj = md.f(int64_t(E) * 2 * D);
         if (!linear_bwd_act(md, cph_adj, ie_adj, E, c2, sv.cph, c0, 1, st)) {
           linear_bwd(md, cph_adj, ie_adj, E, c2, 0.0f, st);
           silu_bwd(md, cph_adj, sv.cph, E, c0, st);
         }
         linear_bwd(md, cn_adj, cph_adj, E, c0, 0.0f, st);
+        ca = cph_adj;
       }
-      float* ca = cph_adj;  // consumed
       ok(pet_norm_rows_bwd(E, 2 * D, ca, 2 * D, 0.0f, cn_adj, 2 * D, sv.concat, 2 * D,
                            md.p("combination_norms." + ls + ".weight"), 1, st));
       if (E) {
