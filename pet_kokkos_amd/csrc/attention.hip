@@ -665,6 +665,16 @@ __global__ void zero_dead_kernel(float* __restrict__ x, int64_t ld, int width, i
   }
 }
 
+// The inverse scales [blocks][T] of a capacity's dead rows (block pairs of
+// qkv_adj, whose pairs zero_dead_kernel clears) set to 0.
+__global__ void zero_dead_inv_kernel(float* __restrict__ inv, int blocks, int N, int T, const int* __restrict__ off) {
+  const int64_t first = int64_t(N) + off[N];
+  const int64_t rows = int64_t(T) - first;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < rows * blocks;
+       i += int64_t(gridDim.x) * blockDim.x)
+    inv[(i / rows) * T + first + i % rows] = 0.f;
+}
+
 // ---- host side ---------------------------------------------------------------
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -776,7 +786,8 @@ size_t pair_bwd_bytes(int HD, int NW);
 const void* pair_bwd_kernel_ptr(int HD);
 int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
-             const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st);
+             const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st,
+             void* qpairs = nullptr, int64_t prows = 0);
 
 template <int HD>
 Plan plan_fwd(const pet_attn_shape& sh, bool xf) {
@@ -1124,6 +1135,43 @@ int bwd_whole(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const int
   return zero_dead(qkv_adj, lda, 3 * sh->heads * sh->head_dim, *sh, off, st);
 }
 }  // namespace
+
+// The core's backward as pet_attn_bwd_xf, with qkv_adj written as block pairs
+// into qpairs instead of fp32: T rows of 3D / 8 groups of 8 values (hi then lo
+// fp16, 16 bytes each), each (row, head, q | k | v) slice of head_dim values
+// scaled by its own power of two, then the slices' inverse scales [3H][T]
+// (block m H + h): the A operand, K blocks of head_dim, of the product that
+// reads qkv_adj next (pet_gemm_nt_pp_blocks). Dead rows hold zeros. Only
+// where the fp16-pair backward takes the shape and 3H is at most 32; else
+// PET_ATTN_ESLOTS, and the caller takes the fp32 form.
+int pet_attn_bwd_xf_blocks(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const float* rs, const float* b,
+                           const int* off, const float* dmerged, int64_t ldg, const float* merged, int64_t ldm,
+                           const float* ml, const float* cf_seq, int64_t ldc, void* qpairs, float* cfh,
+                           float* cf_seq_adj, int64_t ldca, hipStream_t st) {
+  using namespace pet_attn;
+  if (int e = check_shape(sh)) return e;
+  if (sh->n_atoms == 0) return PET_ATTN_OK;
+  if (!cf_seq_adj || ldca < sh->slots || !qpairs || !aligned16(qpairs)) return PET_ATTN_EINVAL;
+  const int HD = sh->head_dim;
+  if (streams(*sh) || (HD != 32 && HD != 64) || 3 * sh->heads > 32) return PET_ATTN_ESLOTS;
+  const bool pair = HD == 32 ? plan_bwd<32>(*sh).pair : plan_bwd<64>(*sh).pair;
+  if (!pair) return PET_ATTN_ESLOTS;
+  const int64_t D = int64_t(sh->heads) * HD, T = sh->n_rows;
+  if (int e = check_matrix(qkv, ldq, 3 * D, HD)) return e;
+  if (int e = check_matrix(dmerged, ldg, D, HD)) return e;
+  if (int e = check_matrix(merged, ldm, D, HD)) return e;
+  if (!off || !ml || !cf_seq || !cfh || ldc < sh->slots) return PET_ATTN_EINVAL;
+  if (int e = pair_bwd(*sh, 0, sh->n_atoms, sh->n_atoms, qkv, ldq, off, dmerged, ldg, merged, ldm, ml, cf_seq, ldc,
+                       nullptr, 0, cfh, QkvXf{rs, b}, st, qpairs, T))
+    return e;
+  if (int e = cf_adjoint(*sh, cfh, cf_seq, ldc, cf_seq_adj, ldca, st)) return e;
+  if (!sh->dead || sh->n_rows == sh->n_atoms) return PET_ATTN_OK;
+  if (int e = zero_dead(static_cast<float*>(qpairs), 3 * D, int(3 * D), *sh, off, st)) return e;
+  hipLaunchKernelGGL(zero_dead_inv_kernel, dim3(256), dim3(256), 0, st,
+                     reinterpret_cast<float*>(static_cast<char*>(qpairs) + size_t(T) * 3 * D * 4), 3 * sh->heads,
+                     sh->n_atoms, sh->n_rows, off);
+  return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
+}
 
 extern "C" {
 

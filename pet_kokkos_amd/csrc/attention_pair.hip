@@ -203,6 +203,12 @@ struct PairBwdArgs {
   int64_t lda;
   float* cfh;
   QkvXf xf;
+  // block pairs in place of qkv_adj (kernel form BP): the rows of qkv_adj as
+  // fp16 pairs (8-value groups of hi then lo 16 bytes, 3D / 8 groups a row),
+  // each (row, head, q | k | v) slice of HD values scaled by its own power of
+  // two, then the slices' inverse scales [3H][prows] (block m H + h)
+  u4* qpairs = nullptr;
+  int64_t prows = 0;
 };
 
 // A lane's raw rows of one item: its slot's q, k, v, dO and O (dims 32kc + 8g
@@ -252,7 +258,7 @@ __device__ __forceinline__ void pair_bwd_load(const PairBwdArgs& a, const Atom& 
 }
 
 // One (atom, head) item of the backward from the lane's loaded rows r.
-template <int HD, int NW, bool XF>
+template <int HD, int NW, bool XF, bool BP = false>
 __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& at, PairRows<HD / 4>& r,
                                               unsigned char* lds) {
   // KC 32-dim chunks of the head: lane (c, g) holds dims 32kc + 8g .. + 7 of its row
@@ -462,7 +468,49 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
 
   // ---- stores: dQ | dK | dV of the own row, lane dims 16t + 4g .. + 3
   const float cft = __builtin_amdgcn_ldexpf(sum_g(cfa), -kS);
-  if (real) {
+  if (BP && real) {
+    // block pairs: each of dQ, dK, dV's HD values of the row (four lanes, DT
+    // float4 each) scaled by the power of two that puts their largest |value|
+    // at [2^14, 2^15), split to nearest into fp16 hi and lo
+    const float f3[3] = {__builtin_amdgcn_ldexpf(sc, -kK - kS), __builtin_amdgcn_ldexpf(sc, -kQ - kS),
+                         __builtin_amdgcn_ldexpf(1.f, -kP - kG)};
+    const int64_t row = at.row(i);
+    unsigned* rowp = reinterpret_cast<unsigned*>(a.qpairs) + row * (3 * int64_t(D) / 8) * 8;
+    float* invp = reinterpret_cast<float*>(a.qpairs + a.prows * (3 * int64_t(D) / 8) * 2);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      const f4* acc = m == 0 ? dq : m == 1 ? dk : dv;
+      float v[DT][4];
+      float mx = 0.f;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[t][e] = acc[t][e] * f3[m], mx = fmaxf(mx, fabsf(v[t][e]));
+      const float s = pet_split::pair_scale(max_g(mx));
+      // lanes g and g ^ 1 (lanes l and l ^ 16) hold the two halves of the
+      // 8-value groups 2t + g / 2: the even lane writes the group of each even
+      // t, the odd lane that of each odd t, each trading the float4 the other
+      // needs, so that every lane stores whole 32-byte groups (hi then lo)
+      static_assert(DT % 2 == 0, "groups in lane pairs");
+#pragma unroll
+      for (int tt = 0; tt < DT; tt += 2) {
+        const bool odd = g & 1;
+        float x[4], y[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = __shfl_xor(odd ? v[tt][e] : v[tt + 1][e], 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = odd ? x[e] : v[tt][e], y[4 + e] = odd ? v[tt + 1][e] : x[e];
+        unsigned h[4], lw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pet_split::pair2(y[2 * e] * s, y[2 * e + 1] * s, h[e], lw[e]);
+        const int col = m * D + at.h * HD + 16 * (tt + (odd ? 1 : 0)) + 8 * (g >> 1);  // the group's first column
+        unsigned* hi = rowp + (col >> 3) * 8;
+        *reinterpret_cast<u4*>(hi) = u4{h[0], h[1], h[2], h[3]};
+        *reinterpret_cast<u4*>(hi + 4) = u4{lw[0], lw[1], lw[2], lw[3]};
+      }
+      if (g == 0) invp[int64_t(m * H + at.h) * a.prows + row] = 1.f / s;
+    }
+  } else if (real) {
     float* o = a.qkv_adj + at.row(i) * a.lda + at.h * HD + 4 * g;
     const float fq = __builtin_amdgcn_ldexpf(sc, -kK - kS), fk = __builtin_amdgcn_ldexpf(sc, -kQ - kS);
     const float fv = __builtin_amdgcn_ldexpf(1.f, -kP - kG);
@@ -478,8 +526,8 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
   if (g == 0 && i < a.S) a.cfh[(size_t(at.n) * H + at.h) * a.S + i] = real ? cft : 0.f;
 }
 
-// One workgroup per item.
-template <int HD, int NW, bool XF>
+// One workgroup per item. BP: block pairs in place of qkv_adj (a.qpairs).
+template <int HD, int NW, bool XF, bool BP = false>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD > 32 ? 4 : NW >= 4 ? 6 : 5)))
 attn_bwd_pair_kernel(PairBwdArgs a) {
   extern __shared__ float lds_f[];
@@ -487,7 +535,7 @@ attn_bwd_pair_kernel(PairBwdArgs a) {
   const Atom at(a.off, xcd_item(blockIdx.x, gridDim.x), a.H, a.N, a.S, a.n0, a.eb);
   PairRows<HD / 4> r;
   pair_bwd_load<HD, XF>(a, at, w, l >> 4, 16 * w + (l & 15), r);
-  pair_bwd_item<HD, NW, XF>(a, at, r, reinterpret_cast<unsigned char*>(lds_f));
+  pair_bwd_item<HD, NW, XF, BP>(a, at, r, reinterpret_cast<unsigned char*>(lds_f));
 }
 
 // ---- forward ---------------------------------------------------------------
@@ -765,22 +813,22 @@ const void* pair_bwd_kernel_ptr(int HD) {
 }
 
 namespace {
-template <int HD, int NW>
+template <int HD, int NW, bool BP = false>
 const void* pair_kernel(bool x) {
-  return x ? reinterpret_cast<const void*>(attn_bwd_pair_kernel<HD, NW, true>)
-           : reinterpret_cast<const void*>(attn_bwd_pair_kernel<HD, NW, false>);
+  return x ? reinterpret_cast<const void*>(attn_bwd_pair_kernel<HD, NW, true, BP>)
+           : reinterpret_cast<const void*>(attn_bwd_pair_kernel<HD, NW, false, BP>);
 }
-template <int HD>
+template <int HD, bool BP = false>
 const void* pair_kernel_nw(int NW, bool x) {
   switch (NW) {
-    case 1: return pair_kernel<HD, 1>(x);
-    case 2: return pair_kernel<HD, 2>(x);
-    case 3: return pair_kernel<HD, 3>(x);
-    case 4: return pair_kernel<HD, 4>(x);
-    case 5: return pair_kernel<HD, 5>(x);
-    case 6: return pair_kernel<HD, 6>(x);
-    case 7: return pair_kernel<HD, 7>(x);
-    default: return pair_kernel<HD, 8>(x);
+    case 1: return pair_kernel<HD, 1, BP>(x);
+    case 2: return pair_kernel<HD, 2, BP>(x);
+    case 3: return pair_kernel<HD, 3, BP>(x);
+    case 4: return pair_kernel<HD, 4, BP>(x);
+    case 5: return pair_kernel<HD, 5, BP>(x);
+    case 6: return pair_kernel<HD, 6, BP>(x);
+    case 7: return pair_kernel<HD, 7, BP>(x);
+    default: return pair_kernel<HD, 8, BP>(x);
   }
 }
 
@@ -805,7 +853,8 @@ int allow_lds_pair(const void* k, size_t bytes) {
 
 int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* qkv, int64_t ldq, const int* off,
              const float* dmerged, int64_t ldg, const float* merged, int64_t ldm, const float* ml,
-             const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st) {
+             const float* cf_seq, int64_t ldc, float* qkv_adj, int64_t lda, float* cfh, QkvXf xf, hipStream_t st,
+             void* qpairs, int64_t prows) {
   const int NW = (sh.slots + 15) / 16, HD = sh.head_dim;
   if (NW > kPairMaxWaves || (HD != 32 && HD != 64)) return PET_ATTN_ESLOTS;
   const int64_t items = int64_t(n1 - n0) * sh.heads;
@@ -813,10 +862,12 @@ int pair_bwd(const pet_attn_shape& sh, int n0, int n1, int64_t eb, const float* 
   if (items > INT32_MAX) return PET_ATTN_EINVAL;
   const size_t bytes = pair_bwd_bytes(HD, NW);
   const bool x = xf.rs || xf.b;
-  const void* k = HD == 64 ? pair_kernel_nw<64>(NW, x) : pair_kernel_nw<32>(NW, x);
+  const void* k = qpairs ? (HD == 64 ? pair_kernel_nw<64, true>(NW, x) : pair_kernel_nw<32, true>(NW, x))
+                         : (HD == 64 ? pair_kernel_nw<64>(NW, x) : pair_kernel_nw<32>(NW, x));
   if (const int e = allow_lds_pair(k, bytes)) return e;
-  const PairBwdArgs a{qkv, ldq, off, sh.n_atoms, n0, eb, sh.slots, sh.heads, sh.scale, dmerged, ldg, merged, ldm,
-                      ml, cf_seq, ldc, qkv_adj, lda, cfh, xf};
+  const PairBwdArgs a{qkv,  ldq,    off,    sh.n_atoms, n0,  eb,   sh.slots, sh.heads,
+                      sh.scale, dmerged, ldg, merged, ldm, ml, cf_seq, ldc, qkv_adj, lda, cfh, xf,
+                      static_cast<u4*>(qpairs), prows};
   void* args[] = {const_cast<PairBwdArgs*>(&a)};
   if (hipLaunchKernel(k, dim3(unsigned(items)), dim3(64 * NW), args, bytes, st) != hipSuccess) return PET_ATTN_ELAUNCH;
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;

@@ -55,6 +55,10 @@ int pet_gemm_nt_split_pairs(int M, int N, int K, const float* A, int64_t lda, co
 int pet_gemm_nt_pp_to_blocks(int M, int N, int K, const void* Ap, const void* Bs, void* pout, const float* bias,
                              const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre, int act,
                              hipStream_t st, int* kb);
+int pet_attn_bwd_xf_blocks(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const float* rs, const float* b,
+                           const int* off, const float* dmerged, int64_t ldg, const float* merged, int64_t ldm,
+                           const float* ml, const float* cf_seq, int64_t ldc, void* qpairs, float* cfh,
+                           float* cf_seq_adj, int64_t ldca, hipStream_t st);
 int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const void* Bs, float* C, int64_t ldc,
                           const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
                           float* pre, int64_t ldpre, int act, hipStream_t st);
@@ -1156,7 +1160,8 @@ struct Pass {
       // the atom rows and eps's (edge_adj, in place) on the edge rows.
       linear_bwd(md, tok_adj, node_adj, N, tl + ".center_expansion", 0.0f, st);
       float* dmerged = md.f(int64_t(T) * D);
-      float* qkv_adj = md.f(int64_t(T) * 3 * D);
+      // (with room for the inverse scales of qkv_adj as block pairs)
+      float* qkv_adj = md.f(int64_t(T) * (3 * D + 3 * md.h.num_heads) + 4);
       float* cfh = md.f(int64_t(N) * md.h.num_heads * S);
       float* in_adj = dmerged;
       linear_bwd(md, dmerged, tok_adj, T, tl + ".attention.output_linear", 0.0f, st);
@@ -1165,9 +1170,23 @@ struct Pass {
         qkv = md.f(int64_t(T) * 3 * D);
         linear_pre(md, qkv, b.tok, T, D, tl + ".attention.input_linear@fold", st);
       }
-      ok(pet_attn_bwd_xf(&sh, qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, dmerged, D,
-                         b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh, cf_seq_adj, S, st));
-      linear_bwd(md, in_adj, qkv_adj, T, tl + ".attention.input_linear", 0.0f, st);
+      // qkv_adj as block pairs straight into the input adjoint's product where
+      // that product takes the pairs-by-pairs form (block pairs); else fp32
+      const Mat& wit = md.w(tl + ".attention.input_linear.weight^T");
+      const void* wsp = md.blocks && md.pairs ? pp_split(md, wit, T, wit.rows, wit.cols) : nullptr;
+      const int rc = wsp ? pet_attn_bwd_xf_blocks(&sh, qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"),
+                                                  e.off, dmerged, D, b.merged, D, b.ml, cf_seq, S, qkv_adj, cfh,
+                                                  cf_seq_adj, S, st)
+                         : int(PET_ATTN_ESLOTS);
+      if (rc == PET_ATTN_OK) {
+        ok(pet_gemm_nt_pp_blocks(T, wit.rows, wit.cols, qkv_adj, md.hd, wsp, in_adj, wit.rows, nullptr, nullptr,
+                                 nullptr, 0, 0.f, nullptr, 0, 0, st));
+      } else {
+        if (rc != PET_ATTN_ESLOTS) ok(rc);
+        ok(pet_attn_bwd_xf(&sh, qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, dmerged, D,
+                           b.merged, D, b.ml, cf_seq, S, qkv_adj, 3 * D, cfh, cf_seq_adj, S, st));
+        linear_bwd(md, in_adj, qkv_adj, T, tl + ".attention.input_linear", 0.0f, st);
+      }
       // through the norm: atom rows set (input_node's adjoint), edge rows onto edge_adj
       ok(pet_rows_norm_bwd_sink(T, D, tok_adj, D, in_adj, D, b.tok, D, md.p(tl + ".norm_attention.weight"), 0, N,
                                 0.0f, 1.0f, e.off, st));

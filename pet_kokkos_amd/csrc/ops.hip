@@ -19,6 +19,13 @@ int pet_gemm_nt_split(int M, int N, int K, const float* A, int64_t lda, const vo
                       float* pre, int64_t ldpre, int act, hipStream_t st, void* scratch = nullptr,
                       size_t scratch_bytes = 0);
 int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st);
+int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const void* Bs, float* C, int64_t ldc,
+                          const float* row_scale, const float* bias, const float* cin, int64_t ldcin, float beta,
+                          float* pre, int64_t ldpre, int act, hipStream_t st);
+int pet_attn_bwd_xf_blocks(const pet_attn_shape* sh, const float* qkv, int64_t ldq, const float* rs, const float* b,
+                           const int* off, const float* dmerged, int64_t ldg, const float* merged, int64_t ldm,
+                           const float* ml, const float* cf_seq, int64_t ldc, void* qpairs, float* cfh,
+                           float* cf_seq_adj, int64_t ldca, hipStream_t st);
 int pet_gemm_nt_split_f32b(int M, int N, int K, const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                            int64_t ldc, const float* bias, const float* cin, int64_t ldcin, float beta, hipStream_t st);
 
@@ -100,6 +107,12 @@ __global__ void fill_bias_kernel(float* __restrict__ out, int64_t ldo, const flo
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+// the backward's qkv_adj [T, 3D] in the workspace, with room for its block
+// pairs' inverse scales (T 3H floats)
+size_t qkv_adj_bytes(const pet_attn_shape& sh) {
+  const size_t D = size_t(sh.heads) * sh.head_dim, T = size_t(sh.n_rows);
+  return align256(sizeof(float) * T * (3 * D + 3 * size_t(sh.heads)));
+}
 
 // Rows N + off[N] .. T-1 of x [T, width]: 0 when beta is 0, else beta times
 // themselves (what in_adj's dead rows get from a zeroed qkv adjoint).
@@ -222,13 +235,28 @@ int attention_bwd_xf(const pet_attn_shape* sh, float* in_adj, int64_t ldi, int d
   const int D = sh->heads * sh->head_dim, T = sh->n_rows;
   float* dmerged = reinterpret_cast<float*>(ws);
   float* qkv_adj = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D));
-  float* cfh = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D) +
-                                        align256(sizeof(float) * size_t(T) * 3 * D));
+  float* cfh = reinterpret_cast<float*>(ws + align256(sizeof(float) * size_t(T) * D) + qkv_adj_bytes(*sh));
   // dmerged = out_adj W_out: B = W_out^T; in_adj = qkv_adj W_in: B = W_in^T
   int se = split_dense(dmerged, D, out_adj, ldo, w_out, D, true, T, D, D, nullptr, 0.0f, split_out_t, st);
   if (se > 0) return se;
   if (se < 0)
     if (int e = gemm_nn(dmerged, D, out_adj, ldo, w_out, T, D, D, 0.0f, st)) return e;
+  // the core's backward writing qkv_adj as block pairs (a scale per row, head
+  // and q | k | v) and the input adjoint from them on the pairs-by-pairs
+  // kernel, with no fp32 qkv_adj and no split pass of it, where the fp16-pair
+  // backward takes the shape and the product is large enough for the split
+  // kernel (C3 op level on MI355X: see pet_attention_bwd)
+  if (split_in_t && 3 * D >= 256 && (3 * D) % 32 == 0 && double(T) * d_in * 3 * D >= 4294967296.0 && ldi % 4 == 0 &&
+      (reinterpret_cast<uintptr_t>(in_adj) & 15) == 0) {
+    const int rc = pet_attn_bwd_xf_blocks(sh, qkv, ldq, rs, b, off, dmerged, D, merged, D, ml, cf_seq, ldc, qkv_adj,
+                                          cfh, cf_seq_adj, ldca, st);
+    if (rc == PET_ATTN_OK) {
+      if (int e = pet_gemm_split_weights(w_in, d_in, 3 * D, d_in, true, split_in_t, st)) return e;
+      return pet_gemm_nt_pp_blocks(T, d_in, 3 * D, qkv_adj, sh->head_dim, split_in_t, in_adj, ldi, nullptr, nullptr,
+                                   beta != 0.f ? in_adj : nullptr, ldi, beta, nullptr, 0, 0, st);
+    }
+    if (rc != PET_ATTN_ESLOTS) return rc;
+  }
   if (int e = pet_attn_bwd_xf(sh, qkv, ldq, rs, b, off, dmerged, D, merged, D, ml, cf_seq, ldc, qkv_adj, 3 * D, cfh,
                               cf_seq_adj, ldca, st))
     return e;
@@ -274,7 +302,7 @@ int pet_attention(const pet_attn_shape* sh, float* out, int64_t ldo, const float
 // on rocBLAS).
 size_t bwd_core_bytes(const pet_attn_shape* sh) {
   const size_t D = size_t(sh->heads) * sh->head_dim, T = size_t(sh->n_rows);
-  return align256(sizeof(float) * T * D) + align256(sizeof(float) * T * 3 * D) +
+  return align256(sizeof(float) * T * D) + qkv_adj_bytes(*sh) +
          align256(sizeof(float) * size_t(sh->n_atoms) * sh->slots * sh->heads);
 }
 size_t bwd_split_bytes(const pet_attn_shape* sh) {
