@@ -349,3 +349,39 @@ def test_backward_before_forward_raises(device):
     ws = A.Workspace(device)
     with pytest.raises(RuntimeError):
         ws.peek2("nothing:merged")
+
+
+def test_op_level_dead_rows_block_pairs(device):
+    # attention_bwd() at C3's size (where the backward writes qkv_adj as block
+    # pairs into the input adjoint's product) with 4096 capacity rows past the
+    # tokens: the real rows as the oracle's without them, the dead rows of
+    # in_adj exactly beta times their value before (a zero qkv adjoint there)
+    conf, tk = systems.config_tokens("c3")
+    H, hd, D = conf.heads, conf.head_dim, conf.d_model
+    inp = systems.attention_inputs(tk, D, H, seed=11)
+    extra, T = 4096, tk.n_rows + 4096
+    rng = np.random.default_rng(12)
+    pad = lambda a: np.concatenate([a, rng.standard_normal((extra, a.shape[1])).astype(np.float32)])
+    qkv_d, oadj_d = pad(inp["qkv"]), pad(inp["out_adj"])
+    in_adj0 = rng.standard_normal((T, D)).astype(np.float32)
+    cf_adj0 = rng.standard_normal((tk.n_atoms, tk.slots)).astype(np.float32)
+    say("[gpu] op level c3 with 4096 dead rows, beta=1")
+    ws = A.Workspace(device)
+    t = A.Tokens(dev(tk.off, device, torch.int32), tk.n_atoms, dead=True)
+    out = torch.empty((T, D), device=device)
+    qkv, cf = dev(qkv_d, device), dev(tk.cf_seq, device)
+    w_in, w_out, b_out = dev(inp["w_in"], device), dev(inp["w_out"], device), dev(inp["b_out"], device)
+    A.attention(ws, "L0.a0", out, qkv, cf, w_out, b_out, t, tk.slots, H, hd, 1.0, True)
+    in_adj, cf_adj = dev(in_adj0, device), dev(cf_adj0, device)
+    A.attention_bwd(ws, "L0.a0", in_adj, cf_adj, dev(oadj_d, device), qkv, cf, w_in, w_out, t, tk.slots, H, hd, 1.0,
+                    1.0)
+    torch.cuda.synchronize()
+    got = in_adj.cpu().numpy()
+    assert np.array_equal(got[tk.n_rows:], in_adj0[tk.n_rows:])
+    _, rm, rml = oracle.attention(inp["qkv"], tk.off, tk.cf_seq, inp["w_out"], inp["b_out"], H, hd, 1.0)
+    rin, rca = oracle.attention_bwd(inp["out_adj"], inp["qkv"], tk.off, tk.cf_seq, inp["w_in"], inp["w_out"], rm, rml,
+                                    H, hd, 1.0, cf_seq_adj=cf_adj0, in_adj=in_adj0[: tk.n_rows], beta=1.0)
+    e = dict(in_adj=row_err(got[: tk.n_rows], rin), cf_seq_adj=row_err(cf_adj.cpu().numpy(), rca))
+    say("    ", {k: f"{v:.2e}" for k, v in e.items()})
+    for k, v in e.items():
+        assert v <= RTOL, k
