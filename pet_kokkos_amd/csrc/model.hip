@@ -969,11 +969,30 @@ struct Pass {
       ok(pet_attn_fwd_xf(&sh, qkv, 3 * D, b.inv, md.p(tl + ".attention.input_linear.bias"), e.off, cf_seq, S,
                          b.merged, D, b.ml, st));
       float* attn_out = md.f(int64_t(T) * D);
-      linear(md, attn_out, b.merged, T, D, tl + ".attention.output_linear", st);
+      const Mat& wi = md.w(tl + ".mlp.w_in.weight");
+      const Mat& wo = md.w(tl + ".mlp.w_out.weight");
+      // Where the output linear takes the split kernel and the edge MLP chains
+      // as block pairs, the edge rows' residual rides in epilogues: the output
+      // linear's edge rows go straight to eps = merged W^T + b + edge_cur (the
+      // same bits as the residual pass's), and the edge MLP's last product adds
+      // its bias and eps itself, so edge_next is never filled by a pass of its
+      // own. The node rows and the edge rows take the kernel the whole matrix
+      // would (a row's results do not depend on the others).
+      const Mat& wout = md.w(tl + ".attention.output_linear.weight");
+      const Sel so = split_for(md, b.merged, D, wout.p, T, D, D);
+      const bool fuse_res = E > 0 && bool(so) && chains(md, wide ? std::min(chunk, E) : E, D, wi, 2, wo);
+      if (fuse_res) {
+        const float* bo = md.p(tl + ".attention.output_linear.bias");
+        if (N) ok(own_nt(md, so, N, D, D, b.merged, D, attn_out, D, nullptr, bo, nullptr, 0, 0.f, nullptr, 0, 0, st));
+        ok(own_nt(md, so, E, D, D, b.merged + int64_t(N) * D, D, b.eps, D, nullptr, bo, edge_cur, D, 1.f, nullptr, 0, 0,
+                  st));
+      } else {
+        linear(md, attn_out, b.merged, T, D, tl + ".attention.output_linear", st);
+      }
       float* node_exp = md.f(int64_t(N) * Dn);
       linear(md, node_exp, attn_out, N, D, tl + ".center_expansion", st);
       // eps = attention's edge rows + edge_cur; edge_next = eps + mlp's output bias
-      if (E) {
+      if (E && !fuse_res) {
         residual_pass(b.eps, edge_next, attn_out + int64_t(N) * D, edge_cur, md.p(tl + ".mlp.w_out.bias"),
                       int64_t(E), D, st);
       }
@@ -990,9 +1009,7 @@ struct Pass {
         swiglu(md, hc, b.pre_c, N, tl + ".center_mlp.w_in", st);
       }
       linear_acc(md, node_next, hc, N, md.cw / 2, tl + ".center_mlp.w_out", st);
-      float* en = attn_out;  // consumed: its edge rows were read by the residual pass
-      const Mat& wi = md.w(tl + ".mlp.w_in.weight");
-      const Mat& wo = md.w(tl + ".mlp.w_out.weight");
+      float* en = attn_out;  // consumed: its edge rows were read by the residual pass (or never written)
       // edge_next += SwiGLU(en W_in^T + b_in) W_out^T over rows [e0, e0 + rows),
       // the pre-activation into pre: the SwiGLU output as block pairs where the
       // two products chain so
@@ -1008,9 +1025,13 @@ struct Pass {
           const Blocks hb = blocks_out_normed(md, epsr, rows, D, tl + ".norm_mlp", false, wi, 2,
                                              md.p(tl + ".mlp.w_in.bias"), pre, st, all ? attn_out : nullptr,
                                              all ? int64_t(T) * D : 0);
-          blocks_in(md, out, hb, rows, wo, nullptr, out, 1.f, st);
+          if (fuse_res)  // edge_next = h W^T + b + eps
+            blocks_in(md, out, hb, rows, wo, md.p(tl + ".mlp.w_out.bias"), epsr, 1.f, st);
+          else  // edge_next (eps + b already) += h W^T
+            blocks_in(md, out, hb, rows, wo, nullptr, out, 1.f, st);
           return;
         }
+        if (fuse_res) bias_add_pass(out, epsr, md.p(tl + ".mlp.w_out.bias"), rows, D, st);  // edge_next = eps + b
         norm(md, enr, epsr, rows, D, tl + ".norm_mlp", false, st);
         float* he = md.f(int64_t(rows) * md.ew / 2);
         if (!linear_act(md, he, pre, enr, rows, D, tl + ".mlp.w_in", 2, st)) {
