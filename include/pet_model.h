@@ -160,13 +160,13 @@ PET_ATTN_API int pet_linear_fused_split_ws(int M, int N, int K, const float* A, 
                                            int act, void* scratch, size_t scratch_bytes, void* stream);
 
 /* The dense layer for a short contraction, K at most 128 (a multiple of 32):
- * W [N, K] given as fp16 pair rows by pet_linear_pair_weights (W's rows each
- * scaled by a power of two and split into a hi and a lo fp16 part, both
- * rounded to nearest; N * K * 4 + N * 4 bytes, 16-byte aligned), A fp32 (lda
- * a multiple of 4, 16-byte aligned), epilogue as pet_linear_fused. Each
- * workgroup keeps 128 rows of A in registers as pairs and runs all four part
- * products on the 16-bit matrix cores, so a row's results depend on that row
- * alone (not on M or the tiling) and repeat bit for bit. No counterpart in
+ * W [N, K] given by pet_linear_pair_weights as rows of three fp16 parts (W's
+ * rows each scaled by a power of two and split into hi, mid and lo, which sum
+ * to it exactly; N * K * 6 + N * 4 bytes, 16-byte aligned), A fp32 (lda a
+ * multiple of 4, 16-byte aligned), epilogue as pet_linear_fused. Each
+ * workgroup keeps 64 rows of A in registers as fp16 pairs and runs five part
+ * products on the 16-bit matrix cores (all but a_lo b_lo), so a row's results
+ * depend on that row alone (not on M or the tiling) and repeat bit for bit. No counterpart in
  * the reference, which runs these layers in fp32 (src/fused_gemm_hip.cpp). */
 PET_ATTN_API int pet_linear_pair_weights(const float* W, int N, int K, int64_t ldw, void* out, void* stream);
 PET_ATTN_API int pet_linear_fused_smallk(int M, int N, int K, const float* A, int64_t lda, const void* Wpairs,

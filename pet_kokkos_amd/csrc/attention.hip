@@ -1015,7 +1015,7 @@ const char* pet_attn_strerror(int code) {
 
 int pet_attn_set_option(int opt, int value) {
   if (opt <= 0 || opt >= PET_OPT_COUNT) return PET_ATTN_EINVAL;
-  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 5, 1, 1, 2, 1};
+  static const int lo[PET_OPT_COUNT] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, hi[PET_OPT_COUNT] = {0, 1, 3, 2, 2, 6, 1, 1, 2, 1};
   if (value < lo[opt] || value > hi[opt]) return PET_ATTN_EINVAL;
   g_options[opt].store(value, std::memory_order_relaxed);
   return PET_ATTN_OK;

@@ -720,12 +720,14 @@ __global__ void __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_pe
 }
 
 // Rows of B = W (transposed false: W [N, K], ld ldw) or B = W^T (transposed
-// true: W [K, N]) as fp16 pairs: out[(n K/8 + j) 2 + p] = part p (hi, lo) of
-// row n's k group j, scaled by the row's s_n; then at byte N K 4 the N
-// inverse scales 1 / s_n. One workgroup a row: its largest |x|, then its
-// groups.
+// true: W [K, N]) as P fp16 parts: out[(n K/8 + j) P + p] = part p of row n's
+// k group j, scaled by the row's s_n (P 2: hi and lo, pair2; P 3: hi, mid and
+// lo, pair3, W exactly); then at byte N K 2 P the N inverse scales 1 / s_n.
+// One workgroup a row: its largest |x|, then its groups.
+template <int P>
 __global__ void __launch_bounds__(256) pair_rows_kernel(const float* __restrict__ W, int N, int K, int64_t ldw,
                                                          bool transposed, u4* __restrict__ out) {
+  static_assert(P == 2 || P == 3, "two or three parts");
   __shared__ float red[4];
   const int n = blockIdx.x, tid = threadIdx.x, KG = K / 8;
   auto at = [&](int k) { return transposed ? W[int64_t(k) * ldw + n] : W[int64_t(n) * ldw + k]; };
@@ -737,17 +739,23 @@ __global__ void __launch_bounds__(256) pair_rows_kernel(const float* __restrict_
   __syncthreads();
   const float s = pair_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
   for (int j = tid; j < KG; j += 256) {
-    u4 hi, lo;
+    u4 pt[P];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      unsigned h, lw;
-      pair2(at(8 * j + 2 * e) * s, at(8 * j + 2 * e + 1) * s, h, lw);
-      hi[e] = h, lo[e] = lw;
+      const float x = at(8 * j + 2 * e) * s, y = at(8 * j + 2 * e + 1) * s;
+      unsigned h, md, lw;
+      if constexpr (P == 2) {
+        pair2(x, y, h, lw);
+        pt[0][e] = h, pt[1][e] = lw;
+      } else {
+        pet_split::pair3(x, y, h, md, lw);
+        pt[0][e] = h, pt[1][e] = md, pt[2][e] = lw;
+      }
     }
-    out[(int64_t(n) * KG + j) * 2] = hi;
-    out[(int64_t(n) * KG + j) * 2 + 1] = lo;
+#pragma unroll
+    for (int p = 0; p < P; ++p) out[(int64_t(n) * KG + j) * P + p] = pt[p];
   }
-  if (tid == 0) reinterpret_cast<float*>(out + int64_t(N) * KG * 2)[n] = 1.f / s;
+  if (tid == 0) reinterpret_cast<float*>(out + int64_t(N) * KG * P)[n] = 1.f / s;
 }
 
 // Rows of an activation X [M, K] (ld ldx) as fp16 pairs in pair_rows_kernel's
@@ -1016,127 +1024,241 @@ __attribute__((amdgpu_waves_per_eu(BM == 128 && BN == 128 ? 4 : 1))) gemm_pp_ker
   if constexpr (!PO) epilogue<WM, WN>(acc, m0, n0, wm, wn, c, g, M, N, C, ldc, epi);  // (block pairs: the host makes sure of the staged one)
 }
 
-// Small K (at most 128): A resident in the waves' registers. A workgroup of
-// four waves takes 128 rows of A (32 a wave), loads them once, finds each
-// row's largest |x| across the four lanes that hold it, and keeps the rows as
-// fp16 pairs in the matrix instruction's a layout (lane (c, g): row c of a
-// 16-row block, k 32 kk + 8 g .. + 7); then for each of its column tiles (BN
-// columns) it stages B's pair rows (pet_gemm_pair_weights' layout: per column
-// n its k groups' hi and lo, then the inverse scales) into LDS, rows padded by
-// 16 bytes so that a 16-lane read of 16 columns meets 16 distinct bank
-// quads, and runs all four part products (hi hi, hi lo, lo hi, lo lo: the
-// dropped term of three is not negligible against the products' own fp32
-// rounding at so short a K), k groups in order. A row's results depend on
-// that row alone: neither the tile shape nor M changes them. Epilogue as the
-// other kernels'.
-template <int KB, int BN, int NWV, int TM>
-__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4)))
-gemm_sk_kernel(int M, int N, const float* __restrict__ A, int64_t lda, const u4* __restrict__ Bp, float* C,
-               int64_t ldc, Epi epi, int cpw) {
-  constexpr int BM = 16 * NWV * TM, TN = BN / 16, KG = 4 * KB, RPB = 2 * KG + 1;
-  constexpr int BT = BN * RPB * 16, ET = BM * BN * 4;  // bytes: the B tile, the staged epilogue's tile
-  __shared__ u4 lds_b[(BT > ET ? BT : ET) / 16];
-  __shared__ float sinv[BM];
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
-  // work items: (row block, cpw of its column tiles), XCD-contiguous as in
-  // gemm_nt_pair_kernel
-  const int NT = (N + BN - 1) / BN, NG = (NT + cpw - 1) / cpw, total = gridDim.x, L = blockIdx.x;
-  const int q = total / 8, r = total % 8, x = L % 8;
-  const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + L / 8;
-  const int tm = t / NG, tn0 = (t % NG) * cpw, tn1 = min(tn0 + cpw, NT);
-  const int m0 = tm * BM;
-
-  u4 av[TM][KB][2];
-  {
-    float4 v[TM][KB][2];
+// epi_elem's arithmetic, in its order, for four consecutive output columns
+// j .. j + 3 of row i (j a multiple of 4; a SwiGLU pair in one lane), with
+// 16-byte accesses where vec (every pointer 16-byte aligned, every leading
+// dimension and N multiples of 4), element by element otherwise.
+template <bool vec, bool bwd>
+__device__ __forceinline__ void epi_quad(float (&v)[4], int i, int j, int M, int N, float* C, int64_t ldc,
+                                         const Epi& epi, const float4* bq = nullptr) {
+  if (i >= M || j >= N) return;
+  if constexpr (bwd) {
+    const float* z = epi.cin + int64_t(i) * epi.ldcin;
+    if (epi.act == 3) {
+      float o[4];
 #pragma unroll
-    for (int a = 0; a < TM; ++a) {
-      const float* row = A + int64_t(min(m0 + 16 * TM * w + 16 * a + c, M - 1)) * lda + 8 * g;
+      for (int e = 0; e < 4; ++e) {
+        if (!vec && j + e >= N) break;
+        const float x = z[j + e] + (epi.bias ? epi.bias[j + e] : 0.f), sg = sig_fast(x);
+        o[e] = v[e] * (sg * (1.0f + x * (1.0f - sg)));
+        if (!vec) C[int64_t(i) * ldc + j + e] = o[e];
+      }
+      if (vec) *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(o[0], o[1], o[2], o[3]);
+    } else {
 #pragma unroll
-      for (int kk = 0; kk < KB; ++kk) {
-        v[a][kk][0] = *reinterpret_cast<const float4*>(row + 32 * kk);
-        v[a][kk][1] = *reinterpret_cast<const float4*>(row + 32 * kk + 4);
+      for (int e = 0; e < 4; ++e) {
+        if (j + e >= N) break;
+        const int jj = j + e;
+        const float u = z[2 * jj] + (epi.bias ? epi.bias[2 * jj] : 0.f);
+        const float sg = sig_fast(z[2 * jj + 1] + (epi.bias ? epi.bias[2 * jj + 1] : 0.f));
+        *reinterpret_cast<float2*>(C + int64_t(i) * ldc + 2 * jj) = make_float2(v[e] * sg, v[e] * u * sg * (1.0f - sg));
       }
     }
+    return;
+  }
+  const int ne = vec ? 4 : min(4, N - j);
+  if (epi.row_scale) {
+    const float rs = epi.row_scale[i];
 #pragma unroll
-    for (int a = 0; a < TM; ++a) {
-      float m = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < KB; ++kk)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float4 u = v[a][kk][h];
-          m = fmaxf(m, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
-        }
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
-      const float sc = pair_scale(m);
-      if (g == 0) sinv[16 * TM * w + 16 * a + c] = 1.f / sc;
-#pragma unroll
-      for (int kk = 0; kk < KB; ++kk) {
-        unsigned h[4], lo[4];
-        pair2(v[a][kk][0].x * sc, v[a][kk][0].y * sc, h[0], lo[0]);
-        pair2(v[a][kk][0].z * sc, v[a][kk][0].w * sc, h[1], lo[1]);
-        pair2(v[a][kk][1].x * sc, v[a][kk][1].y * sc, h[2], lo[2]);
-        pair2(v[a][kk][1].z * sc, v[a][kk][1].w * sc, h[3], lo[3]);
-        av[a][kk][0] = u4{h[0], h[1], h[2], h[3]};
-        av[a][kk][1] = u4{lo[0], lo[1], lo[2], lo[3]};
-      }
+    for (int e = 0; e < 4; ++e) v[e] *= rs;
+  }
+  if (epi.bias) {
+    if (vec) {
+      const float4 b4 = bq ? *bq : *reinterpret_cast<const float4*>(epi.bias + j);
+      v[0] += b4.x, v[1] += b4.y, v[2] += b4.z, v[3] += b4.w;
+    } else {
+      for (int e = 0; e < ne; ++e) v[e] += epi.bias[j + e];
     }
   }
-  const float* inv_b = reinterpret_cast<const float*>(Bp + int64_t(N) * KG * 2);
-  for (int tn = tn0; tn < tn1; ++tn) {
-    const int n0 = tn * BN;
-    __syncthreads();  // the last tile's reads and epilogue are done with the LDS
-    for (int i = tid; i < BN * 2 * KG; i += 64 * NWV) {
-      const int rr = i / (2 * KG), o = i - rr * (2 * KG);
-      lds_b[rr * RPB + o] = Bp[int64_t(min(n0 + rr, N - 1)) * (2 * KG) + o];
+  if (epi.cin) {
+    const float* ci = epi.cin + int64_t(i) * epi.ldcin + j;
+    if (vec) {
+      const float4 c4 = *reinterpret_cast<const float4*>(ci);
+      v[0] += epi.beta * c4.x, v[1] += epi.beta * c4.y, v[2] += epi.beta * c4.z, v[3] += epi.beta * c4.w;
+    } else {
+      for (int e = 0; e < ne; ++e) v[e] += epi.beta * ci[e];
     }
-    __syncthreads();
-    f4 acc[TM][TN];
+  }
+  if (epi.pre) {
+    float* pr = epi.pre + int64_t(i) * epi.ldpre + j;
+    if (vec) {
+      *reinterpret_cast<float4*>(pr) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      for (int e = 0; e < ne; ++e) pr[e] = v[e];
+    }
+  }
+  float* ci = C + int64_t(i) * ldc;
+  if (epi.act == 2) {  // N even: pairs (j, j + 1), (j + 2, j + 3)
+    const float o0 = v[0] * sig_fast(v[1]), o1 = v[2] * sig_fast(v[3]);
+    if (vec) {
+      *reinterpret_cast<float2*>(ci + j / 2) = make_float2(o0, o1);
+    } else {
+      ci[j / 2] = o0;
+      if (ne > 2) ci[j / 2 + 1] = o1;
+    }
+    return;
+  }
+  if (epi.act == 1) {
 #pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-      for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int b = 0; b < TN; ++b)
-#pragma unroll
-      for (int kk = 0; kk < KB; ++kk) {
-        const u4* br = lds_b + (16 * b + c) * RPB + (4 * kk + g) * 2;
-        const u4 bh = br[0], bl = br[1];
-#pragma unroll
-        for (int a = 0; a < TM; ++a) {
-          acc[a][b] = pet_split::mfma_h(av[a][kk][1], bl, acc[a][b]);
-          acc[a][b] = pet_split::mfma_h(av[a][kk][1], bh, acc[a][b]);
-          acc[a][b] = pet_split::mfma_h(av[a][kk][0], bl, acc[a][b]);
-          acc[a][b] = pet_split::mfma_h(av[a][kk][0], bh, acc[a][b]);
-        }
-      }
+    for (int e = 0; e < 4; ++e) v[e] = v[e] * sig_fast(v[e]);
+  }
+  if (vec) {
+    *reinterpret_cast<float4*>(ci + j) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    for (int e = 0; e < ne; ++e) ci[j + e] = v[e];
+  }
+}
+
+// Small K (at most 128), weights in registers. A workgroup of four waves
+// owns four groups of 16 TN output columns, one a wave, each holding its
+// columns' weights as three fp16 parts in registers (loaded once, TN KB 12
+// registers), and streams 16-row blocks of A: per block each thread takes one
+// k group of 8 (a row's groups in KL consecutive lanes, KL the power of two at
+// or above K / 8), the row's largest |x| comes from a shuffle over those
+// lanes, and the rows are split into fp16 pairs once for the workgroup into a
+// double-buffered LDS slice (rows padded to an odd number of 16-byte slots, so
+// that the 16 rows a fragment read meets fall on distinct banks); the thread
+// then loads its group of the next block into the registers it has just read.
+// After one barrier each wave reads its operand fragments and runs the five
+// part products per k group (a_hi and a_lo against w_hi and w_mid, and a_hi
+// w_lo; the dropped a_lo w_lo is below 2^-33 of |a||w|), the column tiles'
+// accumulations interleaved, with the weights as the instruction's first
+// operand: lane (c, g) then holds output row c, columns 4 g .. 4 g + 3 of
+// each 16-column tile, and the epilogue reads and writes 16 bytes a lane.
+// XCD x (workgroup L on x = L mod 8) takes rows [x M / 8, (x + 1) M / 8) in S
+// ranges per set of four column groups, so the sets re-read a range of A
+// from their XCD's L2. A row's results depend on that row alone, and the
+// products are summed in the order of the LDS-staged kernel this replaced:
+// the same bits.
+template <int KB, int TN, bool VEC, bool BWD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TN * KB <= 2 ? 4 : TN * KB <= 4 && !BWD ? 3 : 2)))
+gemm_skt_kernel(int M, int N, const float* __restrict__ A, int64_t lda, const u4* __restrict__ Bp, float* C,
+                int64_t ldc, Epi epi, int S) {
+  // RB 16-row tiles a block (2, with twice the rows in flight, crashes the
+  // ROCm 7.2 compiler's copy propagation at K = 128)
+  constexpr int RB = 1;
+  constexpr int KG = 4 * KB, CW = 16 * TN, RP = 2 * KG + 1, NW = 4, T = 64 * NW, R = 16 * RB;
+  __shared__ u4 sa[2][R * RP];
+  __shared__ float sinv[2][R];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+  const int CG = (N + CW - 1) / CW, CS = (CG + NW - 1) / NW, x = blockIdx.x % 8, li = blockIdx.x / 8;
+  if (li >= CS * S) return;  // (uniform over the workgroup)
+  const int cs = li % CS, rs = li / CS, cg = cs * NW + w, n0 = cg * CW;
+  const bool live = cg < CG;  // a wave past the last column group still splits rows for the others
+  const int xr0 = int(int64_t(x) * M / 8), xr1 = int(int64_t(x + 1) * M / 8);
+  const int nb = (xr1 - xr0 + R - 1) / R;
+  const int b0 = int(int64_t(rs) * nb / S), b1 = int(int64_t(rs + 1) * nb / S);
+  if (b0 >= b1) return;  // (uniform)
+  u4 wh[TN][KB], wm[TN][KB], wl[TN][KB];
+  float ib[TN][4];
+  {
+    const float* inv_b = reinterpret_cast<const float*>(Bp + int64_t(N) * KG * 3);
 #pragma unroll
     for (int b = 0; b < TN; ++b) {
-      const float ib = inv_b[min(n0 + 16 * b + c, N - 1)];
+      const u4* br = Bp + int64_t(min(n0 + 16 * b + c, N - 1)) * (3 * KG);
 #pragma unroll
-      for (int a = 0; a < TM; ++a)
+      for (int kk = 0; kk < KB; ++kk) {
+        wh[b][kk] = br[(4 * kk + g) * 3];
+        wm[b][kk] = br[(4 * kk + g) * 3 + 1];
+        wl[b][kk] = br[(4 * kk + g) * 3 + 2];
+      }
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) acc[a][b][rr] = acc[a][b][rr] * sinv[16 * TM * w + 16 * a + 4 * g + rr] * ib;
+      for (int rr = 0; rr < 4; ++rr) ib[b][rr] = inv_b[min(n0 + 16 * b + 4 * g + rr, N - 1)];
     }
-    if (!staged_epilogue<BM, BN, NWV, 1>(acc, reinterpret_cast<float*>(lds_b), m0, n0, M, N, C, ldc, epi)) {
-      // a partial column tile or unaligned operands: the tile through LDS as
-      // well, then one element a thread a row at a time (a SwiGLU pair in
-      // neighbouring lanes), so no lane holds the addresses of all its
-      // results at once
-      float* tile = reinterpret_cast<float*>(lds_b);
-      __syncthreads();
+  }
+  constexpr bool HB = VEC && !BWD;  // a forward epilogue with 16-byte accesses: the bias held
+  float4 bq[HB ? TN : 1];
+  if constexpr (HB) {
 #pragma unroll
-      for (int a = 0; a < TM; ++a)
+    for (int b = 0; b < TN; ++b)
+      bq[b] = epi.bias && live ? *reinterpret_cast<const float4*>(epi.bias + min(n0 + 16 * b + 4 * g, N - 4))
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // a thread's k groups of a block: item e = tid + T q, row e / KL, group
+  // e % KL (KL the power of two at or above KG: a row's groups are KL
+  // consecutive lanes of one wave, those at KG and above idle); loaded one
+  // block ahead, into the registers the split has just read
+  constexpr int KL = KG <= 4 ? 4 : KG <= 8 ? 8 : 16, ITEMS = R * KL, NI = (ITEMS + T - 1) / T;
+  static_assert(ITEMS % T == 0 || ITEMS < T, "whole passes");
+  float4 v0[NI], v1[NI];
+  auto load_a = [&](int blk) {
 #pragma unroll
-        for (int b = 0; b < TN; ++b)
+    for (int q = 0; q < NI; ++q) {
+      const int e = tid + T * q;
+      if (e < ITEMS && e % KL < KG) {
+        const float* p = A + int64_t(min(xr0 + R * blk + e / KL, xr1 - 1)) * lda + 8 * (e % KL);
+        v0[q] = *reinterpret_cast<const float4*>(p);
+        v1[q] = *reinterpret_cast<const float4*>(p + 4);
+      } else {
+        v0[q] = v1[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  load_a(b0);
+  for (int blk = b0; blk < b1; ++blk) {
+    const int buf = (blk - b0) & 1;
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) tile[(16 * TM * w + 16 * a + 4 * g + rr) * BN + 16 * b + c] = acc[a][b][rr];
-      __syncthreads();
-      for (int e = tid; e < BM * BN; e += 64 * NWV) {
-        const int R = e / BN, cc = e - R * BN;
-        epi_elem(tile[e], m0 + R, n0 + cc, cc & 15, M, N, C, ldc, epi);
+    for (int q = 0; q < NI; ++q) {
+      const int e = tid + T * q, ir = e / KL, ij = e % KL;
+      float m = fmaxf(fmaxf(fmaxf(fabsf(v0[q].x), fabsf(v0[q].y)), fmaxf(fabsf(v0[q].z), fabsf(v0[q].w))),
+                      fmaxf(fmaxf(fabsf(v1[q].x), fabsf(v1[q].y)), fmaxf(fabsf(v1[q].z), fabsf(v1[q].w))));
+#pragma unroll
+      for (int o = 1; o < KL; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));  // the row's KL consecutive lanes
+      const float sc = pair_scale(m);
+      unsigned h[4], lo[4];
+      pair2(v0[q].x * sc, v0[q].y * sc, h[0], lo[0]);
+      pair2(v0[q].z * sc, v0[q].w * sc, h[1], lo[1]);
+      pair2(v1[q].x * sc, v1[q].y * sc, h[2], lo[2]);
+      pair2(v1[q].z * sc, v1[q].w * sc, h[3], lo[3]);
+      if (e < ITEMS && ij < KG) {
+        sa[buf][ir * RP + 2 * ij] = u4{h[0], h[1], h[2], h[3]};
+        sa[buf][ir * RP + 2 * ij + 1] = u4{lo[0], lo[1], lo[2], lo[3]};
+        if (ij == 0) sinv[buf][ir] = 1.f / sc;
+      }
+    }
+    load_a(min(blk + 1, b1 - 1));  // (the last block's rows again at the end: in bounds, unused)
+    __syncthreads();  // the block's pairs are in LDS; (double buffer) no wave still reads the slice two blocks back
+    if (live) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        u4 ah[KB], al[KB];
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk) {
+          ah[kk] = sa[buf][(16 * r + c) * RP + 2 * (4 * kk + g)];
+          al[kk] = sa[buf][(16 * r + c) * RP + 2 * (4 * kk + g) + 1];
+        }
+        const float isc = sinv[buf][16 * r + c];
+        const int i = xr0 + R * blk + 16 * r + c;
+        // the tiles' chains interleaved (each tile's products in the same
+        // order, small ones first), so TN independent accumulations are in
+        // flight
+        f4 acc[TN];
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk) {
+#pragma unroll
+          for (int b = 0; b < TN; ++b) acc[b] = pet_split::mfma_h(wm[b][kk], al[kk], acc[b]);
+#pragma unroll
+          for (int b = 0; b < TN; ++b) acc[b] = pet_split::mfma_h(wl[b][kk], ah[kk], acc[b]);
+#pragma unroll
+          for (int b = 0; b < TN; ++b) acc[b] = pet_split::mfma_h(wh[b][kk], al[kk], acc[b]);
+#pragma unroll
+          for (int b = 0; b < TN; ++b) acc[b] = pet_split::mfma_h(wm[b][kk], ah[kk], acc[b]);
+#pragma unroll
+          for (int b = 0; b < TN; ++b) acc[b] = pet_split::mfma_h(wh[b][kk], ah[kk], acc[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+          float o[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) o[rr] = acc[b][rr] * isc * ib[b][rr];
+          if (i < xr1)
+            epi_quad<VEC, BWD>(o, i, n0 + 16 * b + 4 * g, M, N, C, ldc, epi, HB ? &bq[HB ? b : 0] : nullptr);
+          // (one tile's epilogue at a time: its loads are not hoisted above
+          // the last tile's stores, which would hold every tile's operands)
+          asm volatile("" ::: "memory");
+        }
       }
     }
   }
@@ -1362,7 +1484,7 @@ int pet_gemm_split_weights(const float* W, int N, int K, int64_t ldw, bool trans
   const int64_t n = int64_t(N) * (K / 8);
   if (n == 0) return PET_ATTN_OK;
   if (pair_form(K))
-    hipLaunchKernelGGL(pair_rows_kernel, dim3(unsigned(N)), dim3(256), 0, st, W, N, K, ldw, transposed,
+    hipLaunchKernelGGL(pair_rows_kernel<2>, dim3(unsigned(N)), dim3(256), 0, st, W, N, K, ldw, transposed,
                        static_cast<u4*>(out));
   else if (transposed)
     hipLaunchKernelGGL(split_rows_t_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, W, N, K, ldw,
@@ -1573,39 +1695,59 @@ int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const voi
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
-// B's pair rows at any K (a multiple of 32): the pair form of
-// pet_gemm_split_weights, which takes it from K = 256 only.
+// B's rows as three fp16 parts (hi, mid, lo: W exactly) at any K (a multiple
+// of 32), for the short-K kernel: N K 6 + N 4 bytes.
 int pet_gemm_pair_weights(const float* W, int N, int K, int64_t ldw, bool transposed, void* out, hipStream_t st) {
   if (N < 0 || K < 0 || K % 32 || (reinterpret_cast<uintptr_t>(out) & 15)) return PET_ATTN_EINVAL;
   if (N == 0 || K == 0) return PET_ATTN_OK;
-  hipLaunchKernelGGL(pair_rows_kernel, dim3(unsigned(N)), dim3(256), 0, st, W, N, K, ldw, transposed,
+  hipLaunchKernelGGL(pair_rows_kernel<3>, dim3(unsigned(N)), dim3(256), 0, st, W, N, K, ldw, transposed,
                      static_cast<u4*>(out));
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
-// C = epi(A B^T) for K at most 128 (a multiple of 32), B as pair rows
-// (pet_gemm_pair_weights): gemm_sk_kernel.
+// C = epi(A B^T) for K at most 128 (a multiple of 32), B as rows of three
+// fp16 parts (pet_gemm_pair_weights): gemm_skt_kernel.
 int pet_gemm_nt_sk(int M, int N, int K, const float* A, int64_t lda, const void* Bp, float* C, int64_t ldc,
                    const Epi& e, hipStream_t st) {
   if (M < 0 || N < 0 || K < 32 || K > 128 || K % 32) return PET_ATTN_EINVAL;
   if (M == 0 || N == 0) return PET_ATTN_OK;
   if (lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(Bp) & 15))
     return PET_ATTN_EALIGN;
-  constexpr int BN = 64, NWV = 4, TM = 1, BM = 16 * NWV * TM;
-  const int64_t rb = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
-  if (rb * nt >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
-  // column tiles an item: about 2048 items, so A is loaded as few times as
-  // that allows
-  const int64_t cpw = std::max<int64_t>(1, std::min<int64_t>(nt, rb * nt / 2048));
-  const int64_t items = rb * ((nt + cpw - 1) / cpw);
+  // 32 columns a wave (64 at K <= 64, where the weights take half the
+  // registers); about 64 workgroups an XCD (two a CU), the XCD's rows split
+  // into S ranges per set of four column groups. Measured on MI355X at
+  // 27318 rows (K 128, N 1024: 58 us against 78 for a 64 x 64-tile kernel
+  // staging the weights through LDS; 32 and 128 workgroups an XCD slower).
+  const int KB = K / 32, TN = KB <= 2 ? 4 : 2, CW = 16 * TN;
+  const int64_t CG = (N + CW - 1) / CW, CS = (CG + 3) / 4;
+  const int64_t rows_x = (M + 7) / 8, nbx = (rows_x + 15) / 16;
+  const int64_t S = std::max<int64_t>(1, std::min<int64_t>(std::max<int64_t>(1, 64 / CS), nbx));
+  const int64_t wgx = CS * S;
+  if (wgx * 8 >= (int64_t(1) << 31)) return PET_ATTN_EINDEX;
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool vec = N % 4 == 0 && a16(C) && ldc % 4 == 0 && (!e.bias || a16(e.bias)) &&
+                   (!e.cin || (a16(e.cin) && e.ldcin % 4 == 0)) && (!e.pre || (a16(e.pre) && e.ldpre % 4 == 0));
   const u4* B = static_cast<const u4*>(Bp);
-  const dim3 grid{unsigned(items)}, block{unsigned(64 * NWV)};
-  switch (K / 32) {
-    case 1: hipLaunchKernelGGL((gemm_sk_kernel<1, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
-    case 2: hipLaunchKernelGGL((gemm_sk_kernel<2, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
-    case 3: hipLaunchKernelGGL((gemm_sk_kernel<3, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
-    default: hipLaunchKernelGGL((gemm_sk_kernel<4, BN, NWV, TM>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(cpw)); break;
+  const dim3 grid{unsigned(wgx * 8)}, block{256};
+  // (the backward epilogues element by element: their 16-byte form would
+  // only widen one store)
+#define PET_SKT_LAUNCH(kb, tn, v, bw) \
+  hipLaunchKernelGGL((gemm_skt_kernel<kb, tn, v, bw>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(S))
+#define PET_SKT_GO(kb, tn)                    \
+  if (e.act >= 3)                             \
+    PET_SKT_LAUNCH(kb, tn, false, true);      \
+  else if (vec)                               \
+    PET_SKT_LAUNCH(kb, tn, true, false);      \
+  else                                        \
+    PET_SKT_LAUNCH(kb, tn, false, false)
+  switch (KB) {
+    case 1: PET_SKT_GO(1, 4); break;
+    case 2: PET_SKT_GO(2, 4); break;
+    case 3: PET_SKT_GO(3, 2); break;
+    default: PET_SKT_GO(4, 2); break;
   }
+#undef PET_SKT_GO
+#undef PET_SKT_LAUNCH
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 

@@ -504,7 +504,7 @@ struct pet_model {
   int tier = 1;                // the memory tier of the last evaluation: 1 never, 2 wide
   std::unordered_map<std::string, Mat> m;
   std::unordered_map<const float*, const void*> split;  // a matrix's split-row copy (K a multiple of 32)
-  std::unordered_map<const float*, const void*> psplit;  // its fp16 pair rows at K <= 128 (the short-K kernel)
+  std::unordered_map<const float*, const void*> psplit;  // its fp16 part rows at K <= 128 (the short-K kernel)
   // layers whose saved pre-activation holds its bias (made by the split-product
   // kernel's epilogue in the forward in progress), read by their backward
   std::unordered_map<std::string, bool> pre_biased;
@@ -557,17 +557,18 @@ bool own_gemm(const pet_model& md, int M, int K) {
 // aligned rows. By PET_OPT_MODEL_GEMM: 4 (the default) the split-product
 // kernel for the large products (M N K >= 2^32), rocBLAS for the rest; 5
 // every product on this library's kernels -- the short-K kernel
-// (pet_linear_fused_smallk: A's rows as fp16 pairs in registers, four part
-// products) for K at most 128, the split-product kernel above -- so that no
-// result depends on how many rows come with it and every bias and activation
-// rides in an epilogue; 3 the split-product kernel for every product; 0
-// rocBLAS only. Measured on MI355X (energy+forces, ms): C2 2.81 / 2.06
-// (residual) with mode 4 (no C2 product is large), 2.88 / 1.92 with mode 5
-// (its kernels 2.25 ms of dense products against rocBLAS's 1.78, the
-// activation and bias passes gone), 3.59 / 2.40 with mode 3; C5 171 with mode
-// 4, 170 with mode 5. Mode 5's three-product split above K = 128 leaves C2's
-// energy 5.1e-7 from the float64 oracle (mode 4: 0.7e-7; the float32 oracle
-// 3.3e-7), so mode 4 stays the default.
+// (pet_linear_fused_smallk: the weights exact in three fp16 parts, A's rows
+// as fp16 pairs, five part products) for K at most 128, the split-product
+// kernel above -- so that no result depends on how many rows come with it and
+// every bias and activation rides in an epilogue; 6 as 4, plus the short-K
+// kernel for the K <= 128 products with a bias or activation; 3 the
+// split-product kernel for every product; 0 rocBLAS only. Measured on MI355X
+// (energy+forces, ms): C2 2.79 / 2.06 (residual) with mode 4 (no C2 product
+// is large), 3.05 / 2.07 with mode 5, 2.77 / 2.05 with mode 6, 3.59 / 2.40
+// with mode 3; C5 171 with mode 4, 170 with mode 5. Energies from the float64
+// oracle, C2 / residual: mode 4 0.7e-7 / 4.2e-7, mode 5 1.5e-7 / 8.3e-7, mode 6
+// 3.5e-7 / 5.7e-7 (the float32 oracle 3.3e-7 / 4.2e-7), so mode 4 stays the
+// default.
 // The kernel a product takes (null: rocBLAS): the copy of W it reads and
 // whether it is the short-K kernel.
 struct Sel {
@@ -575,15 +576,18 @@ struct Sel {
   bool sk = false;
   explicit operator bool() const { return p != nullptr; }
 };
-Sel split_for(const pet_model& md, const float* in, int64_t ldi, const float* W, int M, int N, int K) {
+// fuse: the call has a bias or an activation for the epilogue (mode 6 takes
+// the short-K kernel for those products at K <= 128, where it saves a pass).
+Sel split_for(const pet_model& md, const float* in, int64_t ldi, const float* W, int M, int N, int K,
+              bool fuse = false) {
   const int mode = md.gemm_mode;
   const bool big = double(M) * N * K >= 4294967296.0;
   if (ldi % 4 || (reinterpret_cast<uintptr_t>(in) & 15)) return {};
-  if (mode == 5 && K <= 128 && K % 32 == 0) {
+  if ((mode == 5 || (mode == 6 && fuse)) && K <= 128 && K % 32 == 0) {
     auto it = md.psplit.find(W);
     if (it != md.psplit.end()) return {it->second, true};
   }
-  if (mode == 3 || mode == 5 || (mode == 4 && big)) {
+  if (mode == 3 || mode == 5 || ((mode == 4 || mode == 6) && big)) {
     auto it = md.split.find(W);
     if (it != md.split.end()) return {it->second, false};
   }
@@ -618,7 +622,7 @@ void linear(pet_model& md, float* out, const float* in, int M, int K, const std:
     ok(pet_gemm_nt_fused(M, W.rows, K, in, K, W.p, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
-  if (const Sel sp = split_for(md, in, K, W.p, M, W.rows, K)) {  // the bias in the epilogue
+  if (const Sel sp = split_for(md, in, K, W.p, M, W.rows, K, b != nullptr)) {  // the bias in the epilogue
     ok(own_nt(md, sp, M, W.rows, K, in, K, out, W.rows, nullptr, b, nullptr, 0, 0.f, nullptr, 0, 0, st));
     return;
   }
@@ -650,7 +654,7 @@ void linear_acc_bias(pet_model& md, float* out, const float* in, int M, int K, c
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   if (M == 0) return;
-  if (const Sel sp = own_gemm(md, M, K) ? Sel{} : split_for(md, in, K, W.p, M, W.rows, K)) {
+  if (const Sel sp = own_gemm(md, M, K) ? Sel{} : split_for(md, in, K, W.p, M, W.rows, K, true)) {
     ok(own_nt(md, sp, M, W.rows, K, in, K, out, W.rows, nullptr, md.p(key + ".bias"), out, W.rows, 1.f, nullptr, 0, 0,
               st));
     return;
@@ -675,7 +679,7 @@ const float* pass_bias(const pet_model& md, const std::string& key);
 bool linear_bwd_act(pet_model& md, float* out, const float* adj, int M, const std::string& key_out, const float* z,
                     const std::string& key_act, int act, hipStream_t st) {
   const Mat& WT = md.w(key_out + ".weight^T");
-  const Sel sp = M ? split_for(md, adj, WT.cols, WT.p, M, WT.rows, WT.cols) : Sel{};
+  const Sel sp = M ? split_for(md, adj, WT.cols, WT.p, M, WT.rows, WT.cols, true) : Sel{};
   if (!sp) return false;
   const int64_t w = act == 2 ? 2 * int64_t(WT.rows) : WT.rows;
   ok(own_nt(md, sp, M, WT.rows, WT.cols, adj, WT.cols, out, w, nullptr, pass_bias(md, key_act), z, w, 0.f, nullptr, 0,
@@ -701,14 +705,14 @@ void linear_pre(pet_model& md, float* z, const float* in, int M, int K, const st
 // Whether linear_act fuses the layer (then out must be a buffer other than in).
 bool act_fuses(const pet_model& md, const float* in, int M, int K, const std::string& key) {
   const Mat& W = md.w(key + ".weight");
-  return !own_gemm(md, M, K) && bool(split_for(md, in, K, W.p, M, W.rows, K));
+  return !own_gemm(md, M, K) && bool(split_for(md, in, K, W.p, M, W.rows, K, true));
 }
 bool linear_act(pet_model& md, float* out, float* z, const float* in, int M, int K, const std::string& key, int act,
                 hipStream_t st) {
   const Mat& W = md.w(key + ".weight");
   if (W.cols != K) throw Error{PET_MODEL_ESHAPE};
   // (out must not be the GEMM's input: other workgroups still read its rows)
-  const Sel sp = own_gemm(md, M, K) || out == in ? Sel{} : split_for(md, in, K, W.p, M, W.rows, K);
+  const Sel sp = own_gemm(md, M, K) || out == in ? Sel{} : split_for(md, in, K, W.p, M, W.rows, K, true);
   md.pre_biased[key] = bool(sp);
   if (!sp || M == 0) return false;
   ok(own_nt(md, sp, M, W.rows, K, in, K, out, act == 2 ? W.rows / 2 : W.rows, nullptr, md.p(key + ".bias"), nullptr, 0,
@@ -733,7 +737,7 @@ struct Blocks {
 const void* pp_split(const pet_model& md, const Mat& W, int M, int N, int K) {
   const int mode = md.gemm_mode;
   const bool big = double(M) * N * K >= 4294967296.0;
-  if (!(mode == 3 || mode == 5 || (mode == 4 && big)) || (mode == 5 && K <= 128)) return nullptr;
+  if (!(mode == 3 || mode == 5 || ((mode == 4 || mode == 6) && big)) || (mode == 5 && K <= 128)) return nullptr;
   if (K < 256 || K % 32 || N < 512) return nullptr;
   auto it = md.split.find(W.p);
   return it == md.split.end() ? nullptr : it->second;
@@ -1704,12 +1708,12 @@ int pet_model_create(const pet_model_hypers* hy, const pet_model_tensor* tensors
       }
       if (hipDeviceSynchronize() != hipSuccess) throw Error{PET_ATTN_ELAUNCH};
     }
-    // fp16 pair rows of the matrices with K at most 128, for the short-K kernel
+    // the matrices with K at most 128 as rows of three fp16 parts, for the short-K kernel
     std::vector<std::pair<const Mat*, size_t>> pat;
     size_t ptotal = 0;
     for (auto& [n, mt] : md->m)
       if (mt.cols > 0 && mt.cols <= 128 && mt.cols % 32 == 0)
-        pat.push_back({&mt, ptotal}), ptotal += (size_t(4) * mt.rows * mt.cols + size_t(4) * mt.rows + 255) & ~size_t(255);
+        pat.push_back({&mt, ptotal}), ptotal += (size_t(6) * mt.rows * mt.cols + size_t(4) * mt.rows + 255) & ~size_t(255);
     if (ptotal) {
       if (hipMalloc(&md->wpair, ptotal) != hipSuccess) throw Error{PET_MODEL_EMEMORY};
       for (auto& [mt, o] : pat) {

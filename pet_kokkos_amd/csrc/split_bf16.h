@@ -100,6 +100,21 @@ __device__ __forceinline__ void pair2(float x, float y, unsigned& hi, unsigned& 
   hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
 }
+// Two scaled values as three fp16 parts each, hi + mid + lo = the value
+// exactly: hi its nearest fp16, mid the nearest fp16 of the rest (exact in
+// fp32), lo what is left (at most 2 significant bits: exact in fp16 wherever
+// the value is at least 2^-1; below that, within half an fp16 subnormal step).
+// For a matrix used in many products: its representation error would be the
+// same in every one of them, so none is left.
+__device__ __forceinline__ void pair3(float x, float y, unsigned& hi, unsigned& mid, unsigned& lo) {
+  const h2v h = {(_Float16)x, (_Float16)y};
+  const float rx = x - float(h[0]), ry = y - float(h[1]);
+  const h2v m = {(_Float16)rx, (_Float16)ry};
+  const h2v l = {(_Float16)(rx - float(m[0])), (_Float16)(ry - float(m[1]))};
+  hi = __builtin_bit_cast(unsigned, h);
+  mid = __builtin_bit_cast(unsigned, m);
+  lo = __builtin_bit_cast(unsigned, l);
+}
 // The row scale 2^(15 - e) for a largest |x| m = f 2^e (f in [0.5, 1)); 1 for
 // a zero row (and for one holding a NaN, which then propagates).
 __device__ __forceinline__ float pair_scale(float m) {

@@ -36,9 +36,9 @@ class SplitWeights:
 
 
 class PairWeights:
-    """W [N, K] (K a multiple of 32) as fp16 pair rows at any K (each row
-    scaled by a power of two, hi and lo parts both rounded to nearest),
-    N K 4 + N 4 bytes: the weights of the short-contraction layer
+    """W [N, K] (K a multiple of 32) as rows of three fp16 parts at any K
+    (each row scaled by a power of two; hi, mid and lo, their sum W s
+    exactly), N K 6 + N 4 bytes: the weights of the short-contraction layer
     (pet_linear_fused_smallk, K at most 128)."""
 
     def __init__(self, W: torch.Tensor):
@@ -47,7 +47,7 @@ class PairWeights:
         if K % 32:
             raise ValueError(f"W has K = {K}: pair weights need K a multiple of 32")
         self.shape = (N, K)
-        self.data = torch.empty(N * K * 2 + 2 * N + 8, dtype=torch.int16, device=W.device)
+        self.data = torch.empty(N * K * 3 + 2 * N + 8, dtype=torch.int16, device=W.device)
         _lib.check(_lib.load().pet_linear_pair_weights(W.data_ptr(), N, K, W.stride(0), self.data.data_ptr(),
                                                        torch.cuda.current_stream().cuda_stream),
                    "pet_linear_pair_weights")

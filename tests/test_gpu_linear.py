@@ -29,8 +29,10 @@ def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=Non
 
 
 # the last two are large enough for the split form's 128 x 128 and 128 x 64 tiles
+# (1001, 38, 96): a width not a multiple of 4 (the short-K kernel's per-element
+# epilogue) and 12 k groups a row (its rows padded to 16 lanes)
 SHAPES = [(1, 16, 16), (37, 40, 32), (300, 128, 128), (2049, 96, 256), (5000, 384, 128), (1000, 1024, 512),
-          (129, 64, 1024), (16385, 1024, 64), (131071, 96, 64)]
+          (129, 64, 1024), (16385, 1024, 64), (131071, 96, 64), (1001, 38, 96)]
 
 
 @pytest.mark.parametrize("split", [False, True, "smallk"], ids=["fp32", "split", "smallk"])
@@ -55,8 +57,8 @@ def test_plain_and_bias(M, N, K, split, device):
 
 
 @pytest.mark.parametrize("split", [False, True, "smallk"], ids=["fp32", "split", "smallk"])
-def test_epilogues(split, device):
-    M, N, K = 777, 256, 128
+@pytest.mark.parametrize("M,N,K", [(777, 256, 128), (1001, 38, 96)])
+def test_epilogues(M, N, K, split, device):
     g = torch.Generator(device=device).manual_seed(5)
     A = torch.randn(M, K, device=device, generator=g)
     W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
@@ -85,12 +87,14 @@ def test_epilogues(split, device):
     assert (pre.double() - z).abs().max().item() <= 1e-5 * z.abs().max().item()
 
 
-@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split"])
-@pytest.mark.parametrize("M,N,K", [(300, 128, 128), (16385, 512, 256)])
+@pytest.mark.parametrize("split", [False, True, "smallk"], ids=["fp32", "split", "smallk"])
+@pytest.mark.parametrize("M,N,K", [(300, 128, 128), (16385, 512, 256), (1001, 38, 96), (5000, 64, 32)])
 def test_backward_epilogues(M, N, K, split, device):
     """act 3 / 4: the SiLU / SwiGLU backward fused into the input-adjoint
     product (A W^T is the activation output's adjoint, cin the saved
     pre-activation, bias its bias when not yet added), against float64."""
+    if split == "smallk" and K > 128:
+        pytest.skip("the short-contraction layer takes K at most 128")
     g = torch.Generator(device=device).manual_seed(M + N)
     A = torch.randn(M, K, device=device, generator=g)
     W = torch.randn(N, K, device=device, generator=g) / K ** 0.5
@@ -376,14 +380,61 @@ def test_smallk_rows_independent_of_M(K, device):
         assert (pre.double() - z).abs().max().item() <= 1e-5 * z.abs().max().item()
 
 
-def W_ref(W, device):
-    """The fp64 matrix of pair weights: hi + lo over each row's scale."""
+def smallk_parts(W):
+    """The short-K weights' parts [N, K/8, 3, 8] (hi, mid, lo) and inverse scales [N], fp64."""
     N, K = W.shape
     raw = W.data.cpu().numpy().view(np.uint8)
-    parts = raw[: N * K * 4].view(np.float16).reshape(N, K // 8, 2, 8).astype(np.float64)
-    inv = raw[N * K * 4: N * K * 4 + 4 * N].view(np.float32).astype(np.float64)
-    w = (parts[:, :, 0, :] + parts[:, :, 1, :]).reshape(N, K) * inv[:, None]
+    parts = raw[: N * K * 6].view(np.float16).reshape(N, K // 8, 3, 8).astype(np.float64)
+    inv = raw[N * K * 6: N * K * 6 + 4 * N].view(np.float32).astype(np.float64)
+    return parts, inv
+
+
+def W_ref(W, device):
+    """The fp64 matrix of part weights over each row's scale: the short-K
+    weights' hi + mid + lo, or the pair form's hi + lo (SplitWeights from
+    K = 256)."""
+    N, K = W.shape
+    if isinstance(W, L.PairWeights):
+        parts, inv = smallk_parts(W)
+    else:
+        raw = W.data.cpu().numpy().view(np.uint8)
+        parts = raw[: N * K * 4].view(np.float16).reshape(N, K // 8, 2, 8).astype(np.float64)
+        inv = raw[N * K * 4: N * K * 4 + 4 * N].view(np.float32).astype(np.float64)
+    w = parts.sum(axis=2).reshape(N, K) * inv[:, None]
     return torch.from_numpy(w).to(device)
+
+
+def test_smallk_weights_exact(device):
+    """pet_linear_pair_weights: per row a power-of-two scale s (max |w| s in
+    [2^14, 2^15)), per element hi = w s to the nearest fp16, mid = the rest to
+    the nearest fp16, lo = what is left: hi + mid + lo = w s exactly wherever
+    |w s| >= 2^-1 (lo then holds at most 2 bits at an exponent fp16 reaches),
+    within half an fp16 subnormal step below. So the weights the short-K
+    kernel multiplies are W itself: a pair form (22 bits) would be a fixed
+    perturbation of the model, the same error in every row's product."""
+    N, K = 40, 128
+    g = torch.Generator(device=device).manual_seed(16)
+    W = torch.randn(N, K, device=device, generator=g) * torch.logspace(-10, 10, K, device=device)
+    W[3] *= 1e-30  # a row far below fp16's range before scaling
+    W[5] = 0.0  # a zero row
+    W[7] = torch.randn(K, device=device, generator=g)  # an ordinary row
+    parts, inv = smallk_parts(L.PairWeights(W))
+    s = 1.0 / inv
+    assert np.array_equal(np.exp2(np.round(np.log2(s))), s)
+    w = W.cpu().numpy().astype(np.float64).reshape(N, K // 8, 8)
+    m = np.abs(w).reshape(N, K).max(1)
+    live = m > 0
+    assert np.all((m[live] * s[live] >= 2.0 ** 14) & (m[live] * s[live] < 2.0 ** 15))
+    assert s[5] == 1.0 and np.all(parts[5] == 0)
+    ws = w * s[:, None, None]
+    hi, mid, lo = parts[:, :, 0, :], parts[:, :, 1, :], parts[:, :, 2, :]
+    big = np.abs(ws) >= 0.5
+    assert np.array_equal(hi[big], ws[big].astype(np.float32).astype(np.float16).astype(np.float64))
+    assert np.array_equal(mid[big], (ws[big] - hi[big]).astype(np.float32).astype(np.float16).astype(np.float64))
+    assert np.array_equal((hi + mid + lo)[big], ws[big])
+    assert np.all(np.abs(hi + mid + lo - ws) <= 2.0 ** -25)
+    assert np.any(lo[big] != 0)  # the third part carries bits
+    assert np.array_equal((hi + mid + lo)[7], ws[7])  # an ordinary row: every element exact
 
 
 def blocks_ref(B, device):

@@ -139,13 +139,14 @@ def test_odd_widths_match_oracle(name, device):
     compare(got, oracle_of(h, w, comp, x))
 
 
-@pytest.mark.parametrize("mode", ["1", "3"], ids=["fp32", "split"])
+@pytest.mark.parametrize("mode", ["1", "3", "6"], ids=["fp32", "split", "shortk-epilogue"])
 @pytest.mark.parametrize("name", ["tiny", "tiny-residual"])
 def test_model_on_the_fused_dense_layer(name, mode, device):
     # option model_gemm = 1: every forward dense layer with K a multiple of 16
     # on the library's fused GEMM (pet_linear_fused's kernel) instead of
     # rocBLAS; 3: every dense layer with K a multiple of 32 on its
-    # split-product form (pet_linear_fused_split's kernel), backward included
+    # split-product form (pet_linear_fused_split's kernel), backward included;
+    # 6: the short-K kernel for the K <= 128 layers with a bias or activation
     from pet_kokkos_amd import _lib
     h = weights.MODELS[name]
     w = weights.random_weights(h, 15)
