@@ -1034,6 +1034,41 @@ __device__ __forceinline__ void epi_quad(float (&v)[4], int i, int j, int M, int
   if (i >= M || j >= N) return;
   if constexpr (bwd) {
     const float* z = epi.cin + int64_t(i) * epi.ldcin;
+    if constexpr (vec) {  // z, bias and C rows 16-byte aligned, N a multiple of 4
+      if (epi.act == 3) {
+        const float4 z4 = *reinterpret_cast<const float4*>(z + j);
+        const float4 b4 = epi.bias ? *reinterpret_cast<const float4*>(epi.bias + j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float xs[4] = {z4.x + b4.x, z4.y + b4.y, z4.z + b4.z, z4.w + b4.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float sg = sig_fast(xs[e]);
+          o[e] = v[e] * (sg * (1.0f + xs[e] * (1.0f - sg)));
+        }
+        *reinterpret_cast<float4*>(C + int64_t(i) * ldc + j) = make_float4(o[0], o[1], o[2], o[3]);
+      } else {  // (value, gate) pairs 2 j .. 2 j + 7
+        float zz[8];
+        *reinterpret_cast<float4*>(zz) = *reinterpret_cast<const float4*>(z + 2 * j);
+        *reinterpret_cast<float4*>(zz + 4) = *reinterpret_cast<const float4*>(z + 2 * j + 4);
+        if (epi.bias) {
+          const float4 b0 = *reinterpret_cast<const float4*>(epi.bias + 2 * j);
+          const float4 b1 = *reinterpret_cast<const float4*>(epi.bias + 2 * j + 4);
+          zz[0] += b0.x, zz[1] += b0.y, zz[2] += b0.z, zz[3] += b0.w;
+          zz[4] += b1.x, zz[5] += b1.y, zz[6] += b1.z, zz[7] += b1.w;
+        }
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float u = zz[2 * e], sg = sig_fast(zz[2 * e + 1]);
+          o[2 * e] = v[e] * sg;
+          o[2 * e + 1] = v[e] * u * sg * (1.0f - sg);
+        }
+        float* cr = C + int64_t(i) * ldc + 2 * j;
+        *reinterpret_cast<float4*>(cr) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4*>(cr + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      }
+      return;
+    }
     if (epi.act == 3) {
       float o[4];
 #pragma unroll
@@ -1729,12 +1764,12 @@ int pet_gemm_nt_sk(int M, int N, int K, const float* A, int64_t lda, const void*
                    (!e.cin || (a16(e.cin) && e.ldcin % 4 == 0)) && (!e.pre || (a16(e.pre) && e.ldpre % 4 == 0));
   const u4* B = static_cast<const u4*>(Bp);
   const dim3 grid{unsigned(wgx * 8)}, block{256};
-  // (the backward epilogues element by element: their 16-byte form would
-  // only widen one store)
 #define PET_SKT_LAUNCH(kb, tn, v, bw) \
   hipLaunchKernelGGL((gemm_skt_kernel<kb, tn, v, bw>), grid, block, 0, st, M, N, A, lda, B, C, ldc, e, int(S))
 #define PET_SKT_GO(kb, tn)                    \
-  if (e.act >= 3)                             \
+  if (e.act >= 3 && vec)                      \
+    PET_SKT_LAUNCH(kb, tn, true, true);       \
+  else if (e.act >= 3)                        \
     PET_SKT_LAUNCH(kb, tn, false, true);      \
   else if (vec)                               \
     PET_SKT_LAUNCH(kb, tn, true, false);      \

@@ -563,8 +563,8 @@ bool own_gemm(const pet_model& md, int M, int K) {
 // every bias and activation rides in an epilogue; 6 as 4, plus the short-K
 // kernel for the K <= 128 products with a bias or activation; 3 the
 // split-product kernel for every product; 0 rocBLAS only. Measured on MI355X
-// (energy+forces, ms): C2 2.79 / 2.06 (residual) with mode 4 (no C2 product
-// is large), 3.05 / 2.07 with mode 5, 2.77 / 2.05 with mode 6, 3.59 / 2.40
+// (energy+forces, ms): C2 2.80 / 2.07 (residual) with mode 4 (no C2 product
+// is large), 2.89 / 1.95 with mode 5, 2.585 / 1.92 with mode 6, 3.59 / 2.40
 // with mode 3; C5 171 with mode 4, 170 with mode 5. Energies from the float64
 // oracle, C2 / residual: mode 4 0.7e-7 / 4.2e-7, mode 5 1.5e-7 / 8.3e-7, mode 6
 // 3.5e-7 / 5.7e-7 (the float32 oracle 3.3e-7 / 4.2e-7), so mode 4 stays the
