@@ -99,13 +99,13 @@ enum {
                               3: the vector-ALU forward (head_dim <= 64), for comparison */
   PET_OPT_BWD_VLDS = 3,    /* 0 (default): automatic; 1: V staged in LDS; 2: V read from global memory (where it fits) */
   PET_OPT_BWD_NBUF = 4,    /* 0 (default): automatic; 1 or 2 backward tile buffers (where it fits) */
-  PET_OPT_MODEL_GEMM = 5,  /* the model's dense layers: 4 (default) split-product kernel for M*N*K >= 2^32, else rocBLAS;
-                              5 this library's kernels for every product (the short-K kernel for K <= 128, the
-                              split-product kernel above), no result depending on M; 0 rocBLAS only; 1 / 2 the fp32
-                              fused kernel for every / <= 4096-row forward layer; 3 the split-product kernel wherever
-                              K is a multiple of 32; 6 as 4, plus the short-K kernel for the K <= 128 layers
-                              with a bias or activation in the epilogue (faster at small shapes; its fp32 result
-                              carries a small negative mean error, so it is opt-in) */
+  PET_OPT_MODEL_GEMM = 5,  /* the model's dense layers: 6 (default) the split-product kernel for M*N*K >= 2^32, the
+                              short-K kernel for the K <= 128 layers with a bias or activation in the epilogue and
+                              N >= 64, rocBLAS for the rest; 4 as 6 without the short-K kernel; 5 this library's
+                              kernels for every product (the short-K kernel for K <= 128, the split-product kernel
+                              above), no result depending on M; 0 rocBLAS only; 1 / 2 the fp32 fused kernel for
+                              every / <= 4096-row forward layer; 3 the split-product kernel wherever K is a multiple
+                              of 32 */
   PET_OPT_ATTN_STREAM = 6, /* 0 (default): the LDS-staged kernels where they hold the shape; 1: the streaming kernels always */
   PET_OPT_BWD_KERNEL = 7,  /* 0 (default): at head_dim 32 and 64 the fp16-pair backward (every product on the 16-bit
                               matrix cores) where it fits, with PET_OPT_SPLIT 1; 1: the tile-exchange backward */

@@ -715,7 +715,7 @@ int waves_for(int S) { return (S + 15) / 16; }
 
 // Process-wide tuning options (pet_attn_set_option): each an atomic read
 // once per launch, never the environment.
-std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {4}, {0}, {0}, {0}, {1}};
+std::atomic<int> g_options[PET_OPT_COUNT] = {{0}, {1}, {0}, {0}, {0}, {6}, {0}, {0}, {0}, {1}};
 int option(int o) { return g_options[o].load(std::memory_order_relaxed); }
 bool split_enabled() { return option(PET_OPT_SPLIT) != 0; }
 

@@ -499,7 +499,7 @@ using namespace pet_model_impl;
 struct pet_model {
   pet_model_hypers h{};
   int hd = 0, cw = 0, ew = 0;  // head_dim, center / edge MLP pre-activation widths
-  int gemm_mode = 4;           // PET_OPT_MODEL_GEMM for the evaluation in progress
+  int gemm_mode = 6;           // PET_OPT_MODEL_GEMM for the evaluation in progress
   bool blocks = true;          // PET_OPT_MODEL_PAIRS for the evaluation in progress
   int tier = 1;                // the memory tier of the last evaluation: 1 never, 2 wide
   std::unordered_map<std::string, Mat> m;
@@ -554,21 +554,25 @@ bool own_gemm(const pet_model& md, int M, int K) {
 
 // out[M, N] = in W^T + beta out, W a model matrix [N, K]: rocBLAS fp32, or
 // this library's kernels where W has a copy in their form and in is 16-byte
-// aligned rows. By PET_OPT_MODEL_GEMM: 4 (the default) the split-product
-// kernel for the large products (M N K >= 2^32), rocBLAS for the rest; 5
-// every product on this library's kernels -- the short-K kernel
+// aligned rows. By PET_OPT_MODEL_GEMM: 6 (the default) the split-product
+// kernel for the large products (M N K >= 2^32), the short-K kernel
 // (pet_linear_fused_smallk: the weights exact in three fp16 parts, A's rows
-// as fp16 pairs, five part products) for K at most 128, the split-product
-// kernel above -- so that no result depends on how many rows come with it and
-// every bias and activation rides in an epilogue; 6 as 4, plus the short-K
-// kernel for the K <= 128 products with a bias or activation; 3 the
-// split-product kernel for every product; 0 rocBLAS only. Measured on MI355X
-// (energy+forces, ms): C2 2.80 / 2.07 (residual) with mode 4 (no C2 product
-// is large), 2.89 / 1.95 with mode 5, 2.585 / 1.92 with mode 6, 3.59 / 2.40
-// with mode 3; C5 171 with mode 4, 170 with mode 5. Energies from the float64
-// oracle, C2 / residual: mode 4 0.7e-7 / 4.2e-7, mode 5 1.5e-7 / 8.3e-7, mode 6
-// 3.5e-7 / 5.7e-7 (the float32 oracle 3.3e-7 / 4.2e-7), so mode 4 stays the
-// default.
+// as fp16 pairs, five part products) for the K <= 128 products with a bias or
+// activation and N >= 64, rocBLAS for the rest; 4 as 6 without the short-K
+// kernel; 5 every product on this library's kernels -- the short-K kernel for
+// K at most 128, the split-product kernel above -- so that no result depends
+// on how many rows come with it and every bias and activation rides in an
+// epilogue; 3 the split-product kernel for every product; 0 rocBLAS only.
+// Measured on MI355X (energy+forces, ms): C2 2.585 / 1.92 (residual) with
+// mode 6, 2.80 / 2.07 with mode 4 (no C2 product is large), 2.89 / 1.95 with
+// mode 5, 3.59 / 2.40 with mode 3; C5 171 with mode 4, 170 with mode 5.
+// Energies from the float64 oracle, C2 / residual: mode 6 3.0e-7 / 3.8e-7,
+// mode 4 0.7e-7 / 4.2e-7, mode 5 1.5e-7 / 8.3e-7 (the float32 oracle 3.3e-7 /
+// 4.2e-7). The narrow products (N < 64: the readout's) stay off the short-K
+// kernel: its matrix instruction truncates each product toward zero below the
+// result's last place, and with a fixed weight vector and mostly positive
+// inputs those truncations share a sign on every atom and add up over a
+// structure (C2-residual 5.7e-7 with them on it).
 // The kernel a product takes (null: rocBLAS): the copy of W it reads and
 // whether it is the short-K kernel.
 struct Sel {
@@ -577,13 +581,14 @@ struct Sel {
   explicit operator bool() const { return p != nullptr; }
 };
 // fuse: the call has a bias or an activation for the epilogue (mode 6 takes
-// the short-K kernel for those products at K <= 128, where it saves a pass).
+// the short-K kernel for those products at K <= 128 and N >= 64, where it
+// saves a pass).
 Sel split_for(const pet_model& md, const float* in, int64_t ldi, const float* W, int M, int N, int K,
               bool fuse = false) {
   const int mode = md.gemm_mode;
   const bool big = double(M) * N * K >= 4294967296.0;
   if (ldi % 4 || (reinterpret_cast<uintptr_t>(in) & 15)) return {};
-  if ((mode == 5 || (mode == 6 && fuse)) && K <= 128 && K % 32 == 0) {
+  if ((mode == 5 || (mode == 6 && fuse && N >= 64)) && K <= 128 && K % 32 == 0) {
     auto it = md.psplit.find(W);
     if (it != md.psplit.end()) return {it->second, true};
   }

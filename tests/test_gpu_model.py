@@ -27,9 +27,10 @@ error an fp32 restatement of the reference makes on the same structure where
 fp32 itself cannot meet it. On C2's water-648 the tests also assert fixed bars
 that the float32 oracle meets as well: energy 5e-7 relative, forces 5e-5
 eV/A. Measured on
-MI355X, C2 water-648: energy 0.7e-7 relative (float32 oracle 3.3e-7), forces
-2.5e-5 eV/A (float32 oracle 2.6e-5); residual family 4.2e-7 (4.2e-7) and
-1.5e-5 (1.7e-5) eV/A. Runs repeat bit for bit.
+MI355X, C2 water-648: energy 3.0e-7 relative (float32 oracle 3.3e-7), forces
+2.0e-5 eV/A (float32 oracle 2.6e-5); residual family 3.8e-7 (4.2e-7) and
+1.2e-5 (1.7e-5) eV/A; against the float32 oracle, energy 3.4e-8 and 4.1e-8
+relative. Runs repeat bit for bit.
 """
 from __future__ import annotations
 

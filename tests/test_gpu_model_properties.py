@@ -108,7 +108,8 @@ def test_batched_equals_alone_c5(device):
         print(f"    structure {k} ({b - a} atoms): energy {de:.1e} relative, per-atom {dpa:.1e}, forces {df:.1e} eV/A",
               flush=True)
         # the batch's large dense products run on the split-product kernel and
-        # a lone structure's on rocBLAS (the default model_gemm 4): the two
+        # a lone structure's on rocBLAS and the short-K kernel (the default
+        # model_gemm 6): the two
         # differ by fp32 roundings (on C2-size products a per-atom energy
         # differs from the float64 oracle by about 1e-6 of the largest;
         # measured here up to 5.3e-5 eV/A on forces). With every product on
