@@ -40,18 +40,23 @@ PEAK_PAIR_FP32 = PEAK_BF16_MFMA / 3
 # the same on the 16x16x16 fp16 instruction, which issues at half the 16x16x32
 # one's FLOP rate (measured on MI355X: 703 against 1236 TFLOP/s at best)
 PEAK_PAIR16_FP32 = PEAK_BF16_MFMA / 2 / 3
+# the short-K dense kernel: an fp32 product as five fp16 products (the
+# weights in three parts, A in two)
+PEAK_SHORTK_FP32 = PEAK_BF16_MFMA / 5
 PEAK_HBM = 8.0e12  # B/s
 
 
-def mixed_seconds(flops, split_share, pair_share=0.0, pair16_share=0.0):
+def mixed_seconds(flops, split_share, pair_share=0.0, pair16_share=0.0, shortk_share=0.0):
     """Time at the matrix-core ceilings of the instructions that run: the
     split_share of the FLOPs as split-fp32 products on the bf16 matrix cores
     (2.5 PFLOP/s / 6), the pair_share as fp16-pair products (2.5 PFLOP/s / 3),
     the pair16_share as fp16-pair products on the 16x16x16 instruction
-    (1.25 PFLOP/s / 3), the rest on the fp32 matrix cores (157.3 TFLOP/s)."""
-    rest = 1.0 - split_share - pair_share - pair16_share
+    (1.25 PFLOP/s / 3), the shortk_share as the short-K kernel's five fp16
+    products (2.5 PFLOP/s / 5), the rest on the fp32 matrix cores
+    (157.3 TFLOP/s)."""
+    rest = 1.0 - split_share - pair_share - pair16_share - shortk_share
     return flops * (rest / PEAK_FP32_MFMA + split_share / PEAK_SPLIT_FP32 + pair_share / PEAK_PAIR_FP32
-                    + pair16_share / PEAK_PAIR16_FP32)
+                    + pair16_share / PEAK_PAIR16_FP32 + shortk_share / PEAK_SHORTK_FP32)
 
 
 def split_shares(plan, slots):
@@ -235,17 +240,23 @@ def time_ef(device, reps, cpu: bool):
         fl = ef_flops(h, x.n_atoms, x.n_edges, float((cnt * cnt).sum()))
         n = max(3, reps // (5 if name != "c5" else 20))
         # contraction bound at the ceilings of the instructions that run: the
-        # large dense products as fp16 pairs or bf16 parts on the 16-bit matrix
-        # cores, the rest (small products, the attention at head_dim 64) on the
-        # fp32 ones
-        bound_ms = mixed_seconds(fl["forces"], fl["split"] / fl["forces"], fl["pair"] / fl["forces"]) * 1e3
+        # FLOPs this library's dense kernels launched in one evaluation, by
+        # instruction class (pet_gemm_flop_tally: bf16 parts, fp16 pairs, the
+        # short-K kernel's five fp16 products), the rest (rocBLAS's products,
+        # the attention) on the fp32 matrix cores
+        _lib.gemm_flop_tally(reset=True)
         o = m.compute(x, True)
+        torch.cuda.synchronize()
+        tal = _lib.gemm_flop_tally(reset=True)
+        sh = {k: tal[k] / fl["forces"] for k in ("split", "pair", "shortk")}
+        bound_ms = mixed_seconds(fl["forces"], sh["split"], sh["pair"], 0.0, sh["shortk"]) * 1e3
         e_ms = _timed(lambda: m.compute(x, False, out=o), n) / 1e3
         ef_ms = _timed(lambda: m.compute(x, True, out=o), n) / 1e3
         res[name] = dict(featurizer=h.featurizer, structures=len(sts), atoms=x.n_atoms, edges=x.n_edges,
                          d_pet=h.d_pet, heads=h.num_heads, ef_ms=ef_ms, energy_ms=e_ms, ef_tflop=fl["forces"] / 1e12,
                          ef_bound_ms=bound_ms, ef_frac_of_roofline=bound_ms / ef_ms,
-                         ef_split_share=fl["split"] / fl["forces"], ef_pair_share=fl["pair"] / fl["forces"],
+                         ef_split_share=sh["split"], ef_pair_share=sh["pair"], ef_shortk_share=sh["shortk"],
+                         ef_own_kernels_tflop=sum(tal.values()) / 1e12,
                          workspace_gb=m.workspace_bytes / 1e9, tier=m.last_tier,
                          pairs_scratch_gb=m.pairs_scratch_bytes / 1e9)
         if name == "c5":

@@ -221,6 +221,17 @@ PET_ATTN_API int pet_linear_fused_blocks(int M, int N, int K, const void* Ablock
                                          const float* cin, int64_t ldcin, float beta, float* pre, int64_t ldpre,
                                          int act, void* stream);
 
+/* FLOPs (2 M N K per product) of the dense products this library's kernels
+ * have launched in this process, by the instructions that run them:
+ * flops[0] the fp32 fused kernel (fp32 matrix cores), [1] split-fp32 as bf16
+ * parts (six bf16 products each), [2] fp16 pairs (three fp16 products), [3]
+ * the short-K kernel (five fp16 products); products on rocBLAS are not
+ * counted. reset != 0 zeroes the counts after reading them. A measurement aid
+ * with no counterpart in the reference: the bench prices an evaluation's
+ * products at the ceilings of the instructions that ran them. Counted at
+ * launch, process-wide, from every thread. */
+PET_ATTN_API int pet_gemm_flop_tally(double* flops, int reset);
+
 /* Bytes of device workspace the model holds now (its high-water mark). */
 PET_ATTN_API size_t pet_model_workspace_bytes(const pet_model* model);
 /* Bytes of the model's pairs scratch (the large products' A operands as fp16

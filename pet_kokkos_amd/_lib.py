@@ -61,6 +61,7 @@ EXPORTS = (
     "pet_linear_fused_split_blocks",
     "pet_linear_fused_blocks",
     "pet_norm_rows_pairs",
+    "pet_gemm_flop_tally",
 )
 
 OK, EINVAL, EHEADDIM, ESLOTS, EALIGN, ELAUNCH, EBLAS, EWORKSPACE, EINDEX, ESCRATCH = range(10)
@@ -243,6 +244,8 @@ def load() -> ctypes.CDLL:
                                                   _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), _P]
     lib.pet_norm_rows_pairs.restype = ctypes.c_int
     lib.pet_norm_rows_pairs.argtypes = [_I, _I, _P, _P, _I64, _P, _P, _P]
+    lib.pet_gemm_flop_tally.restype = ctypes.c_int
+    lib.pet_gemm_flop_tally.argtypes = [ctypes.POINTER(ctypes.c_double), _I]
     lib.pet_linear_fused_blocks.restype = ctypes.c_int
     lib.pet_linear_fused_blocks.argtypes = [_I, _I, _I, _P, _I, _P, _P, _I64, _P, _P, _P, _I64, _F, _P, _I64, _I, _P]
     lib.pet_model_workspace_bytes.restype = ctypes.c_size_t
@@ -297,3 +300,13 @@ def strerror(code: int) -> str:
 def check(code: int, what: str) -> None:
     if code != OK:
         raise PetAttnError(code, what)
+
+
+def gemm_flop_tally(reset: bool = False) -> dict:
+    """FLOPs (2 M N K) of the dense products this library's kernels have
+    launched in this process, by instruction class (pet_gemm_flop_tally):
+    "fp32" the fp32 fused kernel, "split" bf16 parts (six products), "pair"
+    fp16 pairs (three), "shortk" the short-K kernel (five fp16 products)."""
+    out = (ctypes.c_double * 4)()
+    check(load().pet_gemm_flop_tally(out, int(reset)), "pet_gemm_flop_tally")
+    return dict(fp32=out[0], split=out[1], pair=out[2], shortk=out[3])

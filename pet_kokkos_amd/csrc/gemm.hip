@@ -73,6 +73,16 @@ struct Epi {
   int kgo = 0;
 };
 
+// FLOPs (2 M N K) of the products this library's dense kernels have launched,
+// by the instructions that run them: 0 the fp32 fused kernel (fp32 matrix
+// cores), 1 split-fp32 as three bf16 parts (six bf16 products), 2 fp16 pairs
+// (three fp16 products), 3 the short-K kernel (five fp16 products). A
+// measurement aid, process-wide (pet_gemm_flop_tally).
+std::atomic<uint64_t> g_flops[4];
+inline void tally(int cls, int64_t M, int64_t N, int64_t K) {
+  g_flops[cls].fetch_add(uint64_t(2) * uint64_t(M) * uint64_t(N) * uint64_t(K), std::memory_order_relaxed);
+}
+
 // The epilogue of one result element v at (i, j), shared by the kernels. Every
 // lane of the wave calls it together (SwiGLU pairs neighbouring lanes):
 // (i, j) may lie outside the result, which is then left alone.
@@ -1338,6 +1348,7 @@ int pet_gemm_nt_fused(int M, int N, int K, const float* A, int64_t lda, const fl
     k32 ? go(gemm_nt_kernel<128, 64, 32>, 128, 64) : go(gemm_nt_kernel<128, 64, 16>, 128, 64);
   else
     k32 ? go(gemm_nt_kernel<64, 32, 32>, 64, 32) : go(gemm_nt_kernel<64, 32, 16>, 64, 32);
+  tally(0, M, N, K);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -1421,6 +1432,7 @@ int split_impl(int M, int N, int K, const float* A, int64_t lda, const void* Bs,
     hipLaunchKernelGGL(kern, dim3(unsigned(rb * ((nt + cpw - 1) / cpw))), dim3(threads), 0, st, M, N, K, A, lda,
                        static_cast<const u4*>(Bs), C, ldc, e, static_cast<const float*>(nullptr), int64_t(0),
                        int(cpw));
+    tally(pair ? 2 : 1, M, N, K);
   };
   // measured on MI355X: 128 x 128 tiles of 8 waves where there are many
   // (131072 x 1536 x 512: 1200-1213 us against 1394-1418 for 128 x 64 and
@@ -1501,6 +1513,7 @@ int pet_gemm_nt_split_f32b(int M, int N, int K, const float* A, int64_t lda, con
     const int64_t tiles = int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     hipLaunchKernelGGL(kern, dim3(unsigned(tiles)), dim3(threads), 0, st, M, N, K, A, lda, nullptr, C, ldc, e, B,
                        ldb, 1);
+    tally(1, M, N, K);
   };
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 63) / 64);
   if (N >= 128 && t128 >= 2048)
@@ -1643,6 +1656,7 @@ int pet_gemm_nt_pp(int M, int N, int K, const void* Ap, const void* Bs, float* C
   constexpr int wr = 8;
   hipLaunchKernelGGL(k.kern, dim3(unsigned(tiles)), dim3(k.threads), k.lds(), st, M, N, K,
                      static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e, wr);
+  tally(2, M, N, K);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -1727,6 +1741,7 @@ int pet_gemm_nt_pp_blocks(int M, int N, int K, const void* Ap, int kb, const voi
   const size_t lds = k.lds() + size_t(K / kb) * k.bm * 4;
   hipLaunchKernelGGL(pp_blocks_kernel(sh, kb / 32), dim3(unsigned(tiles)), dim3(k.threads), lds, st, M, N, K,
                      static_cast<const u4*>(Ap), static_cast<const u4*>(Bs), C, ldc, e, 8);
+  tally(2, M, N, K);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -1783,6 +1798,7 @@ int pet_gemm_nt_sk(int M, int N, int K, const float* A, int64_t lda, const void*
   }
 #undef PET_SKT_GO
 #undef PET_SKT_LAUNCH
+  tally(3, M, N, K);
   return hipGetLastError() == hipSuccess ? PET_ATTN_OK : PET_ATTN_ELAUNCH;
 }
 
@@ -1850,4 +1866,12 @@ extern "C" int pet_linear_fused_pairs(int M, int N, int K, const void* Apairs, c
   e.row_scale = row_scale, e.bias = bias, e.cin = cin, e.ldcin = ldcin, e.beta = beta, e.pre = pre, e.ldpre = ldpre;
   e.act = act;
   return pet_gemm_nt_pp(M, N, K, Apairs, Wsplit, C, ldc, e, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pet_gemm_flop_tally(double* flops, int reset) {
+  if (!flops) return PET_ATTN_EINVAL;
+  for (int c = 0; c < 4; ++c)
+    flops[c] = double(reset ? g_flops[c].exchange(0, std::memory_order_relaxed)
+                            : g_flops[c].load(std::memory_order_relaxed));
+  return PET_ATTN_OK;
 }

@@ -569,3 +569,21 @@ def test_norm_pair_rows_same_bits(K, device):
         got = L.norm_pair_rows(X, w, bias)
         used = M * K * 2 + 2 * M
         assert torch.equal(ref.data[:used], got.data[:used]), bias is None
+
+
+def test_flop_tally(device):
+    """pet_gemm_flop_tally: each launch adds 2 M N K to its instruction class
+    (the short-K kernel's, the fp32 fused kernel's), and reset zeroes them."""
+    _lib.gemm_flop_tally(reset=True)
+    M, N, K = 1000, 96, 64
+    g = torch.Generator(device=device).manual_seed(70)
+    A = torch.randn(M, K, device=device, generator=g)
+    W = torch.randn(N, K, device=device, generator=g)
+    C = torch.empty(M, N, device=device)
+    linear_fused(A, W, C, split="smallk")
+    linear_fused(A, W, C, split=False)
+    torch.cuda.synchronize()
+    t = _lib.gemm_flop_tally(reset=True)
+    assert t["shortk"] == 2.0 * M * N * K and t["fp32"] == 2.0 * M * N * K
+    assert t["split"] == 0.0 and t["pair"] == 0.0
+    assert all(v == 0.0 for v in _lib.gemm_flop_tally().values())
