@@ -32,12 +32,14 @@
 // norms).
 // The scales are undone in fp32 where the results are stored.
 //
-// LDS (R = 16 NW rows): Q^T, dO^T, K^T as hi and lo planes [32 dims][R + 8
-// halves] (token-contiguous: the a operand of dK, dV and dQ as 8-byte reads of
-// four consecutive tokens; Q's and dO's rows for S and dP through the
-// transposing read), the per-query (max, 2^15 / sum, scaled dO.O), and two
-// buffers of one dS tile a wave (hi and lo, [16 keys][16 queries + 4 pad]).
-// 47.7 KB at 5 waves: three workgroups a CU.
+// LDS (R = 16 NW rows): Q, dO, K as hi and lo planes, at head_dim 32
+// token-major [R tokens][32 dims + 8 halves] (a lane's 8 dims one 16-byte
+// store; Q's and dO's rows for S and dP read straight, the a operand of dK, dV
+// and dQ -- a dim's four consecutive tokens -- through the transposing read),
+// at 64 dim-major [64 dims][R + 4 halves] (the other way round; two workgroups
+// a CU); the per-query (max, 2^15 / sum, scaled dO.O), and two buffers of one
+// dS tile a wave (hi and lo, [16 keys][16 queries + 4 pad]). 51.1 KB at 5
+// waves and head_dim 32: three workgroups a CU.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -73,11 +75,15 @@ constexpr int kPairMaxWaves = 8;  // 128 slots; beyond, the tile-exchange kernel
 struct PairLds {
   static constexpr int TP = 20;  // halves a dS tile row (16 queries, 4 of pad)
   static constexpr int TS = 16 * TP;  // halves a tile part
-  int R, PT;                     // rows; plane pitch in halves (a 4-half pad at head_dim 64: two workgroups a CU)
+  // The planes: at head_dim 32 token-major (a token's dims a row, rows of
+  // HD + 8 halves: a lane's 8 dims one 16-byte store, and the 16 rows a
+  // 16-byte read meets on distinct banks), at 64 dim-major (a dim's tokens a
+  // row, 16 NW + 4 halves: two workgroups a CU)
+  int R, PT;  // rows; plane pitch in halves
   size_t pl, st, red, tb, bytes;
   __host__ __device__ constexpr PairLds(int HD, int NW)
-      : R(16 * NW), PT(16 * NW + (HD <= 32 ? 8 : 4)), pl(0),
-        st(pl + size_t(6) * HD * PT * 2),  // 6 planes: Q^T, dO^T, K^T, each hi then lo
+      : R(16 * NW), PT(HD <= 32 ? HD + 8 : 16 * NW + 4), pl(0),
+        st(pl + size_t(6) * (HD <= 32 ? 16 * NW : HD) * PT * 2),  // 6 planes: Q, dO, K, each hi then lo
         red(st + size_t(3) * R * 4),            // 8 words a wave: its maxima
         tb(red + size_t(8) * NW * 4), bytes(tb + size_t(2) * NW * 2 * TS * 2) {}
 };
@@ -274,7 +280,8 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
   constexpr PairLds L(HD, NW);
   constexpr int PT = L.PT, TP = PairLds::TP, TS = PairLds::TS;
   _Float16* planes = reinterpret_cast<_Float16*>(lds + L.pl);
-  constexpr int PS = HD * PT;  // halves a plane part
+  constexpr bool TOK = HD <= 32;            // token-major planes (above)
+  constexpr int PS = (TOK ? L.R : HD) * PT;  // halves a plane part
   _Float16* QTh = planes;
   _Float16* GTh = planes + 2 * PS;
   _Float16* KTh = planes + 4 * PS;
@@ -354,15 +361,23 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
       }
     if (active) {
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
+      for (int kc = 0; kc < KC; ++kc) {
+        if constexpr (TOK) {  // the lane's 8 dims of each plane, one 16-byte store
+          const int o = i * PT + 32 * kc + 8 * g;
+          *reinterpret_cast<u4*>(QTh + o) = qs[kc][0], *reinterpret_cast<u4*>(QTh + PS + o) = qs[kc][1];
+          *reinterpret_cast<u4*>(GTh + o) = gs[kc][0], *reinterpret_cast<u4*>(GTh + PS + o) = gs[kc][1];
+          *reinterpret_cast<u4*>(KTh + o) = kb[kc][0], *reinterpret_cast<u4*>(KTh + PS + o) = kb[kc][1];
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int o = (32 * kc + 8 * g + e) * PT + i;
-          auto half = [&](unsigned x) { return __builtin_bit_cast(pet_split::h2v, x)[e & 1]; };
-          QTh[o] = half(qs[kc][0][e >> 1]), QTh[PS + o] = half(qs[kc][1][e >> 1]);
-          GTh[o] = half(gs[kc][0][e >> 1]), GTh[PS + o] = half(gs[kc][1][e >> 1]);
-          KTh[o] = half(kb[kc][0][e >> 1]), KTh[PS + o] = half(kb[kc][1][e >> 1]);
+          for (int e = 0; e < 8; ++e) {
+            const int o = (32 * kc + 8 * g + e) * PT + i;
+            auto half = [&](unsigned x) { return __builtin_bit_cast(pet_split::h2v, x)[e & 1]; };
+            QTh[o] = half(qs[kc][0][e >> 1]), QTh[PS + o] = half(qs[kc][1][e >> 1]);
+            GTh[o] = half(gs[kc][0][e >> 1]), GTh[PS + o] = half(gs[kc][1][e >> 1]);
+            KTh[o] = half(kb[kc][0][e >> 1]), KTh[PS + o] = half(kb[kc][1][e >> 1]);
+          }
         }
+      }
     }
     if (active) {
       if (g == 0) {
@@ -392,13 +407,19 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       u4 qa[2], ga[2];
+      if constexpr (TOK) {  // query 16I + c's row: its dims 32kc + 8g .. + 7 read straight
+        const int o = (16 * I + c) * PT + 32 * kc + 8 * g;
+        qa[0] = *reinterpret_cast<const u4*>(QTh + o), qa[1] = *reinterpret_cast<const u4*>(QTh + PS + o);
+        ga[0] = *reinterpret_cast<const u4*>(GTh + o), ga[1] = *reinterpret_cast<const u4*>(GTh + PS + o);
+      } else {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int o = (32 * kc + 8 * g + 4 * u + (c >> 2)) * PT + 16 * I + 4 * (c & 3);
-        const u2 x0 = lds_tr16(QTh + o), x1 = lds_tr16(QTh + PS + o);
-        const u2 y0 = lds_tr16(GTh + o), y1 = lds_tr16(GTh + PS + o);
-        qa[0][2 * u] = x0[0], qa[0][2 * u + 1] = x0[1], qa[1][2 * u] = x1[0], qa[1][2 * u + 1] = x1[1];
-        ga[0][2 * u] = y0[0], ga[0][2 * u + 1] = y0[1], ga[1][2 * u] = y1[0], ga[1][2 * u + 1] = y1[1];
+        for (int u = 0; u < 2; ++u) {
+          const int o = (32 * kc + 8 * g + 4 * u + (c >> 2)) * PT + 16 * I + 4 * (c & 3);
+          const u2 x0 = lds_tr16(QTh + o), x1 = lds_tr16(QTh + PS + o);
+          const u2 y0 = lds_tr16(GTh + o), y1 = lds_tr16(GTh + PS + o);
+          qa[0][2 * u] = x0[0], qa[0][2 * u + 1] = x0[1], qa[1][2 * u] = x1[0], qa[1][2 * u + 1] = x1[1];
+          ga[0][2 * u] = y0[0], ga[0][2 * u + 1] = y0[1], ga[1][2 * u] = y1[0], ga[1][2 * u + 1] = y1[1];
+        }
       }
       st = mfma3(qa, kb[kc], st);
       dp = mfma3(ga, vb[kc], dp);
@@ -424,9 +445,15 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
     // planes, the block's queries 16I + 4g .. + 3
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      const int o = (16 * t + c) * PT + 16 * I + 4 * g;
-      const u2 gth = *reinterpret_cast<const u2*>(GTh + o), gtl = *reinterpret_cast<const u2*>(GTh + PS + o);
-      const u2 qth = *reinterpret_cast<const u2*>(QTh + o), qtl = *reinterpret_cast<const u2*>(QTh + PS + o);
+      u2 gth, gtl, qth, qtl;
+      if constexpr (TOK) {  // dim 16t + c of queries 16I + 4g .. + 3, read transposed (lane 4m + q: query 16I + 4g + m, dims 16t + 4q .. + 3)
+        const int o = (16 * I + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+        gth = lds_tr16(GTh + o), gtl = lds_tr16(GTh + PS + o), qth = lds_tr16(QTh + o), qtl = lds_tr16(QTh + PS + o);
+      } else {
+        const int o = (16 * t + c) * PT + 16 * I + 4 * g;
+        gth = *reinterpret_cast<const u2*>(GTh + o), gtl = *reinterpret_cast<const u2*>(GTh + PS + o);
+        qth = *reinterpret_cast<const u2*>(QTh + o), qtl = *reinterpret_cast<const u2*>(QTh + PS + o);
+      }
       dv[t] = mfma3_16(gth, gtl, ph, pl, dv[t]);
       dk[t] = mfma3_16(qth, qtl, sh, sl, dk[t]);
     }
@@ -447,8 +474,14 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
     const u2 bh = lds_tr16(tb), bl = lds_tr16(tb + TS);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      const int o = (16 * t + c) * PT + 16 * J + 4 * g;
-      const u2 kth = *reinterpret_cast<const u2*>(KTh + o), ktl = *reinterpret_cast<const u2*>(KTh + PS + o);
+      u2 kth, ktl;
+      if constexpr (TOK) {  // dim 16t + c of keys 16J + 4g .. + 3, read transposed
+        const int o = (16 * J + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+        kth = lds_tr16(KTh + o), ktl = lds_tr16(KTh + PS + o);
+      } else {
+        const int o = (16 * t + c) * PT + 16 * J + 4 * g;
+        kth = *reinterpret_cast<const u2*>(KTh + o), ktl = *reinterpret_cast<const u2*>(KTh + PS + o);
+      }
       dq[t] = mfma3_16(kth, ktl, bh, bl, dq[t]);
     }
   };
@@ -541,22 +574,24 @@ attn_bwd_pair_kernel(PairBwdArgs a) {
 // ---- forward ---------------------------------------------------------------
 // The forward at head_dim 32 from the same pairs: a workgroup per (atom,
 // head), wave w owning query block w. Per key block J:
-//   S^T = K_J Q_w^T on the 16x16x32 instruction (K's rows read transposed from
-//   the K^T plane, Q_w split once in registers), a lane holding query 16w + c
+//   S^T = K_J Q_w^T on the 16x16x32 instruction (K's rows read straight from
+//   the K plane, Q_w split once in registers), a lane holding query 16w + c
 //   against keys 16J + 4g + r, so the online softmax reduces across the four
 //   g lanes only;
 //   O^T += V_J^T P^T on the 16x16x16 instruction, P (scaled by 2^15, split in
-//   registers) already its b operand, V^T's a operand 8-byte reads of the V^T
-//   plane.
+//   registers) already its b operand, V^T's a operand transposing reads of the
+//   V plane.
 // The reference's forward (src/attention.cpp:205-266, :375-449): O_i =
 // sum_j softmax_j(sc q_i.k_j + log cf_j) v_j, (max, 1/sum) saved per query.
-// LDS: K^T and V^T as hi and lo planes [32 dims][R + 8 halves], log cf of
-// the R slots, each key block's two scale exponents: 23.0 KB at five waves.
+// LDS: K and V as hi and lo planes, token-major [R slots][HD + 8 halves] (a
+// lane's 8 dims one 16-byte store; a key's dims read straight, a dim's four
+// keys by the transposing read), log cf of the R slots, each key block's two
+// scale exponents: 26.4 KB at five waves and head_dim 32.
 struct PairFwdLds {
   int R, PT;
   size_t pl, lc, red, bytes;
   __host__ __device__ constexpr PairFwdLds(int HD, int NW)
-      : R(16 * NW), PT(16 * NW + 8), pl(0), lc(size_t(4) * HD * PT * 2), red(lc + size_t(R) * 4),
+      : R(16 * NW), PT(HD + 8), pl(0), lc(size_t(4) * R * PT * 2), red(lc + size_t(R) * 4),
         bytes(red + size_t(8) * NW * 4) {}
 };
 
@@ -577,7 +612,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   unsigned char* lds = reinterpret_cast<unsigned char*>(lds_f);
   const int D = H * HD;
   constexpr PairFwdLds L(HD, NW);
-  constexpr int PT = L.PT, PS = HD * PT;
+  constexpr int PT = L.PT, PS = L.R * PT;  // halves a plane part
   _Float16* KTh = reinterpret_cast<_Float16*>(lds + L.pl);
   _Float16* VTh = KTh + 2 * PS;
   float* lcf = reinterpret_cast<float*>(lds + L.lc);
@@ -635,6 +670,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
   u4 qb[KC][2];
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
+    u4 kp[2], vp[2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int x = 8 * kc + 2 * j;
@@ -643,14 +679,12 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
       pair2s(k[x], k[x + 1], sK, h[1], lo[1]);
       pair2s(v[x], v[x + 1], sV, h[2], lo[2]);
       qb[kc][0][j] = h[0], qb[kc][1][j] = lo[0];
-      if (active) {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int o = (32 * kc + 8 * g + 2 * j + e) * PT + i;
-          KTh[o] = __builtin_bit_cast(pet_split::h2v, h[1])[e], KTh[PS + o] = __builtin_bit_cast(pet_split::h2v, lo[1])[e];
-          VTh[o] = __builtin_bit_cast(pet_split::h2v, h[2])[e], VTh[PS + o] = __builtin_bit_cast(pet_split::h2v, lo[2])[e];
-        }
-      }
+      kp[0][j] = h[1], kp[1][j] = lo[1], vp[0][j] = h[2], vp[1][j] = lo[2];
+    }
+    if (active) {  // the lane's 8 dims of each plane, one 16-byte store
+      const int o = i * PT + 32 * kc + 8 * g;
+      *reinterpret_cast<u4*>(KTh + o) = kp[0], *reinterpret_cast<u4*>(KTh + PS + o) = kp[1];
+      *reinterpret_cast<u4*>(VTh + o) = vp[0], *reinterpret_cast<u4*>(VTh + PS + o) = vp[1];
     }
   }
   if (!active) {  // slots past the atom's tokens: their sentinel statistics, and the workgroup barrier
@@ -675,13 +709,9 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     f4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      u4 a[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int o = (32 * kc + 8 * g + 4 * u + (c >> 2)) * PT + 16 * J + 4 * (c & 3);
-        const u2 x0 = lds_tr16(KTh + o), x1 = lds_tr16(KTh + PS + o);
-        a[0][2 * u] = x0[0], a[0][2 * u + 1] = x0[1], a[1][2 * u] = x1[0], a[1][2 * u + 1] = x1[1];
-      }
+      // key 16J + c's dims 32kc + 8g .. + 7, read straight
+      const int o = (16 * J + c) * PT + 32 * kc + 8 * g;
+      const u4 a[2] = {*reinterpret_cast<const u4*>(KTh + o), *reinterpret_cast<const u4*>(KTh + PS + o)};
       st = mfma3(a, qb[kc], st);
     }
     return st;
@@ -694,9 +724,10 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     const u2 ph = {h[0], h[1]}, pl = {lo[0], lo[1]};
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      const int o = (16 * t + c) * PT + 16 * J + 4 * g;
-      acc[t] = mfma3_16(*reinterpret_cast<const u2*>(VTh + o), *reinterpret_cast<const u2*>(VTh + PS + o), ph, pl,
-                        acc[t]);
+      // dim 16t + c of keys 16J + 4g .. + 3, read transposed (lane 4m + q: key
+      // 16J + 4g + m, dims 16t + 4q .. + 3)
+      const int o = (16 * J + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+      acc[t] = mfma3_16(lds_tr16(VTh + o), lds_tr16(VTh + PS + o), ph, pl, acc[t]);
     }
   };
   // the same for two key blocks at once, on the 16x16x32 instruction: k-slots
@@ -712,9 +743,10 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     const u4 ph = {h[0], h[1], h[2], h[3]}, pl = {lo[0], lo[1], lo[2], lo[3]};
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      const int o0 = (16 * t + c) * PT + 16 * J0 + 4 * g, o1 = (16 * t + c) * PT + 16 * J1 + 4 * g;
-      const u2 h0 = *reinterpret_cast<const u2*>(VTh + o0), h1 = *reinterpret_cast<const u2*>(VTh + o1);
-      const u2 l0 = *reinterpret_cast<const u2*>(VTh + PS + o0), l1 = *reinterpret_cast<const u2*>(VTh + PS + o1);
+      const int o0 = (16 * J0 + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+      const int o1 = (16 * J1 + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+      const u2 h0 = lds_tr16(VTh + o0), h1 = lds_tr16(VTh + o1);
+      const u2 l0 = lds_tr16(VTh + PS + o0), l1 = lds_tr16(VTh + PS + o1);
       const u4 vh = {h0[0], h0[1], h1[0], h1[1]}, vl = {l0[0], l0[1], l1[0], l1[1]};
       acc[t] = pet_split::mfma_h(vl, ph, acc[t]);
       acc[t] = pet_split::mfma_h(vh, pl, acc[t]);
