@@ -121,10 +121,12 @@ __device__ __forceinline__ void pair2x(float x, float y, float one, unsigned& hi
   hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
 }
-// pair2x of x s and y s for a power of two s (exact products): the remainder
-// x s - hi is formed from x and s by the fma_mix itself.
+// pair2x of x s and y s for a power of two s (exact products): hi and the
+// remainder x s - hi are each one fma_mix from x and s (hi's an fma with 0,
+// which the compiler cannot turn back into a multiply: it differs from x s
+// only in the sign of a zero), four instructions for the two values.
 __device__ __forceinline__ void pair2s(float x, float y, float s, unsigned& hi, unsigned& lo) {
-  const pet_split::h2v h = {(_Float16)(x * s), (_Float16)(y * s)};
+  const pet_split::h2v h = {(_Float16)fmaf(x, s, 0.f), (_Float16)fmaf(y, s, 0.f)};
   const pet_split::h2v l = {(_Float16)fmaf(x, s, -float(h[0])), (_Float16)fmaf(y, s, -float(h[1]))};
   hi = __builtin_bit_cast(unsigned, h);
   lo = __builtin_bit_cast(unsigned, l);
