@@ -32,14 +32,14 @@
 // norms).
 // The scales are undone in fp32 where the results are stored.
 //
-// LDS (R = 16 NW rows): Q, dO, K as hi and lo planes, at head_dim 32
-// token-major [R tokens][32 dims + 8 halves] (a lane's 8 dims one 16-byte
-// store; Q's and dO's rows for S and dP read straight, the a operand of dK, dV
-// and dQ -- a dim's four consecutive tokens -- through the transposing read),
-// at 64 dim-major [64 dims][R + 4 halves] (the other way round; two workgroups
-// a CU); the per-query (max, 2^15 / sum, scaled dO.O), and two buffers of one
-// dS tile a wave (hi and lo, [16 keys][16 queries + 4 pad]). 51.1 KB at 5
-// waves and head_dim 32: three workgroups a CU.
+// LDS (R = 16 NW rows): Q, dO, K as hi and lo planes, token-major (a lane's
+// 8 dims one 16-byte store; Q's and dO's rows for S and dP read straight, the
+// a operand of dK, dV and dQ -- a dim's four consecutive tokens -- through the
+// transposing read; rows padded at head_dim 32, unpadded with permuted chunks
+// at 64: tok_off), the per-query (max, 2^15 / sum, scaled dO.O), and two
+// buffers of one dS tile a wave (hi and lo, [16 keys][16 queries + 4 pad]).
+// 51.1 KB at 5 waves and head_dim 32 (three workgroups a CU), 75.4 KB at 64
+// (two).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -75,15 +75,14 @@ constexpr int kPairMaxWaves = 8;  // 128 slots; beyond, the tile-exchange kernel
 struct PairLds {
   static constexpr int TP = 20;  // halves a dS tile row (16 queries, 4 of pad)
   static constexpr int TS = 16 * TP;  // halves a tile part
-  // The planes: at head_dim 32 token-major (a token's dims a row, rows of
-  // HD + 8 halves: a lane's 8 dims one 16-byte store, and the 16 rows a
-  // 16-byte read meets on distinct banks), at 64 dim-major (a dim's tokens a
-  // row, 16 NW + 4 halves: two workgroups a CU)
+  // The planes token-major (a token's dims a row, tok_off: a lane's 8 dims
+  // one 16-byte store), rows padded at head_dim 32
+  static constexpr bool pad(int HD) { return HD <= 32; }
   int R, PT;  // rows; plane pitch in halves
   size_t pl, st, red, tb, bytes;
   __host__ __device__ constexpr PairLds(int HD, int NW)
-      : R(16 * NW), PT(HD <= 32 ? HD + 8 : 16 * NW + 4), pl(0),
-        st(pl + size_t(6) * (HD <= 32 ? 16 * NW : HD) * PT * 2),  // 6 planes: Q, dO, K, each hi then lo
+      : R(16 * NW), PT(pad(HD) ? HD + 8 : HD), pl(0),
+        st(pl + size_t(6) * 16 * NW * PT * 2),  // 6 planes: Q, dO, K, each hi then lo
         red(st + size_t(3) * R * 4),            // 8 words a wave: its maxima
         tb(red + size_t(8) * NW * 4), bytes(tb + size_t(2) * NW * 2 * TS * 2) {}
 };
@@ -96,6 +95,28 @@ typedef short s4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u2 lds_tr16(const _Float16* p) {
   typedef __attribute__((address_space(3))) s4 lds_s4;
   return __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
+}
+
+// Token-major planes of HD dims: the offset in halves of row r's 16-byte
+// chunk ch (8 dims). Padded (PAD): rows of HD + 8 halves, the 16 rows a
+// 16-byte read meets on distinct banks. Unpadded, where LDS allows no pad (the
+// backward at head_dim 64, two workgroups a CU): rows of HD halves with each
+// row's chunks permuted by an XOR of bits of the row, found by a search for
+// conflict-free 16-byte and transposing reads. Measured on MI355X: the padded
+// rows faster at head_dim 32 (C3 backward 242 against 251 us with the
+// permutation) and in the forward at 64 (C5 840 against 850 us); the
+// unpadded rows take the head_dim-64 backward from dim-major planes 2470 to
+// 2227 us (C5).
+template <int HD, bool PAD>
+__device__ __forceinline__ int tok_off(int r, int ch) {
+  static_assert(HD == 32 || HD == 64, "head_dim 32 or 64");
+  if constexpr (PAD) {
+    return r * (HD + 8) + 8 * ch;
+  } else {
+    const int b1 = (r >> 1) & 1, b2 = (r >> 2) & 1, b3 = (r >> 3) & 1;
+    const int h = HD == 32 ? (b2 << 1) ^ b3 : (b1 << 1) ^ (b2 << 2) ^ b3;
+    return r * HD + 8 * (ch ^ h);
+  }
 }
 
 // An opaque 1.0 in a register (an empty asm, no instruction): fmaf(x, one, -h)
@@ -282,8 +303,8 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
   constexpr PairLds L(HD, NW);
   constexpr int PT = L.PT, TP = PairLds::TP, TS = PairLds::TS;
   _Float16* planes = reinterpret_cast<_Float16*>(lds + L.pl);
-  constexpr bool TOK = HD <= 32;            // token-major planes (above)
-  constexpr int PS = (TOK ? L.R : HD) * PT;  // halves a plane part
+  constexpr int PS = L.R * PT;  // halves a plane part
+  constexpr bool PAD = PairLds::pad(HD);
   _Float16* QTh = planes;
   _Float16* GTh = planes + 2 * PS;
   _Float16* KTh = planes + 4 * PS;
@@ -363,22 +384,11 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
       }
     if (active) {
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        if constexpr (TOK) {  // the lane's 8 dims of each plane, one 16-byte store
-          const int o = i * PT + 32 * kc + 8 * g;
-          *reinterpret_cast<u4*>(QTh + o) = qs[kc][0], *reinterpret_cast<u4*>(QTh + PS + o) = qs[kc][1];
-          *reinterpret_cast<u4*>(GTh + o) = gs[kc][0], *reinterpret_cast<u4*>(GTh + PS + o) = gs[kc][1];
-          *reinterpret_cast<u4*>(KTh + o) = kb[kc][0], *reinterpret_cast<u4*>(KTh + PS + o) = kb[kc][1];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int o = (32 * kc + 8 * g + e) * PT + i;
-            auto half = [&](unsigned x) { return __builtin_bit_cast(pet_split::h2v, x)[e & 1]; };
-            QTh[o] = half(qs[kc][0][e >> 1]), QTh[PS + o] = half(qs[kc][1][e >> 1]);
-            GTh[o] = half(gs[kc][0][e >> 1]), GTh[PS + o] = half(gs[kc][1][e >> 1]);
-            KTh[o] = half(kb[kc][0][e >> 1]), KTh[PS + o] = half(kb[kc][1][e >> 1]);
-          }
-        }
+      for (int kc = 0; kc < KC; ++kc) {  // the lane's 8 dims of each plane, one 16-byte store
+        const int o = tok_off<HD, PAD>(i, 4 * kc + g);
+        *reinterpret_cast<u4*>(QTh + o) = qs[kc][0], *reinterpret_cast<u4*>(QTh + PS + o) = qs[kc][1];
+        *reinterpret_cast<u4*>(GTh + o) = gs[kc][0], *reinterpret_cast<u4*>(GTh + PS + o) = gs[kc][1];
+        *reinterpret_cast<u4*>(KTh + o) = kb[kc][0], *reinterpret_cast<u4*>(KTh + PS + o) = kb[kc][1];
       }
     }
     if (active) {
@@ -408,21 +418,10 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
     f4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};  // S: key 16w + c (column), queries 16I + 4g + r
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      u4 qa[2], ga[2];
-      if constexpr (TOK) {  // query 16I + c's row: its dims 32kc + 8g .. + 7 read straight
-        const int o = (16 * I + c) * PT + 32 * kc + 8 * g;
-        qa[0] = *reinterpret_cast<const u4*>(QTh + o), qa[1] = *reinterpret_cast<const u4*>(QTh + PS + o);
-        ga[0] = *reinterpret_cast<const u4*>(GTh + o), ga[1] = *reinterpret_cast<const u4*>(GTh + PS + o);
-      } else {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int o = (32 * kc + 8 * g + 4 * u + (c >> 2)) * PT + 16 * I + 4 * (c & 3);
-          const u2 x0 = lds_tr16(QTh + o), x1 = lds_tr16(QTh + PS + o);
-          const u2 y0 = lds_tr16(GTh + o), y1 = lds_tr16(GTh + PS + o);
-          qa[0][2 * u] = x0[0], qa[0][2 * u + 1] = x0[1], qa[1][2 * u] = x1[0], qa[1][2 * u + 1] = x1[1];
-          ga[0][2 * u] = y0[0], ga[0][2 * u + 1] = y0[1], ga[1][2 * u] = y1[0], ga[1][2 * u + 1] = y1[1];
-        }
-      }
+      // query 16I + c's row: its dims 32kc + 8g .. + 7 read straight
+      const int o = tok_off<HD, PAD>(16 * I + c, 4 * kc + g);
+      const u4 qa[2] = {*reinterpret_cast<const u4*>(QTh + o), *reinterpret_cast<const u4*>(QTh + PS + o)};
+      const u4 ga[2] = {*reinterpret_cast<const u4*>(GTh + o), *reinterpret_cast<const u4*>(GTh + PS + o)};
       st = mfma3(qa, kb[kc], st);
       dp = mfma3(ga, vb[kc], dp);
     }
@@ -447,15 +446,11 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
     // planes, the block's queries 16I + 4g .. + 3
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      u2 gth, gtl, qth, qtl;
-      if constexpr (TOK) {  // dim 16t + c of queries 16I + 4g .. + 3, read transposed (lane 4m + q: query 16I + 4g + m, dims 16t + 4q .. + 3)
-        const int o = (16 * I + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
-        gth = lds_tr16(GTh + o), gtl = lds_tr16(GTh + PS + o), qth = lds_tr16(QTh + o), qtl = lds_tr16(QTh + PS + o);
-      } else {
-        const int o = (16 * t + c) * PT + 16 * I + 4 * g;
-        gth = *reinterpret_cast<const u2*>(GTh + o), gtl = *reinterpret_cast<const u2*>(GTh + PS + o);
-        qth = *reinterpret_cast<const u2*>(QTh + o), qtl = *reinterpret_cast<const u2*>(QTh + PS + o);
-      }
+      // dim 16t + c of queries 16I + 4g .. + 3, read transposed (lane 4m + q:
+      // query 16I + 4g + m, dims 16t + 4q .. + 3)
+      const int o = tok_off<HD, PAD>(16 * I + 4 * g + (c >> 2), 2 * t + ((c & 3) >> 1)) + 4 * (c & 1);
+      const u2 gth = lds_tr16(GTh + o), gtl = lds_tr16(GTh + PS + o), qth = lds_tr16(QTh + o),
+               qtl = lds_tr16(QTh + PS + o);
       dv[t] = mfma3_16(gth, gtl, ph, pl, dv[t]);
       dk[t] = mfma3_16(qth, qtl, sh, sl, dk[t]);
     }
@@ -476,14 +471,9 @@ __device__ __forceinline__ void pair_bwd_item(const PairBwdArgs& a, const Atom& 
     const u2 bh = lds_tr16(tb), bl = lds_tr16(tb + TS);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      u2 kth, ktl;
-      if constexpr (TOK) {  // dim 16t + c of keys 16J + 4g .. + 3, read transposed
-        const int o = (16 * J + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
-        kth = lds_tr16(KTh + o), ktl = lds_tr16(KTh + PS + o);
-      } else {
-        const int o = (16 * t + c) * PT + 16 * J + 4 * g;
-        kth = *reinterpret_cast<const u2*>(KTh + o), ktl = *reinterpret_cast<const u2*>(KTh + PS + o);
-      }
+      // dim 16t + c of keys 16J + 4g .. + 3, read transposed
+      const int o = tok_off<HD, PAD>(16 * J + 4 * g + (c >> 2), 2 * t + ((c & 3) >> 1)) + 4 * (c & 1);
+      const u2 kth = lds_tr16(KTh + o), ktl = lds_tr16(KTh + PS + o);
       dq[t] = mfma3_16(kth, ktl, bh, bl, dq[t]);
     }
   };
@@ -684,7 +674,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
       kp[0][j] = h[1], kp[1][j] = lo[1], vp[0][j] = h[2], vp[1][j] = lo[2];
     }
     if (active) {  // the lane's 8 dims of each plane, one 16-byte store
-      const int o = i * PT + 32 * kc + 8 * g;
+      const int o = tok_off<HD, true>(i, 4 * kc + g);
       *reinterpret_cast<u4*>(KTh + o) = kp[0], *reinterpret_cast<u4*>(KTh + PS + o) = kp[1];
       *reinterpret_cast<u4*>(VTh + o) = vp[0], *reinterpret_cast<u4*>(VTh + PS + o) = vp[1];
     }
@@ -712,7 +702,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       // key 16J + c's dims 32kc + 8g .. + 7, read straight
-      const int o = (16 * J + c) * PT + 32 * kc + 8 * g;
+      const int o = tok_off<HD, true>(16 * J + c, 4 * kc + g);
       const u4 a[2] = {*reinterpret_cast<const u4*>(KTh + o), *reinterpret_cast<const u4*>(KTh + PS + o)};
       st = mfma3(a, qb[kc], st);
     }
@@ -728,7 +718,7 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     for (int t = 0; t < DT; ++t) {
       // dim 16t + c of keys 16J + 4g .. + 3, read transposed (lane 4m + q: key
       // 16J + 4g + m, dims 16t + 4q .. + 3)
-      const int o = (16 * J + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+      const int o = tok_off<HD, true>(16 * J + 4 * g + (c >> 2), 2 * t + ((c & 3) >> 1)) + 4 * (c & 1);
       acc[t] = mfma3_16(lds_tr16(VTh + o), lds_tr16(VTh + PS + o), ph, pl, acc[t]);
     }
   };
@@ -745,8 +735,8 @@ attn_fwd_pair_kernel(const float* __restrict__ qkv, int64_t ldq, const int* __re
     const u4 ph = {h[0], h[1], h[2], h[3]}, pl = {lo[0], lo[1], lo[2], lo[3]};
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      const int o0 = (16 * J0 + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
-      const int o1 = (16 * J1 + 4 * g + (c >> 2)) * PT + 16 * t + 4 * (c & 3);
+      const int o0 = tok_off<HD, true>(16 * J0 + 4 * g + (c >> 2), 2 * t + ((c & 3) >> 1)) + 4 * (c & 1);
+      const int o1 = tok_off<HD, true>(16 * J1 + 4 * g + (c >> 2), 2 * t + ((c & 3) >> 1)) + 4 * (c & 1);
       const u2 h0 = lds_tr16(VTh + o0), h1 = lds_tr16(VTh + o1);
       const u2 l0 = lds_tr16(VTh + PS + o0), l1 = lds_tr16(VTh + PS + o1);
       const u4 vh = {h0[0], h0[1], h1[0], h1[1]}, vl = {l0[0], l0[1], l1[0], l1[1]};
