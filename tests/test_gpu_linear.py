@@ -30,9 +30,10 @@ def linear_fused(A, W, C, row_scale=None, bias=None, cin=None, beta=0.0, pre=Non
 
 # the last two are large enough for the split form's 128 x 128 and 128 x 64 tiles
 # (1001, 38, 96): a width not a multiple of 4 (the short-K kernel's per-element
-# epilogue) and 12 k groups a row (its rows padded to 16 lanes)
+# epilogue) and 12 k groups a row (its rows padded to 16 lanes); (3, 130, 64),
+# (5, 130, 128): fewer rows than one block, most XCDs' row ranges empty
 SHAPES = [(1, 16, 16), (37, 40, 32), (300, 128, 128), (2049, 96, 256), (5000, 384, 128), (1000, 1024, 512),
-          (129, 64, 1024), (16385, 1024, 64), (131071, 96, 64), (1001, 38, 96)]
+          (129, 64, 1024), (16385, 1024, 64), (131071, 96, 64), (1001, 38, 96), (3, 130, 64), (5, 130, 128)]
 
 
 @pytest.mark.parametrize("split", [False, True, "smallk"], ids=["fp32", "split", "smallk"])
