@@ -163,8 +163,9 @@ PET_ATTN_API int pet_linear_fused_split_ws(int M, int N, int K, const float* A, 
  * W [N, K] given by pet_linear_pair_weights as rows of three fp16 parts (W's
  * rows each scaled by a power of two and split into hi, mid and lo, which sum
  * to it exactly; N * K * 6 + N * 4 bytes, 16-byte aligned), A fp32 (lda a
- * multiple of 4, 16-byte aligned), epilogue as pet_linear_fused. Each
- * workgroup keeps 64 rows of A in registers as fp16 pairs and runs five part
+ * multiple of 4, 16-byte aligned), epilogue as pet_linear_fused. The weights
+ * of a wave's output columns stay in its registers; a workgroup splits each
+ * 16-row block of A into fp16 pairs once for its four waves and runs five part
  * products on the 16-bit matrix cores (all but a_lo b_lo), so a row's results
  * depend on that row alone (not on M or the tiling) and repeat bit for bit. No counterpart in
  * the reference, which runs these layers in fp32 (src/fused_gemm_hip.cpp). */
