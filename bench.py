@@ -448,6 +448,34 @@ def main():
         extra["access_floor_note"] = ("pet_attn_access_floor: the fp16-pair kernels' grid, item order and bytes with "
                                       "no arithmetic; the floor their traffic sets on this device")
         del mp, mlp, qap, cfhp
+    # the same step recorded once as a HIP graph and replayed K times: the
+    # kernels and their bytes unchanged, the launches' host and queue overhead
+    # gone (`value` stays the eager calls')
+    try:
+        gs = torch.cuda.Stream()
+        gs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(gs):
+            step()
+            step()
+        torch.cuda.current_stream().wait_stream(gs)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(5):
+            graph.replay()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        g0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        extra["graph_step_us"] = g0.elapsed_time(g1) * 1e3 / args.steps
+        del graph
+    except Exception as ex:  # a measurement aside: report, do not fail the bench
+        extra["graph_step_us"] = None
+        extra["graph_step_note"] = f"not recorded: {ex}"
     # the box's achievable streaming rate, for scale: a plain 1 GiB device copy
     # (read + write) timed the same way; the roofline stays against 8 TB/s
     src = torch.empty(1 << 28, device=device)
