@@ -638,7 +638,11 @@ __global__ void attn_cf_adjoint_kernel(const float* __restrict__ cfh, const floa
   if (i >= int64_t(N) * S) return;
   const int n = int(i / S), k = int(i - int64_t(n) * S);
   const float cf = cf_seq[int64_t(n) * ldc + k];
-  // the heads' loads issued eight at a time (with cf's), then summed in head order
+  // the old value loaded with cf (in bounds either way), so that it does not
+  // wait on cf's test; the heads' loads issued eight at a time, then summed in
+  // head order
+  float* out = cf_seq_adj + int64_t(n) * ldca + k;
+  const float old = *out;
   const float* p = cfh + int64_t(n) * H * S + k;
   float total = 0.f;
   int hh = 0;
@@ -650,7 +654,7 @@ __global__ void attn_cf_adjoint_kernel(const float* __restrict__ cfh, const floa
     for (int u = 0; u < 8; ++u) total += v[u];
   }
   for (; hh < H; ++hh) total += p[int64_t(hh) * S];
-  if (cf > 0.f) cf_seq_adj[int64_t(n) * ldca + k] += total / cf;
+  if (cf > 0.f) *out = old + total / cf;
 }
 
 // A capacity's dead rows, N + off[N] .. T-1, of x[T, width] set to zero
