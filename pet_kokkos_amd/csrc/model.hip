@@ -323,6 +323,54 @@ __global__ void message_bwd_kernel(float* __restrict__ efa, const float* __restr
 
 __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 
+// The 16-byte forms of gather_rows_kernel, compress_kernel, concat_kernel
+// and concat_bwd_kernel (rows of W4 float4 groups, rows4_ok): each thread
+// takes whole groups, with the same arithmetic per element as the scalar
+// forms below, and no 64-bit division an element.
+__global__ void gather_rows4_kernel(float4* __restrict__ out, const float4* __restrict__ table,
+                                    const int* __restrict__ idx, int64_t R, int W4) {
+  ROWS4_LOOP(r, c, R, W4) out[r * W4 + c] = table[int64_t(idx[r]) * W4 + c];
+}
+__global__ void compress4_kernel(float4* __restrict__ sav, float4* __restrict__ out, int gemm,
+                                 const float4* __restrict__ b, const float4* __restrict__ tab,
+                                 const int* __restrict__ nsp, const float4* __restrict__ wx,
+                                 const double* __restrict__ vec, const double* __restrict__ dist, int64_t E, int W4) {
+  ROWS4_LOOP(k, c, E, W4) {
+    const float e0 = float(vec[3 * k]), e1 = float(vec[3 * k + 1]), e2 = float(vec[3 * k + 2]), e3 = float(dist[k]);
+    const int64_t i = k * W4 + c;
+    const float4 g = gemm ? out[i] : make_float4(0.f, 0.f, 0.f, 0.f), bb = b[c], t = tab[int64_t(nsp[k]) * W4 + c];
+    const float gv[4] = {g.x, g.y, g.z, g.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w}, tv[4] = {t.x, t.y, t.z, t.w};
+    float z[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 w = wx[4 * c + u];  // column 4 c + u's four weights
+      z[u] = (gemm ? gv[u] : 0.0f) + bv[u] + tv[u] + w.x * e0 + w.y * e1 + w.z * e2 + w.w * e3;
+    }
+    sav[i] = make_float4(z[0], z[1], z[2], z[3]);
+    out[i] = make_float4(z[0] * sig_exact(z[0]), z[1] * sig_exact(z[1]), z[2] * sig_exact(z[2]),
+                         z[3] * sig_exact(z[3]));
+  }
+}
+__global__ void concat4_kernel(float4* __restrict__ concat, float4* __restrict__ ie, const float4* __restrict__ oe,
+                               const int* __restrict__ rev, int64_t E, int W4) {
+  ROWS4_LOOP(k, c, E, W4) {
+    const int r = rev[k];
+    const int64_t i = k * W4 + c;
+    const float4 v = oe[i];
+    ie[i] = add4(ie[i], v);
+    concat[k * 2 * W4 + c] = v;
+    concat[k * 2 * W4 + W4 + c] = r >= 0 ? oe[int64_t(r) * W4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+__global__ void concat_bwd4_kernel(float4* __restrict__ edge_adj, const float4* __restrict__ ie_adj,
+                                   const float4* __restrict__ ca, const int* __restrict__ rev, int64_t E, int W4) {
+  ROWS4_LOOP(k, c, E, W4) {
+    const int r = rev[k];
+    const float4 back = r >= 0 ? ca[int64_t(r) * 2 * W4 + W4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    edge_adj[k * W4 + c] = add4(add4(ie_adj[k * W4 + c], ca[k * 2 * W4 + c]), back);
+  }
+}
+
 __global__ void fill_rows4_kernel(float4* __restrict__ out, const float4* __restrict__ b, int64_t R, int W4) {
   ROWS4_LOOP(r, c, R, W4) out[r * W4 + c] = b ? b[c] : make_float4(0.f, 0.f, 0.f, 0.f);
 }
@@ -847,6 +895,13 @@ void swiglu_bwd(pet_model& md, float* z_adj, const float* h_adj, const float* z,
   launched();
 }
 // The elementwise passes: the float4 kernels where the width and alignment allow.
+// out[r, :] = table[idx[r], :] for R rows of W floats (16 bytes a thread where the rows allow)
+void gather_rows(float* out, const float* table, const int* idx, int64_t R, int W, hipStream_t st) {
+  if (rows4_ok(W, {out, table}))
+    hipLaunchKernelGGL(gather_rows4_kernel, grid_rows4(R, W / 4), dim3(256), 0, st, v4(out), v4(table), idx, R, W / 4);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel, grid_for(R * W), dim3(256), 0, st, out, table, idx, R, W);
+}
 void residual_pass(float* sv, float* out, const float* a, const float* c, const float* b, int64_t R, int W,
                    hipStream_t st) {
   if (R == 0) return;
@@ -1069,8 +1124,12 @@ struct Pass {
     sv.concat = md.f(int64_t(E) * 2 * D), sv.cph = md.f(int64_t(E) * 2 * D);
     auto scope = md.ws.mark();
     if (E) {
-      hipLaunchKernelGGL(concat_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, sv.concat, input_edge, out_edge,
-                         e.reverse, int64_t(E), D);
+      if (rows4_ok(D, {sv.concat, input_edge, out_edge}))
+        hipLaunchKernelGGL(concat4_kernel, grid_rows4(E, D / 4), dim3(256), 0, st, v4(sv.concat), v4(input_edge),
+                           v4(out_edge), e.reverse, int64_t(E), D / 4);
+      else
+        hipLaunchKernelGGL(concat_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, sv.concat, input_edge, out_edge,
+                           e.reverse, int64_t(E), D);
       launched();
     }
     const std::string c0 = "combination_mlps." + ls + ".0", c2 = "combination_mlps." + ls + ".2";
@@ -1126,8 +1185,12 @@ struct Pass {
       ok(pet_norm_rows_bwd(E, 2 * D, ca, 2 * D, 0.0f, cn_adj, 2 * D, sv.concat, 2 * D,
                            md.p("combination_norms." + ls + ".weight"), 1, st));
       if (E) {
-        hipLaunchKernelGGL(concat_bwd_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, edge_adj, ie_adj, ca,
-                           e.reverse, int64_t(E), D);
+        if (rows4_ok(D, {edge_adj, ie_adj, ca}))
+          hipLaunchKernelGGL(concat_bwd4_kernel, grid_rows4(E, D / 4), dim3(256), 0, st, v4(edge_adj), v4(ie_adj),
+                             v4(ca), e.reverse, int64_t(E), D / 4);
+        else
+          hipLaunchKernelGGL(concat_bwd_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, edge_adj, ie_adj, ca,
+                             e.reverse, int64_t(E), D);
         launched();
       }
       md.ws.release(s2);
@@ -1301,9 +1364,13 @@ struct Pass {
     float* cact = md.f(int64_t(E) * D);
     if (L > 0) ok(gemm_w(md, cact, D, input_edge, D, md.p(c0 + "@in"), E, D, D, 0.0f, st));
     if (E) {
-      hipLaunchKernelGGL(compress_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, cpre, cact, L > 0 ? 1 : 0,
-                         md.p(c0 + "@b"), md.p(c0 + "@tab"), e.neigh_species, md.p(c0 + "@x4"), e.vec, e.dist,
-                         int64_t(E), D);
+      const float *cb = md.p(c0 + "@b"), *ctab = md.p(c0 + "@tab"), *cx4 = md.p(c0 + "@x4");
+      if (rows4_ok(D, {cpre, cact, cb, ctab, cx4}))
+        hipLaunchKernelGGL(compress4_kernel, grid_rows4(E, D / 4), dim3(256), 0, st, v4(cpre), v4(cact), L > 0 ? 1 : 0,
+                           v4(cb), v4(ctab), e.neigh_species, v4(cx4), e.vec, e.dist, int64_t(E), D / 4);
+      else
+        hipLaunchKernelGGL(compress_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, cpre, cact, L > 0 ? 1 : 0, cb,
+                           ctab, e.neigh_species, cx4, e.vec, e.dist, int64_t(E), D);
       launched();
     }
     linear(md, et, cact, E, D, g(L) + ".compress.2", st);
@@ -1343,8 +1410,7 @@ struct Pass {
   void residual_layer_fwd(int L, const float* input_edge, RLayer& sv) {
     sv.tokens = md.f(int64_t(T) * D), sv.cpre = md.f(int64_t(E) * D);
     if (N) {
-      hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(N) * D), dim3(256), 0, st, sv.tokens,
-                         md.p("node_embedders." + std::to_string(L) + ".weight"), e.species, int64_t(N), D);
+      gather_rows(sv.tokens, md.p("node_embedders." + std::to_string(L) + ".weight"), e.species, N, D, st);
       launched();
     }
     compress_fwd(L, input_edge, sv.cpre, sv.tokens + int64_t(N) * D);
@@ -1420,8 +1486,7 @@ struct Pass {
     ok(pet_attn_cf_seq(&sh, e.off, e.cut, cf_seq, S, st));
     float* input_edge = md.f(int64_t(E) * D);
     if (E) {
-      hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(E) * D), dim3(256), 0, st, input_edge,
-                         md.p("edge_embedder.weight"), e.neigh_species, int64_t(E), D);
+      gather_rows(input_edge, md.p("edge_embedder.weight"), e.neigh_species, E, D, st);
       launched();
     }
     float* net = md.f(N);
@@ -1445,8 +1510,7 @@ struct Pass {
     } else {
       float* node = md.f(int64_t(N) * Dn);
       if (N) {
-        hipLaunchKernelGGL(gather_rows_kernel, grid_for(int64_t(N) * Dn), dim3(256), 0, st, node,
-                           md.p("node_embedders.0.weight"), e.species, int64_t(N), Dn);
+        gather_rows(node, md.p("node_embedders.0.weight"), e.species, N, Dn, st);
         launched();
       }
       for (int L = 0; L < G; ++L) layer_fwd(L, node, input_edge, sv[L]);
